@@ -1,0 +1,157 @@
+/*
+ * megamoe.h — C ABI of the MI355X (gfx950) FP8 mixture-of-experts decode layer.
+ *
+ * One call computes, for T tokens, the MoE block that the reference composes
+ * in eager PyTorch:
+ *
+ *   router logits  = fp32(router) @ fp32(x)                 megabench/tasks/frontier.py:343
+ *   routing        = sigmoid + bias, group-limited top-k,   megabench/tasks/frontier.py:229-242
+ *                    or softmax over the top-k logits       megabench/tasks/references/moe.py:68-70,
+ *                                                           megabench/tasks/distributed.py:174-176
+ *   per (token, slot) expert:  W8A8 linear (FP8 E4M3, 128x128 block scales,
+ *                    per-token-per-128 activation scales)   megabench/tasks/frontier.py:180-186,
+ *                                                           megabench/tasks/quantization.py:87-131
+ *                    h = bf16(silu(fp32 g) * fp32 u)        megabench/tasks/frontier.py:337
+ *   combine        = slot-order fp32 sum of bf16(d)*w, plus the shared expert,
+ *                    one bf16 rounding                      megabench/tasks/frontier.py:349-354
+ *
+ * The reference has no native code on this path: each entry point below
+ * replaces a sequence of eager aten calls inside the case's reference(), and
+ * the Python submission that calls it keeps the reference harness contract
+ * build(case) -> run(inputs) -> outputs (megabench/README.md:83-104,
+ * megabench/harness/runner.py:69-87).
+ *
+ * Conventions: all pointers are device pointers unless stated otherwise.
+ * Every call is asynchronous on `stream` (a hipStream_t passed as void*;
+ * NULL is the default stream), allocates nothing and throws nothing. Each
+ * returns a megamoe_status code.
+ */
+#ifndef MEGAMOE_H
+#define MEGAMOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum megamoe_status {
+  MEGAMOE_OK = 0,
+  MEGAMOE_ERR_INVALID_ARGUMENT = 1, /* a required pointer is NULL or a count is negative */
+  MEGAMOE_ERR_SHAPE = 2,            /* geometry the layer does not define (H or I not a multiple of 128, K > E, ...) */
+  MEGAMOE_ERR_WORKSPACE = 3,        /* workspace smaller than megamoe_workspace_bytes() */
+  MEGAMOE_ERR_HIP = 4,              /* a HIP runtime call or kernel launch failed */
+  MEGAMOE_ERR_UNSUPPORTED = 5       /* within the layer's definition but beyond this build's limits */
+};
+
+enum megamoe_gate {
+  MEGAMOE_GATE_SOFTMAX = 0, /* ids = top-k logits (stable); w = softmax over the selected logits (renormalize=1)
+                               or the full softmax at the selected ids (renormalize=0) */
+  MEGAMOE_GATE_SIGMOID = 1  /* p = sigmoid(logits); ids chosen on p + bias (group-limited);
+                               w = p[ids] / (sum + 1e-20) when renormalize=1, else p[ids] */
+};
+
+/* Geometry and routing rule of one MoE layer. The same struct describes
+ * every entry point; fields an entry point does not use are ignored. */
+typedef struct megamoe_desc {
+  int32_t tokens;         /* T >= 0 */
+  int32_t hidden;         /* H, multiple of 128 */
+  int32_t experts;        /* E routed experts, 1..1024 */
+  int32_t topk;           /* K, 1..min(E, 32) */
+  int32_t intermediate;   /* I of one routed expert, multiple of 128 */
+  int32_t shared_experts; /* S >= 0; the shared expert is one MLP of intermediate S*I */
+  int32_t groups;         /* G, divides E; 1 disables group limiting */
+  int32_t top_groups;     /* groups kept, 1..G */
+  int32_t gate;           /* enum megamoe_gate */
+  int32_t renormalize;    /* see enum megamoe_gate */
+  int32_t pow2_scales;    /* 1: activation scales rounded up to a power of two
+                             (quantization.py:57-59 power_of_two=True) */
+  float routed_scaling;   /* multiplies every routed weight (frontier.py:242) */
+} megamoe_desc;
+
+/* Tensors of one forward call. Layouts are row-major and dense, exactly as
+ * the case's inputs hold them (frontier.py:157-176 for the expert stacks):
+ *   x              bf16 [T, H]
+ *   router         fp32 [E, H]
+ *   router_bias    fp32 [E] or NULL (treated as zero)
+ *   gate, up       e4m3fn [E, I, H];  gate_scale, up_scale fp32 [E, I/128, H/128]
+ *   down           e4m3fn [E, H, I];  down_scale          fp32 [E, H/128, I/128]
+ *   shared_gate, shared_up  e4m3fn [S*I, H]; scales fp32 [S*I/128, H/128]
+ *   shared_down             e4m3fn [H, S*I]; scale  fp32 [H/128, S*I/128]
+ *   y              bf16 [T, H]     (output)
+ *   expert_ids     int64 [T, K]    (output, selection order)
+ *   expert_weights fp32 [T, K]     (output)
+ * Inputs are only read. The workspace holds intermediates between the
+ * kernels of one call; it needs no initialisation. */
+typedef struct megamoe_tensors {
+  const void* x;
+  const float* router;
+  const float* router_bias;
+  const uint8_t* gate;
+  const float* gate_scale;
+  const uint8_t* up;
+  const float* up_scale;
+  const uint8_t* down;
+  const float* down_scale;
+  const uint8_t* shared_gate;
+  const float* shared_gate_scale;
+  const uint8_t* shared_up;
+  const float* shared_up_scale;
+  const uint8_t* shared_down;
+  const float* shared_down_scale;
+  void* y;
+  int64_t* expert_ids;
+  float* expert_weights;
+  void* workspace;
+  size_t workspace_bytes;
+} megamoe_tensors;
+
+/* Bytes of device workspace megamoe_forward needs for `desc` (host call).
+ * No reference counterpart: the reference allocates through PyTorch. */
+int megamoe_workspace_bytes(const megamoe_desc* desc, size_t* bytes);
+
+/* The whole layer: router, routing, permute, gate/up + SwiGLU, down, combine.
+ * Replaces the MoE block of megabench/tasks/frontier.py:335-354 (sigmoid
+ * configs) and megabench/tasks/references/moe.py:66-78 (softmax configs). */
+int megamoe_forward(const megamoe_desc* desc, const megamoe_tensors* t, void* stream);
+
+/* megamoe_forward with a device event between its stages; blocks until the
+ * call has finished and writes the elapsed ms of each stage to stage_ms[0..5]
+ * (router+quantize, select, permute, gate/up, down, combine). For
+ * measurement; the results equal megamoe_forward's. */
+int megamoe_forward_timed(const megamoe_desc* desc, const megamoe_tensors* t, void* stream,
+                          float* stage_ms);
+
+/* Router logits only: logits fp32 [T, E] = router @ x, with fp64 accumulation
+ * rounded once to fp32. `workspace` as for megamoe_forward.
+ * Replaces `values['router'].float() @ normalized.float()` (frontier.py:343). */
+int megamoe_router_logits(const megamoe_desc* desc, const void* x, const float* router, float* logits,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
+/* Routing from given logits fp32 [T, E]: expert_ids int64 [T, K] and
+ * expert_weights fp32 [T, K]. bias may be NULL.
+ * Replaces frontier.route (frontier.py:229-242) applied per token and the
+ * stable-argsort softmax routing of distributed.py:174-176. */
+int megamoe_route(const megamoe_desc* desc, const float* logits, const float* bias, int64_t* expert_ids,
+                  float* expert_weights, void* stream);
+
+/* Dynamic E4M3 quantization of bf16 rows [rows, cols] with one fp32 scale
+ * per row per 128 columns (the last block may be partial; padding counts as
+ * zero): q e4m3fn [rows, cols], scales fp32 [rows, ceil(cols/128)].
+ * Replaces pack_fp8_activation(value, power_of_two=pow2)
+ * (megabench/tasks/quantization.py:87-109, scale_format="float"). */
+int megamoe_quantize_rows(int32_t rows, int32_t cols, const void* x, uint8_t* q, float* scales,
+                          int32_t pow2, void* stream);
+
+/* Text for a status code (static storage). */
+const char* megamoe_status_string(int status);
+
+/* ABI version of this library: 1. */
+int megamoe_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MEGAMOE_H */

@@ -1,0 +1,112 @@
+"""The FP8 MoE decode layer on the CPU, restated with the reference's rounding points
+(test infrastructure).
+
+Per token t (megabench/tasks/frontier.py:343-354, with ``linear`` of :180-186):
+    scores      = fp32(router) @ fp32(x[t])                       (one GEMV per token)
+    ids, w      = route(scores, bias)                              oracle/routing.py
+    for slot, e in enumerate(ids):
+        xq, xs  = E4M3 per 128 of x[t]                             quantization.py:87-109
+        g, u    = bf16(deq(W_gate[e]) @ deq(xq, xs)), same for up  frontier.py:184-186
+        h       = bf16(silu(fp32 g) * fp32 u)                      frontier.py:337
+        d       = bf16(deq(W_down[e]) @ deq(E4M3 per 128 of h))
+        acc     = acc + fp32(d) * w[slot]                          frontier.py:349-350
+    acc = acc + fp32(shared expert output)                          frontier.py:352
+    y[t] = bf16(acc)                                                frontier.py:354 (without
+                                                                    the residual add)
+
+Softmax-routed cases use the same expert math with the routing of
+megabench/tasks/references/moe.py:68-70.
+
+The loops run per expert rather than per slot so each expert's weights are
+dequantized once; every per-row product is still the same GEMV call the
+reference makes per token, so the bits do not change. ``widen=True`` is the
+FP32 oracle of megabench/tasks/oracle.py: the same graph with every BF16
+rounding removed and the FP8 payloads and scales kept.
+
+Pinned by tests/test_oracle_layer.py: an fp64 brute-force restatement on tiny
+shapes, linearity and zero-expert invariants, and the golden fixtures written
+by tests/golden/make_golden.py from the reference's own ``route``,
+``linear`` and FP8 packers.
+"""
+
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+
+from . import formats
+from .routing import route
+
+
+def _linear(w_deq: torch.Tensor, act: torch.Tensor, power_of_two: bool, out_dtype) -> torch.Tensor:
+    """frontier.linear with the weight already dequantized: W8A8, fp32 GEMV, one rounding."""
+    payload, scales = formats.pack_activation(act, power_of_two)
+    return (w_deq @ formats.unpack_activation(payload, scales)).to(out_dtype)
+
+
+def _swiglu(g: torch.Tensor, u: torch.Tensor, out_dtype) -> torch.Tensor:
+    return (F.silu(g.float()) * u.float()).to(out_dtype)
+
+
+def _expert(values, name: str, index=None):
+    q, s = values[name], values[name + "_scale"]
+    if index is not None:
+        q, s = q[index], s[index]
+    return formats.unpack_weight(q, s)
+
+
+@torch.no_grad()
+def moe_layer(case, values: dict, *, widen: bool = False, tokens=None) -> dict:
+    """Outputs {'y', 'expert_ids', 'expert_weights'} for ``tokens`` (default: all)."""
+    bf = torch.float32 if widen else torch.bfloat16
+    pw = case.power_of_two
+    x = values["x"].cpu()
+    rows = list(range(x.shape[0])) if tokens is None else list(tokens)
+    router = values["router"].cpu().float()
+    bias = values.get("router_bias")
+    bias = None if bias is None else bias.cpu()
+    act = x.to(bf)
+
+    ids, weights = [], []
+    for t in rows:
+        i, w = route(case, router @ act[t].float(), bias)
+        ids.append(i)
+        weights.append(w)
+    ids_t = torch.stack(ids) if rows else torch.empty((0, case.topk), dtype=torch.int64)
+    w_t = torch.stack(weights) if rows else torch.empty((0, case.topk), dtype=torch.float32)
+
+    H = x.shape[1]
+    down = {}  # (row index, slot) -> bf16 [H]
+    cpu = {k: v.cpu() for k, v in values.items() if k != "x"}
+    for e in sorted(set(ids_t.flatten().tolist())):
+        wg, wu, wd = _expert(cpu, "gate", e), _expert(cpu, "up", e), _expert(cpu, "down", e)
+        for r, t in enumerate(rows):
+            for slot in (ids_t[r] == e).nonzero().flatten().tolist():
+                h = _swiglu(_linear(wg, act[t], pw, bf), _linear(wu, act[t], pw, bf), bf)
+                down[(r, slot)] = _linear(wd, h, pw, bf)
+    shared = {}
+    if case.shared_experts:
+        wg, wu, wd = _expert(cpu, "shared_gate"), _expert(cpu, "shared_up"), _expert(cpu, "shared_down")
+        for r, t in enumerate(rows):
+            h = _swiglu(_linear(wg, act[t], pw, bf), _linear(wu, act[t], pw, bf), bf)
+            shared[r] = _linear(wd, h, pw, bf)
+
+    y = torch.empty((len(rows), H), dtype=bf)
+    for r in range(len(rows)):
+        acc = torch.zeros(H, dtype=torch.float32)
+        for slot in range(case.topk):
+            acc = acc + down[(r, slot)].float() * w_t[r, slot]
+        if case.shared_experts:
+            acc = acc + shared[r].float()
+        y[r] = acc.to(bf)
+    return {"y": y, "expert_ids": ids_t, "expert_weights": w_t}
+
+
+def reference(case, values: dict, **kw) -> dict:
+    """BF16 rounding schedule of the reference (the graded ``reference``)."""
+    return moe_layer(case, values, widen=False, **kw)
+
+
+def oracle(case, values: dict, **kw) -> dict:
+    """FP32 oracle: the same graph without BF16 rounding (megabench/tasks/oracle.py:51-53)."""
+    return moe_layer(case, values, widen=True, **kw)

@@ -1,0 +1,155 @@
+"""GPU parity of the HIP layer against the CPU oracle, through the C ABI.
+
+Bars: expert ids bit-exact; expert weights within 2e-6 relative (fp32, ulp-level
+differences of expf and the order of a K-term sum); y within the band rule of
+megabench/harness/correctness.py:64-85 against the FP32 oracle and within
+max|y - y_ref| / max|y_ref| <= 1e-2 and cosine >= 0.9999 against the BF16
+reference schedule. Quantization and router logits are bit-exact.
+"""
+
+from __future__ import annotations
+
+import sys
+
+import pytest
+import torch
+
+from oracle import formats, layer, metrics, routing
+from vibe_megakernel_amd import cases as C
+from vibe_megakernel_amd import submission, workloads
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+W_RTOL = 2e-6
+
+
+def _log(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def _dev_cases():
+    out = [C.case("moe-fp8-tiny-t4")]
+    for c in C.CASES:
+        out.append(C.development(c))
+    out.append(C.development(C.case(C.HEADLINE), tokens=37))  # ragged token count, multi-row experts
+    out.append(C.development(C.case("moe-fp8-kimi-k2-t128"), tokens=70, experts=8, topk=4))  # hot experts > 16 rows
+    return out
+
+
+def _to(values, device):
+    return {k: v.to(device) for k, v in values.items()}
+
+
+def _compare(case, got, want, exact, rows=None):
+    ids = got["expert_ids"].cpu()
+    w = got["expert_weights"].cpu()
+    y = got["y"].cpu()
+    if rows is not None:
+        ids, w, y = ids[rows], w[rows], y[rows]
+    assert torch.equal(ids, want["expert_ids"]), f"{case.id}: expert ids differ"
+    torch.testing.assert_close(w, want["expert_weights"], rtol=W_RTOL, atol=0)
+    check = metrics.layer_checks(y, want["y"])
+    assert check["pass"], f"{case.id}: {check}"
+    band = metrics.band(want["y"], y, exact["y"], bf16_rtol=case.bf16_rtol, noise_factor=case.noise_factor)
+    assert band["pass"], f"{case.id}: band {band}"
+    return check, band
+
+
+@pytest.mark.parametrize("case", _dev_cases(), ids=lambda c: c.id)
+def test_layer_matches_oracle_on_development_geometry(case):
+    _log(f"layer parity {case.id} T={case.tokens} H={case.hidden} E={case.experts} K={case.topk}")
+    for seed in (104729, 104730):
+        values = workloads.make_inputs(case, seed, "cpu")
+        want, exact = layer.reference(case, values), layer.oracle(case, values)
+        run = submission.build(case.to_dict())
+        got = run(_to(values, DEV))
+        torch.cuda.synchronize()
+        _compare(case, got, want, exact)
+
+
+def test_layer_is_deterministic_and_does_not_mutate_inputs():
+    case = C.development(C.case(C.HEADLINE), tokens=24)
+    _log(f"determinism {case.id}")
+    values = _to(workloads.make_inputs(case, 11, "cpu"), DEV)
+    before = {k: v.clone() for k, v in values.items()}
+    run = submission.build(case.to_dict())
+    a, b = run(values), run(values)
+    torch.cuda.synchronize()
+    for k in a:
+        assert torch.equal(a[k], b[k]), k
+    for k, v in values.items():
+        assert torch.equal(v.view(torch.uint8) if v.dtype == torch.float8_e4m3fn else v,
+                           before[k].view(torch.uint8) if v.dtype == torch.float8_e4m3fn else before[k]), k
+
+
+@pytest.mark.parametrize("pow2", [False, True])
+def test_quantize_rows_bit_exact(pow2):
+    _log(f"quantize_rows pow2={pow2}")
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn((37, 300), generator=g) * torch.logspace(-6, 3, 37)[:, None]
+    edges = torch.tensor([448., 448.00003, 447.99997, 224., 1e-4, 1e-6, 0., 2.0 ** -22 * 448, 896., -0.0])
+    x[:len(edges), 0] = edges
+    x = x.to(torch.bfloat16)
+    q, s = submission.quantize_rows(x.to(DEV), power_of_two=pow2)
+    wq, ws = formats.pack_activation(x, power_of_two=pow2)
+    assert torch.equal(s.cpu(), ws)
+    assert torch.equal(q.cpu().view(torch.uint8), wq.view(torch.uint8))
+
+
+@pytest.mark.parametrize("cid", [c.id for c in C.CASES])
+def test_router_logits_are_correctly_rounded(cid):
+    case = C.case(cid)
+    _log(f"router logits {cid}")
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn((case.tokens, case.hidden), generator=g).to(torch.bfloat16)
+    w = torch.randn((case.experts, case.hidden), generator=g) * 0.02
+    got = submission.router_logits(case, x.to(DEV), w.to(DEV)).cpu()
+    want = (w.double() @ x.double().T).T.float()
+    assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("cid", [c.id for c in C.CASES])
+def test_route_from_logits_matches_oracle_including_ties(cid):
+    case = C.case(cid)
+    _log(f"route {cid}")
+    g = torch.Generator().manual_seed(7)
+    T, E = 64, case.experts
+    logits = torch.randn((T, E), generator=g) * 1.7
+    # Ties: quantize half of the rows to a coarse grid so many scores coincide.
+    logits[: T // 2] = (logits[: T // 2] * 2).round() / 2
+    logits[0] = 0.0
+    bias = workloads.router_bias(case, 1, "cpu")
+    if bias is not None:
+        bias[: E // 2] = bias[E // 2: 2 * (E // 2)]  # equal biases on paired experts
+    tc = C.Case.from_dict({**case.to_dict(), "params": {**case.params, "tokens": T}})
+    ids, w = submission.route(tc, logits.to(DEV), None if bias is None else bias.to(DEV))
+    for t in range(T):
+        wi, ww = routing.route(tc, logits[t], bias)
+        assert torch.equal(ids[t].cpu(), wi), f"token {t}"
+        torch.testing.assert_close(w[t].cpu(), ww, rtol=W_RTOL, atol=0)
+
+
+@pytest.mark.parametrize("cid", [c.id for c in C.CASES if c.id != "moe-fp8-tiny-t4"])
+def test_full_size_layer_on_sampled_tokens(cid):
+    """BASELINE.json geometry, inputs generated on the GPU; ids of every token and y of
+    three sampled tokens (each token's output depends only on its own row) against the
+    oracle."""
+    case = C.case(cid)
+    _log(f"full size {cid}")
+    values = workloads.make_inputs(case, 104729, DEV)
+    got = submission.build(case.to_dict())(values)
+    torch.cuda.synchronize()
+    cpu = {k: v.cpu() for k, v in values.items()}
+    del values
+    torch.cuda.empty_cache()
+    # Routing of every token.
+    x = cpu["x"].float()
+    for t in range(case.tokens):
+        wi, ww = routing.route(case, cpu["router"] @ x[t], cpu.get("router_bias"))
+        assert torch.equal(got["expert_ids"][t].cpu(), wi), f"token {t}"
+        torch.testing.assert_close(got["expert_weights"][t].cpu(), ww, rtol=W_RTOL, atol=0)
+    rows = [0, case.tokens // 2, case.tokens - 1]
+    want, exact = layer.reference(case, cpu, tokens=rows), layer.oracle(case, cpu, tokens=rows)
+    check, band = _compare(case, got, want, exact, rows=rows)
+    _log(f"  {cid}: {check} band_rel={band['relative_error']:.3e} ref_rel={band['reference_relative_error']:.3e}")

@@ -1,0 +1,218 @@
+"""Case family of the FP8 MoE decode layer.
+
+The case record keeps the shape of the reference's ``Case`` contract
+(megabench/cases.py:19-113: id, family, model, phase, params, tolerances,
+execution geometry, launch budget, band gate) so a ``build(case.to_dict())``
+call looks exactly like the reference harness's (megabench/harness/runner.py:
+80-87). The reference catalog has no FP8 MoE-layer cases; the five configs
+below are the ones this layer is measured on, with routing parameters taken
+from each model's published configuration:
+
+* Mixtral / Qwen3-30B-A3B: softmax over the top-k logits (== softmax over all
+  experts, then renormalised), megabench/tasks/references/moe.py:68-70,
+  megabench/tasks/model_specs.json:24 (``norm_topk_prob``).
+* DeepSeek-V3: sigmoid + correction bias, 8 groups / top-4 groups / top-8,
+  routed scaling 2.5 (megabench/tasks/model_specs.json:171,204-207).
+* Kimi-K2: sigmoid + correction bias, one group (group limit trivially met,
+  as in the reference's Kimi use of ``frontier.route(..., 1, 1, ...)``,
+  megabench/tasks/kimi_layer.py:200), routed scaling 2.827; the bias is a
+  Zipf(s=1.1) profile over a seeded expert permutation, so a few experts are
+  hot.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import asdict, dataclass, field, replace
+
+FAMILY = "moe_fp8_layer"
+ROUTERS = ("softmax", "sigmoid")
+BIASES = ("none", "normal", "zipf")
+GATES = ("band",)
+
+
+@dataclass(frozen=True)
+class Case:
+    """One MoE decode-layer problem (fields as megabench/cases.py:19-56, plus routing)."""
+
+    id: str
+    family: str
+    model: str
+    phase: str
+    params: dict
+    category: str = "layer"
+    suite: str = "p1"
+    backend: str = "hip"
+    gpus: int = 1
+    tp: int = 1
+    ep: int = 1
+    # The layer runs as six stream-ordered kernels (router+quantize, select,
+    # permute, gate/up, down, combine) plus the x quantization kernel.
+    max_gpu_launches: int = 7
+    atol: float = 0.0
+    rtol: float = 0.0
+    bf16_rtol: float = 0.008
+    noise_factor: float = 2.0
+    ready: bool = True
+    note: str = ""
+    gate: str = "band"
+    # Routing rule (not part of the reference Case; the reference fixes it per task module).
+    router: str = "softmax"
+    renormalize: bool = True
+    routed_scaling: float = 1.0
+    bias: str = "none"
+    bias_std: float = 0.1
+    zipf_s: float = 1.1
+    zipf_c: float = 1.0
+    power_of_two: bool = False
+    weight_std: float = 0.02
+    router_std: float = 0.02
+
+    def __post_init__(self) -> None:
+        if not self.id or self.family != FAMILY or not self.model or not self.phase:
+            raise ValueError(f"invalid case {self.id}")
+        p = self.params
+        for name in ("tokens", "hidden", "experts", "topk", "intermediate"):
+            if name not in p:
+                raise ValueError(f"{self.id}: missing param {name}")
+        if any(isinstance(v, bool) or not isinstance(v, int) or v < 1 for v in p.values()):
+            raise ValueError(f"invalid dimensions in {self.id}")
+        if min(self.gpus, self.tp, self.ep, self.max_gpu_launches) < 1:
+            raise ValueError(f"invalid execution geometry in {self.id}")
+        if min(self.atol, self.rtol, self.bf16_rtol) < 0 or self.noise_factor < 1:
+            raise ValueError(f"invalid tolerance in {self.id}")
+        if self.suite not in ("p0", "p1", "p2", "p3") or self.gate not in GATES:
+            raise ValueError(f"invalid priority or gate in {self.id}")
+        if self.router not in ROUTERS or self.bias not in BIASES:
+            raise ValueError(f"invalid routing rule in {self.id}")
+        if self.router == "softmax" and self.bias != "none":
+            raise ValueError(f"{self.id}: softmax routing takes no correction bias")
+        groups, top = self.groups, self.top_groups
+        if p["topk"] > p["experts"] or p["experts"] % groups or top > groups:
+            raise ValueError(f"invalid routing geometry in {self.id}")
+        if groups > 1 and top * (p["experts"] // groups) < p["topk"]:
+            raise ValueError(f"{self.id}: kept groups hold fewer than topk experts")
+        object.__setattr__(self, "params", dict(p))
+
+    # -- derived geometry ------------------------------------------------------------
+    @property
+    def tokens(self) -> int:
+        return self.params["tokens"]
+
+    @property
+    def hidden(self) -> int:
+        return self.params["hidden"]
+
+    @property
+    def experts(self) -> int:
+        return self.params["experts"]
+
+    @property
+    def topk(self) -> int:
+        return self.params["topk"]
+
+    @property
+    def intermediate(self) -> int:
+        return self.params["intermediate"]
+
+    @property
+    def shared_experts(self) -> int:
+        return self.params.get("shared_experts", 0)
+
+    @property
+    def groups(self) -> int:
+        return self.params.get("router_groups", 1)
+
+    @property
+    def top_groups(self) -> int:
+        return self.params.get("router_top_groups", 1)
+
+    def to_dict(self) -> dict:
+        values = asdict(self)
+        values["params"] = dict(self.params)
+        return values
+
+    @classmethod
+    def from_dict(cls, values: dict) -> "Case":
+        known = {f for f in cls.__dataclass_fields__}
+        return cls(**{k: v for k, v in values.items() if k in known})
+
+
+def _case(cid: str, model: str, *, note: str = "", **kw) -> Case:
+    return Case(id=cid, family=FAMILY, model=model, phase="decode", note=note, **kw)
+
+
+CASES: tuple[Case, ...] = (
+    _case("moe-fp8-tiny-t4", "tiny-moe",
+          params=dict(tokens=4, hidden=1024, experts=8, topk=2, intermediate=512),
+          router="softmax", renormalize=True,
+          note="CPU-runnable: x ~ N(0,1) bf16, router N(0,0.02) fp32, experts N(0,0.02) E4M3 128x128"),
+    _case("moe-fp8-mixtral-t16", "mistralai/Mixtral-8x7B (MoE shape)",
+          params=dict(tokens=16, hidden=4096, experts=8, topk=2, intermediate=14336),
+          router="softmax", renormalize=True),
+    _case("moe-fp8-qwen3-30b-a3b-t32", "Qwen/Qwen3-30B-A3B (MoE shape)",
+          params=dict(tokens=32, hidden=2048, experts=128, topk=8, intermediate=768),
+          router="softmax", renormalize=True),
+    _case("moe-fp8-deepseek-v3-t64", "deepseek-ai/DeepSeek-V3 (MoE shape)",
+          params=dict(tokens=64, hidden=7168, experts=256, topk=8, intermediate=2048, shared_experts=1,
+                      router_groups=8, router_top_groups=4),
+          router="sigmoid", renormalize=True, routed_scaling=2.5, bias="normal", bias_std=0.1),
+    _case("moe-fp8-kimi-k2-t128", "moonshotai/Kimi-K2 (MoE shape, Zipf-skewed router bias)",
+          params=dict(tokens=128, hidden=7168, experts=384, topk=8, intermediate=2048, shared_experts=1,
+                      router_groups=1, router_top_groups=1),
+          router="sigmoid", renormalize=True, routed_scaling=2.827, bias="zipf", zipf_s=1.1, zipf_c=1.0),
+)
+
+HEADLINE = "moe-fp8-deepseek-v3-t64"
+
+
+def case(case_id: str) -> Case:
+    for c in CASES:
+        if c.id == case_id:
+            return c
+    raise KeyError(case_id)
+
+
+def development(c: Case, **params) -> Case:
+    """Reduced geometry of a catalog case with its routing rule kept.
+
+    Like the reference's development geometries (megabench/verify_megamoe.py:32,
+    megabench/tests/test_frontier.py:17-27): small enough for the CPU oracle to
+    finish in well under a second, large enough to exercise groups, the shared
+    expert and multi-row experts.
+    """
+    p = dict(c.params)
+    small = dict(hidden=256, intermediate=256, experts=min(c.experts, 16), topk=min(c.topk, 4))
+    if c.groups > 1:
+        small.update(router_groups=4, router_top_groups=2)
+    p.update(small)
+    p.update(params)
+    if p.get("router_groups", 1) > 1 and p["experts"] % p["router_groups"]:
+        raise ValueError("development geometry breaks the group split")
+    return replace(c, id=c.id + "-dev", params=p)
+
+
+def algorithmic_bytes(c: Case, hit_experts: int) -> int:
+    """HBM bytes one step must move: weights of the hit experts and the shared expert
+    (E4M3 payload + fp32 128x128 scales), the fp32 router and bias, x and y in bf16,
+    ids (int64) and weights (fp32)."""
+    T, H, E, K, I, S = c.tokens, c.hidden, c.experts, c.topk, c.intermediate, c.shared_experts
+    bh, bi = math.ceil(H / 128), math.ceil(I / 128)
+    per_expert = 3 * I * H + 4 * (2 * bi * bh + bh * bi)
+    shared = 0
+    if S:
+        si = S * I
+        bsi = math.ceil(si / 128)
+        shared = 3 * si * H + 4 * (2 * bsi * bh + bh * bsi)
+    bias = 4 * E if c.router == "sigmoid" else 0
+    return hit_experts * per_expert + shared + 4 * E * H + bias + 2 * T * H + 2 * T * H + 12 * T * K
+
+
+def algorithmic_flops(c: Case) -> int:
+    T, H, E, K, I, S = c.tokens, c.hidden, c.experts, c.topk, c.intermediate, c.shared_experts
+    return 2 * T * E * H + 2 * T * K * 3 * I * H + 2 * T * S * 3 * I * H
+
+
+def expected_hit_experts(c: Case) -> float:
+    """E[U] under uniform routing: E * (1 - (1 - K/E)^T)."""
+    return c.experts * (1.0 - (1.0 - c.topk / c.experts) ** c.tokens)

@@ -1,0 +1,185 @@
+"""Drop-in submission for the reference harness: ``build(case) -> run(inputs) -> outputs``.
+
+The contract is the reference's (megabench/README.md:83-104; loaded by path as
+megabench/harness/runner.py:69-87 does): ``build`` receives ``Case.to_dict()``
+(plus an optional ``execution`` entry, ignored on one GPU), ``run`` takes the
+case's input tensors on the GPU, never mutates them, allocates its outputs and
+returns ``{"y", "expert_ids", "expert_weights"}`` with the dtypes and shapes of
+the reference outputs. All work is issued on torch's current stream through
+the C ABI of libmegamoe.so; there is no other code path.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+from .cases import Case
+
+_INPUTS = ("x", "router", "router_bias", "gate", "gate_scale", "up", "up_scale", "down", "down_scale",
+           "shared_gate", "shared_gate_scale", "shared_up", "shared_up_scale", "shared_down", "shared_down_scale")
+
+
+def make_desc(case: Case) -> _lib.Desc:
+    return _lib.Desc(tokens=case.tokens, hidden=case.hidden, experts=case.experts, topk=case.topk,
+                     intermediate=case.intermediate, shared_experts=case.shared_experts, groups=case.groups,
+                     top_groups=case.top_groups,
+                     gate=_lib.GATE_SIGMOID if case.router == "sigmoid" else _lib.GATE_SOFTMAX,
+                     renormalize=int(case.renormalize), pow2_scales=int(case.power_of_two),
+                     routed_scaling=float(case.routed_scaling))
+
+
+def _expect(t: torch.Tensor, name: str, dtype, shape, device) -> torch.Tensor:
+    if not isinstance(t, torch.Tensor):
+        raise ValueError(f"{name}: expected a tensor")
+    if t.dtype != dtype or tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name}: expected {tuple(shape)} {dtype}, got {tuple(t.shape)} {t.dtype}")
+    if t.device != device:
+        raise ValueError(f"{name}: on {t.device}, expected {device}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name}: must be contiguous")
+    return t
+
+
+class MoELayer:
+    """The layer for one case; holds the workspace between calls (it carries no state
+    from one call to the next)."""
+
+    def __init__(self, case: Case):
+        self.case = case
+        self.lib = _lib.load()
+        self.desc = make_desc(case)
+        size = ctypes.c_size_t(0)
+        _lib.check(self.lib.megamoe_workspace_bytes(ctypes.byref(self.desc), ctypes.byref(size)),
+                   f"{case.id}: workspace size")
+        self.workspace_bytes = int(size.value)
+        self._workspace: dict[torch.device, torch.Tensor] = {}
+
+    def workspace(self, device: torch.device) -> torch.Tensor:
+        ws = self._workspace.get(device)
+        if ws is None:
+            ws = torch.empty(self.workspace_bytes, dtype=torch.uint8, device=device)
+            self._workspace[device] = ws
+        return ws
+
+    def check_inputs(self, inputs: dict) -> torch.device:
+        c = self.case
+        T, H, E, I, S = c.tokens, c.hidden, c.experts, c.intermediate, c.shared_experts
+        x = inputs.get("x")
+        if not isinstance(x, torch.Tensor):
+            raise ValueError("inputs must hold 'x'")
+        device = x.device
+        if device.type != "cuda":
+            raise RuntimeError(f"the HIP layer runs on a GPU; inputs are on {device}")
+        bh, bi = -(-H // 128), -(-I // 128)
+        f8, f32 = torch.float8_e4m3fn, torch.float32
+        _expect(x, "x", torch.bfloat16, (T, H), device)
+        _expect(inputs["router"], "router", f32, (E, H), device)
+        if c.bias != "none":
+            _expect(inputs["router_bias"], "router_bias", f32, (E,), device)
+        _expect(inputs["gate"], "gate", f8, (E, I, H), device)
+        _expect(inputs["gate_scale"], "gate_scale", f32, (E, bi, bh), device)
+        _expect(inputs["up"], "up", f8, (E, I, H), device)
+        _expect(inputs["up_scale"], "up_scale", f32, (E, bi, bh), device)
+        _expect(inputs["down"], "down", f8, (E, H, I), device)
+        _expect(inputs["down_scale"], "down_scale", f32, (E, bh, bi), device)
+        if S:
+            bs = -(-(S * I) // 128)
+            _expect(inputs["shared_gate"], "shared_gate", f8, (S * I, H), device)
+            _expect(inputs["shared_gate_scale"], "shared_gate_scale", f32, (bs, bh), device)
+            _expect(inputs["shared_up"], "shared_up", f8, (S * I, H), device)
+            _expect(inputs["shared_up_scale"], "shared_up_scale", f32, (bs, bh), device)
+            _expect(inputs["shared_down"], "shared_down", f8, (H, S * I), device)
+            _expect(inputs["shared_down_scale"], "shared_down_scale", f32, (bh, bs), device)
+        return device
+
+    def _call(self, inputs: dict, timed: bool):
+        device = self.check_inputs(inputs)
+        c = self.case
+        y = torch.empty((c.tokens, c.hidden), dtype=torch.bfloat16, device=device)
+        ids = torch.empty((c.tokens, c.topk), dtype=torch.int64, device=device)
+        weights = torch.empty((c.tokens, c.topk), dtype=torch.float32, device=device)
+        ws = self.workspace(device)
+        ptr = {name: (inputs[name].data_ptr() if name in inputs and (name != "router_bias" or c.bias != "none")
+                      else None) for name in _INPUTS}
+        if not c.shared_experts:
+            for name in _INPUTS:
+                if name.startswith("shared_"):
+                    ptr[name] = None
+        tensors = _lib.Tensors(**ptr, y=y.data_ptr(), expert_ids=ids.data_ptr(),
+                               expert_weights=weights.data_ptr(), workspace=ws.data_ptr(),
+                               workspace_bytes=self.workspace_bytes)
+        stream = ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+        with torch.cuda.device(device):
+            if timed:
+                ms = (ctypes.c_float * 6)()
+                _lib.check(self.lib.megamoe_forward_timed(ctypes.byref(self.desc), ctypes.byref(tensors), stream,
+                                                          ms), f"{c.id}: forward")
+                return {"y": y, "expert_ids": ids, "expert_weights": weights}, list(ms)
+            _lib.check(self.lib.megamoe_forward(ctypes.byref(self.desc), ctypes.byref(tensors), stream),
+                       f"{c.id}: forward")
+        return {"y": y, "expert_ids": ids, "expert_weights": weights}
+
+    def __call__(self, inputs: dict) -> dict:
+        return self._call(inputs, timed=False)
+
+    def timed(self, inputs: dict) -> tuple[dict, list[float]]:
+        """One call with a device event between stages; returns (outputs, per-stage ms)."""
+        return self._call(inputs, timed=True)
+
+
+def build(case: dict):
+    layer = MoELayer(Case.from_dict({k: v for k, v in case.items() if k != "execution"}))
+
+    def run(inputs: dict) -> dict:
+        return layer(inputs)
+
+    run.layer = layer
+    return run
+
+
+# -- single-stage entry points (the C ABI's test surface) ---------------------------------
+
+def quantize_rows(x: torch.Tensor, power_of_two: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
+    """E4M3 payload and fp32 scales per row per 128 columns of a bf16 [rows, cols] tensor."""
+    if x.dtype != torch.bfloat16 or x.dim() != 2 or x.device.type != "cuda":
+        raise ValueError("quantize_rows takes a 2-D bf16 GPU tensor")
+    x = x.contiguous()
+    rows, cols = x.shape
+    q = torch.empty((rows, cols), dtype=torch.float8_e4m3fn, device=x.device)
+    s = torch.empty((rows, -(-cols // 128)), dtype=torch.float32, device=x.device)
+    lib = _lib.load()
+    with torch.cuda.device(x.device):
+        stream = ctypes.c_void_p(torch.cuda.current_stream(x.device).cuda_stream)
+        _lib.check(lib.megamoe_quantize_rows(rows, cols, x.data_ptr(), q.data_ptr(), s.data_ptr(),
+                                             int(power_of_two), stream), "quantize_rows")
+    return q, s
+
+
+def router_logits(case: Case, x: torch.Tensor, router: torch.Tensor) -> torch.Tensor:
+    layer = MoELayer(case)
+    logits = torch.empty((case.tokens, case.experts), dtype=torch.float32, device=x.device)
+    ws = layer.workspace(x.device)
+    with torch.cuda.device(x.device):
+        stream = ctypes.c_void_p(torch.cuda.current_stream(x.device).cuda_stream)
+        _lib.check(layer.lib.megamoe_router_logits(ctypes.byref(layer.desc), x.contiguous().data_ptr(),
+                                                   router.contiguous().data_ptr(), logits.data_ptr(),
+                                                   ws.data_ptr(), layer.workspace_bytes, stream), "router_logits")
+    return logits
+
+
+def route(case: Case, logits: torch.Tensor, bias: torch.Tensor | None) -> tuple[torch.Tensor, torch.Tensor]:
+    lib = _lib.load()
+    desc = make_desc(case)
+    T, K = logits.shape[0], case.topk
+    desc.tokens = T
+    ids = torch.empty((T, K), dtype=torch.int64, device=logits.device)
+    w = torch.empty((T, K), dtype=torch.float32, device=logits.device)
+    with torch.cuda.device(logits.device):
+        stream = ctypes.c_void_p(torch.cuda.current_stream(logits.device).cuda_stream)
+        _lib.check(lib.megamoe_route(ctypes.byref(desc), logits.contiguous().data_ptr(),
+                                     None if bias is None else bias.contiguous().data_ptr(), ids.data_ptr(),
+                                     w.data_ptr(), stream), "route")
+    return ids, w
