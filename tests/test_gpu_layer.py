@@ -1,7 +1,8 @@
 """GPU parity of the HIP layer against the CPU oracle, through the C ABI.
 
-Bars: expert ids bit-exact; expert weights within 2e-6 relative (fp32, ulp-level
-differences of expf and the order of a K-term sum); y within the band rule of
+Bars: expert ids bit-exact; expert weights within 2e-6 relative when both sides
+route the same logits (ulp-level differences of expf and of a K-term sum), 1e-4
+against the fp32-GEMV logits of the reference; y within the band rule of
 megabench/harness/correctness.py:64-85 against the FP32 oracle and within
 max|y - y_ref| / max|y_ref| <= 1e-2 and cosine >= 0.9999 against the BF16
 reference schedule. Quantization and router logits are bit-exact.
@@ -21,6 +22,7 @@ from vibe_megakernel_amd import submission, workloads
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
 W_RTOL = 2e-6
+LOGIT_RTOL = 1e-4
 
 
 def _log(msg):
@@ -48,7 +50,7 @@ def _compare(case, got, want, exact, rows=None):
     if rows is not None:
         ids, w, y = ids[rows], w[rows], y[rows]
     assert torch.equal(ids, want["expert_ids"]), f"{case.id}: expert ids differ"
-    torch.testing.assert_close(w, want["expert_weights"], rtol=W_RTOL, atol=0)
+    torch.testing.assert_close(w, want["expert_weights"], rtol=LOGIT_RTOL, atol=0)
     check = metrics.layer_checks(y, want["y"])
     assert check["pass"], f"{case.id}: {check}"
     band = metrics.band(want["y"], y, exact["y"], bf16_rtol=case.bf16_rtol, noise_factor=case.noise_factor)
@@ -143,12 +145,21 @@ def test_full_size_layer_on_sampled_tokens(cid):
     cpu = {k: v.cpu() for k, v in values.items()}
     del values
     torch.cuda.empty_cache()
-    # Routing of every token.
+    # Routing of every token. The ids must equal the reference's (logits from an fp32
+    # GEMV, as frontier.py:343 computes them). The weights are checked two ways: at
+    # W_RTOL against the oracle's routing of the correctly rounded logits the kernel
+    # uses (fp64 accumulation), and at LOGIT_RTOL against the fp32-GEMV reference, whose
+    # logits carry up to ~1e-5 absolute rounding error at H = 7168 that a sigmoid or
+    # softmax passes on to the weights.
     x = cpu["x"].float()
+    exact_logits = (cpu["router"].double() @ x.double().T).T.float()
     for t in range(case.tokens):
         wi, ww = routing.route(case, cpu["router"] @ x[t], cpu.get("router_bias"))
         assert torch.equal(got["expert_ids"][t].cpu(), wi), f"token {t}"
-        torch.testing.assert_close(got["expert_weights"][t].cpu(), ww, rtol=W_RTOL, atol=0)
+        torch.testing.assert_close(got["expert_weights"][t].cpu(), ww, rtol=LOGIT_RTOL, atol=0)
+        ei, ew = routing.route(case, exact_logits[t], cpu.get("router_bias"))
+        assert torch.equal(ei, wi), f"token {t}: a top-k margin below the logits' rounding error"
+        torch.testing.assert_close(got["expert_weights"][t].cpu(), ew, rtol=W_RTOL, atol=0)
     rows = [0, case.tokens // 2, case.tokens - 1]
     want, exact = layer.reference(case, cpu, tokens=rows), layer.oracle(case, cpu, tokens=rows)
     check, band = _compare(case, got, want, exact, rows=rows)

@@ -1,18 +1,20 @@
 // megamoe.hip — FP8 (E4M3, 128x128 block-scaled) MoE decode layer for MI355X (gfx950).
 //
-// The layer, as six stream-ordered kernels (one process, one GPU):
-//   k_router / k_quant_rows   router logits (fp64-accumulated GEMV over H splits) and the
-//                             per-token-per-128 E4M3 quantization of x
+// The layer, as eight stream-ordered kernel launches (one process, one GPU):
+//   k_router, k_logits        router logits: fp64-accumulated GEMV over 256-wide splits of H,
+//                             splits added in order and rounded once to fp32
+//   k_quant_rows              per-token-per-128 E4M3 quantization of x
 //   k_select                  one wavefront per token: sigmoid/softmax gate, group-limited
 //                             top-k with a (value desc, index asc) total order
 //   k_permute                 one workgroup: expert histogram, exclusive scan, stable
-//                             (token, slot)-ordered permutation, list of hit experts
-//   k_gateup                  persistent grid over (hit expert, 128-row block of I) units:
-//                             gate and up rows streamed from HBM into fp8 MFMA
-//                             (16x16x128, weights as the M operand, tokens as N),
-//                             128x128 block scales applied per K block, SwiGLU and the
-//                             per-128 E4M3 requantization of h fused in the epilogue
-//   k_down                    persistent grid over (hit expert, 128-row block of H) units
+//                             (token, slot)-ordered permutation, and the expert work lists
+//                             (chunks of <= 64 rows, heaviest first)
+//   k_gateup                  persistent workgroups draining a work queue of
+//                             (chunk, 128-row block of I) units: gate and up rows streamed
+//                             from HBM into fp8 MFMA (16x16x128, weights as the M operand,
+//                             tokens as N), 128x128 block scales applied per K block, SwiGLU
+//                             and the per-128 E4M3 requantization of h fused in the epilogue
+//   k_down                    the same over (chunk, 128-row block of H) units
 //   k_combine                 slot-order fp32 sum of bf16(d)*w plus the shared expert,
 //                             rounded once to bf16
 //
@@ -96,69 +98,20 @@ __device__ __forceinline__ float wave_max(float v) {
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
 
 // ---------------------------------------------------------------------------------------
-// Router logits: partial[split][t][e] = sum over one H split of x[t,h] * W[e,h] in fp64.
-// Products of a bf16 and an fp32 value are exact in fp64, so the only rounding that
-// survives is the final fp64 -> fp32 one in k_select.
+// Dynamic E4M3 quantization of one full 128-wide block by one wavefront (two values per
+// lane): scale = max(amax, 1e-4)/448, code = RNE(clamp(v / scale, +-448)).
 // ---------------------------------------------------------------------------------------
 
-constexpr int kRouterE = 16;   // experts per workgroup
-constexpr int kRouterT = 64;   // tokens per workgroup
-constexpr int kRouterH = 256;  // hidden channels per split
-
-__global__ __launch_bounds__(256) void k_router(const uint16_t* __restrict__ x, const float* __restrict__ w,
-                                                double* __restrict__ partial, int T, int H, int E) {
-  __shared__ float ws[kRouterE][kRouterH + 1];
-  __shared__ uint16_t xs[kRouterT][kRouterH + 8];
-  const int e0 = blockIdx.x * kRouterE, split = blockIdx.y, t0 = blockIdx.z * kRouterT;
-  const int h0 = split * kRouterH;
-  const int hc = min(kRouterH, H - h0);
-  const int tid = threadIdx.x;
-
-  for (int i = tid; i < kRouterE * (kRouterH / 4); i += 256) {
-    const int r = i / (kRouterH / 4), c = (i % (kRouterH / 4)) * 4;
-    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (e0 + r < E && c < hc) v = *reinterpret_cast<const float4*>(w + (size_t)(e0 + r) * H + h0 + c);
-    ws[r][c] = v.x;
-    ws[r][c + 1] = v.y;
-    ws[r][c + 2] = v.z;
-    ws[r][c + 3] = v.w;
-  }
-  for (int i = tid; i < kRouterT * (kRouterH / 8); i += 256) {
-    const int r = i / (kRouterH / 8), c = (i % (kRouterH / 8)) * 8;
-    uint4 v = make_uint4(0u, 0u, 0u, 0u);
-    if (t0 + r < T && c < hc) v = *reinterpret_cast<const uint4*>(x + (size_t)(t0 + r) * H + h0 + c);
-    *reinterpret_cast<uint4*>(&xs[r][c]) = v;
-  }
-  __syncthreads();
-
-  const int el = tid % kRouterE, tg = tid / kRouterE;  // 16 experts x 16 token groups
-  double acc[4] = {0.0, 0.0, 0.0, 0.0};
-  for (int k = 0; k < hc; ++k) {
-    const double wv = (double)ws[el][k];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[j] = fma(wv, (double)bf16_bits_to_f32(xs[tg + 16 * j][k]), acc[j]);
-  }
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int t = t0 + tg + 16 * j, e = e0 + el;
-    if (t < T && e < E) partial[((size_t)split * T + t) * E + e] = acc[j];
-  }
+__device__ __forceinline__ void quant_block(const uint16_t* src, uint8_t* dst, float* scale, int pow2, int lane) {
+  const uint32_t two = *reinterpret_cast<const uint32_t*>(src + 2 * lane);
+  const float v0 = bf16_bits_to_f32(two & 0xffffu), v1 = bf16_bits_to_f32(two >> 16);
+  const float s = act_scale(wave_max(fmaxf(fabsf(v0), fabsf(v1))), pow2);
+  const uint32_t q = f32_to_e4m3(clamp448(v0 / s)) | (f32_to_e4m3(clamp448(v1 / s)) << 8);
+  *reinterpret_cast<uint16_t*>(dst + 2 * lane) = (uint16_t)q;
+  if (lane == 0) *scale = s;
 }
 
-// logits[t][e] = fp32(sum of the splits in split order)
-__global__ __launch_bounds__(256) void k_logits(const double* __restrict__ partial, int nsplit, int T, int E,
-                                                float* __restrict__ logits) {
-  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= (size_t)T * E) return;
-  double s = 0.0;
-  for (int p = 0; p < nsplit; ++p) s += partial[(size_t)p * T * E + i];
-  logits[i] = (float)s;
-}
-
-// ---------------------------------------------------------------------------------------
-// Dynamic E4M3 quantization, one wavefront per (row, 128-column block).
-// ---------------------------------------------------------------------------------------
-
+// Ragged rows (any column count): one wavefront per (row, 128-column block).
 __global__ __launch_bounds__(256) void k_quant_rows(const uint16_t* __restrict__ x, uint8_t* __restrict__ q,
                                                     float* __restrict__ scales, int rows, int cols, int pow2) {
   const int nb = (cols + kBlock - 1) / kBlock;
@@ -180,164 +133,290 @@ __global__ __launch_bounds__(256) void k_quant_rows(const uint16_t* __restrict__
 }
 
 // ---------------------------------------------------------------------------------------
-// Routing, one wavefront per token. Lane l holds experts l, l+64, ...
-// Selection order is (score descending, expert index ascending), the order a stable
-// descending argsort produces (frontier.py:236,240; distributed.py:174).
+// Router logits on fp64 MFMA: partial[split][t][e] = sum over one 256-wide split of H of
+// x[t,h] * W[e,h]. v_mfma_f64_16x16x4f64 multiplies a 16-expert x 4-channel tile of W by
+// a 4-channel x 16-token tile of x; products of a bf16 and an fp32 value are exact in
+// fp64, so after the splits are added in order (k_select) and rounded once to fp32 the
+// logits are the correctly rounded dot products except when an fp64 sum lands within
+// ~2^-50 of an fp32 rounding boundary.
+//
+// Operand layout of the 16x16x4 f64 MFMA: lane l supplies A[l%16][k] and B[k][l%16] for
+// its k = l/16; the result holds row 4*(l/16)+v, column l%16 in element v. Over a
+// 16-channel step, lane group g feeds channels 4g .. 4g+3 in four MFMAs (one 16-byte W
+// load and one 8-byte x load per lane), the same channel order for A and B.
+//
+// The workgroups of the extra expert tile (blockIdx.x == number of expert tiles)
+// quantize x instead: the 128-blocks of their split for their 64 tokens.
 // ---------------------------------------------------------------------------------------
 
-constexpr int kMaxVPL = 16;  // experts per lane: E <= 1024
-constexpr int kMaxTopK = 32;
+typedef double f64x4 __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ bool ranks_before(float va, int ia, float vb, int ib) {
-  return va > vb || (va == vb && ia < ib);
+constexpr int kRouterE = 16;   // experts per workgroup (one MFMA row tile)
+constexpr int kRouterT = 64;   // tokens per workgroup (one 16-token column tile per wavefront)
+constexpr int kRouterH = 256;  // hidden channels per split
+
+__global__ __launch_bounds__(256) void k_router(const uint16_t* __restrict__ x, const float* __restrict__ w,
+                                                double* __restrict__ partial, uint8_t* __restrict__ xq,
+                                                float* __restrict__ xs, int T, int H, int E, int pow2) {
+  const int et = blockIdx.x, split = blockIdx.y, t0 = blockIdx.z * kRouterT;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int h0 = split * kRouterH, hc = min(kRouterH, H - h0);
+  if (et == (int)gridDim.x - 1) {
+    const int nb = hc / kBlock, nbh = H / kBlock;
+    for (int it = wv; it < kRouterT * nb; it += 4) {
+      const int t = t0 + it / nb, cb = it % nb;
+      if (t >= T) break;
+      const size_t o = (size_t)t * H + h0 + (size_t)cb * kBlock;
+      quant_block(x + o, xq + o, xs + (size_t)t * nbh + h0 / kBlock + cb, pow2, lane);
+    }
+    return;
+  }
+  const int g = lane >> 4;
+  const int e = et * kRouterE + (lane & 15), t = t0 + 16 * wv + (lane & 15);
+  const bool e_ok = e < E, t_ok = t < T;
+  const float* wp = w + (size_t)(e_ok ? e : 0) * H + h0 + 4 * g;
+  const uint16_t* xp = x + (size_t)(t_ok ? t : 0) * H + h0 + 4 * g;
+  f64x4 acc = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+  for (int k = 0; k < kRouterH; k += 16) {
+    if (k < hc) {  // hc is 128 or 256
+    float4 a = e_ok ? *reinterpret_cast<const float4*>(wp + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+    uint2 b = t_ok ? *reinterpret_cast<const uint2*>(xp + k) : make_uint2(0u, 0u);
+    acc = __builtin_amdgcn_mfma_f64_16x16x4f64((double)a.x, (double)bf16_bits_to_f32(b.x & 0xffffu), acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f64_16x16x4f64((double)a.y, (double)bf16_bits_to_f32(b.x >> 16), acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f64_16x16x4f64((double)a.z, (double)bf16_bits_to_f32(b.y & 0xffffu), acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f64_16x16x4f64((double)a.w, (double)bf16_bits_to_f32(b.y >> 16), acc, 0, 0, 0);
+    }
+  }
+  if (t_ok) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int eo = et * kRouterE + 4 * g + v;
+      if (eo < E) partial[((size_t)split * T + t) * E + eo] = acc[v];
+    }
+  }
 }
 
+// logits[t][e] = fp32(sum of the splits in split order); used by megamoe_router_logits.
+__global__ __launch_bounds__(256) void k_logits(const double* __restrict__ partial, int nsplit, int T, int E,
+                                                float* __restrict__ logits) {
+  const size_t n = (size_t)T * E;
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  const double* p = partial + i;
+  double s = 0.0;
+#pragma unroll 4
+  for (int q = 0; q < nsplit; ++q) s += p[(size_t)q * n];
+  logits[i] = (float)s;
+}
+
+// ---------------------------------------------------------------------------------------
+// Routing, one wavefront per token; lane l holds experts l, l+64, ... (VPL per lane).
+// Selection order is (score descending, expert index ascending), the order a stable
+// descending argsort produces (frontier.py:236,240; distributed.py:174).
+//
+// The K-th largest score is found by a radix search over order-preserving 32-bit score
+// codes (one ballot per bit and register), ties at it are filled with the lowest expert
+// indices, and the K picks are ordered by ranking them against each other in LDS.
+// ---------------------------------------------------------------------------------------
+
+constexpr int kMaxTopK = 32;
+constexpr int kMaxExperts = 1024;
+constexpr int kMaxGroups = 64;
+
+// Order-preserving code of a float (larger float, larger code); -0 and +0 coincide.
+__device__ __forceinline__ uint32_t order_code(float f) {
+  const uint32_t u = __float_as_uint(f == 0.0f ? 0.0f : f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ unsigned long long lanes_below() {
+  const int lane = threadIdx.x & 63;
+  return lane ? (~0ull >> (64 - lane)) : 0ull;
+}
+
+// Picks the k largest codes (ties: lowest expert index) among valid entries; returns the
+// per-register pick mask of this lane.
+template <int VPL>
+__device__ __forceinline__ unsigned top_codes(const uint32_t (&code)[VPL], const bool (&valid)[VPL], int k) {
+  uint32_t tau = 0;
+  for (int b = 31; b >= 0; --b) {
+    const uint32_t cand = tau | (1u << b);
+    int cnt = 0;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) cnt += __popcll(__ballot(valid[j] && code[j] >= cand));
+    if (cnt >= k) tau = cand;
+  }
+  int need = k;
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) need -= __popcll(__ballot(valid[j] && code[j] > tau));
+  unsigned pick = 0u;
+  const unsigned long long below = lanes_below();
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    const unsigned long long eq = __ballot(valid[j] && code[j] == tau);
+    const int before = __popcll(eq & below);
+    if ((valid[j] && code[j] > tau) || (valid[j] && code[j] == tau && before < need)) pick |= 1u << j;
+    need -= __popcll(eq);
+    if (need < 0) need = 0;
+  }
+  return pick;
+}
+
+template <int VPL>
 __global__ __launch_bounds__(64) void k_select(const double* __restrict__ partial, int nsplit,
                                                const float* __restrict__ logits_in, const float* __restrict__ bias,
                                                int T, int E, int K, int G, int TG, int gate, int renorm,
                                                float scaling, int64_t* __restrict__ ids_out,
                                                float* __restrict__ w_out) {
+  __shared__ float choice_lds[kMaxExperts];
+  __shared__ float gscore[kMaxGroups];
+  __shared__ uint32_t pick_code[kMaxTopK];
+  __shared__ int pick_id[kMaxTopK];
+  __shared__ float pick_val[kMaxTopK];
   const int t = blockIdx.x, lane = threadIdx.x;
-  float logit[kMaxVPL], prob[kMaxVPL], choice[kMaxVPL];
+  float logit[VPL], prob[VPL], choice[VPL];
+  bool valid[VPL];
+  if (logits_in) {
 #pragma unroll
-  for (int j = 0; j < kMaxVPL; ++j) {
-    const int e = lane + 64 * j;
-    float v = -INFINITY;
-    if (e < E) {
-      if (logits_in) {
-        v = logits_in[(size_t)t * E + e];
-      } else {
-        double s = 0.0;
-        for (int p = 0; p < nsplit; ++p) s += partial[((size_t)p * T + t) * E + e];
-        v = (float)s;
-      }
+    for (int j = 0; j < VPL; ++j) {
+      const int e = lane + 64 * j;
+      logit[j] = e < E ? logits_in[(size_t)t * E + e] : -INFINITY;
     }
-    logit[j] = v;
+  } else {
+    double s[VPL];
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) s[j] = 0.0;
+    const double* p = partial + (size_t)t * E + lane;
+    const size_t stride = (size_t)T * E;
+#pragma unroll 4
+    for (int q = 0; q < nsplit; ++q) {
+#pragma unroll
+      for (int j = 0; j < VPL; ++j)
+        if (lane + 64 * j < E) s[j] += p[(size_t)q * stride + 64 * j];
+    }
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) logit[j] = lane + 64 * j < E ? (float)s[j] : -INFINITY;
+  }
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    const int e = lane + 64 * j;
+    valid[j] = e < E;
     if (gate == MEGAMOE_GATE_SIGMOID) {
-      const float p = 1.0f / (1.0f + expf(-v));
+      const float p = 1.0f / (1.0f + expf(-logit[j]));
       prob[j] = p;
-      choice[j] = e < E ? p + (bias ? bias[e] : 0.0f) : -INFINITY;
+      choice[j] = p + (bias && valid[j] ? bias[e] : 0.0f);
     } else {
-      prob[j] = v;
-      choice[j] = v;
+      prob[j] = logit[j];
+      choice[j] = logit[j];
     }
   }
 
   if (G > 1) {
-    // Group score: sum of the two largest choices in the group (frontier.py:234).
+    // Group score: the sum of the two largest choices of the group (frontier.py:234).
     const int gs = E / G;
-    float my_group_score = -INFINITY;
-    for (int g = 0; g < G; ++g) {
+#pragma unroll
+    for (int j = 0; j < VPL; ++j)
+      if (valid[j]) choice_lds[lane + 64 * j] = choice[j];
+    __syncthreads();
+    if (lane < G) {
       float b1 = -INFINITY, b2 = -INFINITY;
-#pragma unroll
-      for (int j = 0; j < kMaxVPL; ++j) {
-        const int e = lane + 64 * j;
-        if (e < E && e / gs == g) {
-          const float v = choice[j];
-          if (v > b1) {
-            b2 = b1;
-            b1 = v;
-          } else if (v > b2) {
-            b2 = v;
-          }
+      for (int i = 0; i < gs; ++i) {
+        const float v = choice_lds[lane * gs + i];
+        if (v > b1) {
+          b2 = b1;
+          b1 = v;
+        } else if (v > b2) {
+          b2 = v;
         }
       }
-#pragma unroll
-      for (int o = 32; o > 0; o >>= 1) {
-        const float o1 = __shfl_xor(b1, o), o2 = __shfl_xor(b2, o);
-        const float n2 = fmaxf(fminf(b1, o1), fmaxf(b2, o2));
-        b1 = fmaxf(b1, o1);
-        b2 = n2;
-      }
-      const float score = gs >= 2 ? b1 + b2 : b1;
-      if (lane == g) my_group_score = score;
+      gscore[lane] = gs >= 2 ? b1 + b2 : b1;
     }
-    // Keep the top TG groups, ties to the lower group index (frontier.py:235).
+    __syncthreads();
+    // Keep the TG best groups, ties to the lower group index (frontier.py:235).
     bool keep = false;
-    for (int r = 0; r < TG; ++r) {
-      float bv = (lane < G && !keep) ? my_group_score : -INFINITY;
-      int bi = (lane < G && !keep) ? lane : 0x7fffffff;
-#pragma unroll
-      for (int o = 32; o > 0; o >>= 1) {
-        const float ov = __shfl_xor(bv, o);
-        const int oi = __shfl_xor(bi, o);
-        if (ranks_before(ov, oi, bv, bi)) {
-          bv = ov;
-          bi = oi;
-        }
+    if (lane < G) {
+      const float mine = gscore[lane];
+      int rank = 0;
+      for (int h = 0; h < G; ++h) {
+        const float o = gscore[h];
+        rank += (o > mine) || (o == mine && h < lane);
       }
-      if (lane == bi) keep = true;
+      keep = rank < TG;
     }
     const unsigned long long kept = __ballot(keep);
 #pragma unroll
-    for (int j = 0; j < kMaxVPL; ++j) {
-      const int e = lane + 64 * j;
-      if (e < E && !((kept >> (e / gs)) & 1ull)) choice[j] = -INFINITY;
-    }
+    for (int j = 0; j < VPL; ++j)
+      if (valid[j] && !((kept >> ((lane + 64 * j) / gs)) & 1ull)) choice[j] = -INFINITY;
   }
 
-  // Top-K, one expert per round.
-  unsigned taken = 0u;
-  int my_id = 0;
+  uint32_t code[VPL];
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) code[j] = order_code(choice[j]);
+  const unsigned pick = top_codes<VPL>(code, valid, K);
+
+  // Compact the K picks into LDS, then rank them: (code desc, index asc).
+  int base = 0;
+  const unsigned long long below = lanes_below();
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    const bool mine = (pick >> j) & 1u;
+    const unsigned long long m = __ballot(mine);
+    if (mine) {
+      const int slot = base + __popcll(m & below);
+      pick_code[slot] = code[j];
+      pick_id[slot] = lane + 64 * j;
+      pick_val[slot] = prob[j];
+    }
+    base += __popcll(m);
+  }
+  __syncthreads();
+  int my_id = 0, rank = 0;
   float my_val = 0.0f;
-  for (int r = 0; r < K; ++r) {
-    float bv = -INFINITY;
-    int bi = 0x7fffffff;
-#pragma unroll
-    for (int j = 0; j < kMaxVPL; ++j) {
-      const int e = lane + 64 * j;
-      if (e < E && !((taken >> j) & 1u) && ranks_before(choice[j], e, bv, bi)) {
-        bv = choice[j];
-        bi = e;
-      }
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const float ov = __shfl_xor(bv, o);
-      const int oi = __shfl_xor(bi, o);
-      if (ranks_before(ov, oi, bv, bi)) {
-        bv = ov;
-        bi = oi;
-      }
-    }
-    const int owner = bi & 63, slot = bi >> 6;
-    float pv = 0.0f;
-#pragma unroll
-    for (int j = 0; j < kMaxVPL; ++j)
-      if (j == slot) pv = prob[j];
-    pv = __shfl(pv, owner);
-    if (lane == owner) taken |= 1u << slot;
-    if (lane == r) {
-      my_id = bi;
-      my_val = pv;
+  if (lane < K) {
+    const uint32_t c = pick_code[lane];
+    my_id = pick_id[lane];
+    my_val = pick_val[lane];
+    for (int i = 0; i < K; ++i) {
+      const uint32_t o = pick_code[i];
+      rank += (o > c) || (o == c && pick_id[i] < my_id);
     }
   }
+  __syncthreads();
+  if (lane < K) {
+    pick_id[rank] = my_id;
+    pick_val[rank] = my_val;
+  }
+  __syncthreads();
+  if (lane < K) {
+    my_id = pick_id[lane];
+    my_val = pick_val[lane];
+  }
 
-  // Weights, in slot order.
+  // Weights; sums run in slot order.
   float w = 0.0f;
   if (gate == MEGAMOE_GATE_SIGMOID) {
     if (renorm) {
       float s = 0.0f;
-      for (int r = 0; r < K; ++r) s += __shfl(my_val, r);
+      for (int r = 0; r < K; ++r) s += pick_val[r];
       w = my_val / (s + 1e-20f) * scaling;
     } else {
       w = my_val * scaling;
     }
   } else if (renorm) {
-    const float m = __shfl(my_val, 0);  // the first pick holds the largest logit
-    const float ex = expf(my_val - m);
+    const float m = pick_val[0];  // the first pick holds the largest logit
     float s = 0.0f;
-    for (int r = 0; r < K; ++r) s += __shfl(ex, r);
-    w = ex / s * scaling;
+    for (int r = 0; r < K; ++r) s += expf(pick_val[r] - m);
+    w = expf(my_val - m) / s * scaling;
   } else {
     float m = -INFINITY;
 #pragma unroll
-    for (int j = 0; j < kMaxVPL; ++j) m = fmaxf(m, logit[j]);
+    for (int j = 0; j < VPL; ++j) m = fmaxf(m, logit[j]);
     m = wave_max(m);
     float s = 0.0f;
 #pragma unroll
-    for (int j = 0; j < kMaxVPL; ++j)
-      if (lane + 64 * j < E) s += expf(logit[j] - m);
+    for (int j = 0; j < VPL; ++j)
+      if (valid[j]) s += expf(logit[j] - m);
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
     w = expf(my_val - m) / s * scaling;
@@ -349,54 +428,69 @@ __global__ __launch_bounds__(64) void k_select(const double* __restrict__ partia
 }
 
 // ---------------------------------------------------------------------------------------
-// Histogram, scan and stable permutation in one workgroup (megamoe.py:138-149 order):
-// rows of expert e are its (token, slot) entries in increasing token order, and each
-// token picks an expert at most once, so an entry's rank is the number of earlier
-// tokens that picked the same expert: a popcount over a per-expert token bitmap.
+// Histogram, scan, stable permutation and the expert work lists, in one workgroup.
+//
+// Rows of expert e are its (token, slot) entries in increasing token order
+// (megamoe.py:138-149); each token picks an expert at most once, so an entry's rank is
+// the number of earlier tokens that picked the same expert: a popcount over a
+// per-expert token bitmap.
+//
+// Work lists: each expert's rows split into chunks of at most 64 (the most one pass of
+// the expert kernels multiplies); chunks are listed heaviest class first (33-64 rows,
+// then 17-32, then 1-16) so the dynamic work queues of the expert kernels start the
+// long units first. The shared expert (all T tokens) is listed like a routed expert;
+// in the gate/up list it appears once per I-sized slice of its S*I rows.
 // ---------------------------------------------------------------------------------------
 
-__device__ int block_exclusive_scan(int v, int* tmp, int* total) {
+// Exclusive scan over the workgroup of a value packing four counters:
+// bits 0-20 rows, 21-35 chunks of 33-64 rows, 36-46 chunks of 17-32, 47-57 chunks of 1-16.
+__device__ unsigned long long block_exclusive_scan(unsigned long long v, unsigned long long* tmp,
+                                                   unsigned long long* total) {
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6, nw = blockDim.x >> 6;
-  int x = v;
+  unsigned long long x = v;
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) {
-    const int y = __shfl_up(x, o);
+    const unsigned long long y = __shfl_up(x, o);
     if (lane >= o) x += y;
   }
   if (lane == 63) tmp[wid] = x;
   __syncthreads();
   if (wid == 0) {
-    int s = lane < nw ? tmp[lane] : 0;
+    unsigned long long s = lane < nw ? tmp[lane] : 0ull;
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
-      const int y = __shfl_up(s, o);
+      const unsigned long long y = __shfl_up(s, o);
       if (lane >= o) s += y;
     }
     if (lane < nw) tmp[lane] = s;
   }
   __syncthreads();
-  const int base = wid ? tmp[wid - 1] : 0;
+  const unsigned long long base = wid ? tmp[wid - 1] : 0ull;
   *total = tmp[nw - 1];
-  __syncthreads();
   return base + x - v;
 }
+
+constexpr int kMetaHit = 0, kMetaUnitsGU = 1, kMetaUnitsDN = 2, kMetaQueueGU = 3, kMetaQueueDN = 4;
+constexpr int kChunkRows = 64;
 
 struct PermuteOut {
   int* counts;   // [E]
   int* offsets;  // [E+1]
-  int* hit;      // [E] hit experts in increasing order
-  int* meta;     // [0] hit count U, [1] gate/up units, [2] down units
-  int* perm;     // [T*K] row -> flat (token*K + slot)
-  int* inv;      // [T*K] flat -> row
+  int* meta;     // kMeta*
+  int* perm;     // [T*K] grouped row -> token*K + slot
+  int* inv;      // [T*K] token*K + slot -> grouped row
+  int4* gu;      // gate/up chunks {expert (E = shared), first row, rows, first 128-block}
+  int4* dn;      // down chunks
 };
 
-__global__ __launch_bounds__(1024) void k_permute(const int64_t* __restrict__ ids, int T, int K, int E,
-                                                  int units_shared_gu, int units_per_expert_gu,
-                                                  int units_shared_dn, int units_per_expert_dn, PermuteOut out) {
+__device__ __forceinline__ int chunk_class(int rows) { return rows > 32 ? 0 : (rows > 16 ? 1 : 2); }
+
+__global__ __launch_bounds__(1024) void k_permute(const int64_t* __restrict__ ids, int T, int K, int E, int S,
+                                                  int nbI, int nbH, PermuteOut out) {
   extern __shared__ int smem[];
-  int* cnt = smem;             // E
-  int* tmp = cnt + E;          // 16
-  unsigned* bm = (unsigned*)(tmp + 16);  // E * words
+  unsigned long long* tmp = (unsigned long long*)smem;  // 16
+  int* cnt = smem + 32;                                  // E
+  unsigned* bm = (unsigned*)(cnt + E);                   // E * words
   const int words = (T + 31) / 32;
   const int tid = threadIdx.x, n = T * K;
   for (int i = tid; i < E; i += blockDim.x) cnt[i] = 0;
@@ -408,23 +502,67 @@ __global__ __launch_bounds__(1024) void k_permute(const int64_t* __restrict__ id
     atomicOr(&bm[e * words + (t >> 5)], 1u << (t & 31));
   }
   __syncthreads();
-  // E <= 1024 = blockDim: one expert per thread for the scans.
+  // E <= 1024 = blockDim: one expert per thread.
   const int c = tid < E ? cnt[tid] : 0;
-  int total = 0, nhit = 0;
-  const int off = block_exclusive_scan(c, tmp, &total);
-  const int hpos = block_exclusive_scan(c > 0 ? 1 : 0, tmp, &nhit);
+  const int full = c / kChunkRows, rem = c % kChunkRows;
+  const int a4 = full + (rem > 32 ? 1 : 0), a2 = (rem > 16 && rem <= 32) ? 1 : 0, a1 = (rem > 0 && rem <= 16) ? 1 : 0;
+  const int nhit = __syncthreads_count(c > 0);
+  unsigned long long tot = 0;
+  const unsigned long long packed =
+      block_exclusive_scan((unsigned long long)c | ((unsigned long long)a4 << 21) |
+                               ((unsigned long long)a2 << 36) | ((unsigned long long)a1 << 47), tmp, &tot);
+  const int off = (int)(packed & 0x1fffffu), p4 = (int)((packed >> 21) & 0x7fffu),
+            p2 = (int)((packed >> 36) & 0x7ffu), p1 = (int)((packed >> 47) & 0x7ffu);
+  const int total = (int)(tot & 0x1fffffu), t4 = (int)((tot >> 21) & 0x7fffu), t2 = (int)((tot >> 36) & 0x7ffu),
+            t1 = (int)((tot >> 47) & 0x7ffu);
+  // Shared expert chunks of T rows.
+  const int sf = T / kChunkRows, sr = T % kChunkRows;
+  const int s4 = S ? sf + (sr > 32 ? 1 : 0) : 0, s2 = S ? ((sr > 16 && sr <= 32) ? 1 : 0) : 0,
+            s1 = S ? ((sr > 0 && sr <= 16) ? 1 : 0) : 0;
+  // gate/up list: [S*s4 | t4 | S*s2 | t2 | S*s1 | t1]; down list: [s4 | t4 | s2 | t2 | s1 | t1]
+  const int gbase[3] = {0, S * s4 + t4, S * s4 + t4 + S * s2 + t2};
+  const int dbase[3] = {0, s4 + t4, s4 + t4 + s2 + t2};
+  const int gshared[3] = {S * s4, S * s2, S * s1};
+  const int dshared[3] = {s4, s2, s1};
   if (tid < E) {
     out.counts[tid] = c;
     out.offsets[tid] = off;
-    if (c > 0) out.hit[hpos] = tid;
-    cnt[tid] = off;  // reuse as offsets
+    for (int i = 0; i < a4; ++i) {
+      const int4 ch = make_int4(tid, kChunkRows * i, min(kChunkRows, c - kChunkRows * i), 0);
+      out.gu[gbase[0] + gshared[0] + p4 + i] = ch;
+      out.dn[dbase[0] + dshared[0] + p4 + i] = ch;
+    }
+    if (a2) {
+      const int4 ch = make_int4(tid, kChunkRows * full, rem, 0);
+      out.gu[gbase[1] + gshared[1] + p2] = ch;
+      out.dn[dbase[1] + dshared[1] + p2] = ch;
+    }
+    if (a1) {
+      const int4 ch = make_int4(tid, kChunkRows * full, rem, 0);
+      out.gu[gbase[2] + gshared[2] + p1] = ch;
+      out.dn[dbase[2] + dshared[2] + p1] = ch;
+    }
   }
   if (tid == 0) {
+    if (S > 0) {
+      for (int i = 0; i * kChunkRows < T; ++i) {
+        const int rows = min(kChunkRows, T - kChunkRows * i);
+        const int cls = chunk_class(rows);
+        const int idx = cls == 0 ? i : 0;        // index within the shared part of the class
+        const int per_copy = cls == 0 ? s4 : 1;  // shared chunks of this class per copy
+        for (int s = 0; s < S; ++s)
+          out.gu[gbase[cls] + s * per_copy + idx] = make_int4(E, kChunkRows * i, rows, s * nbI);
+        out.dn[dbase[cls] + idx] = make_int4(E, kChunkRows * i, rows, 0);
+      }
+    }
     out.offsets[E] = total;
-    out.meta[0] = nhit;
-    out.meta[1] = units_shared_gu + nhit * units_per_expert_gu;
-    out.meta[2] = units_shared_dn + nhit * units_per_expert_dn;
+    out.meta[kMetaHit] = nhit;
+    out.meta[kMetaUnitsGU] = (S * (s4 + s2 + s1) + t4 + t2 + t1) * nbI;
+    out.meta[kMetaUnitsDN] = (s4 + s2 + s1 + t4 + t2 + t1) * nbH;
+    out.meta[kMetaQueueGU] = 0;
+    out.meta[kMetaQueueDN] = 0;
   }
+  if (tid < E) cnt[tid] = off;  // reuse as offsets (every thread read its count above)
   __syncthreads();
   for (int i = tid; i < n; i += blockDim.x) {
     const int e = (int)ids[i], t = i / K;
@@ -528,16 +666,24 @@ __device__ __forceinline__ void stream_gemm(const Operands<RT, NCT, SG>& op, int
   }
 }
 
-// Work unit description shared by the two expert kernels.
-struct ExpertRows {
-  int n;            // rows (token, slot entries) of this expert
-  int row0;         // first output row in the grouped buffers
-  const int* perm;  // grouped row -> token*K + slot, or NULL for the shared expert (row = token)
+// Rows of one chunk: rows r = 0 .. n-1 map to grouped buffer row row0 + r and to token
+// perm[row0 + r] / K (routed) or row0 + r (shared expert, perm == NULL).
+struct ChunkRows {
+  int n;
+  int row0;
+  const int* perm;
   int K;
 };
 
-__device__ __forceinline__ int row_token(const ExpertRows& er, int r) {
-  return er.perm ? er.perm[er.row0 + r] / er.K : r;
+__device__ __forceinline__ int row_token(const ChunkRows& cr, int r) {
+  return cr.perm ? cr.perm[cr.row0 + r] / cr.K : cr.row0 + r;
+}
+
+// Takes the next unit of a dynamic work queue for the whole workgroup. Each workgroup
+// starts on unit blockIdx.x without touching the queue, so the queue only sees one
+// atomic per unit beyond the first wave of units, spread over the kernel's run.
+__device__ __forceinline__ void next_unit(int* queue, int* slot, int first_dynamic) {
+  if (threadIdx.x == 0) *slot = first_dynamic + atomicAdd(queue, 1);
 }
 
 struct GateUpArgs {
@@ -547,20 +693,21 @@ struct GateUpArgs {
   const uint8_t* up; const float* up_scale;
   const uint8_t* sgate; const float* sgate_scale;
   const uint8_t* sup; const float* sup_scale;
-  const int* counts; const int* offsets; const int* hit; const int* meta; const int* perm;
+  const int* offsets; const int* perm; const int4* chunks;
+  int* meta;
   uint8_t* hq_r; float* hs_r;   // routed rows [T*K, I], [T*K, I/128]
   uint8_t* hq_s; float* hs_s;   // shared rows [T, S*I], [T, S*I/128]
-  int T, H, I, K, S, pow2;
+  int T, H, I, K, S, E, pow2;
 };
 
-// One gate/up unit: rows [j*128, j*128+128) of gate and of up against the activation
-// rows c0 .. c0+16*NCT-1 of the expert. Wave w owns gate and up rows 32w .. 32w+31 of the
+// One gate/up unit: rows [jb*128, jb*128+128) of gate and of up against the chunk's
+// activation rows (at most 16*NCT). Wave w owns gate and up rows 32w .. 32w+31 of the
 // block, so SwiGLU pairs matching registers; the per-row amax over the 128-block for the
 // requantization of h is reduced across the four wavefronts through LDS.
 template <int NCT>
-__device__ void gateup_chunk(const GateUpArgs& a, const uint8_t* wg, const uint8_t* wu, const float* sg,
-                             const float* su, const ExpertRows& er, int c0, int j, uint8_t* hq, float* hs,
-                             int ldh, float (*red)[64]) {
+__device__ void gateup_unit(const GateUpArgs& a, const uint8_t* wg, const uint8_t* wu, const float* sg,
+                            const float* su, const ChunkRows& cr, int jb, uint8_t* hq, float* hs, int ldh,
+                            float (*red)[64]) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int kofs = 16 * (lane >> 4);
   const int H = a.H, nkb = H / kBlock, nbh = ldh / kBlock;
@@ -575,13 +722,13 @@ __device__ void gateup_chunk(const GateUpArgs& a, const uint8_t* wg, const uint8
   op.sw[1] = su;
 #pragma unroll
   for (int c = 0; c < NCT; ++c) {
-    const int r = min(c0 + 16 * c + (lane & 15), er.n - 1);  // padding columns repeat a valid row
-    const int tok = row_token(er, r);
+    const int r = min(16 * c + (lane & 15), cr.n - 1);  // padding columns repeat a valid row
+    const int tok = row_token(cr, r);
     op.b[c] = a.xq + (size_t)tok * H + kofs;
     op.sx[c] = a.xs + (size_t)tok * nkb;
   }
   f32x4 acc[4][NCT];
-  stream_gemm<4, NCT, 2, 3>(op, nkb, acc);
+  stream_gemm<4, NCT, 2, NCT == 1 ? 3 : 2>(op, nkb, acc);
 
   // h = bf16(silu(fp32 bf16(g)) * fp32 bf16(u)) (frontier.py:184-186,337)
   float hv[NCT][2][4];
@@ -608,9 +755,8 @@ __device__ void gateup_chunk(const GateUpArgs& a, const uint8_t* wg, const uint8
     const int col = 16 * c + (lane & 15);
     const float amax = fmaxf(fmaxf(red[0][col], red[1][col]), fmaxf(red[2][col], red[3][col]));
     const float s = act_scale(amax, a.pow2);
-    const int r = c0 + col;
-    if (r < er.n) {
-      uint8_t* dst = hq + (size_t)(er.row0 + r) * ldh + (size_t)j * kBlock + 32 * w + 4 * (lane >> 4);
+    if (col < cr.n) {
+      uint8_t* dst = hq + (size_t)(cr.row0 + col) * ldh + (size_t)jb * kBlock + 32 * w + 4 * (lane >> 4);
 #pragma unroll
       for (int p = 0; p < 2; ++p) {
         uint32_t packed = 0;
@@ -618,68 +764,145 @@ __device__ void gateup_chunk(const GateUpArgs& a, const uint8_t* wg, const uint8
         for (int v = 0; v < 4; ++v) packed |= f32_to_e4m3(clamp448(hv[c][p][v] / s)) << (8 * v);
         *reinterpret_cast<uint32_t*>(dst + 16 * p) = packed;
       }
-      if (w == 0 && lane < 16) hs[(size_t)(er.row0 + r) * nbh + j] = s;
+      if (w == 0 && lane < 16) hs[(size_t)(cr.row0 + col) * nbh + jb] = s;
     }
   }
-  __syncthreads();
 }
 
-__global__ __launch_bounds__(256) void k_gateup(GateUpArgs a) {
+// Gate/up unit for 33..64 activation rows (four column tiles). To keep the accumulators
+// of four column tiles within the register budget, the 128-row block is done in two
+// 64-row halves: in half hf, wave w owns gate and up rows 64*hf + 16w .. +15.
+__device__ void gateup_unit_wide(const GateUpArgs& a, const uint8_t* wg, const uint8_t* wu, const float* sg,
+                                 const float* su, const ChunkRows& cr, int jb, uint8_t* hq, float* hs, int ldh,
+                                 float (*red)[64]) {
+  constexpr int NCT = 4;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int kofs = 16 * (lane >> 4);
+  const int H = a.H, nkb = H / kBlock, nbh = ldh / kBlock;
+  Operands<2, NCT, 2> op;
+  op.sw[0] = sg;
+  op.sw[1] = su;
+#pragma unroll
+  for (int c = 0; c < NCT; ++c) {
+    const int r = min(16 * c + (lane & 15), cr.n - 1);
+    const int tok = row_token(cr, r);
+    op.b[c] = a.xq + (size_t)tok * H + kofs;
+    op.sx[c] = a.xs + (size_t)tok * nkb;
+  }
+  float hv[2][NCT][4];
+#pragma unroll
+  for (int hf = 0; hf < 2; ++hf) {
+    const size_t row = (size_t)(64 * hf + 16 * w + (lane & 15));
+    op.a[0] = wg + row * H + kofs;
+    op.a[1] = wu + row * H + kofs;
+    f32x4 acc[2][NCT];
+    stream_gemm<2, NCT, 2, 2>(op, nkb, acc);
+#pragma unroll
+    for (int c = 0; c < NCT; ++c)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const float g = round_bf16(acc[0][c][v]);
+        const float u = round_bf16(acc[1][c][v]);
+        hv[hf][c][v] = round_bf16(silu(g) * u);
+      }
+  }
+#pragma unroll
+  for (int c = 0; c < NCT; ++c) {
+    float amax = 0.0f;
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) amax = fmaxf(amax, fabsf(hv[hf][c][v]));
+    amax = fmaxf(amax, __shfl_xor(amax, 16));
+    amax = fmaxf(amax, __shfl_xor(amax, 32));
+    if (lane < 16) red[w][16 * c + lane] = amax;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int c = 0; c < NCT; ++c) {
+    const int col = 16 * c + (lane & 15);
+    const float amax = fmaxf(fmaxf(red[0][col], red[1][col]), fmaxf(red[2][col], red[3][col]));
+    const float s = act_scale(amax, a.pow2);
+    if (col < cr.n) {
+      uint8_t* dst = hq + (size_t)(cr.row0 + col) * ldh + (size_t)jb * kBlock + 16 * w + 4 * (lane >> 4);
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+        uint32_t packed = 0;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) packed |= f32_to_e4m3(clamp448(hv[hf][c][v] / s)) << (8 * v);
+        *reinterpret_cast<uint32_t*>(dst + 64 * hf) = packed;
+      }
+      if (w == 0 && lane < 16) hs[(size_t)(cr.row0 + col) * nbh + jb] = s;
+    }
+  }
+}
+
+__global__ __launch_bounds__(256, 2) void k_gateup(GateUpArgs a) {
   __shared__ float red[4][64];
+  __shared__ int slot;
   const int nbI = a.I / kBlock, nkb = a.H / kBlock;
-  const int nsh = a.S * nbI;  // shared expert: S*I rows of gate/up
-  const int total = a.meta[1];
-  for (int u = blockIdx.x; u < total; u += gridDim.x) {
+  const int total = a.meta[kMetaUnitsGU];
+  // First unit: blockIdx.x; after that, units gridDim.x, gridDim.x+1, ... from the queue.
+  int u = blockIdx.x;
+  while (u < total) {
+    __syncthreads();
+    next_unit(&a.meta[kMetaQueueGU], &slot, gridDim.x);  // arrives while this unit streams
+    const int4 ch = a.chunks[u / nbI];
+    const int j = u % nbI, jb = ch.w + j;
     const uint8_t *wg, *wu;
     const float *sg, *su;
-    ExpertRows er;
     uint8_t* hq;
     float* hs;
-    int ldh, j;
-    if (u < nsh) {
-      j = u;
-      wg = a.sgate + (size_t)j * kBlock * a.H;
-      wu = a.sup + (size_t)j * kBlock * a.H;
-      sg = a.sgate_scale + (size_t)j * nkb;
-      su = a.sup_scale + (size_t)j * nkb;
-      er = ExpertRows{a.T, 0, nullptr, a.K};
+    int ldh;
+    ChunkRows cr;
+    if (ch.x == a.E) {  // shared expert: rows of its S*I-row gate/up matrices
+      wg = a.sgate + (size_t)jb * kBlock * a.H;
+      wu = a.sup + (size_t)jb * kBlock * a.H;
+      sg = a.sgate_scale + (size_t)jb * nkb;
+      su = a.sup_scale + (size_t)jb * nkb;
+      cr = ChunkRows{ch.z, ch.y, nullptr, a.K};
       hq = a.hq_s;
       hs = a.hs_s;
       ldh = a.S * a.I;
     } else {
-      const int v = u - nsh, e = a.hit[v / nbI];
-      j = v % nbI;
-      const size_t rowblk = (size_t)e * nbI + j;
+      const size_t rowblk = (size_t)ch.x * nbI + jb;
       wg = a.gate + rowblk * kBlock * a.H;
       wu = a.up + rowblk * kBlock * a.H;
       sg = a.gate_scale + rowblk * nkb;
       su = a.up_scale + rowblk * nkb;
-      er = ExpertRows{a.counts[e], a.offsets[e], a.perm, a.K};
+      cr = ChunkRows{ch.z, a.offsets[ch.x] + ch.y, a.perm, a.K};
       hq = a.hq_r;
       hs = a.hs_r;
       ldh = a.I;
     }
-    // Experts with more than 16 rows stream their unit once per 16 rows.
-    for (int c0 = 0; c0 < er.n; c0 += 16) gateup_chunk<1>(a, wg, wu, sg, su, er, c0, j, hq, hs, ldh, red);
+    if (cr.n <= 16)
+      gateup_unit<1>(a, wg, wu, sg, su, cr, jb, hq, hs, ldh, red);
+    else if (cr.n <= 32)
+      gateup_unit<2>(a, wg, wu, sg, su, cr, jb, hq, hs, ldh, red);
+    else
+      gateup_unit_wide(a, wg, wu, sg, su, cr, jb, hq, hs, ldh, red);
+    __syncthreads();
+    u = slot;
   }
 }
 
 struct DownArgs {
   const uint8_t* down; const float* down_scale;
   const uint8_t* sdown; const float* sdown_scale;
-  const int* counts; const int* offsets; const int* hit; const int* meta; const int* perm;
+  const int* offsets; const int* perm; const int4* chunks;
+  int* meta;
   const uint8_t* hq_r; const float* hs_r;
   const uint8_t* hq_s; const float* hs_s;
   uint16_t* d_r;  // [T*K, H] bf16, grouped rows
   uint16_t* d_s;  // [T, H] bf16
-  int T, H, I, K, S;
+  int T, H, I, K, S, E;
 };
 
-// One down unit: rows [j*128, j*128+128) of the down matrix [H, ldk] against the
-// expert's requantized h rows. Wave w owns rows 32w .. 32w+31.
+// One down unit: rows [j*128, j*128+128) of a down matrix [H, ldk] against the chunk's
+// requantized h rows. Wave w owns rows 32w .. 32w+31.
 template <int NCT>
-__device__ void down_chunk(const DownArgs& a, const uint8_t* wd, const float* sd, int ldk, const uint8_t* hq,
-                           const float* hs, const ExpertRows& er, int c0, int j, uint16_t* d) {
+__device__ void down_unit(const DownArgs& a, const uint8_t* wd, const float* sd, int ldk, const uint8_t* hq,
+                          const float* hs, const ChunkRows& cr, int j, uint16_t* d) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int kofs = 16 * (lane >> 4);
   const int nkb = ldk / kBlock;
@@ -689,61 +912,62 @@ __device__ void down_chunk(const DownArgs& a, const uint8_t* wd, const float* sd
   op.sw[0] = sd;
 #pragma unroll
   for (int c = 0; c < NCT; ++c) {
-    const int r = min(c0 + 16 * c + (lane & 15), er.n - 1);
-    op.b[c] = hq + (size_t)(er.row0 + r) * ldk + kofs;
-    op.sx[c] = hs + (size_t)(er.row0 + r) * nkb;
+    const int r = min(16 * c + (lane & 15), cr.n - 1);
+    op.b[c] = hq + (size_t)(cr.row0 + r) * ldk + kofs;
+    op.sx[c] = hs + (size_t)(cr.row0 + r) * nkb;
   }
   f32x4 acc[2][NCT];
-  stream_gemm<2, NCT, 1, 4>(op, nkb, acc);
+  stream_gemm<2, NCT, 1, NCT == 1 ? 4 : (NCT == 2 ? 3 : 2)>(op, nkb, acc);
 #pragma unroll
   for (int c = 0; c < NCT; ++c) {
-    const int r = c0 + 16 * c + (lane & 15);
-    if (r < er.n) {
+    const int r = 16 * c + (lane & 15);
+    if (r < cr.n) {
 #pragma unroll
       for (int p = 0; p < 2; ++p) {
         const uint32_t lo = f32_to_bf16_bits(acc[p][c][0]) | (f32_to_bf16_bits(acc[p][c][1]) << 16);
         const uint32_t hi = f32_to_bf16_bits(acc[p][c][2]) | (f32_to_bf16_bits(acc[p][c][3]) << 16);
-        uint16_t* dst = d + (size_t)(er.row0 + r) * a.H + (size_t)j * kBlock + 32 * w + 16 * p + 4 * (lane >> 4);
+        uint16_t* dst = d + (size_t)(cr.row0 + r) * a.H + (size_t)j * kBlock + 32 * w + 16 * p + 4 * (lane >> 4);
         *reinterpret_cast<uint2*>(dst) = make_uint2(lo, hi);
       }
     }
   }
 }
 
-__global__ __launch_bounds__(256) void k_down(DownArgs a) {
+__global__ __launch_bounds__(256, 2) void k_down(DownArgs a) {
+  __shared__ int slot;
   const int nbH = a.H / kBlock, nbI = a.I / kBlock;
-  const int nsh = a.S > 0 ? nbH : 0;
-  const int total = a.meta[2];
-  for (int u = blockIdx.x; u < total; u += gridDim.x) {
-    const uint8_t* wd;
-    const float* sd;
-    const uint8_t* hq;
-    const float* hs;
-    uint16_t* d;
-    int ldk, j;
-    ExpertRows er;
-    if (u < nsh) {
-      j = u;
-      ldk = a.S * a.I;
-      wd = a.sdown + (size_t)j * kBlock * ldk;
-      sd = a.sdown_scale + (size_t)j * (ldk / kBlock);
-      hq = a.hq_s;
-      hs = a.hs_s;
-      d = a.d_s;
-      er = ExpertRows{a.T, 0, nullptr, a.K};
+  const int total = a.meta[kMetaUnitsDN];
+  int u = blockIdx.x;
+  while (u < total) {
+    __syncthreads();
+    next_unit(&a.meta[kMetaQueueDN], &slot, gridDim.x);
+    const int4 ch = a.chunks[u / nbH];
+    const int j = u % nbH;
+    if (ch.x == a.E) {
+      const int ldk = a.S * a.I;
+      const ChunkRows cr{ch.z, ch.y, nullptr, a.K};
+      const uint8_t* wd = a.sdown + (size_t)j * kBlock * ldk;
+      const float* sd = a.sdown_scale + (size_t)j * (ldk / kBlock);
+      if (cr.n <= 16)
+        down_unit<1>(a, wd, sd, ldk, a.hq_s, a.hs_s, cr, j, a.d_s);
+      else if (cr.n <= 32)
+        down_unit<2>(a, wd, sd, ldk, a.hq_s, a.hs_s, cr, j, a.d_s);
+      else
+        down_unit<4>(a, wd, sd, ldk, a.hq_s, a.hs_s, cr, j, a.d_s);
     } else {
-      const int v = u - nsh, e = a.hit[v / nbH];
-      j = v % nbH;
-      ldk = a.I;
-      const size_t rowblk = (size_t)e * nbH + j;
-      wd = a.down + rowblk * kBlock * ldk;
-      sd = a.down_scale + rowblk * nbI;
-      hq = a.hq_r;
-      hs = a.hs_r;
-      d = a.d_r;
-      er = ExpertRows{a.counts[e], a.offsets[e], a.perm, a.K};
+      const ChunkRows cr{ch.z, a.offsets[ch.x] + ch.y, a.perm, a.K};
+      const size_t rowblk = (size_t)ch.x * nbH + j;
+      const uint8_t* wd = a.down + rowblk * kBlock * a.I;
+      const float* sd = a.down_scale + rowblk * nbI;
+      if (cr.n <= 16)
+        down_unit<1>(a, wd, sd, a.I, a.hq_r, a.hs_r, cr, j, a.d_r);
+      else if (cr.n <= 32)
+        down_unit<2>(a, wd, sd, a.I, a.hq_r, a.hs_r, cr, j, a.d_r);
+      else
+        down_unit<4>(a, wd, sd, a.I, a.hq_r, a.hs_r, cr, j, a.d_r);
     }
-    for (int c0 = 0; c0 < er.n; c0 += 16) down_chunk<1>(a, wd, sd, ldk, hq, hs, er, c0, j, d);
+    __syncthreads();
+    u = slot;
   }
 }
 
@@ -794,9 +1018,17 @@ constexpr size_t kAlign = 256;
 inline size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
 struct Layout {
-  size_t partial, xq, xs, counts, offsets, hit, meta, perm, inv, hq_r, hs_r, hq_s, hs_s, d_r, d_s, total;
+  size_t partial, xq, xs, counts, offsets, meta, perm, inv, gu, dn, hq_r, hs_r, hq_s, hs_s, d_r, d_s, total;
   int nsplit;
 };
+
+// Upper bound of list entries: every hit expert has at most ceil(rows/64) chunks, so the
+// routed chunks number at most min(E, T*K) + T*K/64; the shared expert adds ceil(T/64)
+// per copy.
+size_t max_chunks(const megamoe_desc& d, int copies) {
+  const size_t T = d.tokens, TK = (size_t)d.tokens * d.topk, E = d.experts;
+  return (E < TK ? E : TK) + TK / kChunkRows + 1 + (size_t)copies * ((T + kChunkRows - 1) / kChunkRows);
+}
 
 Layout make_layout(const megamoe_desc& d) {
   Layout L{};
@@ -813,10 +1045,11 @@ Layout make_layout(const megamoe_desc& d) {
   L.xs = take(T * (H / kBlock) * sizeof(float));
   L.counts = take(E * sizeof(int));
   L.offsets = take((E + 1) * sizeof(int));
-  L.hit = take(E * sizeof(int));
   L.meta = take(16 * sizeof(int));
   L.perm = take(T * K * sizeof(int));
   L.inv = take(T * K * sizeof(int));
+  L.gu = take(max_chunks(d, (int)S) * sizeof(int4));
+  L.dn = take(max_chunks(d, S > 0 ? 1 : 0) * sizeof(int4));
   L.hq_r = take(T * K * I);
   L.hs_r = take(T * K * (I / kBlock) * sizeof(float));
   L.hq_s = take(T * S * I);
@@ -836,11 +1069,12 @@ int validate(const megamoe_desc* d) {
   if (d->topk > d->experts || d->experts % d->groups || d->top_groups > d->groups) return MEGAMOE_ERR_SHAPE;
   if (d->gate != MEGAMOE_GATE_SOFTMAX && d->gate != MEGAMOE_GATE_SIGMOID) return MEGAMOE_ERR_SHAPE;
   if (d->groups > 1 && (size_t)d->top_groups * (d->experts / d->groups) < (size_t)d->topk) return MEGAMOE_ERR_SHAPE;
-  if (d->experts > 64 * kMaxVPL || d->topk > kMaxTopK || d->groups > 64) return MEGAMOE_ERR_UNSUPPORTED;
-  // Permute bitmap in LDS: (E counts + 16 scan words + E*ceil(T/32) bitmap words) * 4 bytes.
+  if (d->experts > kMaxExperts || d->topk > kMaxTopK || d->groups > 64) return MEGAMOE_ERR_UNSUPPORTED;
+  // Permute bitmap in LDS: (32 scan words + E counts + E*ceil(T/32) bitmap words) * 4 bytes.
   const size_t words = ((size_t)d->tokens + 31) / 32;
-  if (((size_t)d->experts * (1 + words) + 16) * 4 > 64 * 1024) return MEGAMOE_ERR_UNSUPPORTED;
-  if ((size_t)d->tokens * d->topk > (size_t)1 << 30) return MEGAMOE_ERR_UNSUPPORTED;
+  if (((size_t)d->experts * (1 + words) + 32) * 4 > 64 * 1024) return MEGAMOE_ERR_UNSUPPORTED;
+  // The permute kernel's packed scan holds up to 2^21-1 rows and 2^15-1 chunks.
+  if ((size_t)d->tokens * d->topk >= ((size_t)1 << 21) - kMaxExperts * 64) return MEGAMOE_ERR_UNSUPPORTED;
   return MEGAMOE_OK;
 }
 
@@ -869,16 +1103,28 @@ int device_info(DeviceInfo* out) {
   return MEGAMOE_OK;
 }
 
-#define MEGAMOE_LAUNCH_CHECK()                              \
-  do {                                                      \
+#define MEGAMOE_LAUNCH_CHECK()                                   \
+  do {                                                           \
     if (hipGetLastError() != hipSuccess) return MEGAMOE_ERR_HIP; \
   } while (0)
 
+// Router partials (and, with the extra expert tile, the quantized x) for all tokens.
 int launch_router(const megamoe_desc& d, const Layout& L, const void* x, const float* router, char* ws,
                   hipStream_t st) {
-  const dim3 grid((d.experts + kRouterE - 1) / kRouterE, L.nsplit, (d.tokens + kRouterT - 1) / kRouterT);
+  const dim3 grid((d.experts + kRouterE - 1) / kRouterE + 1, L.nsplit, (d.tokens + kRouterT - 1) / kRouterT);
   hipLaunchKernelGGL(k_router, grid, dim3(256), 0, st, (const uint16_t*)x, router, (double*)(ws + L.partial),
-                     d.tokens, d.hidden, d.experts);
+                     (uint8_t*)(ws + L.xq), (float*)(ws + L.xs), d.tokens, d.hidden, d.experts, d.pow2_scales);
+  MEGAMOE_LAUNCH_CHECK();
+  return MEGAMOE_OK;
+}
+
+int launch_logits(const megamoe_desc& d, const Layout& L, const void* x, const float* router, char* ws,
+                  float* logits, hipStream_t st) {
+  int rc = launch_router(d, L, x, router, ws, st);
+  if (rc) return rc;
+  const size_t n = (size_t)d.tokens * d.experts;
+  hipLaunchKernelGGL(k_logits, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, (const double*)(ws + L.partial),
+                     L.nsplit, d.tokens, d.experts, logits);
   MEGAMOE_LAUNCH_CHECK();
   return MEGAMOE_OK;
 }
@@ -887,6 +1133,28 @@ int launch_quant(int rows, int cols, const void* x, uint8_t* q, float* s, int po
   const long blocks = ((long)rows * ((cols + kBlock - 1) / kBlock) + 3) / 4;
   const int grid = (int)(blocks < 4096 ? (blocks > 0 ? blocks : 1) : 4096);
   hipLaunchKernelGGL(k_quant_rows, dim3(grid), dim3(256), 0, st, (const uint16_t*)x, q, s, rows, cols, pow2);
+  MEGAMOE_LAUNCH_CHECK();
+  return MEGAMOE_OK;
+}
+
+// Routing from fp32 logits, or (logits == NULL) from the router's fp64 split partials.
+int launch_select(const megamoe_desc& d, const double* partial, int nsplit, const float* logits, const float* bias,
+                  int64_t* ids, float* w, hipStream_t st) {
+  const dim3 grid(d.tokens), block(64);
+#define MEGAMOE_SELECT(VPL)                                                                                   \
+  hipLaunchKernelGGL(k_select<VPL>, grid, block, 0, st, partial, nsplit, logits, bias, d.tokens, d.experts,   \
+                     d.topk, d.groups, d.top_groups, d.gate, d.renormalize, d.routed_scaling, ids, w)
+  if (d.experts <= 64)
+    MEGAMOE_SELECT(1);
+  else if (d.experts <= 128)
+    MEGAMOE_SELECT(2);
+  else if (d.experts <= 256)
+    MEGAMOE_SELECT(4);
+  else if (d.experts <= 512)
+    MEGAMOE_SELECT(8);
+  else
+    MEGAMOE_SELECT(16);
+#undef MEGAMOE_SELECT
   MEGAMOE_LAUNCH_CHECK();
   return MEGAMOE_OK;
 }
@@ -918,21 +1186,18 @@ int forward_impl(const megamoe_desc* desc, const megamoe_tensors* t, hipStream_t
 
   if (mark(0) != hipSuccess) return MEGAMOE_ERR_HIP;
   if ((rc = launch_router(d, L, t->x, t->router, ws, st))) return rc;
-  if ((rc = launch_quant(T, H, t->x, (uint8_t*)(ws + L.xq), (float*)(ws + L.xs), d.pow2_scales, st))) return rc;
   if (mark(1) != hipSuccess) return MEGAMOE_ERR_HIP;
 
-  hipLaunchKernelGGL(k_select, dim3(T), dim3(64), 0, st, (const double*)(ws + L.partial), L.nsplit,
-                     (const float*)nullptr, t->router_bias, T, E, K, d.groups, d.top_groups, d.gate, d.renormalize,
-                     d.routed_scaling, t->expert_ids, t->expert_weights);
-  MEGAMOE_LAUNCH_CHECK();
+  if ((rc = launch_select(d, (const double*)(ws + L.partial), L.nsplit, nullptr, t->router_bias, t->expert_ids,
+                          t->expert_weights, st)))
+    return rc;
   if (mark(2) != hipSuccess) return MEGAMOE_ERR_HIP;
 
-  PermuteOut po{(int*)(ws + L.counts), (int*)(ws + L.offsets), (int*)(ws + L.hit),
-                (int*)(ws + L.meta),   (int*)(ws + L.perm),    (int*)(ws + L.inv)};
+  PermuteOut po{(int*)(ws + L.counts), (int*)(ws + L.offsets), (int*)(ws + L.meta), (int*)(ws + L.perm),
+                (int*)(ws + L.inv),    (int4*)(ws + L.gu),     (int4*)(ws + L.dn)};
   const int nbI = I / kBlock, nbH = H / kBlock;
-  const size_t lds = ((size_t)E * (1 + (T + 31) / 32) + 16) * 4;
-  hipLaunchKernelGGL(k_permute, dim3(1), dim3(1024), lds, st, t->expert_ids, T, K, E, S * nbI, nbI,
-                     S > 0 ? nbH : 0, nbH, po);
+  const size_t lds = ((size_t)E * (1 + (T + 31) / 32) + 32) * 4;
+  hipLaunchKernelGGL(k_permute, dim3(1), dim3(1024), lds, st, t->expert_ids, T, K, E, S, nbI, nbH, po);
   MEGAMOE_LAUNCH_CHECK();
   if (mark(3) != hipSuccess) return MEGAMOE_ERR_HIP;
 
@@ -943,22 +1208,26 @@ int forward_impl(const megamoe_desc* desc, const megamoe_tensors* t, hipStream_t
   ga.up = t->up; ga.up_scale = t->up_scale;
   ga.sgate = t->shared_gate; ga.sgate_scale = t->shared_gate_scale;
   ga.sup = t->shared_up; ga.sup_scale = t->shared_up_scale;
-  ga.counts = po.counts; ga.offsets = po.offsets; ga.hit = po.hit; ga.meta = po.meta; ga.perm = po.perm;
+  ga.offsets = po.offsets; ga.perm = po.perm; ga.chunks = po.gu; ga.meta = po.meta;
   ga.hq_r = (uint8_t*)(ws + L.hq_r); ga.hs_r = (float*)(ws + L.hs_r);
   ga.hq_s = (uint8_t*)(ws + L.hq_s); ga.hs_s = (float*)(ws + L.hs_s);
-  ga.T = T; ga.H = H; ga.I = I; ga.K = K; ga.S = S; ga.pow2 = d.pow2_scales;
-  hipLaunchKernelGGL(k_gateup, dim3(di.cus * di.gateup_per_cu), dim3(256), 0, st, ga);
+  ga.T = T; ga.H = H; ga.I = I; ga.K = K; ga.S = S; ga.E = E; ga.pow2 = d.pow2_scales;
+  // No more workgroups than the largest unit count the routing can produce.
+  const size_t gu_max = max_chunks(d, S) * (size_t)nbI, dn_max = max_chunks(d, S > 0 ? 1 : 0) * (size_t)nbH;
+  const unsigned gu_grid = (unsigned)(gu_max < (size_t)di.cus * di.gateup_per_cu ? gu_max : (size_t)di.cus * di.gateup_per_cu);
+  const unsigned dn_grid = (unsigned)(dn_max < (size_t)di.cus * di.down_per_cu ? dn_max : (size_t)di.cus * di.down_per_cu);
+  hipLaunchKernelGGL(k_gateup, dim3(gu_grid), dim3(256), 0, st, ga);
   MEGAMOE_LAUNCH_CHECK();
   if (mark(4) != hipSuccess) return MEGAMOE_ERR_HIP;
 
   DownArgs da;
   da.down = t->down; da.down_scale = t->down_scale;
   da.sdown = t->shared_down; da.sdown_scale = t->shared_down_scale;
-  da.counts = po.counts; da.offsets = po.offsets; da.hit = po.hit; da.meta = po.meta; da.perm = po.perm;
+  da.offsets = po.offsets; da.perm = po.perm; da.chunks = po.dn; da.meta = po.meta;
   da.hq_r = ga.hq_r; da.hs_r = ga.hs_r; da.hq_s = ga.hq_s; da.hs_s = ga.hs_s;
   da.d_r = (uint16_t*)(ws + L.d_r); da.d_s = (uint16_t*)(ws + L.d_s);
-  da.T = T; da.H = H; da.I = I; da.K = K; da.S = S;
-  hipLaunchKernelGGL(k_down, dim3(di.cus * di.down_per_cu), dim3(256), 0, st, da);
+  da.T = T; da.H = H; da.I = I; da.K = K; da.S = S; da.E = E;
+  hipLaunchKernelGGL(k_down, dim3(dn_grid), dim3(256), 0, st, da);
   MEGAMOE_LAUNCH_CHECK();
   if (mark(5) != hipSuccess) return MEGAMOE_ERR_HIP;
 
@@ -1025,14 +1294,7 @@ int megamoe_router_logits(const megamoe_desc* desc, const void* x, const float* 
   if (!x || !router || !logits || !workspace) return MEGAMOE_ERR_INVALID_ARGUMENT;
   const Layout L = make_layout(*desc);
   if (workspace_bytes < L.total) return MEGAMOE_ERR_WORKSPACE;
-  hipStream_t st = (hipStream_t)stream;
-  char* ws = (char*)workspace;
-  if ((rc = launch_router(*desc, L, x, router, ws, st))) return rc;
-  const size_t n = (size_t)desc->tokens * desc->experts;
-  hipLaunchKernelGGL(k_logits, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, (const double*)(ws + L.partial),
-                     L.nsplit, desc->tokens, desc->experts, logits);
-  MEGAMOE_LAUNCH_CHECK();
-  return MEGAMOE_OK;
+  return launch_logits(*desc, L, x, router, (char*)workspace, logits, (hipStream_t)stream);
 }
 
 int megamoe_route(const megamoe_desc* desc, const float* logits, const float* bias, int64_t* expert_ids,
@@ -1041,12 +1303,7 @@ int megamoe_route(const megamoe_desc* desc, const float* logits, const float* bi
   if (rc) return rc;
   if (desc->tokens == 0) return MEGAMOE_OK;
   if (!logits || !expert_ids || !expert_weights) return MEGAMOE_ERR_INVALID_ARGUMENT;
-  const megamoe_desc& d = *desc;
-  hipLaunchKernelGGL(k_select, dim3(d.tokens), dim3(64), 0, (hipStream_t)stream, (const double*)nullptr, 0, logits,
-                     bias, d.tokens, d.experts, d.topk, d.groups, d.top_groups, d.gate, d.renormalize,
-                     d.routed_scaling, expert_ids, expert_weights);
-  MEGAMOE_LAUNCH_CHECK();
-  return MEGAMOE_OK;
+  return launch_select(*desc, nullptr, 0, logits, bias, expert_ids, expert_weights, (hipStream_t)stream);
 }
 
 int megamoe_quantize_rows(int32_t rows, int32_t cols, const void* x, uint8_t* q, float* scales, int32_t pow2,
