@@ -133,66 +133,123 @@ __global__ __launch_bounds__(256) void k_quant_rows(const uint16_t* __restrict__
 }
 
 // ---------------------------------------------------------------------------------------
-// Router logits on fp64 MFMA: partial[split][t][e] = sum over one 256-wide split of H of
+// Router logits on fp64 MFMA: partial[split][t][e] = sum over one split of H of
 // x[t,h] * W[e,h]. v_mfma_f64_16x16x4f64 multiplies a 16-expert x 4-channel tile of W by
 // a 4-channel x 16-token tile of x; products of a bf16 and an fp32 value are exact in
 // fp64, so after the splits are added in order (k_select) and rounded once to fp32 the
 // logits are the correctly rounded dot products except when an fp64 sum lands within
 // ~2^-50 of an fp32 rounding boundary.
 //
-// Operand layout of the 16x16x4 f64 MFMA: lane l supplies A[l%16][k] and B[k][l%16] for
-// its k = l/16; the result holds row 4*(l/16)+v, column l%16 in element v. Over a
-// 16-channel step, lane group g feeds channels 4g .. 4g+3 in four MFMAs (one 16-byte W
-// load and one 8-byte x load per lane), the same channel order for A and B.
+// A workgroup owns one 16-expert x 16-token tile and one split of H; its four
+// wavefronts take consecutive quarters of the split and their tiles are added in
+// wavefront order through LDS. Splits number up to four, so a DeepSeek-V3-sized router
+// keeps about a thousand wavefronts busy and routing sums at most four partials.
 //
-// The workgroups of the extra expert tile (blockIdx.x == number of expert tiles)
-// quantize x instead: the 128-blocks of their split for their 64 tokens.
+// Operand layout of the 16x16x4 f64 MFMA: lane l supplies A[l%16][k] and B[k][l%16] for
+// its k = l/16; the result holds row l/16 + 4v, column l%16 in element v (measured on
+// gfx950; the fp8 MFMA below puts row 4*(l/16) + v there instead). Over a 16-channel
+// step, lane group g feeds channels 4g .. 4g+3 in four MFMAs (one 16-byte W load and one
+// 8-byte x load per lane), the same channel order for A and B.
+//
+// Workgroups past the router tiles (blockIdx.x >= n_router) quantize x instead,
+// kQuantPerWave 128-blocks per wavefront.
 // ---------------------------------------------------------------------------------------
 
 typedef double f64x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kRouterE = 16;   // experts per workgroup (one MFMA row tile)
-constexpr int kRouterT = 64;   // tokens per workgroup (one 16-token column tile per wavefront)
-constexpr int kRouterH = 256;  // hidden channels per split
+constexpr int kRouterTile = 16;   // experts and tokens per workgroup tile
+constexpr int kQuantPerWave = 2;  // x blocks quantized per wavefront by the quantizing workgroups
+constexpr int kRouterDepth = 8;   // 16-channel steps of loads in flight per wavefront
+
+// Splits of H: the largest of 4, 2, 1 whose per-wavefront quarter is a whole number of
+// 16-channel steps.
+inline int router_splits(int H) { return H % 256 == 0 ? 4 : (H % 128 == 0 ? 2 : 1); }
+
+inline int router_quant_groups(int T, int H) {
+  return (T * (H / kBlock) + 4 * kQuantPerWave - 1) / (4 * kQuantPerWave);
+}
 
 __global__ __launch_bounds__(256) void k_router(const uint16_t* __restrict__ x, const float* __restrict__ w,
                                                 double* __restrict__ partial, uint8_t* __restrict__ xq,
-                                                float* __restrict__ xs, int T, int H, int E, int pow2) {
-  const int et = blockIdx.x, split = blockIdx.y, t0 = blockIdx.z * kRouterT;
+                                                float* __restrict__ xs, int T, int H, int E, int n_et, int n_tt,
+                                                int nsplit, int pow2) {
+  __shared__ f64x4 red[3][64];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const int h0 = split * kRouterH, hc = min(kRouterH, H - h0);
-  if (et == (int)gridDim.x - 1) {
-    const int nb = hc / kBlock, nbh = H / kBlock;
-    for (int it = wv; it < kRouterT * nb; it += 4) {
-      const int t = t0 + it / nb, cb = it % nb;
-      if (t >= T) break;
-      const size_t o = (size_t)t * H + h0 + (size_t)cb * kBlock;
-      quant_block(x + o, xq + o, xs + (size_t)t * nbh + h0 / kBlock + cb, pow2, lane);
+  const int n_router = n_et * n_tt * nsplit;
+  if ((int)blockIdx.x >= n_router) {
+    const int nbh = H / kBlock;
+    const int first = (((int)blockIdx.x - n_router) * 4 + wv) * kQuantPerWave;
+#pragma unroll
+    for (int q = 0; q < kQuantPerWave; ++q) {
+      const int it = first + q;
+      if (it < T * nbh) {
+        const int t = it / nbh, cb = it % nbh;
+        const size_t o = (size_t)t * H + (size_t)cb * kBlock;
+        quant_block(x + o, xq + o, xs + (size_t)t * nbh + cb, pow2, lane);
+      }
     }
     return;
   }
+  const int et = blockIdx.x % n_et, tt = (blockIdx.x / n_et) % n_tt, split = blockIdx.x / (n_et * n_tt);
+  const int span = H / nsplit / 4;  // channels per wavefront, a multiple of 16
+  const int k0 = split * (H / nsplit) + wv * span;
   const int g = lane >> 4;
-  const int e = et * kRouterE + (lane & 15), t = t0 + 16 * wv + (lane & 15);
+  const int e = et * kRouterTile + (lane & 15), t = tt * kRouterTile + (lane & 15);
   const bool e_ok = e < E, t_ok = t < T;
-  const float* wp = w + (size_t)(e_ok ? e : 0) * H + h0 + 4 * g;
-  const uint16_t* xp = x + (size_t)(t_ok ? t : 0) * H + h0 + 4 * g;
+  // Rows past E or T read row 0 and are zeroed after the load: the loads themselves stay
+  // unconditional so the compiler keeps several of them in flight.
+  const float* wp = w + (size_t)(e_ok ? e : 0) * H + k0 + 4 * g;
+  const uint16_t* xp = x + (size_t)(t_ok ? t : 0) * H + k0 + 4 * g;
+  const int steps = span / 16;
   f64x4 acc = {0.0, 0.0, 0.0, 0.0};
+  float4 a[kRouterDepth];
+  uint2 b[kRouterDepth];
 #pragma unroll
-  for (int k = 0; k < kRouterH; k += 16) {
-    if (k < hc) {  // hc is 128 or 256
-    float4 a = e_ok ? *reinterpret_cast<const float4*>(wp + k) : make_float4(0.f, 0.f, 0.f, 0.f);
-    uint2 b = t_ok ? *reinterpret_cast<const uint2*>(xp + k) : make_uint2(0u, 0u);
-    acc = __builtin_amdgcn_mfma_f64_16x16x4f64((double)a.x, (double)bf16_bits_to_f32(b.x & 0xffffu), acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f64_16x16x4f64((double)a.y, (double)bf16_bits_to_f32(b.x >> 16), acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f64_16x16x4f64((double)a.z, (double)bf16_bits_to_f32(b.y & 0xffffu), acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f64_16x16x4f64((double)a.w, (double)bf16_bits_to_f32(b.y >> 16), acc, 0, 0, 0);
+  for (int u = 0; u < kRouterDepth; ++u) {
+    const int k = min(u, steps - 1) * 16;
+    a[u] = *reinterpret_cast<const float4*>(wp + k);
+    b[u] = *reinterpret_cast<const uint2*>(xp + k);
+  }
+  for (int s0 = 0; s0 < steps; s0 += kRouterDepth) {
+#pragma unroll
+    for (int u = 0; u < kRouterDepth; ++u) {
+      const float4 av = a[u];
+      const uint2 bv = b[u];
+      // Refill this slot with the step kRouterDepth ahead (clamped; the tail re-reads).
+      const int k = min(s0 + u + kRouterDepth, steps - 1) * 16;
+      a[u] = *reinterpret_cast<const float4*>(wp + k);
+      b[u] = *reinterpret_cast<const uint2*>(xp + k);
+      // Steps past the end contribute zero (their operands are zeroed, not skipped).
+      const bool live = s0 + u < steps;
+      const bool ok_a = e_ok && live, ok_b = t_ok && live;
+      const double a0 = ok_a ? (double)av.x : 0.0, a1 = ok_a ? (double)av.y : 0.0;
+      const double a2 = ok_a ? (double)av.z : 0.0, a3 = ok_a ? (double)av.w : 0.0;
+      const double b0 = ok_b ? (double)bf16_bits_to_f32(bv.x & 0xffffu) : 0.0;
+      const double b1 = ok_b ? (double)bf16_bits_to_f32(bv.x >> 16) : 0.0;
+      const double b2 = ok_b ? (double)bf16_bits_to_f32(bv.y & 0xffffu) : 0.0;
+      const double b3 = ok_b ? (double)bf16_bits_to_f32(bv.y >> 16) : 0.0;
+      acc = __builtin_amdgcn_mfma_f64_16x16x4f64(a0, b0, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f64_16x16x4f64(a1, b1, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f64_16x16x4f64(a2, b2, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f64_16x16x4f64(a3, b3, acc, 0, 0, 0);
     }
   }
-  if (t_ok) {
+  // Quarters of the split, added in wavefront order.
+  if (wv > 0) red[wv - 1][lane] = acc;
+  __syncthreads();
+  if (wv == 0) {
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int eo = et * kRouterE + 4 * g + v;
-      if (eo < E) partial[((size_t)split * T + t) * E + eo] = acc[v];
+    for (int q = 0; q < 3; ++q) {
+      const f64x4 o = red[q][lane];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) acc[v] += o[v];
+    }
+    if (t_ok) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int eo = et * kRouterTile + g + 4 * v;
+        if (eo < E) partial[((size_t)split * T + t) * E + eo] = acc[v];
+      }
     }
   }
 }
@@ -263,54 +320,93 @@ __device__ __forceinline__ unsigned top_codes(const uint32_t (&code)[VPL], const
   return pick;
 }
 
+constexpr int kSelectTokens = 4;  // tokens per workgroup, one wavefront each
+constexpr int kMaxSplits = 4;     // router splits of H (router_splits)
+
 template <int VPL>
-__global__ __launch_bounds__(64) void k_select(const double* __restrict__ partial, int nsplit,
-                                               const float* __restrict__ logits_in, const float* __restrict__ bias,
-                                               int T, int E, int K, int G, int TG, int gate, int renorm,
-                                               float scaling, int64_t* __restrict__ ids_out,
-                                               float* __restrict__ w_out) {
-  __shared__ float choice_lds[kMaxExperts];
-  __shared__ float gscore[kMaxGroups];
-  __shared__ uint32_t pick_code[kMaxTopK];
-  __shared__ int pick_id[kMaxTopK];
-  __shared__ float pick_val[kMaxTopK];
-  const int t = blockIdx.x, lane = threadIdx.x;
-  float logit[VPL], prob[VPL], choice[VPL];
-  bool valid[VPL];
+__global__ __launch_bounds__(256) void k_select(const double* __restrict__ partial, int nsplit,
+                                                const float* __restrict__ logits_in, const float* __restrict__ bias,
+                                                int T, int E, int K, int G, int TG, int gate, int renorm,
+                                                float scaling, int64_t* __restrict__ ids_out,
+                                                float* __restrict__ w_out) {
+  __shared__ float lds_logit[kSelectTokens][kMaxExperts];
+  __shared__ float gscore[kSelectTokens][kMaxGroups];
+  __shared__ uint32_t pick_code_s[kSelectTokens][kMaxTopK];
+  __shared__ int pick_id_s[kSelectTokens][kMaxTopK];
+  __shared__ float pick_val_s[kSelectTokens][kMaxTopK];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int t0 = blockIdx.x * kSelectTokens, t = t0 + wv;
+  const bool token_ok = t < T;
+  float* choice_lds = lds_logit[wv];
+  uint32_t* pick_code = pick_code_s[wv];
+  int* pick_id = pick_id_s[wv];
+  float* pick_val = pick_val_s[wv];
+
+  float bias_v[VPL];
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    const float v = bias ? bias[min(lane + 64 * j, E - 1)] : 0.0f;
+    bias_v[j] = lane + 64 * j < E ? v : 0.0f;
+  }
+
+  // Logits of the workgroup's tokens into LDS: thread i sums the splits (in split order)
+  // of entries i, i+256, ... (at most 4*VPL of them, up to kMaxSplits splits each), every
+  // load issued before the first add.
+  const int n_here = min(kSelectTokens, T - t0) * E;
   if (logits_in) {
 #pragma unroll
-    for (int j = 0; j < VPL; ++j) {
-      const int e = lane + 64 * j;
-      logit[j] = e < E ? logits_in[(size_t)t * E + e] : -INFINITY;
+    for (int r = 0; r < 4 * VPL; ++r) {
+      const int i = threadIdx.x + 256 * r;
+      const float v = logits_in[(size_t)t0 * E + min(i, n_here - 1)];
+      if (i < n_here) lds_logit[i / E][i % E] = v;
     }
   } else {
-    double s[VPL];
-#pragma unroll
-    for (int j = 0; j < VPL; ++j) s[j] = 0.0;
-    const double* p = partial + (size_t)t * E + lane;
     const size_t stride = (size_t)T * E;
-#pragma unroll 4
-    for (int q = 0; q < nsplit; ++q) {
+    const double* p = partial + (size_t)t0 * E;
+    constexpr int R = 4 * VPL < 8 ? 4 * VPL : 8;  // entries per round of loads
 #pragma unroll
-      for (int j = 0; j < VPL; ++j)
-        if (lane + 64 * j < E) s[j] += p[(size_t)q * stride + 64 * j];
+    for (int r0 = 0; r0 < 4 * VPL; r0 += R) {
+      double part[R][kMaxSplits];
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int i = threadIdx.x + 256 * (r0 + r);
+#pragma unroll
+        for (int q = 0; q < kMaxSplits; ++q) {
+          // Clamped, unconditional loads (entries past the end are dropped below).
+          const double v = p[(size_t)min(q, nsplit - 1) * stride + min(i, n_here - 1)];
+          part[r][q] = q < nsplit ? v : 0.0;
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int i = threadIdx.x + 256 * (r0 + r);
+        double s = 0.0;
+#pragma unroll
+        for (int q = 0; q < kMaxSplits; ++q)
+          if (q < nsplit) s += part[r][q];
+        if (i < n_here) lds_logit[i / E][i % E] = (float)s;
+      }
     }
-#pragma unroll
-    for (int j = 0; j < VPL; ++j) logit[j] = lane + 64 * j < E ? (float)s[j] : -INFINITY;
   }
+  __syncthreads();
+
+  float logit[VPL], prob[VPL], choice[VPL];
+  bool valid[VPL];
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
     const int e = lane + 64 * j;
-    valid[j] = e < E;
+    valid[j] = token_ok && e < E;
+    logit[j] = valid[j] ? lds_logit[wv][e] : -INFINITY;
     if (gate == MEGAMOE_GATE_SIGMOID) {
       const float p = 1.0f / (1.0f + expf(-logit[j]));
       prob[j] = p;
-      choice[j] = p + (bias && valid[j] ? bias[e] : 0.0f);
+      choice[j] = p + bias_v[j];
     } else {
       prob[j] = logit[j];
       choice[j] = logit[j];
     }
   }
+  __syncthreads();  // lds_logit is reused below for the choices
 
   if (G > 1) {
     // Group score: the sum of the two largest choices of the group (frontier.py:234).
@@ -319,8 +415,9 @@ __global__ __launch_bounds__(64) void k_select(const double* __restrict__ partia
     for (int j = 0; j < VPL; ++j)
       if (valid[j]) choice_lds[lane + 64 * j] = choice[j];
     __syncthreads();
-    if (lane < G) {
+    if (lane < G && token_ok) {
       float b1 = -INFINITY, b2 = -INFINITY;
+#pragma unroll 8
       for (int i = 0; i < gs; ++i) {
         const float v = choice_lds[lane * gs + i];
         if (v > b1) {
@@ -330,16 +427,16 @@ __global__ __launch_bounds__(64) void k_select(const double* __restrict__ partia
           b2 = v;
         }
       }
-      gscore[lane] = gs >= 2 ? b1 + b2 : b1;
+      gscore[wv][lane] = gs >= 2 ? b1 + b2 : b1;
     }
     __syncthreads();
     // Keep the TG best groups, ties to the lower group index (frontier.py:235).
     bool keep = false;
-    if (lane < G) {
-      const float mine = gscore[lane];
+    if (lane < G && token_ok) {
+      const float mine = gscore[wv][lane];
       int rank = 0;
       for (int h = 0; h < G; ++h) {
-        const float o = gscore[h];
+        const float o = gscore[wv][h];
         rank += (o > mine) || (o == mine && h < lane);
       }
       keep = rank < TG;
@@ -353,7 +450,7 @@ __global__ __launch_bounds__(64) void k_select(const double* __restrict__ partia
   uint32_t code[VPL];
 #pragma unroll
   for (int j = 0; j < VPL; ++j) code[j] = order_code(choice[j]);
-  const unsigned pick = top_codes<VPL>(code, valid, K);
+  const unsigned pick = token_ok ? top_codes<VPL>(code, valid, K) : 0u;
 
   // Compact the K picks into LDS, then rank them: (code desc, index asc).
   int base = 0;
@@ -373,7 +470,7 @@ __global__ __launch_bounds__(64) void k_select(const double* __restrict__ partia
   __syncthreads();
   int my_id = 0, rank = 0;
   float my_val = 0.0f;
-  if (lane < K) {
+  if (lane < K && token_ok) {
     const uint32_t c = pick_code[lane];
     my_id = pick_id[lane];
     my_val = pick_val[lane];
@@ -383,11 +480,12 @@ __global__ __launch_bounds__(64) void k_select(const double* __restrict__ partia
     }
   }
   __syncthreads();
-  if (lane < K) {
+  if (lane < K && token_ok) {
     pick_id[rank] = my_id;
     pick_val[rank] = my_val;
   }
   __syncthreads();
+  if (!token_ok) return;
   if (lane < K) {
     my_id = pick_id[lane];
     my_val = pick_val[lane];
@@ -982,15 +1080,25 @@ __global__ __launch_bounds__(256) void k_combine(const uint16_t* __restrict__ d_
   float acc[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
-  for (int s = 0; s < K; ++s) {
-    const int pos = inv[t * K + s];
-    const float wv = wts[t * K + s];
-    const uint4 v = *reinterpret_cast<const uint4*>(d_r + (size_t)pos * H + h0);
-    const uint32_t q[4] = {v.x, v.y, v.z, v.w};
+  for (int s0 = 0; s0 < K; s0 += 8) {  // eight slots' loads in flight at a time
+    uint4 v[8];
+    float wv[8];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      acc[2 * i] = __fadd_rn(acc[2 * i], __fmul_rn(bf16_bits_to_f32(q[i] & 0xffffu), wv));
-      acc[2 * i + 1] = __fadd_rn(acc[2 * i + 1], __fmul_rn(bf16_bits_to_f32(q[i] >> 16), wv));
+    for (int u = 0; u < 8; ++u) {
+      const int s = min(s0 + u, K - 1);  // clamped, unconditional loads
+      v[u] = *reinterpret_cast<const uint4*>(d_r + (size_t)inv[t * K + s] * H + h0);
+      wv[u] = wts[t * K + s];
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      if (s0 + u < K) {
+        const uint32_t q[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          acc[2 * i] = __fadd_rn(acc[2 * i], __fmul_rn(bf16_bits_to_f32(q[i] & 0xffffu), wv[u]));
+          acc[2 * i + 1] = __fadd_rn(acc[2 * i + 1], __fmul_rn(bf16_bits_to_f32(q[i] >> 16), wv[u]));
+        }
+      }
     }
   }
   if (S > 0) {
@@ -1033,7 +1141,7 @@ size_t max_chunks(const megamoe_desc& d, int copies) {
 Layout make_layout(const megamoe_desc& d) {
   Layout L{};
   const size_t T = d.tokens, H = d.hidden, E = d.experts, K = d.topk, I = d.intermediate, S = d.shared_experts;
-  L.nsplit = (int)((H + kRouterH - 1) / kRouterH);
+  L.nsplit = router_splits((int)H);
   size_t at = 0;
   auto take = [&](size_t bytes) {
     const size_t o = at;
@@ -1111,9 +1219,11 @@ int device_info(DeviceInfo* out) {
 // Router partials (and, with the extra expert tile, the quantized x) for all tokens.
 int launch_router(const megamoe_desc& d, const Layout& L, const void* x, const float* router, char* ws,
                   hipStream_t st) {
-  const dim3 grid((d.experts + kRouterE - 1) / kRouterE + 1, L.nsplit, (d.tokens + kRouterT - 1) / kRouterT);
-  hipLaunchKernelGGL(k_router, grid, dim3(256), 0, st, (const uint16_t*)x, router, (double*)(ws + L.partial),
-                     (uint8_t*)(ws + L.xq), (float*)(ws + L.xs), d.tokens, d.hidden, d.experts, d.pow2_scales);
+  const int n_et = (d.experts + kRouterTile - 1) / kRouterTile, n_tt = (d.tokens + kRouterTile - 1) / kRouterTile;
+  const int n_router = n_et * n_tt * L.nsplit;
+  hipLaunchKernelGGL(k_router, dim3(n_router + router_quant_groups(d.tokens, d.hidden)), dim3(256), 0, st,
+                     (const uint16_t*)x, router, (double*)(ws + L.partial), (uint8_t*)(ws + L.xq),
+                     (float*)(ws + L.xs), d.tokens, d.hidden, d.experts, n_et, n_tt, L.nsplit, d.pow2_scales);
   MEGAMOE_LAUNCH_CHECK();
   return MEGAMOE_OK;
 }
@@ -1140,7 +1250,7 @@ int launch_quant(int rows, int cols, const void* x, uint8_t* q, float* s, int po
 // Routing from fp32 logits, or (logits == NULL) from the router's fp64 split partials.
 int launch_select(const megamoe_desc& d, const double* partial, int nsplit, const float* logits, const float* bias,
                   int64_t* ids, float* w, hipStream_t st) {
-  const dim3 grid(d.tokens), block(64);
+  const dim3 grid((d.tokens + kSelectTokens - 1) / kSelectTokens), block(256);
 #define MEGAMOE_SELECT(VPL)                                                                                   \
   hipLaunchKernelGGL(k_select<VPL>, grid, block, 0, st, partial, nsplit, logits, bias, d.tokens, d.experts,   \
                      d.topk, d.groups, d.top_groups, d.gate, d.renormalize, d.routed_scaling, ids, w)
