@@ -42,7 +42,7 @@ def _log(msg: str) -> None:
 
 
 def kernel_bytes(case, hit: int) -> dict:
-    """Algorithmic HBM bytes of the two expert kernels for U = hit experts."""
+    """Algorithmic HBM bytes of the gate/up and down halves of the expert kernel for U = hit experts."""
     H, I, S, T, K = case.hidden, case.intermediate, case.shared_experts, case.tokens, case.topk
     bh, bi = math.ceil(H / 128), math.ceil(I / 128)
     gu = hit * (2 * I * H + 4 * 2 * bi * bh)
@@ -92,6 +92,7 @@ def bench_case(case, steps: int, warmup: int, want_cpu: bool, cpu_budget: float)
     import torch
 
     pkg = __graft_entry__.load_package()  # noqa: F841
+    from vibe_megakernel_amd import _lib
     from vibe_megakernel_amd import cases as C
     from vibe_megakernel_amd import submission, workloads
 
@@ -133,11 +134,12 @@ def bench_case(case, steps: int, warmup: int, want_cpu: bool, cpu_budget: float)
     for i in range(max(3, min(steps, 10))):
         _, st = layer.timed(sets[i % n_sets])
         stage.append(st)
-    stage_ms = [statistics.median(s[i] for s in stage) for i in range(6)]
+    stage_ms = [statistics.median(s[i] for s in stage) for i in range(len(stage[0]))]
 
     bytes_step = C.algorithmic_bytes(case, 0) + (C.algorithmic_bytes(case, 1) - C.algorithmic_bytes(case, 0)) * hit
     kb = kernel_bytes(case, hit)
-    gu_ms = stage_ms[3]
+    ex_ms = stage_ms[3]
+    ex_bytes = kb["gate_up"] + kb["down"]
     result = {
         "case": case.id, "ms_per_step": ms, "us_per_step": ms * 1e3,
         "p50_us": statistics.median(step_ms) * 1e3,
@@ -146,13 +148,11 @@ def bench_case(case, steps: int, warmup: int, want_cpu: bool, cpu_budget: float)
         "tb_per_s": bytes_step / (ms * 1e-3) / 1e12,
         "hbm_frac": bytes_step / (ms * 1e-3) / PEAK_HBM,
         "mfma_frac": C.algorithmic_flops(case) / (ms * 1e-3) / PEAK_FP8,
-        "stage_us": {name: v * 1e3 for name, v in zip(
-            ("router_quant", "select", "permute", "gate_up", "down", "combine"), stage_ms)},
+        "stage_us": {name: v * 1e3 for name, v in zip(_lib.STAGES, stage_ms)},
         "rotation_sets": n_sets,
-        "roofline": {"bound": "hbm", "achieved": kb["gate_up"] / (gu_ms * 1e-3) / 1e9, "peak": PEAK_HBM / 1e9,
-                     "unit": "GB/s", "frac": kb["gate_up"] / (gu_ms * 1e-3) / PEAK_HBM, "traffic": None,
-                     "kernel": "k_gateup", "kernel_us": gu_ms * 1e3, "bytes_per_launch": kb["gate_up"]},
-        "down_roofline_frac": kb["down"] / (stage_ms[4] * 1e-3) / PEAK_HBM,
+        "roofline": {"bound": "hbm", "achieved": ex_bytes / (ex_ms * 1e-3) / 1e9, "peak": PEAK_HBM / 1e9,
+                     "unit": "GB/s", "frac": ex_bytes / (ex_ms * 1e-3) / PEAK_HBM, "traffic": None,
+                     "kernel": "k_experts", "kernel_us": ex_ms * 1e3, "bytes_per_launch": ex_bytes},
     }
     if want_cpu:
         _log(f"[bench] {case.id}: CPU oracle baseline")
@@ -207,7 +207,7 @@ def main() -> int:
         "roofline": r["roofline"],
         "cpu_baseline": r.get("cpu_baseline"),
         "configs": {cid: {"us_per_step": v["us_per_step"], "tb_per_s": v["tb_per_s"], "hbm_frac": v["hbm_frac"],
-                          "hit_experts": v["hit_experts"], "gate_up_frac": v["roofline"]["frac"]}
+                          "hit_experts": v["hit_experts"], "experts_frac": v["roofline"]["frac"]}
                     for cid, v in results.items()},
     }
     print(json.dumps(line), flush=True)

@@ -117,8 +117,8 @@ int megamoe_workspace_bytes(const megamoe_desc* desc, size_t* bytes);
 int megamoe_forward(const megamoe_desc* desc, const megamoe_tensors* t, void* stream);
 
 /* megamoe_forward with a device event between its stages; blocks until the
- * call has finished and writes the elapsed ms of each stage to stage_ms[0..5]
- * (router+quantize, select, permute, gate/up, down, combine). For
+ * call has finished and writes the elapsed ms of each stage to stage_ms[0..4]
+ * (router+quantize, select, permute, experts = gate/up + down, combine). For
  * measurement; the results equal megamoe_forward's. */
 int megamoe_forward_timed(const megamoe_desc* desc, const megamoe_tensors* t, void* stream,
                           float* stage_ms);

@@ -1,20 +1,21 @@
 // megamoe.hip — FP8 (E4M3, 128x128 block-scaled) MoE decode layer for MI355X (gfx950).
 //
-// The layer, as eight stream-ordered kernel launches (one process, one GPU):
-//   k_router, k_logits        router logits: fp64-accumulated GEMV over 256-wide splits of H,
-//                             splits added in order and rounded once to fp32
-//   k_quant_rows              per-token-per-128 E4M3 quantization of x
-//   k_select                  one wavefront per token: sigmoid/softmax gate, group-limited
-//                             top-k with a (value desc, index asc) total order
+// The layer, as five stream-ordered kernel launches (one process, one GPU):
+//   k_router                  router logits on fp64 MFMA as split partials over H; its extra
+//                             workgroups quantize x (E4M3, one fp32 scale per token per 128)
+//   k_select                  adds the split partials in order and rounds once to fp32, then
+//                             per token (one wavefront each): sigmoid/softmax gate,
+//                             group-limited top-k with a (value desc, index asc) total order
 //   k_permute                 one workgroup: expert histogram, exclusive scan, stable
 //                             (token, slot)-ordered permutation, and the expert work lists
 //                             (chunks of <= 64 rows, heaviest first)
-//   k_gateup                  persistent workgroups draining a work queue of
-//                             (chunk, 128-row block of I) units: gate and up rows streamed
-//                             from HBM into fp8 MFMA (16x16x128, weights as the M operand,
-//                             tokens as N), 128x128 block scales applied per K block, SwiGLU
-//                             and the per-128 E4M3 requantization of h fused in the epilogue
-//   k_down                    the same over (chunk, 128-row block of H) units
+//   k_experts                 one persistent kernel draining a work queue of gate/up units
+//                             (chunk, 128-row block of I), then down units (chunk, 128-row
+//                             block of H): weights streamed from HBM into fp8 MFMA
+//                             (16x16x128, weights as the M operand, tokens as N), 128x128
+//                             block scales applied per K block, SwiGLU and the per-128 E4M3
+//                             requantization of h fused into gate/up; a down unit starts
+//                             as soon as the gate/up units of its rows are done
 //   k_combine                 slot-order fp32 sum of bf16(d)*w plus the shared expert,
 //                             rounded once to bf16
 //
@@ -33,6 +34,10 @@
 namespace {
 
 constexpr int kBlock = 128;  // quantization block edge (weights 128x128, activations 1x128)
+
+// Row stride (in floats) of the h scale rows: whole 128-byte lines, so rows of different
+// chunks never share a cache line (see the hand-over notes of the expert kernel).
+__host__ __device__ constexpr int scale_ld(int blocks) { return (blocks + 31) / 32 * 32; }
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x8 __attribute__((ext_vector_type(8)));
@@ -568,7 +573,8 @@ __device__ unsigned long long block_exclusive_scan(unsigned long long v, unsigne
   return base + x - v;
 }
 
-constexpr int kMetaHit = 0, kMetaUnitsGU = 1, kMetaUnitsDN = 2, kMetaQueueGU = 3, kMetaQueueDN = 4;
+constexpr int kMetaHit = 0, kMetaUnitsGU = 1, kMetaUnitsDN = 2, kMetaQueueGU = 3, kMetaQueueDN = 4,
+              kMetaError = 6;
 constexpr int kChunkRows = 64;
 
 struct PermuteOut {
@@ -579,6 +585,8 @@ struct PermuteOut {
   int* inv;      // [T*K] token*K + slot -> grouped row
   int4* gu;      // gate/up chunks {expert (E = shared), first row, rows, first 128-block}
   int4* dn;      // down chunks
+  int* dn_of_gu; // gate/up chunk -> down chunk of the same rows
+  int* ready;    // [down chunks] zeroed here, counted by the expert kernel
 };
 
 __device__ __forceinline__ int chunk_class(int rows) { return rows > 32 ? 0 : (rows > 16 ? 1 : 2); }
@@ -629,16 +637,19 @@ __global__ __launch_bounds__(1024) void k_permute(const int64_t* __restrict__ id
       const int4 ch = make_int4(tid, kChunkRows * i, min(kChunkRows, c - kChunkRows * i), 0);
       out.gu[gbase[0] + gshared[0] + p4 + i] = ch;
       out.dn[dbase[0] + dshared[0] + p4 + i] = ch;
+      out.dn_of_gu[gbase[0] + gshared[0] + p4 + i] = dbase[0] + dshared[0] + p4 + i;
     }
     if (a2) {
       const int4 ch = make_int4(tid, kChunkRows * full, rem, 0);
       out.gu[gbase[1] + gshared[1] + p2] = ch;
       out.dn[dbase[1] + dshared[1] + p2] = ch;
+      out.dn_of_gu[gbase[1] + gshared[1] + p2] = dbase[1] + dshared[1] + p2;
     }
     if (a1) {
       const int4 ch = make_int4(tid, kChunkRows * full, rem, 0);
       out.gu[gbase[2] + gshared[2] + p1] = ch;
       out.dn[dbase[2] + dshared[2] + p1] = ch;
+      out.dn_of_gu[gbase[2] + gshared[2] + p1] = dbase[2] + dshared[2] + p1;
     }
   }
   if (tid == 0) {
@@ -648,8 +659,10 @@ __global__ __launch_bounds__(1024) void k_permute(const int64_t* __restrict__ id
         const int cls = chunk_class(rows);
         const int idx = cls == 0 ? i : 0;        // index within the shared part of the class
         const int per_copy = cls == 0 ? s4 : 1;  // shared chunks of this class per copy
-        for (int s = 0; s < S; ++s)
+        for (int s = 0; s < S; ++s) {
           out.gu[gbase[cls] + s * per_copy + idx] = make_int4(E, kChunkRows * i, rows, s * nbI);
+          out.dn_of_gu[gbase[cls] + s * per_copy + idx] = dbase[cls] + idx;
+        }
         out.dn[dbase[cls] + idx] = make_int4(E, kChunkRows * i, rows, 0);
       }
     }
@@ -659,7 +672,10 @@ __global__ __launch_bounds__(1024) void k_permute(const int64_t* __restrict__ id
     out.meta[kMetaUnitsDN] = (s4 + s2 + s1 + t4 + t2 + t1) * nbH;
     out.meta[kMetaQueueGU] = 0;
     out.meta[kMetaQueueDN] = 0;
+    out.meta[kMetaError] = 0;
   }
+  const int dtot = s4 + s2 + s1 + t4 + t2 + t1;
+  for (int i = tid; i < dtot; i += blockDim.x) out.ready[i] = 0;
   if (tid < E) cnt[tid] = off;  // reuse as offsets (every thread read its count above)
   __syncthreads();
   for (int i = tid; i < n; i += blockDim.x) {
@@ -672,6 +688,29 @@ __global__ __launch_bounds__(1024) void k_permute(const int64_t* __restrict__ id
     out.inv[i] = pos;
   }
 }
+
+// ---------------------------------------------------------------------------------------
+// Cross-workgroup hand-over inside the expert kernel (h from gate/up units to down
+// units). h and its scales are written with device-coherent stores (relaxed agent-scope
+// atomic stores, which write through the XCD's L2 to memory), so publishing them takes
+// only a wait for the stores to complete, not a writeback of the whole L2. Readers use
+// ordinary loads, which cannot return a stale line: every cache is coherent when the
+// kernel starts (kernel-boundary acquire), each 128-byte line of h and of the padded
+// scale rows is written by exactly one unit, and no workgroup reads a line before the
+// count of its writer has landed, so no cache can hold an old copy of it.
+// ---------------------------------------------------------------------------------------
+
+__device__ __forceinline__ void store_coherent(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_coherent(uint64_t* p, uint64_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_coherent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// All of this wavefront's memory operations complete (vmcnt, expcnt and lgkmcnt zero).
+__device__ __forceinline__ void publish_fence() { __builtin_amdgcn_s_waitcnt(0); }
 
 // ---------------------------------------------------------------------------------------
 // Expert GEMM core. One wavefront multiplies RT row tiles (16 weight rows each) by NCT
@@ -808,7 +847,7 @@ __device__ void gateup_unit(const GateUpArgs& a, const uint8_t* wg, const uint8_
                             float (*red)[64]) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int kofs = 16 * (lane >> 4);
-  const int H = a.H, nkb = H / kBlock, nbh = ldh / kBlock;
+  const int H = a.H, nkb = H / kBlock, nbh = scale_ld(ldh / kBlock);
   Operands<4, NCT, 2> op;
 #pragma unroll
   for (int r = 0; r < 2; ++r) {
@@ -860,23 +899,24 @@ __device__ void gateup_unit(const GateUpArgs& a, const uint8_t* wg, const uint8_
         uint32_t packed = 0;
 #pragma unroll
         for (int v = 0; v < 4; ++v) packed |= f32_to_e4m3(clamp448(hv[c][p][v] / s)) << (8 * v);
-        *reinterpret_cast<uint32_t*>(dst + 16 * p) = packed;
+        store_coherent(reinterpret_cast<uint32_t*>(dst + 16 * p), packed);
       }
-      if (w == 0 && lane < 16) hs[(size_t)(cr.row0 + col) * nbh + jb] = s;
+      if (w == 0 && lane < 16) store_coherent(hs + (size_t)(cr.row0 + col) * nbh + jb, s);
     }
   }
 }
 
 // Gate/up unit for 33..64 activation rows (four column tiles). To keep the accumulators
 // of four column tiles within the register budget, the 128-row block is done in two
-// 64-row halves: in half hf, wave w owns gate and up rows 64*hf + 16w .. +15.
+// 64-row halves: in half hf, wave w owns gate and up rows 64*hf + 16w .. +15. The h
+// values of the first half wait in LDS (hbuf) while the second half streams.
 __device__ void gateup_unit_wide(const GateUpArgs& a, const uint8_t* wg, const uint8_t* wu, const float* sg,
                                  const float* su, const ChunkRows& cr, int jb, uint8_t* hq, float* hs, int ldh,
-                                 float (*red)[64]) {
+                                 float (*red)[64], float* hbuf) {
   constexpr int NCT = 4;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int kofs = 16 * (lane >> 4);
-  const int H = a.H, nkb = H / kBlock, nbh = ldh / kBlock;
+  const int H = a.H, nkb = H / kBlock, nbh = scale_ld(ldh / kBlock);
   Operands<2, NCT, 2> op;
   op.sw[0] = sg;
   op.sw[1] = su;
@@ -887,8 +927,11 @@ __device__ void gateup_unit_wide(const GateUpArgs& a, const uint8_t* wg, const u
     op.b[c] = a.xq + (size_t)tok * H + kofs;
     op.sx[c] = a.xs + (size_t)tok * nkb;
   }
-  float hv[2][NCT][4];
+  float* mine = hbuf + (size_t)threadIdx.x * (NCT * 4);  // this lane's first-half h values
+  float amax[NCT];
 #pragma unroll
+  for (int c = 0; c < NCT; ++c) amax[c] = 0.0f;
+#pragma unroll 1
   for (int hf = 0; hf < 2; ++hf) {
     const size_t row = (size_t)(64 * hf + 16 * w + (lane & 15));
     op.a[0] = wg + row * H + kofs;
@@ -899,89 +942,83 @@ __device__ void gateup_unit_wide(const GateUpArgs& a, const uint8_t* wg, const u
     for (int c = 0; c < NCT; ++c)
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        const float g = round_bf16(acc[0][c][v]);
-        const float u = round_bf16(acc[1][c][v]);
-        hv[hf][c][v] = round_bf16(silu(g) * u);
+        const float h = round_bf16(silu(round_bf16(acc[0][c][v])) * round_bf16(acc[1][c][v]));
+        acc[0][c][v] = h;
+        amax[c] = fmaxf(amax[c], fabsf(h));
       }
-  }
+    if (hf == 0) {
 #pragma unroll
-  for (int c = 0; c < NCT; ++c) {
-    float amax = 0.0f;
+      for (int c = 0; c < NCT; ++c)
 #pragma unroll
-    for (int hf = 0; hf < 2; ++hf)
+        for (int v = 0; v < 4; ++v) mine[4 * c + v] = acc[0][c][v];
+    } else {
 #pragma unroll
-      for (int v = 0; v < 4; ++v) amax = fmaxf(amax, fabsf(hv[hf][c][v]));
-    amax = fmaxf(amax, __shfl_xor(amax, 16));
-    amax = fmaxf(amax, __shfl_xor(amax, 32));
-    if (lane < 16) red[w][16 * c + lane] = amax;
-  }
-  __syncthreads();
-#pragma unroll
-  for (int c = 0; c < NCT; ++c) {
-    const int col = 16 * c + (lane & 15);
-    const float amax = fmaxf(fmaxf(red[0][col], red[1][col]), fmaxf(red[2][col], red[3][col]));
-    const float s = act_scale(amax, a.pow2);
-    if (col < cr.n) {
-      uint8_t* dst = hq + (size_t)(cr.row0 + col) * ldh + (size_t)jb * kBlock + 16 * w + 4 * (lane >> 4);
-#pragma unroll
-      for (int hf = 0; hf < 2; ++hf) {
-        uint32_t packed = 0;
-#pragma unroll
-        for (int v = 0; v < 4; ++v) packed |= f32_to_e4m3(clamp448(hv[hf][c][v] / s)) << (8 * v);
-        *reinterpret_cast<uint32_t*>(dst + 64 * hf) = packed;
+      for (int c = 0; c < NCT; ++c) {
+        float m = fmaxf(amax[c], __shfl_xor(amax[c], 16));
+        m = fmaxf(m, __shfl_xor(m, 32));
+        if (lane < 16) red[w][16 * c + lane] = m;
       }
-      if (w == 0 && lane < 16) hs[(size_t)(cr.row0 + col) * nbh + jb] = s;
+      __syncthreads();
+#pragma unroll
+      for (int c = 0; c < NCT; ++c) {
+        const int col = 16 * c + (lane & 15);
+        const float amx = fmaxf(fmaxf(red[0][col], red[1][col]), fmaxf(red[2][col], red[3][col]));
+        const float s = act_scale(amx, a.pow2);
+        if (col < cr.n) {
+          uint8_t* dst = hq + (size_t)(cr.row0 + col) * ldh + (size_t)jb * kBlock + 16 * w + 4 * (lane >> 4);
+          uint32_t p0 = 0, p1 = 0;
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            p0 |= f32_to_e4m3(clamp448(mine[4 * c + v] / s)) << (8 * v);
+            p1 |= f32_to_e4m3(clamp448(acc[0][c][v] / s)) << (8 * v);
+          }
+          store_coherent(reinterpret_cast<uint32_t*>(dst), p0);
+          store_coherent(reinterpret_cast<uint32_t*>(dst + 64), p1);
+          if (w == 0 && lane < 16) store_coherent(hs + (size_t)(cr.row0 + col) * nbh + jb, s);
+        }
+      }
     }
   }
 }
 
-__global__ __launch_bounds__(256, 2) void k_gateup(GateUpArgs a) {
-  __shared__ float red[4][64];
-  __shared__ int slot;
+// Gate/up unit u of the work list: chunk u / nbI, 128-row block u % nbI of the chunk's
+// expert (plus the slice offset of a shared-expert copy).
+__device__ void gateup_work(const GateUpArgs& a, int u, float (*red)[64], float* hbuf) {
   const int nbI = a.I / kBlock, nkb = a.H / kBlock;
-  const int total = a.meta[kMetaUnitsGU];
-  // First unit: blockIdx.x; after that, units gridDim.x, gridDim.x+1, ... from the queue.
-  int u = blockIdx.x;
-  while (u < total) {
-    __syncthreads();
-    next_unit(&a.meta[kMetaQueueGU], &slot, gridDim.x);  // arrives while this unit streams
-    const int4 ch = a.chunks[u / nbI];
-    const int j = u % nbI, jb = ch.w + j;
-    const uint8_t *wg, *wu;
-    const float *sg, *su;
-    uint8_t* hq;
-    float* hs;
-    int ldh;
-    ChunkRows cr;
-    if (ch.x == a.E) {  // shared expert: rows of its S*I-row gate/up matrices
-      wg = a.sgate + (size_t)jb * kBlock * a.H;
-      wu = a.sup + (size_t)jb * kBlock * a.H;
-      sg = a.sgate_scale + (size_t)jb * nkb;
-      su = a.sup_scale + (size_t)jb * nkb;
-      cr = ChunkRows{ch.z, ch.y, nullptr, a.K};
-      hq = a.hq_s;
-      hs = a.hs_s;
-      ldh = a.S * a.I;
-    } else {
-      const size_t rowblk = (size_t)ch.x * nbI + jb;
-      wg = a.gate + rowblk * kBlock * a.H;
-      wu = a.up + rowblk * kBlock * a.H;
-      sg = a.gate_scale + rowblk * nkb;
-      su = a.up_scale + rowblk * nkb;
-      cr = ChunkRows{ch.z, a.offsets[ch.x] + ch.y, a.perm, a.K};
-      hq = a.hq_r;
-      hs = a.hs_r;
-      ldh = a.I;
-    }
-    if (cr.n <= 16)
-      gateup_unit<1>(a, wg, wu, sg, su, cr, jb, hq, hs, ldh, red);
-    else if (cr.n <= 32)
-      gateup_unit<2>(a, wg, wu, sg, su, cr, jb, hq, hs, ldh, red);
-    else
-      gateup_unit_wide(a, wg, wu, sg, su, cr, jb, hq, hs, ldh, red);
-    __syncthreads();
-    u = slot;
+  const int4 ch = a.chunks[u / nbI];
+  const int j = u % nbI, jb = ch.w + j;
+  const uint8_t *wg, *wu;
+  const float *sg, *su;
+  uint8_t* hq;
+  float* hs;
+  int ldh;
+  ChunkRows cr;
+  if (ch.x == a.E) {  // shared expert: rows of its S*I-row gate/up matrices
+    wg = a.sgate + (size_t)jb * kBlock * a.H;
+    wu = a.sup + (size_t)jb * kBlock * a.H;
+    sg = a.sgate_scale + (size_t)jb * nkb;
+    su = a.sup_scale + (size_t)jb * nkb;
+    cr = ChunkRows{ch.z, ch.y, nullptr, a.K};
+    hq = a.hq_s;
+    hs = a.hs_s;
+    ldh = a.S * a.I;
+  } else {
+    const size_t rowblk = (size_t)ch.x * nbI + jb;
+    wg = a.gate + rowblk * kBlock * a.H;
+    wu = a.up + rowblk * kBlock * a.H;
+    sg = a.gate_scale + rowblk * nkb;
+    su = a.up_scale + rowblk * nkb;
+    cr = ChunkRows{ch.z, a.offsets[ch.x] + ch.y, a.perm, a.K};
+    hq = a.hq_r;
+    hs = a.hs_r;
+    ldh = a.I;
   }
+  if (cr.n <= 16)
+    gateup_unit<1>(a, wg, wu, sg, su, cr, jb, hq, hs, ldh, red);
+  else if (cr.n <= 32)
+    gateup_unit<2>(a, wg, wu, sg, su, cr, jb, hq, hs, ldh, red);
+  else
+    gateup_unit_wide(a, wg, wu, sg, su, cr, jb, hq, hs, ldh, red, hbuf);
 }
 
 struct DownArgs {
@@ -1012,7 +1049,7 @@ __device__ void down_unit(const DownArgs& a, const uint8_t* wd, const float* sd,
   for (int c = 0; c < NCT; ++c) {
     const int r = min(16 * c + (lane & 15), cr.n - 1);
     op.b[c] = hq + (size_t)(cr.row0 + r) * ldk + kofs;
-    op.sx[c] = hs + (size_t)(cr.row0 + r) * nkb;
+    op.sx[c] = hs + (size_t)(cr.row0 + r) * scale_ld(nkb);
   }
   f32x4 acc[2][NCT];
   stream_gemm<2, NCT, 1, NCT == 1 ? 4 : (NCT == 2 ? 3 : 2)>(op, nkb, acc);
@@ -1031,52 +1068,41 @@ __device__ void down_unit(const DownArgs& a, const uint8_t* wd, const float* sd,
   }
 }
 
-__global__ __launch_bounds__(256, 2) void k_down(DownArgs a) {
-  __shared__ int slot;
+// Down unit v of the work list: chunk v / nbH, 128-row block v % nbH of the down matrix.
+__device__ void down_work(const DownArgs& a, int v) {
   const int nbH = a.H / kBlock, nbI = a.I / kBlock;
-  const int total = a.meta[kMetaUnitsDN];
-  int u = blockIdx.x;
-  while (u < total) {
-    __syncthreads();
-    next_unit(&a.meta[kMetaQueueDN], &slot, gridDim.x);
-    const int4 ch = a.chunks[u / nbH];
-    const int j = u % nbH;
-    if (ch.x == a.E) {
-      const int ldk = a.S * a.I;
-      const ChunkRows cr{ch.z, ch.y, nullptr, a.K};
-      const uint8_t* wd = a.sdown + (size_t)j * kBlock * ldk;
-      const float* sd = a.sdown_scale + (size_t)j * (ldk / kBlock);
-      if (cr.n <= 16)
-        down_unit<1>(a, wd, sd, ldk, a.hq_s, a.hs_s, cr, j, a.d_s);
-      else if (cr.n <= 32)
-        down_unit<2>(a, wd, sd, ldk, a.hq_s, a.hs_s, cr, j, a.d_s);
-      else
-        down_unit<4>(a, wd, sd, ldk, a.hq_s, a.hs_s, cr, j, a.d_s);
-    } else {
-      const ChunkRows cr{ch.z, a.offsets[ch.x] + ch.y, a.perm, a.K};
-      const size_t rowblk = (size_t)ch.x * nbH + j;
-      const uint8_t* wd = a.down + rowblk * kBlock * a.I;
-      const float* sd = a.down_scale + rowblk * nbI;
-      if (cr.n <= 16)
-        down_unit<1>(a, wd, sd, a.I, a.hq_r, a.hs_r, cr, j, a.d_r);
-      else if (cr.n <= 32)
-        down_unit<2>(a, wd, sd, a.I, a.hq_r, a.hs_r, cr, j, a.d_r);
-      else
-        down_unit<4>(a, wd, sd, a.I, a.hq_r, a.hs_r, cr, j, a.d_r);
-    }
-    __syncthreads();
-    u = slot;
+  const int4 ch = a.chunks[v / nbH];
+  const int j = v % nbH;
+  if (ch.x == a.E) {
+    const int ldk = a.S * a.I;
+    const ChunkRows cr{ch.z, ch.y, nullptr, a.K};
+    const uint8_t* wd = a.sdown + (size_t)j * kBlock * ldk;
+    const float* sd = a.sdown_scale + (size_t)j * (ldk / kBlock);
+    if (cr.n <= 16)
+      down_unit<1>(a, wd, sd, ldk, a.hq_s, a.hs_s, cr, j, a.d_s);
+    else if (cr.n <= 32)
+      down_unit<2>(a, wd, sd, ldk, a.hq_s, a.hs_s, cr, j, a.d_s);
+    else
+      down_unit<4>(a, wd, sd, ldk, a.hq_s, a.hs_s, cr, j, a.d_s);
+  } else {
+    const ChunkRows cr{ch.z, a.offsets[ch.x] + ch.y, a.perm, a.K};
+    const size_t rowblk = (size_t)ch.x * nbH + j;
+    const uint8_t* wd = a.down + rowblk * kBlock * a.I;
+    const float* sd = a.down_scale + rowblk * nbI;
+    if (cr.n <= 16)
+      down_unit<1>(a, wd, sd, a.I, a.hq_r, a.hs_r, cr, j, a.d_r);
+    else if (cr.n <= 32)
+      down_unit<2>(a, wd, sd, a.I, a.hq_r, a.hs_r, cr, j, a.d_r);
+    else
+      down_unit<4>(a, wd, sd, a.I, a.hq_r, a.hs_r, cr, j, a.d_r);
   }
 }
 
-// y[t] = bf16( sum_slot fp32(d[t,slot]) * w[t,slot]  (slot order, each product rounded)
-//              + fp32(shared[t]) )                      frontier.py:349-354
-__global__ __launch_bounds__(256) void k_combine(const uint16_t* __restrict__ d_r, const uint16_t* __restrict__ d_s,
-                                                 const int* __restrict__ inv, const float* __restrict__ wts, int H,
-                                                 int K, int S, uint16_t* __restrict__ y) {
-  const int t = blockIdx.y;
-  const int h0 = (blockIdx.x * 256 + threadIdx.x) * 8;
-  if (h0 >= H) return;
+// y[t, h0 .. h0+7] = bf16( sum_slot fp32(d[t,slot]) * w[t,slot]  (slot order, each product
+//                          rounded) + fp32(shared[t]) )          frontier.py:349-354
+__device__ __forceinline__ void combine8(const uint16_t* __restrict__ d_r, const uint16_t* __restrict__ d_s,
+                                         const int* __restrict__ inv, const float* __restrict__ wts, int H, int K,
+                                         int S, int t, int h0, uint16_t* __restrict__ y) {
   float acc[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
@@ -1118,15 +1144,84 @@ __global__ __launch_bounds__(256) void k_combine(const uint16_t* __restrict__ d_
   *reinterpret_cast<uint4*>(y + (size_t)t * H + h0) = o;
 }
 
+__global__ __launch_bounds__(256) void k_combine(const uint16_t* __restrict__ d_r, const uint16_t* __restrict__ d_s,
+                                                 const int* __restrict__ inv, const float* __restrict__ wts, int T,
+                                                 int H, int K, int S, uint16_t* __restrict__ y) {
+  const int i = blockIdx.x * 256 + threadIdx.x, per_row = H / 8;
+  if (i < T * per_row) combine8(d_r, d_s, inv, wts, H, K, S, i / per_row, (i % per_row) * 8, y);
+}
+
+// ---------------------------------------------------------------------------------------
+// The expert stage as one persistent kernel. One work queue lists every gate/up unit,
+// then every down unit; each workgroup starts on unit blockIdx.x and takes further units
+// from the queue, so workgroups that run out of gate/up work go straight on to down
+// units instead of idling through the gate/up tail.
+//
+// A down unit of chunk c needs the h rows of chunk c, i.e. every gate/up unit of the
+// chunk: ready[c] counts them (nbI per routed chunk, S*nbI for the shared expert), and
+// the down unit's workgroup waits for the count. The wait is bounded and in practice
+// short: every gate/up unit precedes every down unit in the queue, so the units it waits
+// for are already running (all workgroups of the grid are resident at once). The
+// combine runs as its own small kernel after this one.
+// ---------------------------------------------------------------------------------------
+
+constexpr int kSpinLimit = 1 << 22;  // ~1 s of polling: past it the wait gives up and flags
+
+struct ExpertArgs {
+  GateUpArgs gu;
+  DownArgs dn;
+  const int* dn_of_gu;  // gate/up chunk -> down chunk
+  int* ready;           // [down chunks] finished gate/up units
+};
+
+__global__ __launch_bounds__(256, 2) void k_experts(ExpertArgs a) {
+  __shared__ float red[4][64];
+  __shared__ float hbuf[256 * 16];  // first-half h values of the 64-row gate/up path
+  __shared__ int slot;
+  int* meta = a.gu.meta;
+  const int nbI = a.gu.I / kBlock, nbH = a.dn.H / kBlock;
+  const int total_gu = meta[kMetaUnitsGU];
+  const int total = total_gu + meta[kMetaUnitsDN];
+  int u = blockIdx.x;
+  while (u < total) {
+    __syncthreads();
+    next_unit(&meta[kMetaQueueGU], &slot, gridDim.x);  // the next index arrives while this unit streams
+    if (u < total_gu) {
+      gateup_work(a.gu, u, red, hbuf);
+      publish_fence();
+      __syncthreads();
+      if (threadIdx.x == 0) atomicAdd(&a.ready[a.dn_of_gu[u / nbI]], 1);
+    } else {
+      const int v = u - total_gu, c = v / nbH;
+      if (threadIdx.x == 0) {
+        const int need = a.dn.chunks[c].x == a.dn.E ? a.dn.S * nbI : nbI;
+        int spins = 0;
+        while (__hip_atomic_load(&a.ready[c], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < need) {
+          if (++spins > kSpinLimit) {
+            atomicExch(&meta[kMetaError], 1);
+            break;
+          }
+          __builtin_amdgcn_s_sleep(2);
+        }
+      }
+      __syncthreads();
+      down_work(a.dn, v);
+    }
+    __syncthreads();
+    u = slot;
+  }
+}
+
 // ---------------------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------------------
 
+constexpr int kStages = 5;  // router+quantize, select, permute, experts, combine
 constexpr size_t kAlign = 256;
 inline size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
 struct Layout {
-  size_t partial, xq, xs, counts, offsets, meta, perm, inv, gu, dn, hq_r, hs_r, hq_s, hs_s, d_r, d_s, total;
+  size_t partial, xq, xs, counts, offsets, meta, perm, inv, gu, dn, dn_of_gu, ready, hq_r, hs_r, hq_s, hs_s, d_r, d_s, total;
   int nsplit;
 };
 
@@ -1158,10 +1253,12 @@ Layout make_layout(const megamoe_desc& d) {
   L.inv = take(T * K * sizeof(int));
   L.gu = take(max_chunks(d, (int)S) * sizeof(int4));
   L.dn = take(max_chunks(d, S > 0 ? 1 : 0) * sizeof(int4));
+  L.dn_of_gu = take(max_chunks(d, (int)S) * sizeof(int));
+  L.ready = take(max_chunks(d, S > 0 ? 1 : 0) * sizeof(int));
   L.hq_r = take(T * K * I);
-  L.hs_r = take(T * K * (I / kBlock) * sizeof(float));
+  L.hs_r = take(T * K * scale_ld((int)(I / kBlock)) * sizeof(float));
   L.hq_s = take(T * S * I);
-  L.hs_s = take(T * (S * I / kBlock) * sizeof(float));
+  L.hs_s = take(T * scale_ld((int)(S * I / kBlock)) * sizeof(float));
   L.d_r = take(T * K * H * 2);
   L.d_s = take(T * H * 2);
   L.total = at;
@@ -1188,8 +1285,7 @@ int validate(const megamoe_desc* d) {
 
 struct DeviceInfo {
   int cus = 0;
-  int gateup_per_cu = 0;
-  int down_per_cu = 0;
+  int experts_per_cu = 0;  // resident k_experts workgroups per CU
 };
 
 int device_info(DeviceInfo* out) {
@@ -1198,13 +1294,10 @@ int device_info(DeviceInfo* out) {
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return MEGAMOE_ERR_HIP;
   DeviceInfo& di = cache[dev];
   if (di.cus == 0) {
-    int cus = 0;
+    int cus = 0, per_cu = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return MEGAMOE_ERR_HIP;
-    int g = 0, dn = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&g, k_gateup, 256, 0) != hipSuccess) return MEGAMOE_ERR_HIP;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&dn, k_down, 256, 0) != hipSuccess) return MEGAMOE_ERR_HIP;
-    di.gateup_per_cu = g > 0 ? g : 1;
-    di.down_per_cu = dn > 0 ? dn : 1;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_experts, 256, 0) != hipSuccess) return MEGAMOE_ERR_HIP;
+    di.experts_per_cu = per_cu > 0 ? per_cu : 1;
     di.cus = cus > 0 ? cus : 1;
   }
   *out = di;
@@ -1276,7 +1369,7 @@ int forward_impl(const megamoe_desc* desc, const megamoe_tensors* t, hipStream_t
   const megamoe_desc& d = *desc;
   if (d.tokens == 0) {
     if (ev)
-      for (int i = 0; i < 7; ++i)
+      for (int i = 0; i < kStages + 1; ++i)
         if (hipEventRecord(ev[i], st) != hipSuccess) return MEGAMOE_ERR_HIP;
     return MEGAMOE_OK;
   }
@@ -1304,14 +1397,16 @@ int forward_impl(const megamoe_desc* desc, const megamoe_tensors* t, hipStream_t
   if (mark(2) != hipSuccess) return MEGAMOE_ERR_HIP;
 
   PermuteOut po{(int*)(ws + L.counts), (int*)(ws + L.offsets), (int*)(ws + L.meta), (int*)(ws + L.perm),
-                (int*)(ws + L.inv),    (int4*)(ws + L.gu),     (int4*)(ws + L.dn)};
+                (int*)(ws + L.inv),    (int4*)(ws + L.gu),     (int4*)(ws + L.dn),  (int*)(ws + L.dn_of_gu),
+                (int*)(ws + L.ready)};
   const int nbI = I / kBlock, nbH = H / kBlock;
   const size_t lds = ((size_t)E * (1 + (T + 31) / 32) + 32) * 4;
   hipLaunchKernelGGL(k_permute, dim3(1), dim3(1024), lds, st, t->expert_ids, T, K, E, S, nbI, nbH, po);
   MEGAMOE_LAUNCH_CHECK();
   if (mark(3) != hipSuccess) return MEGAMOE_ERR_HIP;
 
-  GateUpArgs ga;
+  ExpertArgs ea;
+  GateUpArgs& ga = ea.gu;
   ga.xq = (const uint8_t*)(ws + L.xq);
   ga.xs = (const float*)(ws + L.xs);
   ga.gate = t->gate; ga.gate_scale = t->gate_scale;
@@ -1322,30 +1417,30 @@ int forward_impl(const megamoe_desc* desc, const megamoe_tensors* t, hipStream_t
   ga.hq_r = (uint8_t*)(ws + L.hq_r); ga.hs_r = (float*)(ws + L.hs_r);
   ga.hq_s = (uint8_t*)(ws + L.hq_s); ga.hs_s = (float*)(ws + L.hs_s);
   ga.T = T; ga.H = H; ga.I = I; ga.K = K; ga.S = S; ga.E = E; ga.pow2 = d.pow2_scales;
-  // No more workgroups than the largest unit count the routing can produce.
-  const size_t gu_max = max_chunks(d, S) * (size_t)nbI, dn_max = max_chunks(d, S > 0 ? 1 : 0) * (size_t)nbH;
-  const unsigned gu_grid = (unsigned)(gu_max < (size_t)di.cus * di.gateup_per_cu ? gu_max : (size_t)di.cus * di.gateup_per_cu);
-  const unsigned dn_grid = (unsigned)(dn_max < (size_t)di.cus * di.down_per_cu ? dn_max : (size_t)di.cus * di.down_per_cu);
-  hipLaunchKernelGGL(k_gateup, dim3(gu_grid), dim3(256), 0, st, ga);
-  MEGAMOE_LAUNCH_CHECK();
-  if (mark(4) != hipSuccess) return MEGAMOE_ERR_HIP;
-
-  DownArgs da;
+  DownArgs& da = ea.dn;
   da.down = t->down; da.down_scale = t->down_scale;
   da.sdown = t->shared_down; da.sdown_scale = t->shared_down_scale;
   da.offsets = po.offsets; da.perm = po.perm; da.chunks = po.dn; da.meta = po.meta;
   da.hq_r = ga.hq_r; da.hs_r = ga.hs_r; da.hq_s = ga.hq_s; da.hs_s = ga.hs_s;
   da.d_r = (uint16_t*)(ws + L.d_r); da.d_s = (uint16_t*)(ws + L.d_s);
   da.T = T; da.H = H; da.I = I; da.K = K; da.S = S; da.E = E;
-  hipLaunchKernelGGL(k_down, dim3(dn_grid), dim3(256), 0, st, da);
+  ea.dn_of_gu = po.dn_of_gu;
+  ea.ready = po.ready;
+  // Every workgroup resident at once (a down unit may wait on gate/up units of lower
+  // queue positions), and no more of them than the most units the routing can produce.
+  const size_t units_max = max_chunks(d, S) * (size_t)nbI + max_chunks(d, S > 0 ? 1 : 0) * (size_t)nbH;
+  const size_t resident = (size_t)di.cus * di.experts_per_cu;
+  const unsigned grid = (unsigned)(units_max < resident ? units_max : resident);
+  hipLaunchKernelGGL(k_experts, dim3(grid), dim3(256), 0, st, ea);
   MEGAMOE_LAUNCH_CHECK();
-  if (mark(5) != hipSuccess) return MEGAMOE_ERR_HIP;
+  if (mark(4) != hipSuccess) return MEGAMOE_ERR_HIP;
 
-  hipLaunchKernelGGL(k_combine, dim3((H / 8 + 255) / 256, T), dim3(256), 0, st, (const uint16_t*)da.d_r,
-                     (const uint16_t*)da.d_s, (const int*)po.inv, (const float*)t->expert_weights, H, K, S,
+  const int rows8 = T * (H / 8);
+  hipLaunchKernelGGL(k_combine, dim3((rows8 + 255) / 256), dim3(256), 0, st, (const uint16_t*)da.d_r,
+                     (const uint16_t*)da.d_s, (const int*)po.inv, (const float*)t->expert_weights, T, H, K, S,
                      (uint16_t*)t->y);
   MEGAMOE_LAUNCH_CHECK();
-  if (mark(6) != hipSuccess) return MEGAMOE_ERR_HIP;
+  if (mark(5) != hipSuccess) return MEGAMOE_ERR_HIP;
   return MEGAMOE_OK;
 }
 
@@ -1381,16 +1476,16 @@ int megamoe_forward(const megamoe_desc* desc, const megamoe_tensors* t, void* st
 
 int megamoe_forward_timed(const megamoe_desc* desc, const megamoe_tensors* t, void* stream, float* stage_ms) {
   if (!stage_ms) return MEGAMOE_ERR_INVALID_ARGUMENT;
-  hipEvent_t ev[7];
+  hipEvent_t ev[kStages + 1];
   int made = 0, rc = MEGAMOE_OK;
-  for (; made < 7; ++made)
+  for (; made < kStages + 1; ++made)
     if (hipEventCreate(&ev[made]) != hipSuccess) {
       rc = MEGAMOE_ERR_HIP;
       break;
     }
   if (rc == MEGAMOE_OK) rc = forward_impl(desc, t, (hipStream_t)stream, ev);
-  if (rc == MEGAMOE_OK && hipEventSynchronize(ev[6]) != hipSuccess) rc = MEGAMOE_ERR_HIP;
-  for (int i = 0; rc == MEGAMOE_OK && i < 6; ++i)
+  if (rc == MEGAMOE_OK && hipEventSynchronize(ev[kStages]) != hipSuccess) rc = MEGAMOE_ERR_HIP;
+  for (int i = 0; rc == MEGAMOE_OK && i < kStages; ++i)
     if (hipEventElapsedTime(&stage_ms[i], ev[i], ev[i + 1]) != hipSuccess) rc = MEGAMOE_ERR_HIP;
   for (int i = 0; i < made; ++i) (void)hipEventDestroy(ev[i]);
   return rc;

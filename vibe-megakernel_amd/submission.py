@@ -114,7 +114,7 @@ class MoELayer:
         stream = ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
         with torch.cuda.device(device):
             if timed:
-                ms = (ctypes.c_float * 6)()
+                ms = (ctypes.c_float * len(_lib.STAGES))()
                 _lib.check(self.lib.megamoe_forward_timed(ctypes.byref(self.desc), ctypes.byref(tensors), stream,
                                                           ms), f"{c.id}: forward")
                 return {"y": y, "expert_ids": ids, "expert_weights": weights}, list(ms)
