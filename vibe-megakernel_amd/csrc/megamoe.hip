@@ -39,6 +39,8 @@ constexpr int kBlock = 128;  // quantization block edge (weights 128x128, activa
 // chunks never share a cache line (see the hand-over notes of the expert kernel).
 __host__ __device__ constexpr int scale_ld(int blocks) { return (blocks + 31) / 32 * 32; }
 
+constexpr int kSpinLimit = 1 << 22;  // ~1 s of polling: past it a wait gives up and flags an error
+
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -754,16 +756,49 @@ struct Operands {
 };
 
 template <int RT, int NCT, int SG>
-__device__ __forceinline__ void load_stage(Stage<RT, NCT, SG>& s, const Operands<RT, NCT, SG>& op, int kb) {
+__device__ __forceinline__ void load_stage_a(Stage<RT, NCT, SG>& s, const Operands<RT, NCT, SG>& op, int kb) {
   const size_t o = (size_t)kb * kBlock;
 #pragma unroll
   for (int r = 0; r < RT; ++r) s.a[r] = load_k32(op.a[r] + o);
 #pragma unroll
+  for (int g = 0; g < SG; ++g) s.sw[g] = op.sw[g][kb];
+}
+
+template <int RT, int NCT, int SG>
+__device__ __forceinline__ void load_stage_b(Stage<RT, NCT, SG>& s, const Operands<RT, NCT, SG>& op, int kb) {
+  const size_t o = (size_t)kb * kBlock;
+#pragma unroll
   for (int c = 0; c < NCT; ++c) s.b[c] = load_k32(op.b[c] + o);
 #pragma unroll
-  for (int g = 0; g < SG; ++g) s.sw[g] = op.sw[g][kb];
-#pragma unroll
   for (int c = 0; c < NCT; ++c) s.sx[c] = op.sx[c][kb];
+}
+
+template <int RT, int NCT, int SG>
+__device__ __forceinline__ void load_stage(Stage<RT, NCT, SG>& s, const Operands<RT, NCT, SG>& op, int kb) {
+  load_stage_a(s, op, kb);
+  load_stage_b(s, op, kb);
+}
+
+// A count another workgroup raises, and the value the work needs from it.
+struct ReadyWait {
+  const int* count;  // NULL: nothing to wait for
+  int need;
+  int* error;        // set to 1 if the bounded wait gives up
+};
+
+// Thread 0 polls the count (bounded), then the workgroup passes a barrier.
+__device__ __forceinline__ void wait_ready(const ReadyWait& w) {
+  if (w.count && threadIdx.x == 0) {
+    int spins = 0;
+    while (__hip_atomic_load(w.count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < w.need) {
+      if (++spins > kSpinLimit) {
+        atomicExch(w.error, 1);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(2);
+    }
+  }
+  __syncthreads();
 }
 
 template <int RT, int NCT, int SG>
@@ -782,15 +817,22 @@ __device__ __forceinline__ void compute_stage(const Stage<RT, NCT, SG>& s, f32x4
 }
 
 // Streams nkb K blocks with D stages of loads in flight per wavefront.
+// With a ReadyWait, the weight operands of the first stages are requested before the
+// wait and the activation operands (which another workgroup produces) after it, so the
+// wait's round trip overlaps the first weight loads.
 template <int RT, int NCT, int SG, int D>
-__device__ __forceinline__ void stream_gemm(const Operands<RT, NCT, SG>& op, int nkb, f32x4 (&acc)[RT][NCT]) {
+__device__ __forceinline__ void stream_gemm(const Operands<RT, NCT, SG>& op, int nkb, f32x4 (&acc)[RT][NCT],
+                                            const ReadyWait& ready = ReadyWait{nullptr, 0, nullptr}) {
 #pragma unroll
   for (int r = 0; r < RT; ++r)
 #pragma unroll
     for (int c = 0; c < NCT; ++c) acc[r][c] = f32x4{0.f, 0.f, 0.f, 0.f};
   Stage<RT, NCT, SG> st[D];
 #pragma unroll
-  for (int s = 0; s < D - 1; ++s) load_stage(st[s], op, min(s, nkb - 1));
+  for (int s = 0; s < D - 1; ++s) load_stage_a(st[s], op, min(s, nkb - 1));
+  wait_ready(ready);
+#pragma unroll
+  for (int s = 0; s < D - 1; ++s) load_stage_b(st[s], op, min(s, nkb - 1));
   for (int kb0 = 0; kb0 < nkb; kb0 += D) {
 #pragma unroll
     for (int s = 0; s < D; ++s) {
@@ -816,12 +858,6 @@ __device__ __forceinline__ int row_token(const ChunkRows& cr, int r) {
   return cr.perm ? cr.perm[cr.row0 + r] / cr.K : cr.row0 + r;
 }
 
-// Takes the next unit of a dynamic work queue for the whole workgroup. Each workgroup
-// starts on unit blockIdx.x without touching the queue, so the queue only sees one
-// atomic per unit beyond the first wave of units, spread over the kernel's run.
-__device__ __forceinline__ void next_unit(int* queue, int* slot, int first_dynamic) {
-  if (threadIdx.x == 0) *slot = first_dynamic + atomicAdd(queue, 1);
-}
 
 struct GateUpArgs {
   const uint8_t* xq;   // [T, H] e4m3
@@ -1037,7 +1073,7 @@ struct DownArgs {
 // requantized h rows. Wave w owns rows 32w .. 32w+31.
 template <int NCT>
 __device__ void down_unit(const DownArgs& a, const uint8_t* wd, const float* sd, int ldk, const uint8_t* hq,
-                          const float* hs, const ChunkRows& cr, int j, uint16_t* d) {
+                          const float* hs, const ChunkRows& cr, int j, uint16_t* d, const ReadyWait& ready) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int kofs = 16 * (lane >> 4);
   const int nkb = ldk / kBlock;
@@ -1052,7 +1088,7 @@ __device__ void down_unit(const DownArgs& a, const uint8_t* wd, const float* sd,
     op.sx[c] = hs + (size_t)(cr.row0 + r) * scale_ld(nkb);
   }
   f32x4 acc[2][NCT];
-  stream_gemm<2, NCT, 1, NCT == 1 ? 4 : (NCT == 2 ? 3 : 2)>(op, nkb, acc);
+  stream_gemm<2, NCT, 1, NCT == 1 ? 4 : (NCT == 2 ? 3 : 2)>(op, nkb, acc, ready);
 #pragma unroll
   for (int c = 0; c < NCT; ++c) {
     const int r = 16 * c + (lane & 15);
@@ -1069,7 +1105,7 @@ __device__ void down_unit(const DownArgs& a, const uint8_t* wd, const float* sd,
 }
 
 // Down unit v of the work list: chunk v / nbH, 128-row block v % nbH of the down matrix.
-__device__ void down_work(const DownArgs& a, int v) {
+__device__ void down_work(const DownArgs& a, int v, const ReadyWait& ready) {
   const int nbH = a.H / kBlock, nbI = a.I / kBlock;
   const int4 ch = a.chunks[v / nbH];
   const int j = v % nbH;
@@ -1079,22 +1115,22 @@ __device__ void down_work(const DownArgs& a, int v) {
     const uint8_t* wd = a.sdown + (size_t)j * kBlock * ldk;
     const float* sd = a.sdown_scale + (size_t)j * (ldk / kBlock);
     if (cr.n <= 16)
-      down_unit<1>(a, wd, sd, ldk, a.hq_s, a.hs_s, cr, j, a.d_s);
+      down_unit<1>(a, wd, sd, ldk, a.hq_s, a.hs_s, cr, j, a.d_s, ready);
     else if (cr.n <= 32)
-      down_unit<2>(a, wd, sd, ldk, a.hq_s, a.hs_s, cr, j, a.d_s);
+      down_unit<2>(a, wd, sd, ldk, a.hq_s, a.hs_s, cr, j, a.d_s, ready);
     else
-      down_unit<4>(a, wd, sd, ldk, a.hq_s, a.hs_s, cr, j, a.d_s);
+      down_unit<4>(a, wd, sd, ldk, a.hq_s, a.hs_s, cr, j, a.d_s, ready);
   } else {
     const ChunkRows cr{ch.z, a.offsets[ch.x] + ch.y, a.perm, a.K};
     const size_t rowblk = (size_t)ch.x * nbH + j;
     const uint8_t* wd = a.down + rowblk * kBlock * a.I;
     const float* sd = a.down_scale + rowblk * nbI;
     if (cr.n <= 16)
-      down_unit<1>(a, wd, sd, a.I, a.hq_r, a.hs_r, cr, j, a.d_r);
+      down_unit<1>(a, wd, sd, a.I, a.hq_r, a.hs_r, cr, j, a.d_r, ready);
     else if (cr.n <= 32)
-      down_unit<2>(a, wd, sd, a.I, a.hq_r, a.hs_r, cr, j, a.d_r);
+      down_unit<2>(a, wd, sd, a.I, a.hq_r, a.hs_r, cr, j, a.d_r, ready);
     else
-      down_unit<4>(a, wd, sd, a.I, a.hq_r, a.hs_r, cr, j, a.d_r);
+      down_unit<4>(a, wd, sd, a.I, a.hq_r, a.hs_r, cr, j, a.d_r, ready);
   }
 }
 
@@ -1159,13 +1195,13 @@ __global__ __launch_bounds__(256) void k_combine(const uint16_t* __restrict__ d_
 //
 // A down unit of chunk c needs the h rows of chunk c, i.e. every gate/up unit of the
 // chunk: ready[c] counts them (nbI per routed chunk, S*nbI for the shared expert), and
-// the down unit's workgroup waits for the count. The wait is bounded and in practice
+// the down unit's workgroup waits for the count after requesting its first weight
+// stages (the weights do not depend on it). The wait is bounded and in practice
 // short: every gate/up unit precedes every down unit in the queue, so the units it waits
 // for are already running (all workgroups of the grid are resident at once). The
 // combine runs as its own small kernel after this one.
 // ---------------------------------------------------------------------------------------
 
-constexpr int kSpinLimit = 1 << 22;  // ~1 s of polling: past it the wait gives up and flags
 
 struct ExpertArgs {
   GateUpArgs gu;
@@ -1182,10 +1218,12 @@ __global__ __launch_bounds__(256, 2) void k_experts(ExpertArgs a) {
   const int nbI = a.gu.I / kBlock, nbH = a.dn.H / kBlock;
   const int total_gu = meta[kMetaUnitsGU];
   const int total = total_gu + meta[kMetaUnitsDN];
-  int u = blockIdx.x;
+  int u = blockIdx.x, next = 0;
   while (u < total) {
     __syncthreads();
-    next_unit(&meta[kMetaQueueGU], &slot, gridDim.x);  // the next index arrives while this unit streams
+    // Thread 0 takes the next unit index now and hands it out after this unit: the
+    // atomic's round trip overlaps the unit instead of holding up wavefront 0.
+    if (threadIdx.x == 0) next = gridDim.x + atomicAdd(&meta[kMetaQueueGU], 1);
     if (u < total_gu) {
       gateup_work(a.gu, u, red, hbuf);
       publish_fence();
@@ -1193,20 +1231,10 @@ __global__ __launch_bounds__(256, 2) void k_experts(ExpertArgs a) {
       if (threadIdx.x == 0) atomicAdd(&a.ready[a.dn_of_gu[u / nbI]], 1);
     } else {
       const int v = u - total_gu, c = v / nbH;
-      if (threadIdx.x == 0) {
-        const int need = a.dn.chunks[c].x == a.dn.E ? a.dn.S * nbI : nbI;
-        int spins = 0;
-        while (__hip_atomic_load(&a.ready[c], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < need) {
-          if (++spins > kSpinLimit) {
-            atomicExch(&meta[kMetaError], 1);
-            break;
-          }
-          __builtin_amdgcn_s_sleep(2);
-        }
-      }
-      __syncthreads();
-      down_work(a.dn, v);
+      const ReadyWait ready{&a.ready[c], a.dn.chunks[c].x == a.dn.E ? a.dn.S * nbI : nbI, &meta[kMetaError]};
+      down_work(a.dn, v, ready);
     }
+    if (threadIdx.x == 0) slot = next;
     __syncthreads();
     u = slot;
   }
