@@ -722,12 +722,26 @@ __device__ __forceinline__ void publish_fence() { __builtin_amdgcn_s_waitcnt(0);
 // 1x128 activation scale block meets exactly one MFMA result, which is scaled in fp32
 // and added to the accumulator.
 //
-// Operand layout: lane l supplies row (l % 16) of its tile and the 32 K bytes
-// [16*(l/16), +16) and [64 + 16*(l/16), +16) of the block, the same byte positions for
-// the weight (A) and the activation (B) operand, so A and B agree on K. Each 16-byte
-// load instruction of a wavefront covers 64 contiguous bytes of 16 rows. Result layout:
-// lane l holds rows 4*(l/16) .. +3 of column (l % 16).
+// MFMA operand layout: lane l supplies row (l % 16) of its tile and the 32 K bytes
+// [16*(l/16), +16) and [64 + 16*(l/16), +16) of the block (16-byte chunks g and g + 4,
+// g = l/16), the same byte positions for the weight (A) and the activation (B) operand.
+// Result layout: lane l holds rows 4*(l/16) .. +3 of column (l % 16).
+//
+// Weights stream HBM -> LDS with non-temporal global_load_lds_dwordx4: one instruction
+// moves 8 whole 128-byte K-block rows of a tile, lane l fetching chunk (l%8) ^ (l/8) of
+// row l/8 into the instruction's LDS slot l, so the chunks of each row sit XOR-swizzled by
+// the row index. Two ds_read_b128 per tile give the MFMA layout back (chunk c of row r is
+// at slot position c ^ (r % 8)). Full-line requests stream close to the HBM peak where
+// 64-byte half lines loaded straight into the MFMA layout do not, and the stages in
+// flight take no registers. Each wavefront owns a private ring of D stages in LDS, so no
+// barrier is involved: the wait for a stage is an explicit vmcnt (below).
+//
+// Activations and scales are loaded into registers D-1 stages ahead.
 // ---------------------------------------------------------------------------------------
+
+constexpr int kTileBytes = 16 * kBlock;  // one 16-row tile of one K block
+constexpr int kRingWave = 16384;         // LDS ring bytes per wavefront
+constexpr int kNonTemporal = 2;          // cache policy of the weight loads
 
 __device__ __forceinline__ f32x4 mfma_e4m3(const i32x8& a, const i32x8& b, f32x4 c) {
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 127, 0, 127);
@@ -739,9 +753,39 @@ __device__ __forceinline__ i32x8 load_k32(const uint8_t* p) {
   return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
-template <int RT, int NCT, int SG>
+// Waits until at most N vector memory operations of this wavefront are outstanding.
+// The memory clobber keeps the compiler from moving loads across the wait.
+template <int N>
+__device__ __forceinline__ void wait_vmem() {
+  static_assert(N >= 0 && N <= 63, "vmcnt holds 6 bits");
+  // gfx9 s_waitcnt immediate: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] << 14
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | (((N >> 4) & 3) << 14));
+  asm volatile("" ::: "memory");
+}
+
+// This lane's byte offsets for one tile: `dma` in global memory relative to the tile's
+// row 0 (row l/8, swizzled chunk), rd0/rd1 of its two MFMA chunks in the LDS tile.
+struct LaneTile {
+  int dma, rd0, rd1;
+};
+
+// threadIdx.x % 64 behind an empty asm: what the expert units derive from it is computed
+// where it is used, not hoisted out of the persistent loop and held (or spilled) across it.
+__device__ __forceinline__ int opaque_lane() {
+  int l = threadIdx.x & 63;
+  asm volatile("" : "+v"(l));
+  return l;
+}
+
+__device__ __forceinline__ LaneTile lane_tile(int lda) {
+  const int lane = opaque_lane();
+  const int lr = lane >> 3, row = lane & 15, rr = row & 7, g = lane >> 4;
+  const int base = (row >> 3) * 1024 + rr * kBlock;
+  return LaneTile{lr * lda + (((lane & 7) ^ lr) << 4), base + ((g ^ rr) << 4), base + (((g + 4) ^ rr) << 4)};
+}
+
+template <int NCT, int SG>
 struct Stage {
-  i32x8 a[RT];
   i32x8 b[NCT];
   float sw[SG];
   float sx[NCT];
@@ -749,34 +793,36 @@ struct Stage {
 
 template <int RT, int NCT, int SG>
 struct Operands {
-  const uint8_t* a[RT];    // lane's weight row at its K byte offset
+  const uint8_t* a[RT];    // row 0 of each 16-row weight tile (wave-uniform)
+  int lda;                 // weight row length in bytes
   const float* sw[SG];     // per-K-block weight scales of scale group g (wave-uniform)
   const uint8_t* b[NCT];   // lane's activation row at its K byte offset
   const float* sx[NCT];    // lane's activation scale row
 };
 
+// 2*RT weight loads of K block kb into one ring slot.
 template <int RT, int NCT, int SG>
-__device__ __forceinline__ void load_stage_a(Stage<RT, NCT, SG>& s, const Operands<RT, NCT, SG>& op, int kb) {
-  const size_t o = (size_t)kb * kBlock;
+__device__ __forceinline__ void issue_a(uint8_t* slot, const Operands<RT, NCT, SG>& op, int dma, int kb) {
 #pragma unroll
-  for (int r = 0; r < RT; ++r) s.a[r] = load_k32(op.a[r] + o);
+  for (int t = 0; t < RT; ++t)
 #pragma unroll
-  for (int g = 0; g < SG; ++g) s.sw[g] = op.sw[g][kb];
+    for (int i = 0; i < 2; ++i)
+      __builtin_amdgcn_global_load_lds(
+          (const __attribute__((address_space(1))) void*)(op.a[t] + (size_t)kb * kBlock +
+                                                          (uint32_t)(dma + 8 * i * op.lda)),
+          (__attribute__((address_space(3))) void*)(slot + t * kTileBytes + i * 1024), 16, 0, kNonTemporal);
 }
 
+// At least 3*NCT vector loads: two 16-byte loads and one scale per column tile.
 template <int RT, int NCT, int SG>
-__device__ __forceinline__ void load_stage_b(Stage<RT, NCT, SG>& s, const Operands<RT, NCT, SG>& op, int kb) {
+__device__ __forceinline__ void load_stage_b(Stage<NCT, SG>& s, const Operands<RT, NCT, SG>& op, int kb) {
   const size_t o = (size_t)kb * kBlock;
 #pragma unroll
   for (int c = 0; c < NCT; ++c) s.b[c] = load_k32(op.b[c] + o);
 #pragma unroll
   for (int c = 0; c < NCT; ++c) s.sx[c] = op.sx[c][kb];
-}
-
-template <int RT, int NCT, int SG>
-__device__ __forceinline__ void load_stage(Stage<RT, NCT, SG>& s, const Operands<RT, NCT, SG>& op, int kb) {
-  load_stage_a(s, op, kb);
-  load_stage_b(s, op, kb);
+#pragma unroll
+  for (int g = 0; g < SG; ++g) s.sw[g] = op.sw[g][kb];
 }
 
 // A count another workgroup raises, and the value the work needs from it.
@@ -786,9 +832,13 @@ struct ReadyWait {
   int* error;        // set to 1 if the bounded wait gives up
 };
 
-// Thread 0 polls the count (bounded), then the workgroup passes a barrier.
+// Thread 0 polls the count (bounded), then the workgroup passes a barrier. The barrier
+// carries no release fence (this workgroup publishes nothing here, and a release would
+// wait for the weight loads in flight); the acquire fence after it keeps the loads that
+// follow from moving above it.
 __device__ __forceinline__ void wait_ready(const ReadyWait& w) {
-  if (w.count && threadIdx.x == 0) {
+  if (!w.count) return;
+  if (threadIdx.x == 0) {
     int spins = 0;
     while (__hip_atomic_load(w.count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < w.need) {
       if (++spins > kSpinLimit) {
@@ -798,17 +848,49 @@ __device__ __forceinline__ void wait_ready(const ReadyWait& w) {
       __builtin_amdgcn_s_sleep(2);
     }
   }
-  __syncthreads();
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 }
 
+// The RT tiles of one ring slot in MFMA layout. The reads are inline asm: the compiler
+// takes any LDS read that follows a global_load_lds as depending on the most recent one
+// and would wait for every load in flight (vmcnt 0) before it, while the ring's own vmcnt
+// wait already covers the slot read here. The lgkmcnt wait names the results as operands,
+// so no use of them can be scheduled before it.
+template <int RT>
+__device__ __forceinline__ void read_slot(i32x8 (&a)[RT], uint32_t p0, uint32_t p1) {
+  i32x4 lo[RT], hi[RT];
+#pragma unroll
+  for (int r = 0; r < RT; ++r)
+    asm volatile("ds_read_b128 %0, %2\n\tds_read_b128 %1, %3"
+                 : "=&v"(lo[r]), "=&v"(hi[r])
+                 : "v"(p0 + r * kTileBytes), "v"(p1 + r * kTileBytes)
+                 : "memory");
+  if constexpr (RT == 2) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(lo[0]), "+v"(hi[0]), "+v"(lo[1]), "+v"(hi[1]));
+  } else {
+    static_assert(RT == 4, "two or four row tiles");
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(lo[0]), "+v"(hi[0]), "+v"(lo[1]), "+v"(hi[1]), "+v"(lo[2]), "+v"(hi[2]), "+v"(lo[3]),
+                   "+v"(hi[3]));
+  }
+#pragma unroll
+  for (int r = 0; r < RT; ++r) a[r] = __builtin_shufflevector(lo[r], hi[r], 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+// `slot` is the LDS byte address of the ring slot.
 template <int RT, int NCT, int SG>
-__device__ __forceinline__ void compute_stage(const Stage<RT, NCT, SG>& s, f32x4 (&acc)[RT][NCT]) {
+__device__ __forceinline__ void compute_stage(uint32_t slot, const LaneTile& lt, const Stage<NCT, SG>& s,
+                                              f32x4 (&acc)[RT][NCT]) {
   const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+  i32x8 at[RT];
+  read_slot<RT>(at, slot + lt.rd0, slot + lt.rd1);
 #pragma unroll
   for (int r = 0; r < RT; ++r) {
+    const i32x8& a = at[r];
 #pragma unroll
     for (int c = 0; c < NCT; ++c) {
-      const f32x4 p = mfma_e4m3(s.a[r], s.b[c], zero);
+      const f32x4 p = mfma_e4m3(a, s.b[c], zero);
       const float k = s.sw[r * SG / RT] * s.sx[c];
 #pragma unroll
       for (int v = 0; v < 4; ++v) acc[r][c][v] = __builtin_fmaf(p[v], k, acc[r][c][v]);
@@ -816,31 +898,50 @@ __device__ __forceinline__ void compute_stage(const Stage<RT, NCT, SG>& s, f32x4
   }
 }
 
-// Streams nkb K blocks with D stages of loads in flight per wavefront.
-// With a ReadyWait, the weight operands of the first stages are requested before the
-// wait and the activation operands (which another workgroup produces) after it, so the
-// wait's round trip overlaps the first weight loads.
+// Streams nkb K blocks through the wavefront's LDS ring (D slots) with D-1 stages of loads
+// in flight. With a ReadyWait, the weights of the first stages are requested before the
+// wait and the activations (which another workgroup produces) after it, so the wait's
+// round trip overlaps the first weight loads.
+//
+// The wait for stage s: a wavefront's vector memory loads (to LDS or to registers)
+// complete in issue order, and the compiler's own counters do not cover the LDS that
+// global_load_lds writes. When stage s is consumed, each of stages s+1 .. s+D-1 has been
+// issued after stage s's weights, as a group of 2*RT weight loads and at least 3*NCT
+// activation loads, so vmcnt <= (D-1)*(2*RT + 3*NCT) implies stage s has landed.
+// Loads past the last K block are clamped to it, not skipped: a branch around them would
+// merge paths with different load counts, and the compiler then waits for vmcnt 0 before
+// the next MFMA, which drains the pipeline at every stage. The clamped loads re-read the
+// block just fetched (an L2 hit) into slots nothing reads any more; they land before any
+// later load into the ring (issue order), and no other LDS data shares those slots. The
+// slot a stage overwrites was read (ds_read, issued in program order before the
+// overwriting load) one stage earlier.
 template <int RT, int NCT, int SG, int D>
-__device__ __forceinline__ void stream_gemm(const Operands<RT, NCT, SG>& op, int nkb, f32x4 (&acc)[RT][NCT],
+__device__ __forceinline__ void stream_gemm(const Operands<RT, NCT, SG>& op, int nkb, uint8_t* ring,
+                                            f32x4 (&acc)[RT][NCT],
                                             const ReadyWait& ready = ReadyWait{nullptr, 0, nullptr}) {
+  constexpr int kSlot = RT * kTileBytes;
+  constexpr int kAfter = (D - 1) * (2 * RT + 3 * NCT);
+  static_assert(D >= 2 && D * kSlot <= kRingWave, "LDS ring");
+  const LaneTile lt = lane_tile(op.lda);
+  const uint32_t ring_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)ring;
 #pragma unroll
   for (int r = 0; r < RT; ++r)
 #pragma unroll
     for (int c = 0; c < NCT; ++c) acc[r][c] = f32x4{0.f, 0.f, 0.f, 0.f};
-  Stage<RT, NCT, SG> st[D];
+  Stage<NCT, SG> st[D];
 #pragma unroll
-  for (int s = 0; s < D - 1; ++s) load_stage_a(st[s], op, min(s, nkb - 1));
+  for (int s = 0; s < D - 1; ++s) issue_a(ring + s * kSlot, op, lt.dma, min(s, nkb - 1));
   wait_ready(ready);
 #pragma unroll
   for (int s = 0; s < D - 1; ++s) load_stage_b(st[s], op, min(s, nkb - 1));
   for (int kb0 = 0; kb0 < nkb; kb0 += D) {
 #pragma unroll
     for (int s = 0; s < D; ++s) {
-      const int kb = kb0 + s;
-      // The load index is clamped rather than skipped so the loop body stays
-      // branch-free; the clamped tail re-reads the last block, which is in cache.
-      load_stage(st[(s + D - 1) % D], op, min(kb + D - 1, nkb - 1));
-      if (kb < nkb) compute_stage(st[s], acc);
+      const int kb = kb0 + s, kn = min(kb + D - 1, nkb - 1);
+      load_stage_b(st[(s + D - 1) % D], op, kn);
+      issue_a(ring + ((s + D - 1) % D) * kSlot, op, lt.dma, kn);
+      wait_vmem<kAfter>();
+      if (kb < nkb) compute_stage(ring_lds + s * kSlot, lt, st[s], acc);
     }
   }
 }
@@ -880,16 +981,17 @@ struct GateUpArgs {
 template <int NCT>
 __device__ void gateup_unit(const GateUpArgs& a, const uint8_t* wg, const uint8_t* wu, const float* sg,
                             const float* su, const ChunkRows& cr, int jb, uint8_t* hq, float* hs, int ldh,
-                            float (*red)[64]) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+                            float (*red)[64], uint8_t* ring) {
+  const int lane = opaque_lane(), w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int kofs = 16 * (lane >> 4);
   const int H = a.H, nkb = H / kBlock, nbh = scale_ld(ldh / kBlock);
   Operands<4, NCT, 2> op;
+  op.lda = H;
 #pragma unroll
   for (int r = 0; r < 2; ++r) {
-    const size_t row = (size_t)(32 * w + 16 * r + (lane & 15));
-    op.a[r] = wg + row * H + kofs;
-    op.a[r + 2] = wu + row * H + kofs;
+    const size_t row = (size_t)(32 * w + 16 * r);
+    op.a[r] = wg + row * H;
+    op.a[r + 2] = wu + row * H;
   }
   op.sw[0] = sg;
   op.sw[1] = su;
@@ -901,7 +1003,7 @@ __device__ void gateup_unit(const GateUpArgs& a, const uint8_t* wg, const uint8_
     op.sx[c] = a.xs + (size_t)tok * nkb;
   }
   f32x4 acc[4][NCT];
-  stream_gemm<4, NCT, 2, NCT == 1 ? 3 : 2>(op, nkb, acc);
+  stream_gemm<4, NCT, 2, 2>(op, nkb, ring, acc);
 
   // h = bf16(silu(fp32 bf16(g)) * fp32 bf16(u)) (frontier.py:184-186,337)
   float hv[NCT][2][4];
@@ -945,15 +1047,18 @@ __device__ void gateup_unit(const GateUpArgs& a, const uint8_t* wg, const uint8_
 // Gate/up unit for 33..64 activation rows (four column tiles). To keep the accumulators
 // of four column tiles within the register budget, the 128-row block is done in two
 // 64-row halves: in half hf, wave w owns gate and up rows 64*hf + 16w .. +15. The h
-// values of the first half wait in LDS (hbuf) while the second half streams.
+// values of the first half wait in LDS (past the three ring slots this path streams
+// through) while the second half streams.
 __device__ void gateup_unit_wide(const GateUpArgs& a, const uint8_t* wg, const uint8_t* wu, const float* sg,
                                  const float* su, const ChunkRows& cr, int jb, uint8_t* hq, float* hs, int ldh,
-                                 float (*red)[64], float* hbuf) {
+                                 float (*red)[64], uint8_t* ring) {
   constexpr int NCT = 4;
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int lane = opaque_lane(), w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int kofs = 16 * (lane >> 4);
   const int H = a.H, nkb = H / kBlock, nbh = scale_ld(ldh / kBlock);
+  constexpr int D = 3;
   Operands<2, NCT, 2> op;
+  op.lda = H;
   op.sw[0] = sg;
   op.sw[1] = su;
 #pragma unroll
@@ -963,17 +1068,18 @@ __device__ void gateup_unit_wide(const GateUpArgs& a, const uint8_t* wg, const u
     op.b[c] = a.xq + (size_t)tok * H + kofs;
     op.sx[c] = a.xs + (size_t)tok * nkb;
   }
-  float* mine = hbuf + (size_t)threadIdx.x * (NCT * 4);  // this lane's first-half h values
+  static_assert(D * 2 * kTileBytes + 64 * NCT * 4 * sizeof(float) <= kRingWave, "ring + h values");
+  float* mine = reinterpret_cast<float*>(ring + D * 2 * kTileBytes) + lane * (NCT * 4);  // first-half h values
   float amax[NCT];
 #pragma unroll
   for (int c = 0; c < NCT; ++c) amax[c] = 0.0f;
 #pragma unroll 1
   for (int hf = 0; hf < 2; ++hf) {
-    const size_t row = (size_t)(64 * hf + 16 * w + (lane & 15));
-    op.a[0] = wg + row * H + kofs;
-    op.a[1] = wu + row * H + kofs;
+    const size_t row = (size_t)(64 * hf + 16 * w);
+    op.a[0] = wg + row * H;
+    op.a[1] = wu + row * H;
     f32x4 acc[2][NCT];
-    stream_gemm<2, NCT, 2, 2>(op, nkb, acc);
+    stream_gemm<2, NCT, 2, D>(op, nkb, ring, acc);
 #pragma unroll
     for (int c = 0; c < NCT; ++c)
 #pragma unroll
@@ -1019,7 +1125,7 @@ __device__ void gateup_unit_wide(const GateUpArgs& a, const uint8_t* wg, const u
 
 // Gate/up unit u of the work list: chunk u / nbI, 128-row block u % nbI of the chunk's
 // expert (plus the slice offset of a shared-expert copy).
-__device__ void gateup_work(const GateUpArgs& a, int u, float (*red)[64], float* hbuf) {
+__device__ void gateup_work(const GateUpArgs& a, int u, float (*red)[64], uint8_t* ring) {
   const int nbI = a.I / kBlock, nkb = a.H / kBlock;
   const int4 ch = a.chunks[u / nbI];
   const int j = u % nbI, jb = ch.w + j;
@@ -1050,11 +1156,11 @@ __device__ void gateup_work(const GateUpArgs& a, int u, float (*red)[64], float*
     ldh = a.I;
   }
   if (cr.n <= 16)
-    gateup_unit<1>(a, wg, wu, sg, su, cr, jb, hq, hs, ldh, red);
+    gateup_unit<1>(a, wg, wu, sg, su, cr, jb, hq, hs, ldh, red, ring);
   else if (cr.n <= 32)
-    gateup_unit<2>(a, wg, wu, sg, su, cr, jb, hq, hs, ldh, red);
+    gateup_unit<2>(a, wg, wu, sg, su, cr, jb, hq, hs, ldh, red, ring);
   else
-    gateup_unit_wide(a, wg, wu, sg, su, cr, jb, hq, hs, ldh, red, hbuf);
+    gateup_unit_wide(a, wg, wu, sg, su, cr, jb, hq, hs, ldh, red, ring);
 }
 
 struct DownArgs {
@@ -1073,13 +1179,14 @@ struct DownArgs {
 // requantized h rows. Wave w owns rows 32w .. 32w+31.
 template <int NCT>
 __device__ void down_unit(const DownArgs& a, const uint8_t* wd, const float* sd, int ldk, const uint8_t* hq,
-                          const float* hs, const ChunkRows& cr, int j, uint16_t* d, const ReadyWait& ready) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+                          const float* hs, const ChunkRows& cr, int j, uint16_t* d, const ReadyWait& ready, uint8_t* ring) {
+  const int lane = opaque_lane(), w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int kofs = 16 * (lane >> 4);
   const int nkb = ldk / kBlock;
   Operands<2, NCT, 1> op;
 #pragma unroll
-  for (int r = 0; r < 2; ++r) op.a[r] = wd + (size_t)(32 * w + 16 * r + (lane & 15)) * ldk + kofs;
+  for (int r = 0; r < 2; ++r) op.a[r] = wd + (size_t)(32 * w + 16 * r) * ldk;
+  op.lda = ldk;
   op.sw[0] = sd;
 #pragma unroll
   for (int c = 0; c < NCT; ++c) {
@@ -1088,7 +1195,7 @@ __device__ void down_unit(const DownArgs& a, const uint8_t* wd, const float* sd,
     op.sx[c] = hs + (size_t)(cr.row0 + r) * scale_ld(nkb);
   }
   f32x4 acc[2][NCT];
-  stream_gemm<2, NCT, 1, NCT == 1 ? 4 : (NCT == 2 ? 3 : 2)>(op, nkb, acc, ready);
+  stream_gemm<2, NCT, 1, NCT == 4 ? 2 : 4>(op, nkb, ring, acc, ready);
 #pragma unroll
   for (int c = 0; c < NCT; ++c) {
     const int r = 16 * c + (lane & 15);
@@ -1105,7 +1212,7 @@ __device__ void down_unit(const DownArgs& a, const uint8_t* wd, const float* sd,
 }
 
 // Down unit v of the work list: chunk v / nbH, 128-row block v % nbH of the down matrix.
-__device__ void down_work(const DownArgs& a, int v, const ReadyWait& ready) {
+__device__ void down_work(const DownArgs& a, int v, const ReadyWait& ready, uint8_t* ring) {
   const int nbH = a.H / kBlock, nbI = a.I / kBlock;
   const int4 ch = a.chunks[v / nbH];
   const int j = v % nbH;
@@ -1115,22 +1222,22 @@ __device__ void down_work(const DownArgs& a, int v, const ReadyWait& ready) {
     const uint8_t* wd = a.sdown + (size_t)j * kBlock * ldk;
     const float* sd = a.sdown_scale + (size_t)j * (ldk / kBlock);
     if (cr.n <= 16)
-      down_unit<1>(a, wd, sd, ldk, a.hq_s, a.hs_s, cr, j, a.d_s, ready);
+      down_unit<1>(a, wd, sd, ldk, a.hq_s, a.hs_s, cr, j, a.d_s, ready, ring);
     else if (cr.n <= 32)
-      down_unit<2>(a, wd, sd, ldk, a.hq_s, a.hs_s, cr, j, a.d_s, ready);
+      down_unit<2>(a, wd, sd, ldk, a.hq_s, a.hs_s, cr, j, a.d_s, ready, ring);
     else
-      down_unit<4>(a, wd, sd, ldk, a.hq_s, a.hs_s, cr, j, a.d_s, ready);
+      down_unit<4>(a, wd, sd, ldk, a.hq_s, a.hs_s, cr, j, a.d_s, ready, ring);
   } else {
     const ChunkRows cr{ch.z, a.offsets[ch.x] + ch.y, a.perm, a.K};
     const size_t rowblk = (size_t)ch.x * nbH + j;
     const uint8_t* wd = a.down + rowblk * kBlock * a.I;
     const float* sd = a.down_scale + rowblk * nbI;
     if (cr.n <= 16)
-      down_unit<1>(a, wd, sd, a.I, a.hq_r, a.hs_r, cr, j, a.d_r, ready);
+      down_unit<1>(a, wd, sd, a.I, a.hq_r, a.hs_r, cr, j, a.d_r, ready, ring);
     else if (cr.n <= 32)
-      down_unit<2>(a, wd, sd, a.I, a.hq_r, a.hs_r, cr, j, a.d_r, ready);
+      down_unit<2>(a, wd, sd, a.I, a.hq_r, a.hs_r, cr, j, a.d_r, ready, ring);
     else
-      down_unit<4>(a, wd, sd, a.I, a.hq_r, a.hs_r, cr, j, a.d_r, ready);
+      down_unit<4>(a, wd, sd, a.I, a.hq_r, a.hs_r, cr, j, a.d_r, ready, ring);
   }
 }
 
@@ -1210,29 +1317,40 @@ struct ExpertArgs {
   int* ready;           // [down chunks] finished gate/up units
 };
 
-__global__ __launch_bounds__(256, 2) void k_experts(ExpertArgs a) {
+__global__ __launch_bounds__(256, 2) void k_experts(ExpertArgs args) {
+  typedef const __attribute__((address_space(4))) ExpertArgs* ArgsPtr;
   __shared__ float red[4][64];
-  __shared__ float hbuf[256 * 16];  // first-half h values of the 64-row gate/up path
+  __shared__ __attribute__((aligned(16))) uint8_t rings[4 * kRingWave];  // one weight ring per wavefront
   __shared__ int slot;
-  int* meta = a.gu.meta;
-  const int nbI = a.gu.I / kBlock, nbH = a.dn.H / kBlock;
+  static_assert(sizeof(ExpertArgs) % 8 == 0, "argument segment layout");
+  int* meta = args.gu.meta;
   const int total_gu = meta[kMetaUnitsGU];
   const int total = total_gu + meta[kMetaUnitsDN];
   int u = blockIdx.x, next = 0;
   while (u < total) {
+    // The arguments are re-read from the kernel argument segment (where `args`, the only
+    // argument, sits at offset 0) through a pointer behind an empty asm, so each unit
+    // derives its addresses afresh instead of every path's values being hoisted out of
+    // this loop and held (or spilled) across it.
+    ArgsPtr ap = (ArgsPtr)__builtin_amdgcn_kernarg_segment_ptr();
+    asm volatile("" : "+s"(ap));
+    ExpertArgs a;
+    __builtin_memcpy(&a, (const ExpertArgs*)ap, sizeof(a));
+    const int nbI = a.gu.I / kBlock, nbH = a.dn.H / kBlock;
+    uint8_t* ring = rings + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) * kRingWave;
     __syncthreads();
     // Thread 0 takes the next unit index now and hands it out after this unit: the
     // atomic's round trip overlaps the unit instead of holding up wavefront 0.
     if (threadIdx.x == 0) next = gridDim.x + atomicAdd(&meta[kMetaQueueGU], 1);
     if (u < total_gu) {
-      gateup_work(a.gu, u, red, hbuf);
+      gateup_work(a.gu, u, red, ring);
       publish_fence();
       __syncthreads();
       if (threadIdx.x == 0) atomicAdd(&a.ready[a.dn_of_gu[u / nbI]], 1);
     } else {
       const int v = u - total_gu, c = v / nbH;
       const ReadyWait ready{&a.ready[c], a.dn.chunks[c].x == a.dn.E ? a.dn.S * nbI : nbI, &meta[kMetaError]};
-      down_work(a.dn, v, ready);
+      down_work(a.dn, v, ready, ring);
     }
     if (threadIdx.x == 0) slot = next;
     __syncthreads();
