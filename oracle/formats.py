@@ -7,10 +7,11 @@ in the amax only. Activations: the same rule per row and 128-column block.
 Dequantization multiplies the payload by the broadcast scale in fp32.
 
 Pinned by tests/test_oracle_formats.py: explicit per-block loops (the
-re-derivation of megabench/tests/test_frontier.py:224-248), the reference's
-edge vectors (megabench/tests/test_megamoe.py:59-81), an exhaustive E4M3 code
-table and round-to-nearest-even midpoints against the plain-C codec in
-oracle/codec.c, and the reference's own functions through the golden fixtures.
+re-derivation of megabench/tests/test_frontier.py:224-248), the padded
+restatement and edge vectors of megabench/tests/test_megamoe.py:56-81, the
+E4M3 format decoded field by field for all 256 codes, and round-to-nearest-even
+at every midpoint between adjacent codes, each against both torch's cast and
+the plain-C codec in oracle/codec.c.
 """
 
 from __future__ import annotations

@@ -11,6 +11,12 @@ import __graft_entry__  # noqa: E402
 
 __graft_entry__.load_package()
 
+# The library is built by __graft_entry__.build(); build it here only if it is missing.
+from vibe_megakernel_amd import _lib, build as _build  # noqa: E402
+
+if not _lib.LIBRARY.exists():
+    _build.build_library()
+
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (runs the HIP kernels)")

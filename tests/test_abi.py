@@ -1,0 +1,127 @@
+"""The C ABI of libmegamoe.so on the CPU: the library loads, exports every function the
+header declares, and its host-side checks (geometry, pointers, workspace size) answer
+without touching a GPU. No compute entry point runs here."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+from vibe_megakernel_amd import _lib
+from vibe_megakernel_amd import cases as C
+from vibe_megakernel_amd import submission
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "megamoe.h"
+
+
+def _declared() -> set[str]:
+    text = HEADER.read_text()
+    return set(re.findall(r"^\s*(?:const\s+)?[a-z_0-9]+\s*\*?\s*(megamoe_[a-z_]+)\s*\(", text, flags=re.M))
+
+
+def test_library_exports_every_declared_function():
+    declared = _declared()
+    assert declared == set(_lib.SYMBOLS)
+    lib = _lib.load()
+    for name in declared:
+        assert getattr(lib, name) is not None
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIBRARY)], capture_output=True, text=True,
+                         check=True).stdout
+    exported = set(re.findall(r"\bT (megamoe_[a-z_]+)$", out, flags=re.M))
+    assert declared <= exported
+
+
+def test_version_and_status_strings():
+    lib = _lib.load()
+    assert lib.megamoe_abi_version() == 1
+    texts = {code: _lib.status_string(code) for code in range(6)}
+    assert texts[_lib.OK] == "ok" and len(set(texts.values())) == 6
+    assert _lib.status_string(99) == "unknown status"
+
+
+@pytest.mark.parametrize("case", C.CASES, ids=lambda c: c.id)
+def test_workspace_bytes_for_every_config(case):
+    layer = submission.MoELayer(case)
+    T, H, K, I, S = case.tokens, case.hidden, case.topk, case.intermediate, case.shared_experts
+    # At least the grouped intermediates: quantized x, h rows, bf16 down rows.
+    assert layer.workspace_bytes >= T * H + T * K * (I + 2 * H) + T * S * I
+    assert layer.workspace_bytes % 256 == 0
+    assert layer.workspace_bytes < 64 << 20
+
+
+def _status(desc, **tensors):
+    lib = _lib.load()
+    size = ctypes.c_size_t(0)
+    return lib.megamoe_workspace_bytes(ctypes.byref(desc), ctypes.byref(size))
+
+
+@pytest.mark.parametrize("change,status", [
+    (dict(hidden=1000), _lib.ERR_SHAPE),                      # H not a multiple of 128
+    (dict(intermediate=200), _lib.ERR_SHAPE),
+    (dict(topk=300), _lib.ERR_SHAPE),                         # K > E
+    (dict(groups=3), _lib.ERR_SHAPE),                         # G does not divide E
+    (dict(top_groups=9), _lib.ERR_SHAPE),                     # TG > G
+    (dict(groups=64, top_groups=1), _lib.ERR_SHAPE),          # kept groups hold fewer than K experts
+    (dict(gate=7), _lib.ERR_SHAPE),
+    (dict(tokens=-1), _lib.ERR_SHAPE),
+    (dict(experts=2048, groups=1, top_groups=1), _lib.ERR_UNSUPPORTED),
+    (dict(topk=40, groups=1, top_groups=1), _lib.ERR_UNSUPPORTED),
+    (dict(), _lib.OK),
+])
+def test_geometry_checks(change, status):
+    desc = submission.make_desc(C.case(C.HEADLINE))
+    for k, v in change.items():
+        setattr(desc, k, v)
+    assert _status(desc) == status
+
+
+def test_null_and_workspace_checks_answer_before_any_gpu_call():
+    lib = _lib.load()
+    case = C.case(C.HEADLINE)
+    desc = submission.make_desc(case)
+    size = ctypes.c_size_t(0)
+    assert lib.megamoe_workspace_bytes(None, ctypes.byref(size)) == _lib.ERR_INVALID_ARGUMENT
+    assert lib.megamoe_workspace_bytes(ctypes.byref(desc), None) == _lib.ERR_INVALID_ARGUMENT
+    assert lib.megamoe_forward(ctypes.byref(desc), None, None) == _lib.ERR_INVALID_ARGUMENT
+    t = _lib.Tensors()
+    assert lib.megamoe_forward(ctypes.byref(desc), ctypes.byref(t), None) == _lib.ERR_INVALID_ARGUMENT
+    # Every pointer set (never dereferenced: the workspace check fails first).
+    fake = {name: 256 for name, _ in _lib.Tensors._fields_ if name != "workspace_bytes"}
+    t = _lib.Tensors(**fake, workspace_bytes=16)
+    assert lib.megamoe_forward(ctypes.byref(desc), ctypes.byref(t), None) == _lib.ERR_WORKSPACE
+    # Shared expert pointers are required when S > 0.
+    t = _lib.Tensors(**{**fake, "shared_down": None}, workspace_bytes=1 << 40)
+    assert lib.megamoe_forward(ctypes.byref(desc), ctypes.byref(t), None) == _lib.ERR_INVALID_ARGUMENT
+    # No tokens: nothing to do, no pointer needed.
+    desc.tokens = 0
+    assert lib.megamoe_forward(ctypes.byref(desc), ctypes.byref(_lib.Tensors()), None) == _lib.OK
+    assert lib.megamoe_route(ctypes.byref(desc), None, None, None, None, None) == _lib.OK
+    desc.tokens = 4
+    assert lib.megamoe_route(ctypes.byref(desc), None, None, None, None, None) == _lib.ERR_INVALID_ARGUMENT
+    assert lib.megamoe_router_logits(ctypes.byref(desc), None, None, None, None, 0, None) == \
+        _lib.ERR_INVALID_ARGUMENT
+    assert lib.megamoe_quantize_rows(-1, 128, None, None, None, 0, None) == _lib.ERR_INVALID_ARGUMENT
+    assert lib.megamoe_quantize_rows(0, 128, None, None, None, 0, None) == _lib.OK
+    assert lib.megamoe_quantize_rows(4, 128, None, None, None, 0, None) == _lib.ERR_INVALID_ARGUMENT
+
+
+def test_python_errors_follow_the_reference_behaviour():
+    """Bad geometry raises ValueError (as the reference's builders do); inputs off the
+    GPU are refused before any launch."""
+    import torch
+
+    with pytest.raises(ValueError):
+        C.Case.from_dict({**C.case(C.HEADLINE).to_dict(), "params": {**C.case(C.HEADLINE).params, "topk": 999}})
+    layer = submission.MoELayer(C.development(C.case("moe-fp8-tiny-t4")))
+    with pytest.raises(RuntimeError):
+        layer({"x": torch.zeros((4, 256), dtype=torch.bfloat16)})
+    with pytest.raises(ValueError):
+        layer({})
+    with pytest.raises(ValueError):
+        _lib.check(_lib.ERR_SHAPE, "probe")
+    with pytest.raises(_lib.MegaMoEError):
+        _lib.check(_lib.ERR_HIP, "probe")

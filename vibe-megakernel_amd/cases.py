@@ -46,9 +46,9 @@ class Case:
     gpus: int = 1
     tp: int = 1
     ep: int = 1
-    # The layer runs as six stream-ordered kernels (router+quantize, select,
-    # permute, gate/up, down, combine) plus the x quantization kernel.
-    max_gpu_launches: int = 7
+    # The layer runs as five stream-ordered kernels: router + x quantization,
+    # select, permute, experts (gate/up + SwiGLU + down), combine.
+    max_gpu_launches: int = 5
     atol: float = 0.0
     rtol: float = 0.0
     bf16_rtol: float = 0.008
