@@ -10,9 +10,15 @@ independent input sets as it takes to move >= 1 GB per rotation, so the 256 MB
 Infinity Cache cannot hold a step's weights.
 
 Printed: one JSON line (rank 0) with the headline metric of the DeepSeek-V3
-shape (or --case), the roofline of the dominant kernel (gate/up) from the
-library's per-stage device events, and the CPU oracle timed on a bounded
-sample. --all adds one line per config to stderr.
+shape (or --case), the roofline of the dominant kernel (k_experts: gate/up +
+SwiGLU + down) and the CPU oracle timed on a bounded sample. --all adds one
+line per config to stderr.
+
+The kernel's duration comes from a second loop of K steps in which the library
+records HIP events at its stage boundaries on the stream its kernels run on
+(megamoe_forward_events); the mean over those K launches divides the kernel's
+algorithmic bytes. ``traffic`` (measured HBM bytes per launch) is read from the
+committed rocprofv3 counter summary of the case, when there is one.
 """
 
 from __future__ import annotations
@@ -32,6 +38,7 @@ sys.path.insert(0, str(REPO))
 
 import __graft_entry__  # noqa: E402
 
+PROFILES = REPO / "profiles"
 PEAK_HBM = 8.0e12          # B/s, MI355X HBM3E
 PEAK_FP8 = 5.0e15          # flop/s, dense E4M3 MFMA
 ROTATE_BYTES = 1.0e9
@@ -58,6 +65,37 @@ def kernel_bytes(case, hit: int) -> dict:
     return {"gate_up": gu, "down": dn}
 
 
+def measured_traffic(case) -> float | None:
+    """HBM bytes per k_experts launch from profiles/k_experts_<case>_counters.md: the line
+    ``traffic_bytes_per_launch: <number>`` (FETCH_SIZE + WRITE_SIZE, calibrated on a copy)."""
+    path = PROFILES / f"k_experts_{case.id}_counters.md"
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return float(line.split(":", 1)[1])
+    return None
+
+
+def copy_probe(mib: int) -> None:
+    """A plain device copy of ``mib`` MiB, three times: the calibration kernel that a
+    rocprofv3 counter run of this script records beside k_experts."""
+    import torch
+
+    src = torch.ones(mib << 18, dtype=torch.float32, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    _log(f"[bench] copy probe: 3 x {mib} MiB read + {mib} MiB written")
+
+
+def cpu_threads() -> int:
+    n = len(os.sched_getaffinity(0))
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    return min(n, int(env)) if env.isdigit() and int(env) > 0 else n
+
+
 def cpu_baseline(case, values_gpu, hit: int, budget_s: float) -> dict:
     """The CPU oracle (BF16 schedule) on the first tokens of the same inputs, scaled by
     distinct experts computed (the oracle's cost is dominated by dequantizing each hit
@@ -66,7 +104,7 @@ def cpu_baseline(case, values_gpu, hit: int, budget_s: float) -> dict:
 
     from oracle import layer
 
-    threads = len(os.sched_getaffinity(0))
+    threads = cpu_threads()
     torch.set_num_threads(threads)
     cpu = {k: v.cpu() for k, v in values_gpu.items()}
     sample = 1
@@ -129,12 +167,19 @@ def bench_case(case, steps: int, warmup: int, want_cpu: bool, cpu_budget: float)
     step_ms = [a.elapsed_time(b) for a, b in per_step]
     ms = total_ms / steps
 
-    # Per-stage device time (events on the stream the kernels run on, inside the library).
-    stage = []
-    for i in range(max(3, min(steps, 10))):
-        _, st = layer.timed(sets[i % n_sets])
-        stage.append(st)
-    stage_ms = [statistics.median(s[i] for s in stage) for i in range(len(stage[0]))]
+    # Per-stage device time over a second loop of the same K steps: the library records
+    # events at its stage boundaries on the stream its kernels run on.
+    nev = len(_lib.STAGES) + 1
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(nev)] for _ in range(steps)]
+    for row in events:
+        for e in row:
+            e.record(stream)  # creates the HIP event
+    torch.cuda.synchronize()
+    for i in range(steps):
+        layer.record(sets[i % n_sets], events[i])
+    torch.cuda.synchronize()
+    stage = [[row[j].elapsed_time(row[j + 1]) for j in range(nev - 1)] for row in events]
+    stage_ms = [statistics.mean(s[j] for s in stage) for j in range(nev - 1)]
 
     bytes_step = C.algorithmic_bytes(case, 0) + (C.algorithmic_bytes(case, 1) - C.algorithmic_bytes(case, 0)) * hit
     kb = kernel_bytes(case, hit)
@@ -151,7 +196,8 @@ def bench_case(case, steps: int, warmup: int, want_cpu: bool, cpu_budget: float)
         "stage_us": {name: v * 1e3 for name, v in zip(_lib.STAGES, stage_ms)},
         "rotation_sets": n_sets,
         "roofline": {"bound": "hbm", "achieved": ex_bytes / (ex_ms * 1e-3) / 1e9, "peak": PEAK_HBM / 1e9,
-                     "unit": "GB/s", "frac": ex_bytes / (ex_ms * 1e-3) / PEAK_HBM, "traffic": None,
+                     "unit": "GB/s", "frac": ex_bytes / (ex_ms * 1e-3) / PEAK_HBM,
+                     "traffic": measured_traffic(case),
                      "kernel": "k_experts", "kernel_us": ex_ms * 1e3, "bytes_per_launch": ex_bytes},
     }
     if want_cpu:
@@ -171,6 +217,8 @@ def main() -> int:
     ap.add_argument("--all", action="store_true", help="also measure the other four configs")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU oracle work")
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="run a plain copy of this many MiB first (counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported by this build "
@@ -185,6 +233,8 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         return 2
+    if args.copy_probe_mib > 0:
+        copy_probe(args.copy_probe_mib)
     head = C.case(args.case or C.HEADLINE)
     others = [c for c in C.CASES if c.id != head.id] if args.all else []
     results = {}

@@ -123,6 +123,13 @@ int megamoe_forward(const megamoe_desc* desc, const megamoe_tensors* t, void* st
 int megamoe_forward_timed(const megamoe_desc* desc, const megamoe_tensors* t, void* stream,
                           float* stage_ms);
 
+/* megamoe_forward that also records events[0..5] (hipEvent_t, created by the caller)
+ * on `stream` at the stage boundaries: before the router, then after each stage
+ * (router+quantize, select, permute, experts, combine). Asynchronous like
+ * megamoe_forward; for measuring a timed loop. No reference counterpart. */
+int megamoe_forward_events(const megamoe_desc* desc, const megamoe_tensors* t, void* stream,
+                           void* const* events);
+
 /* Router logits only: logits fp32 [T, E] = router @ x, with fp64 accumulation
  * rounded once to fp32. `workspace` as for megamoe_forward.
  * Replaces `values['router'].float() @ normalized.float()` (frontier.py:343). */

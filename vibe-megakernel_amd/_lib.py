@@ -18,8 +18,9 @@ GATE_SOFTMAX, GATE_SIGMOID = 0, 1
 STAGES = ("router_quant", "select", "permute", "experts", "combine")
 
 # Every symbol the header declares; tests check the library exports them all.
-SYMBOLS = ("megamoe_workspace_bytes", "megamoe_forward", "megamoe_forward_timed", "megamoe_router_logits",
-           "megamoe_route", "megamoe_quantize_rows", "megamoe_status_string", "megamoe_abi_version")
+SYMBOLS = ("megamoe_workspace_bytes", "megamoe_forward", "megamoe_forward_events", "megamoe_forward_timed",
+           "megamoe_router_logits", "megamoe_route", "megamoe_quantize_rows", "megamoe_status_string",
+           "megamoe_abi_version")
 
 
 class Desc(ctypes.Structure):
@@ -59,6 +60,7 @@ def load() -> ctypes.CDLL:
     P = ctypes.POINTER
     lib.megamoe_workspace_bytes.argtypes = [P(Desc), P(c_size_t)]
     lib.megamoe_forward.argtypes = [P(Desc), P(Tensors), c_void_p]
+    lib.megamoe_forward_events.argtypes = [P(Desc), P(Tensors), c_void_p, P(c_void_p)]
     lib.megamoe_forward_timed.argtypes = [P(Desc), P(Tensors), c_void_p, P(ctypes.c_float)]
     lib.megamoe_router_logits.argtypes = [P(Desc), c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]
     lib.megamoe_route.argtypes = [P(Desc), c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]

@@ -741,6 +741,7 @@ __device__ __forceinline__ void publish_fence() { __builtin_amdgcn_s_waitcnt(0);
 
 constexpr int kTileBytes = 16 * kBlock;  // one 16-row tile of one K block
 constexpr int kRingWave = 16384;         // LDS ring bytes per wavefront
+constexpr int kSpareBytes = 8192;        // workspace region read by loads past the last K block
 constexpr int kNonTemporal = 2;          // cache policy of the weight loads
 
 __device__ __forceinline__ f32x4 mfma_e4m3(const i32x8& a, const i32x8& b, f32x4 c) {
@@ -764,9 +765,10 @@ __device__ __forceinline__ void wait_vmem() {
 }
 
 // This lane's byte offsets for one tile: `dma` in global memory relative to the tile's
-// row 0 (row l/8, swizzled chunk), rd0/rd1 of its two MFMA chunks in the LDS tile.
+// row 0 (row l/8, swizzled chunk), rd0/rd1 of its two MFMA chunks in the LDS tile, and
+// `spare` (16 * lane) in the spare region.
 struct LaneTile {
-  int dma, rd0, rd1;
+  int dma, rd0, rd1, spare;
 };
 
 // threadIdx.x % 64 behind an empty asm: what the expert units derive from it is computed
@@ -781,7 +783,8 @@ __device__ __forceinline__ LaneTile lane_tile(int lda) {
   const int lane = opaque_lane();
   const int lr = lane >> 3, row = lane & 15, rr = row & 7, g = lane >> 4;
   const int base = (row >> 3) * 1024 + rr * kBlock;
-  return LaneTile{lr * lda + (((lane & 7) ^ lr) << 4), base + ((g ^ rr) << 4), base + (((g + 4) ^ rr) << 4)};
+  return LaneTile{lr * lda + (((lane & 7) ^ lr) << 4), base + ((g ^ rr) << 4), base + (((g + 4) ^ rr) << 4),
+                  lane << 4};
 }
 
 template <int NCT, int SG>
@@ -795,22 +798,28 @@ template <int RT, int NCT, int SG>
 struct Operands {
   const uint8_t* a[RT];    // row 0 of each 16-row weight tile (wave-uniform)
   int lda;                 // weight row length in bytes
+  const uint8_t* spare;    // kSpareBytes that loads past the last K block read instead
   const float* sw[SG];     // per-K-block weight scales of scale group g (wave-uniform)
   const uint8_t* b[NCT];   // lane's activation row at its K byte offset
   const float* sx[NCT];    // lane's activation scale row
 };
 
-// 2*RT weight loads of K block kb into one ring slot.
+// 2*RT weight loads of K block kb into one ring slot, or (live == false, past the last
+// block) the same number of loads from the spare region.
 template <int RT, int NCT, int SG>
-__device__ __forceinline__ void issue_a(uint8_t* slot, const Operands<RT, NCT, SG>& op, int dma, int kb) {
+__device__ __forceinline__ void issue_a(uint8_t* slot, const Operands<RT, NCT, SG>& op, const LaneTile& lt, int kb,
+                                        bool live) {
+  static_assert(RT * kTileBytes <= kSpareBytes, "spare region");
 #pragma unroll
   for (int t = 0; t < RT; ++t)
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
-      __builtin_amdgcn_global_load_lds(
-          (const __attribute__((address_space(1))) void*)(op.a[t] + (size_t)kb * kBlock +
-                                                          (uint32_t)(dma + 8 * i * op.lda)),
-          (__attribute__((address_space(3))) void*)(slot + t * kTileBytes + i * 1024), 16, 0, kNonTemporal);
+    for (int i = 0; i < 2; ++i) {
+      const uint8_t* src = live ? op.a[t] + (size_t)kb * kBlock + (uint32_t)(lt.dma + 8 * i * op.lda)
+                                : op.spare + (t * kTileBytes + i * 1024 + lt.spare);
+      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                       (__attribute__((address_space(3))) void*)(slot + t * kTileBytes + i * 1024),
+                                       16, 0, kNonTemporal);
+    }
 }
 
 // At least 3*NCT vector loads: two 16-byte loads and one scale per column tile.
@@ -908,13 +917,13 @@ __device__ __forceinline__ void compute_stage(uint32_t slot, const LaneTile& lt,
 // global_load_lds writes. When stage s is consumed, each of stages s+1 .. s+D-1 has been
 // issued after stage s's weights, as a group of 2*RT weight loads and at least 3*NCT
 // activation loads, so vmcnt <= (D-1)*(2*RT + 3*NCT) implies stage s has landed.
-// Loads past the last K block are clamped to it, not skipped: a branch around them would
-// merge paths with different load counts, and the compiler then waits for vmcnt 0 before
-// the next MFMA, which drains the pipeline at every stage. The clamped loads re-read the
-// block just fetched (an L2 hit) into slots nothing reads any more; they land before any
-// later load into the ring (issue order), and no other LDS data shares those slots. The
-// slot a stage overwrites was read (ds_read, issued in program order before the
-// overwriting load) one stage earlier.
+// Loads past the last K block are not skipped: a branch around them would merge paths with
+// different load counts, and the compiler then waits for vmcnt 0 before the next MFMA,
+// which drains the pipeline at every stage. They read the spare region instead (every
+// workgroup reads it, so it stays in L2; re-reading the last weight block would go to HBM,
+// since non-temporal lines do not stay in L2) into slots nothing reads any more, and they
+// land before any later load into the ring (issue order). The slot a stage overwrites was
+// read (ds_read, issued in program order before the overwriting load) one stage earlier.
 template <int RT, int NCT, int SG, int D>
 __device__ __forceinline__ void stream_gemm(const Operands<RT, NCT, SG>& op, int nkb, uint8_t* ring,
                                             f32x4 (&acc)[RT][NCT],
@@ -930,7 +939,7 @@ __device__ __forceinline__ void stream_gemm(const Operands<RT, NCT, SG>& op, int
     for (int c = 0; c < NCT; ++c) acc[r][c] = f32x4{0.f, 0.f, 0.f, 0.f};
   Stage<NCT, SG> st[D];
 #pragma unroll
-  for (int s = 0; s < D - 1; ++s) issue_a(ring + s * kSlot, op, lt.dma, min(s, nkb - 1));
+  for (int s = 0; s < D - 1; ++s) issue_a(ring + s * kSlot, op, lt, min(s, nkb - 1), s < nkb);
   wait_ready(ready);
 #pragma unroll
   for (int s = 0; s < D - 1; ++s) load_stage_b(st[s], op, min(s, nkb - 1));
@@ -939,7 +948,7 @@ __device__ __forceinline__ void stream_gemm(const Operands<RT, NCT, SG>& op, int
     for (int s = 0; s < D; ++s) {
       const int kb = kb0 + s, kn = min(kb + D - 1, nkb - 1);
       load_stage_b(st[(s + D - 1) % D], op, kn);
-      issue_a(ring + ((s + D - 1) % D) * kSlot, op, lt.dma, kn);
+      issue_a(ring + ((s + D - 1) % D) * kSlot, op, lt, kn, kb + D - 1 < nkb);
       wait_vmem<kAfter>();
       if (kb < nkb) compute_stage(ring_lds + s * kSlot, lt, st[s], acc);
     }
@@ -971,6 +980,7 @@ struct GateUpArgs {
   int* meta;
   uint8_t* hq_r; float* hs_r;   // routed rows [T*K, I], [T*K, I/128]
   uint8_t* hq_s; float* hs_s;   // shared rows [T, S*I], [T, S*I/128]
+  const uint8_t* spare;         // kSpareBytes of workspace
   int T, H, I, K, S, E, pow2;
 };
 
@@ -987,6 +997,7 @@ __device__ void gateup_unit(const GateUpArgs& a, const uint8_t* wg, const uint8_
   const int H = a.H, nkb = H / kBlock, nbh = scale_ld(ldh / kBlock);
   Operands<4, NCT, 2> op;
   op.lda = H;
+  op.spare = a.spare;
 #pragma unroll
   for (int r = 0; r < 2; ++r) {
     const size_t row = (size_t)(32 * w + 16 * r);
@@ -1059,6 +1070,7 @@ __device__ void gateup_unit_wide(const GateUpArgs& a, const uint8_t* wg, const u
   constexpr int D = 3;
   Operands<2, NCT, 2> op;
   op.lda = H;
+  op.spare = a.spare;
   op.sw[0] = sg;
   op.sw[1] = su;
 #pragma unroll
@@ -1172,6 +1184,7 @@ struct DownArgs {
   const uint8_t* hq_s; const float* hs_s;
   uint16_t* d_r;  // [T*K, H] bf16, grouped rows
   uint16_t* d_s;  // [T, H] bf16
+  const uint8_t* spare;  // kSpareBytes of workspace
   int T, H, I, K, S, E;
 };
 
@@ -1187,6 +1200,7 @@ __device__ void down_unit(const DownArgs& a, const uint8_t* wd, const float* sd,
 #pragma unroll
   for (int r = 0; r < 2; ++r) op.a[r] = wd + (size_t)(32 * w + 16 * r) * ldk;
   op.lda = ldk;
+  op.spare = a.spare;
   op.sw[0] = sd;
 #pragma unroll
   for (int c = 0; c < NCT; ++c) {
@@ -1367,7 +1381,8 @@ constexpr size_t kAlign = 256;
 inline size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
 struct Layout {
-  size_t partial, xq, xs, counts, offsets, meta, perm, inv, gu, dn, dn_of_gu, ready, hq_r, hs_r, hq_s, hs_s, d_r, d_s, total;
+  size_t partial, xq, xs, counts, offsets, meta, perm, inv, gu, dn, dn_of_gu, ready, hq_r, hs_r, hq_s, hs_s, d_r, d_s,
+      spare, total;
   int nsplit;
 };
 
@@ -1407,6 +1422,7 @@ Layout make_layout(const megamoe_desc& d) {
   L.hs_s = take(T * scale_ld((int)(S * I / kBlock)) * sizeof(float));
   L.d_r = take(T * K * H * 2);
   L.d_s = take(T * H * 2);
+  L.spare = take(kSpareBytes);
   L.total = at;
   return L;
 }
@@ -1562,6 +1578,7 @@ int forward_impl(const megamoe_desc* desc, const megamoe_tensors* t, hipStream_t
   ga.offsets = po.offsets; ga.perm = po.perm; ga.chunks = po.gu; ga.meta = po.meta;
   ga.hq_r = (uint8_t*)(ws + L.hq_r); ga.hs_r = (float*)(ws + L.hs_r);
   ga.hq_s = (uint8_t*)(ws + L.hq_s); ga.hs_s = (float*)(ws + L.hs_s);
+  ga.spare = (const uint8_t*)(ws + L.spare);
   ga.T = T; ga.H = H; ga.I = I; ga.K = K; ga.S = S; ga.E = E; ga.pow2 = d.pow2_scales;
   DownArgs& da = ea.dn;
   da.down = t->down; da.down_scale = t->down_scale;
@@ -1569,6 +1586,7 @@ int forward_impl(const megamoe_desc* desc, const megamoe_tensors* t, hipStream_t
   da.offsets = po.offsets; da.perm = po.perm; da.chunks = po.dn; da.meta = po.meta;
   da.hq_r = ga.hq_r; da.hs_r = ga.hs_r; da.hq_s = ga.hq_s; da.hs_s = ga.hs_s;
   da.d_r = (uint16_t*)(ws + L.d_r); da.d_s = (uint16_t*)(ws + L.d_s);
+  da.spare = ga.spare;
   da.T = T; da.H = H; da.I = I; da.K = K; da.S = S; da.E = E;
   ea.dn_of_gu = po.dn_of_gu;
   ea.ready = po.ready;
@@ -1618,6 +1636,15 @@ int megamoe_workspace_bytes(const megamoe_desc* desc, size_t* bytes) {
 
 int megamoe_forward(const megamoe_desc* desc, const megamoe_tensors* t, void* stream) {
   return forward_impl(desc, t, (hipStream_t)stream, nullptr);
+}
+
+int megamoe_forward_events(const megamoe_desc* desc, const megamoe_tensors* t, void* stream, void* const* events) {
+  if (!events) return MEGAMOE_ERR_INVALID_ARGUMENT;
+  for (int i = 0; i < kStages + 1; ++i)
+    if (!events[i]) return MEGAMOE_ERR_INVALID_ARGUMENT;
+  hipEvent_t ev[kStages + 1];
+  for (int i = 0; i < kStages + 1; ++i) ev[i] = (hipEvent_t)events[i];
+  return forward_impl(desc, t, (hipStream_t)stream, ev);
 }
 
 int megamoe_forward_timed(const megamoe_desc* desc, const megamoe_tensors* t, void* stream, float* stage_ms) {

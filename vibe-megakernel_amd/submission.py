@@ -95,7 +95,7 @@ class MoELayer:
             _expect(inputs["shared_down_scale"], "shared_down_scale", f32, (bh, bs), device)
         return device
 
-    def _call(self, inputs: dict, timed: bool):
+    def _call(self, inputs: dict, timed: bool, events=None):
         device = self.check_inputs(inputs)
         c = self.case
         y = torch.empty((c.tokens, c.hidden), dtype=torch.bfloat16, device=device)
@@ -113,6 +113,11 @@ class MoELayer:
                                workspace_bytes=self.workspace_bytes)
         stream = ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
         with torch.cuda.device(device):
+            if events is not None:
+                handles = (ctypes.c_void_p * len(events))(*[e.cuda_event for e in events])
+                _lib.check(self.lib.megamoe_forward_events(ctypes.byref(self.desc), ctypes.byref(tensors), stream,
+                                                           handles), f"{c.id}: forward")
+                return {"y": y, "expert_ids": ids, "expert_weights": weights}
             if timed:
                 ms = (ctypes.c_float * len(_lib.STAGES))()
                 _lib.check(self.lib.megamoe_forward_timed(ctypes.byref(self.desc), ctypes.byref(tensors), stream,
@@ -128,6 +133,13 @@ class MoELayer:
     def timed(self, inputs: dict) -> tuple[dict, list[float]]:
         """One call with a device event between stages; returns (outputs, per-stage ms)."""
         return self._call(inputs, timed=True)
+
+    def record(self, inputs: dict, events) -> dict:
+        """One asynchronous call that records ``events`` (len(STAGES) + 1 torch.cuda.Event
+        objects, each recorded once before so its HIP event exists) at the stage boundaries."""
+        if len(events) != len(_lib.STAGES) + 1 or not all(e.cuda_event for e in events):
+            raise ValueError("record() takes len(STAGES) + 1 created events")
+        return self._call(inputs, timed=False, events=events)
 
 
 def build(case: dict):
