@@ -141,6 +141,7 @@ def bench_case(case, steps: int, warmup: int, want_cpu: bool, cpu_budget: float)
     _log(f"[bench] {case.id}: generating {n_sets} input set(s) on the GPU")
     sets = [workloads.make_inputs(case, 7301 + i, dev) for i in range(n_sets)]
     torch.cuda.synchronize()
+    _log(f"[bench] {case.id}: inputs ready; warmup")
 
     outs = []
     for i in range(max(warmup, n_sets)):

@@ -39,7 +39,10 @@ constexpr int kBlock = 128;  // quantization block edge (weights 128x128, activa
 // chunks never share a cache line (see the hand-over notes of the expert kernel).
 __host__ __device__ constexpr int scale_ld(int blocks) { return (blocks + 31) / 32 * 32; }
 
-constexpr int kSpinLimit = 1 << 22;  // ~1 s of polling: past it a wait gives up and flags an error
+// Bound of one readiness wait, in ticks of the 100 MHz real-time clock (s_memrealtime):
+// past it (or once any wait has given up) the wait ends and flags an error, and the
+// combine then writes NaN to every output element.
+constexpr uint64_t kWaitTicks = 20000000;  // 0.2 s
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x8 __attribute__((ext_vector_type(8)));
@@ -575,8 +578,10 @@ __device__ unsigned long long block_exclusive_scan(unsigned long long v, unsigne
   return base + x - v;
 }
 
+// Ints of the meta block. The error flag has a 128-byte line of its own, apart from the
+// queue counter that every workgroup updates.
 constexpr int kMetaHit = 0, kMetaUnitsGU = 1, kMetaUnitsDN = 2, kMetaQueueGU = 3, kMetaQueueDN = 4,
-              kMetaError = 6;
+              kMetaError = 32, kMetaInts = 64;
 constexpr int kChunkRows = 64;
 
 struct PermuteOut {
@@ -741,7 +746,7 @@ __device__ __forceinline__ void publish_fence() { __builtin_amdgcn_s_waitcnt(0);
 
 constexpr int kTileBytes = 16 * kBlock;  // one 16-row tile of one K block
 constexpr int kRingWave = 16384;         // LDS ring bytes per wavefront
-constexpr int kSpareBytes = 8192;        // workspace region read by loads past the last K block
+
 constexpr int kNonTemporal = 2;          // cache policy of the weight loads
 
 __device__ __forceinline__ f32x4 mfma_e4m3(const i32x8& a, const i32x8& b, f32x4 c) {
@@ -765,10 +770,9 @@ __device__ __forceinline__ void wait_vmem() {
 }
 
 // This lane's byte offsets for one tile: `dma` in global memory relative to the tile's
-// row 0 (row l/8, swizzled chunk), rd0/rd1 of its two MFMA chunks in the LDS tile, and
-// `spare` (16 * lane) in the spare region.
+// row 0 (row l/8, swizzled chunk), rd0/rd1 of its two MFMA chunks in the LDS tile.
 struct LaneTile {
-  int dma, rd0, rd1, spare;
+  int dma, rd0, rd1;
 };
 
 // threadIdx.x % 64 behind an empty asm: what the expert units derive from it is computed
@@ -783,8 +787,7 @@ __device__ __forceinline__ LaneTile lane_tile(int lda) {
   const int lane = opaque_lane();
   const int lr = lane >> 3, row = lane & 15, rr = row & 7, g = lane >> 4;
   const int base = (row >> 3) * 1024 + rr * kBlock;
-  return LaneTile{lr * lda + (((lane & 7) ^ lr) << 4), base + ((g ^ rr) << 4), base + (((g + 4) ^ rr) << 4),
-                  lane << 4};
+  return LaneTile{lr * lda + (((lane & 7) ^ lr) << 4), base + ((g ^ rr) << 4), base + (((g + 4) ^ rr) << 4)};
 }
 
 template <int NCT, int SG>
@@ -798,28 +801,28 @@ template <int RT, int NCT, int SG>
 struct Operands {
   const uint8_t* a[RT];    // row 0 of each 16-row weight tile (wave-uniform)
   int lda;                 // weight row length in bytes
-  const uint8_t* spare;    // kSpareBytes that loads past the last K block read instead
+  const uint8_t* spare;    // 16 * lda bytes that loads past the last K block read instead
   const float* sw[SG];     // per-K-block weight scales of scale group g (wave-uniform)
   const uint8_t* b[NCT];   // lane's activation row at its K byte offset
   const float* sx[NCT];    // lane's activation scale row
 };
 
 // 2*RT weight loads of K block kb into one ring slot, or (live == false, past the last
-// block) the same number of loads from the spare region.
+// block) the same number of loads from the spare region, which has the shape of one tile
+// (16 rows of lda bytes): only the wave-uniform base changes, the lane offsets do not.
 template <int RT, int NCT, int SG>
 __device__ __forceinline__ void issue_a(uint8_t* slot, const Operands<RT, NCT, SG>& op, const LaneTile& lt, int kb,
                                         bool live) {
-  static_assert(RT * kTileBytes <= kSpareBytes, "spare region");
 #pragma unroll
-  for (int t = 0; t < RT; ++t)
+  for (int t = 0; t < RT; ++t) {
+    const uint8_t* base = live ? op.a[t] + (size_t)kb * kBlock : op.spare;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const uint8_t* src = live ? op.a[t] + (size_t)kb * kBlock + (uint32_t)(lt.dma + 8 * i * op.lda)
-                                : op.spare + (t * kTileBytes + i * 1024 + lt.spare);
-      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+    for (int i = 0; i < 2; ++i)
+      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(base +
+                                                                                     (uint32_t)(lt.dma + 8 * i * op.lda)),
                                        (__attribute__((address_space(3))) void*)(slot + t * kTileBytes + i * 1024),
                                        16, 0, kNonTemporal);
-    }
+  }
 }
 
 // At least 3*NCT vector loads: two 16-byte loads and one scale per column tile.
@@ -841,16 +844,17 @@ struct ReadyWait {
   int* error;        // set to 1 if the bounded wait gives up
 };
 
-// Thread 0 polls the count (bounded), then the workgroup passes a barrier. The barrier
+// Thread 0 polls the count (bounded in time), then the workgroup passes a barrier. The barrier
 // carries no release fence (this workgroup publishes nothing here, and a release would
 // wait for the weight loads in flight); the acquire fence after it keeps the loads that
 // follow from moving above it.
 __device__ __forceinline__ void wait_ready(const ReadyWait& w) {
   if (!w.count) return;
   if (threadIdx.x == 0) {
-    int spins = 0;
-    while (__hip_atomic_load(w.count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < w.need) {
-      if (++spins > kSpinLimit) {
+    const uint64_t t0 = wall_clock64();
+    for (int polls = 0; __hip_atomic_load(w.count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < w.need; ++polls) {
+      if ((polls & 15) == 15 && (__hip_atomic_load(w.error, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ||
+                                 wall_clock64() - t0 > kWaitTicks)) {
         atomicExch(w.error, 1);
         break;
       }
@@ -980,7 +984,7 @@ struct GateUpArgs {
   int* meta;
   uint8_t* hq_r; float* hs_r;   // routed rows [T*K, I], [T*K, I/128]
   uint8_t* hq_s; float* hs_s;   // shared rows [T, S*I], [T, S*I/128]
-  const uint8_t* spare;         // kSpareBytes of workspace
+  const uint8_t* spare;         // 16 rows of the longest weight row, in the workspace
   int T, H, I, K, S, E, pow2;
 };
 
@@ -1055,86 +1059,6 @@ __device__ void gateup_unit(const GateUpArgs& a, const uint8_t* wg, const uint8_
   }
 }
 
-// Gate/up unit for 33..64 activation rows (four column tiles). To keep the accumulators
-// of four column tiles within the register budget, the 128-row block is done in two
-// 64-row halves: in half hf, wave w owns gate and up rows 64*hf + 16w .. +15. The h
-// values of the first half wait in LDS (past the three ring slots this path streams
-// through) while the second half streams.
-__device__ void gateup_unit_wide(const GateUpArgs& a, const uint8_t* wg, const uint8_t* wu, const float* sg,
-                                 const float* su, const ChunkRows& cr, int jb, uint8_t* hq, float* hs, int ldh,
-                                 float (*red)[64], uint8_t* ring) {
-  constexpr int NCT = 4;
-  const int lane = opaque_lane(), w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int kofs = 16 * (lane >> 4);
-  const int H = a.H, nkb = H / kBlock, nbh = scale_ld(ldh / kBlock);
-  constexpr int D = 3;
-  Operands<2, NCT, 2> op;
-  op.lda = H;
-  op.spare = a.spare;
-  op.sw[0] = sg;
-  op.sw[1] = su;
-#pragma unroll
-  for (int c = 0; c < NCT; ++c) {
-    const int r = min(16 * c + (lane & 15), cr.n - 1);
-    const int tok = row_token(cr, r);
-    op.b[c] = a.xq + (size_t)tok * H + kofs;
-    op.sx[c] = a.xs + (size_t)tok * nkb;
-  }
-  static_assert(D * 2 * kTileBytes + 64 * NCT * 4 * sizeof(float) <= kRingWave, "ring + h values");
-  float* mine = reinterpret_cast<float*>(ring + D * 2 * kTileBytes) + lane * (NCT * 4);  // first-half h values
-  float amax[NCT];
-#pragma unroll
-  for (int c = 0; c < NCT; ++c) amax[c] = 0.0f;
-#pragma unroll 1
-  for (int hf = 0; hf < 2; ++hf) {
-    const size_t row = (size_t)(64 * hf + 16 * w);
-    op.a[0] = wg + row * H;
-    op.a[1] = wu + row * H;
-    f32x4 acc[2][NCT];
-    stream_gemm<2, NCT, 2, D>(op, nkb, ring, acc);
-#pragma unroll
-    for (int c = 0; c < NCT; ++c)
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const float h = round_bf16(silu(round_bf16(acc[0][c][v])) * round_bf16(acc[1][c][v]));
-        acc[0][c][v] = h;
-        amax[c] = fmaxf(amax[c], fabsf(h));
-      }
-    if (hf == 0) {
-#pragma unroll
-      for (int c = 0; c < NCT; ++c)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) mine[4 * c + v] = acc[0][c][v];
-    } else {
-#pragma unroll
-      for (int c = 0; c < NCT; ++c) {
-        float m = fmaxf(amax[c], __shfl_xor(amax[c], 16));
-        m = fmaxf(m, __shfl_xor(m, 32));
-        if (lane < 16) red[w][16 * c + lane] = m;
-      }
-      __syncthreads();
-#pragma unroll
-      for (int c = 0; c < NCT; ++c) {
-        const int col = 16 * c + (lane & 15);
-        const float amx = fmaxf(fmaxf(red[0][col], red[1][col]), fmaxf(red[2][col], red[3][col]));
-        const float s = act_scale(amx, a.pow2);
-        if (col < cr.n) {
-          uint8_t* dst = hq + (size_t)(cr.row0 + col) * ldh + (size_t)jb * kBlock + 16 * w + 4 * (lane >> 4);
-          uint32_t p0 = 0, p1 = 0;
-#pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            p0 |= f32_to_e4m3(clamp448(mine[4 * c + v] / s)) << (8 * v);
-            p1 |= f32_to_e4m3(clamp448(acc[0][c][v] / s)) << (8 * v);
-          }
-          store_coherent(reinterpret_cast<uint32_t*>(dst), p0);
-          store_coherent(reinterpret_cast<uint32_t*>(dst + 64), p1);
-          if (w == 0 && lane < 16) store_coherent(hs + (size_t)(cr.row0 + col) * nbh + jb, s);
-        }
-      }
-    }
-  }
-}
-
 // Gate/up unit u of the work list: chunk u / nbI, 128-row block u % nbI of the chunk's
 // expert (plus the slice offset of a shared-expert copy).
 __device__ void gateup_work(const GateUpArgs& a, int u, float (*red)[64], uint8_t* ring) {
@@ -1172,7 +1096,7 @@ __device__ void gateup_work(const GateUpArgs& a, int u, float (*red)[64], uint8_
   else if (cr.n <= 32)
     gateup_unit<2>(a, wg, wu, sg, su, cr, jb, hq, hs, ldh, red, ring);
   else
-    gateup_unit_wide(a, wg, wu, sg, su, cr, jb, hq, hs, ldh, red, ring);
+    gateup_unit<4>(a, wg, wu, sg, su, cr, jb, hq, hs, ldh, red, ring);
 }
 
 struct DownArgs {
@@ -1184,7 +1108,7 @@ struct DownArgs {
   const uint8_t* hq_s; const float* hs_s;
   uint16_t* d_r;  // [T*K, H] bf16, grouped rows
   uint16_t* d_s;  // [T, H] bf16
-  const uint8_t* spare;  // kSpareBytes of workspace
+  const uint8_t* spare;  // 16 rows of the longest weight row, in the workspace
   int T, H, I, K, S, E;
 };
 
@@ -1209,7 +1133,7 @@ __device__ void down_unit(const DownArgs& a, const uint8_t* wd, const float* sd,
     op.sx[c] = hs + (size_t)(cr.row0 + r) * scale_ld(nkb);
   }
   f32x4 acc[2][NCT];
-  stream_gemm<2, NCT, 1, NCT == 4 ? 2 : 4>(op, nkb, ring, acc, ready);
+  stream_gemm<2, NCT, 1, NCT == 4 ? 3 : 4>(op, nkb, ring, acc, ready);
 #pragma unroll
   for (int c = 0; c < NCT; ++c) {
     const int r = 16 * c + (lane & 15);
@@ -1301,26 +1225,34 @@ __device__ __forceinline__ void combine8(const uint16_t* __restrict__ d_r, const
   *reinterpret_cast<uint4*>(y + (size_t)t * H + h0) = o;
 }
 
+// If a readiness wait of the expert kernel gave up, every element of y is NaN.
 __global__ __launch_bounds__(256) void k_combine(const uint16_t* __restrict__ d_r, const uint16_t* __restrict__ d_s,
                                                  const int* __restrict__ inv, const float* __restrict__ wts, int T,
-                                                 int H, int K, int S, uint16_t* __restrict__ y) {
+                                                 int H, int K, int S, const int* __restrict__ meta,
+                                                 uint16_t* __restrict__ y) {
   const int i = blockIdx.x * 256 + threadIdx.x, per_row = H / 8;
-  if (i < T * per_row) combine8(d_r, d_s, inv, wts, H, K, S, i / per_row, (i % per_row) * 8, y);
+  if (i >= T * per_row) return;
+  if (meta[kMetaError]) {
+    *reinterpret_cast<uint4*>(y + (size_t)i * 8) = make_uint4(0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u);
+    return;
+  }
+  combine8(d_r, d_s, inv, wts, H, K, S, i / per_row, (i % per_row) * 8, y);
 }
 
 // ---------------------------------------------------------------------------------------
 // The expert stage as one persistent kernel. One work queue lists every gate/up unit,
-// then every down unit; each workgroup starts on unit blockIdx.x and takes further units
-// from the queue, so workgroups that run out of gate/up work go straight on to down
-// units instead of idling through the gate/up tail.
+// then every down unit; each workgroup claims its units from the queue, so workgroups
+// that run out of gate/up work go straight on to down units instead of idling through
+// the gate/up tail.
 //
 // A down unit of chunk c needs the h rows of chunk c, i.e. every gate/up unit of the
 // chunk: ready[c] counts them (nbI per routed chunk, S*nbI for the shared expert), and
 // the down unit's workgroup waits for the count after requesting its first weight
-// stages (the weights do not depend on it). The wait is bounded and in practice
-// short: every gate/up unit precedes every down unit in the queue, so the units it waits
-// for are already running (all workgroups of the grid are resident at once). The
-// combine runs as its own small kernel after this one.
+// stages (the weights do not depend on it). Every gate/up unit precedes every down unit
+// in the queue, so when a down unit is claimed, each unit it waits for has been claimed
+// by a workgroup that is running it (gate/up units wait for nothing): the wait ends
+// however many workgroups are resident. It is also bounded in time. The combine runs
+// as its own small kernel after this one.
 // ---------------------------------------------------------------------------------------
 
 
@@ -1340,7 +1272,12 @@ __global__ __launch_bounds__(256, 2) void k_experts(ExpertArgs args) {
   int* meta = args.gu.meta;
   const int total_gu = meta[kMetaUnitsGU];
   const int total = total_gu + meta[kMetaUnitsDN];
-  int u = blockIdx.x, next = 0;
+  // Every unit, the first included, is claimed from the queue: a unit that a down unit
+  // waits for is then always held by a running workgroup (one that has not started yet
+  // holds nothing), whatever number of workgroups the device keeps resident.
+  if (threadIdx.x == 0) slot = atomicAdd(&meta[kMetaQueueGU], 1);
+  __syncthreads();
+  int u = slot, next = 0;
   while (u < total) {
     // The arguments are re-read from the kernel argument segment (where `args`, the only
     // argument, sits at offset 0) through a pointer behind an empty asm, so each unit
@@ -1354,8 +1291,10 @@ __global__ __launch_bounds__(256, 2) void k_experts(ExpertArgs args) {
     uint8_t* ring = rings + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) * kRingWave;
     __syncthreads();
     // Thread 0 takes the next unit index now and hands it out after this unit: the
-    // atomic's round trip overlaps the unit instead of holding up wavefront 0.
-    if (threadIdx.x == 0) next = gridDim.x + atomicAdd(&meta[kMetaQueueGU], 1);
+    // atomic's round trip overlaps the unit instead of holding up wavefront 0. A
+    // workgroup on a down unit can only hold later (down) units this way, so no gate/up
+    // unit waits behind a waiting workgroup.
+    if (threadIdx.x == 0) next = atomicAdd(&meta[kMetaQueueGU], 1);
     if (u < total_gu) {
       gateup_work(a.gu, u, red, ring);
       publish_fence();
@@ -1409,7 +1348,7 @@ Layout make_layout(const megamoe_desc& d) {
   L.xs = take(T * (H / kBlock) * sizeof(float));
   L.counts = take(E * sizeof(int));
   L.offsets = take((E + 1) * sizeof(int));
-  L.meta = take(16 * sizeof(int));
+  L.meta = take(kMetaInts * sizeof(int));
   L.perm = take(T * K * sizeof(int));
   L.inv = take(T * K * sizeof(int));
   L.gu = take(max_chunks(d, (int)S) * sizeof(int4));
@@ -1422,7 +1361,7 @@ Layout make_layout(const megamoe_desc& d) {
   L.hs_s = take(T * scale_ld((int)(S * I / kBlock)) * sizeof(float));
   L.d_r = take(T * K * H * 2);
   L.d_s = take(T * H * 2);
-  L.spare = take(kSpareBytes);
+  L.spare = take(16 * (H > I * (S > 1 ? S : 1) ? H : I * (S > 1 ? S : 1)));
   L.total = at;
   return L;
 }
@@ -1590,8 +1529,8 @@ int forward_impl(const megamoe_desc* desc, const megamoe_tensors* t, hipStream_t
   da.T = T; da.H = H; da.I = I; da.K = K; da.S = S; da.E = E;
   ea.dn_of_gu = po.dn_of_gu;
   ea.ready = po.ready;
-  // Every workgroup resident at once (a down unit may wait on gate/up units of lower
-  // queue positions), and no more of them than the most units the routing can produce.
+  // As many workgroups as fit on the device at once, and no more than the most units the
+  // routing can produce.
   const size_t units_max = max_chunks(d, S) * (size_t)nbI + max_chunks(d, S > 0 ? 1 : 0) * (size_t)nbH;
   const size_t resident = (size_t)di.cus * di.experts_per_cu;
   const unsigned grid = (unsigned)(units_max < resident ? units_max : resident);
@@ -1602,7 +1541,7 @@ int forward_impl(const megamoe_desc* desc, const megamoe_tensors* t, hipStream_t
   const int rows8 = T * (H / 8);
   hipLaunchKernelGGL(k_combine, dim3((rows8 + 255) / 256), dim3(256), 0, st, (const uint16_t*)da.d_r,
                      (const uint16_t*)da.d_s, (const int*)po.inv, (const float*)t->expert_weights, T, H, K, S,
-                     (uint16_t*)t->y);
+                     (const int*)po.meta, (uint16_t*)t->y);
   MEGAMOE_LAUNCH_CHECK();
   if (mark(5) != hipSuccess) return MEGAMOE_ERR_HIP;
   return MEGAMOE_OK;
