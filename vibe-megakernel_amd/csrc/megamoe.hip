@@ -220,18 +220,14 @@ __global__ __launch_bounds__(256) void k_router(const uint16_t* __restrict__ x, 
     a[u] = *reinterpret_cast<const float4*>(wp + k);
     b[u] = *reinterpret_cast<const uint2*>(xp + k);
   }
-  for (int s0 = 0; s0 < steps; s0 += kRouterDepth) {
+  if (steps <= kRouterDepth) {
+    // Every step is in flight already: consume them, no refills.
 #pragma unroll
     for (int u = 0; u < kRouterDepth; ++u) {
+      const bool live = u < steps;
+      const bool ok_a = e_ok && live, ok_b = t_ok && live;
       const float4 av = a[u];
       const uint2 bv = b[u];
-      // Refill this slot with the step kRouterDepth ahead (clamped; the tail re-reads).
-      const int k = min(s0 + u + kRouterDepth, steps - 1) * 16;
-      a[u] = *reinterpret_cast<const float4*>(wp + k);
-      b[u] = *reinterpret_cast<const uint2*>(xp + k);
-      // Steps past the end contribute zero (their operands are zeroed, not skipped).
-      const bool live = s0 + u < steps;
-      const bool ok_a = e_ok && live, ok_b = t_ok && live;
       const double a0 = ok_a ? (double)av.x : 0.0, a1 = ok_a ? (double)av.y : 0.0;
       const double a2 = ok_a ? (double)av.z : 0.0, a3 = ok_a ? (double)av.w : 0.0;
       const double b0 = ok_b ? (double)bf16_bits_to_f32(bv.x & 0xffffu) : 0.0;
@@ -242,6 +238,31 @@ __global__ __launch_bounds__(256) void k_router(const uint16_t* __restrict__ x, 
       acc = __builtin_amdgcn_mfma_f64_16x16x4f64(a1, b1, acc, 0, 0, 0);
       acc = __builtin_amdgcn_mfma_f64_16x16x4f64(a2, b2, acc, 0, 0, 0);
       acc = __builtin_amdgcn_mfma_f64_16x16x4f64(a3, b3, acc, 0, 0, 0);
+    }
+  } else {
+    for (int s0 = 0; s0 < steps; s0 += kRouterDepth) {
+#pragma unroll
+      for (int u = 0; u < kRouterDepth; ++u) {
+        const float4 av = a[u];
+        const uint2 bv = b[u];
+        // Refill this slot with the step kRouterDepth ahead (clamped; the tail re-reads).
+        const int k = min(s0 + u + kRouterDepth, steps - 1) * 16;
+        a[u] = *reinterpret_cast<const float4*>(wp + k);
+        b[u] = *reinterpret_cast<const uint2*>(xp + k);
+        // Steps past the end contribute zero (their operands are zeroed, not skipped).
+        const bool live = s0 + u < steps;
+        const bool ok_a = e_ok && live, ok_b = t_ok && live;
+        const double a0 = ok_a ? (double)av.x : 0.0, a1 = ok_a ? (double)av.y : 0.0;
+        const double a2 = ok_a ? (double)av.z : 0.0, a3 = ok_a ? (double)av.w : 0.0;
+        const double b0 = ok_b ? (double)bf16_bits_to_f32(bv.x & 0xffffu) : 0.0;
+        const double b1 = ok_b ? (double)bf16_bits_to_f32(bv.x >> 16) : 0.0;
+        const double b2 = ok_b ? (double)bf16_bits_to_f32(bv.y & 0xffffu) : 0.0;
+        const double b3 = ok_b ? (double)bf16_bits_to_f32(bv.y >> 16) : 0.0;
+        acc = __builtin_amdgcn_mfma_f64_16x16x4f64(a0, b0, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f64_16x16x4f64(a1, b1, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f64_16x16x4f64(a2, b2, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f64_16x16x4f64(a3, b3, acc, 0, 0, 0);
+      }
     }
   }
   // Quarters of the split, added in wavefront order.
@@ -282,9 +303,8 @@ __global__ __launch_bounds__(256) void k_logits(const double* __restrict__ parti
 // Selection order is (score descending, expert index ascending), the order a stable
 // descending argsort produces (frontier.py:236,240; distributed.py:174).
 //
-// The K-th largest score is found by a radix search over order-preserving 32-bit score
-// codes (one ballot per bit and register), ties at it are filled with the lowest expert
-// indices, and the K picks are ordered by ranking them against each other in LDS.
+// The K picks come out in selection order from K rounds of a wavefront-wide maximum over
+// 64-bit keys (score code, complemented index); each round's winner drops its key.
 // ---------------------------------------------------------------------------------------
 
 constexpr int kMaxTopK = 32;
@@ -302,32 +322,81 @@ __device__ __forceinline__ unsigned long long lanes_below() {
   return lane ? (~0ull >> (64 - lane)) : 0ull;
 }
 
-// Picks the k largest codes (ties: lowest expert index) among valid entries; returns the
-// per-register pick mask of this lane.
-template <int VPL>
-__device__ __forceinline__ unsigned top_codes(const uint32_t (&code)[VPL], const bool (&valid)[VPL], int k) {
-  uint32_t tau = 0;
-  for (int b = 31; b >= 0; --b) {
-    const uint32_t cand = tau | (1u << b);
-    int cnt = 0;
-#pragma unroll
-    for (int j = 0; j < VPL; ++j) cnt += __popcll(__ballot(valid[j] && code[j] >= cand));
-    if (cnt >= k) tau = cand;
+// Cross-lane butterfly steps without LDS: DPP within rows of 16 lanes (quad_perm [1,0,3,2]
+// and [2,3,0,1], row_half_mirror, row_mirror), then the permlane16/32 swaps across rows.
+// Applied smallest first, step s leaves every lane with the max (or merged top-2) of its
+// aligned group of 2^(s+1) lanes. They need every lane of the wavefront active.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, false);
+}
+
+// The value of the partner lane at butterfly step `step` (0..5); for steps 4 and 5 the two
+// halves of the swap are returned as (mine, other) in lane order.
+template <int STEP>
+__device__ __forceinline__ void lane_pair(uint32_t v, uint32_t& a, uint32_t& b) {
+  if constexpr (STEP == 0) {
+    a = v; b = dpp_u32<0xB1>(v);
+  } else if constexpr (STEP == 1) {
+    a = v; b = dpp_u32<0x4E>(v);
+  } else if constexpr (STEP == 2) {
+    a = v; b = dpp_u32<0x141>(v);
+  } else if constexpr (STEP == 3) {
+    a = v; b = dpp_u32<0x140>(v);
+  } else if constexpr (STEP == 4) {
+    const auto p = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    a = p[0]; b = p[1];
+  } else {
+    const auto p = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    a = p[0]; b = p[1];
   }
-  int need = k;
-#pragma unroll
-  for (int j = 0; j < VPL; ++j) need -= __popcll(__ballot(valid[j] && code[j] > tau));
-  unsigned pick = 0u;
-  const unsigned long long below = lanes_below();
-#pragma unroll
-  for (int j = 0; j < VPL; ++j) {
-    const unsigned long long eq = __ballot(valid[j] && code[j] == tau);
-    const int before = __popcll(eq & below);
-    if ((valid[j] && code[j] > tau) || (valid[j] && code[j] == tau && before < need)) pick |= 1u << j;
-    need -= __popcll(eq);
-    if (need < 0) need = 0;
-  }
-  return pick;
+}
+
+template <int STEP>
+__device__ __forceinline__ unsigned long long max_step_u64(unsigned long long v) {
+  uint32_t la, lb, ha, hb;
+  lane_pair<STEP>((uint32_t)v, la, lb);
+  lane_pair<STEP>((uint32_t)(v >> 32), ha, hb);
+  const unsigned long long a = ((unsigned long long)ha << 32) | la, b = ((unsigned long long)hb << 32) | lb;
+  return a > b ? a : b;
+}
+
+// Largest 64-bit value over the wavefront (every lane gets it).
+__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v) {
+  v = max_step_u64<0>(v);
+  v = max_step_u64<1>(v);
+  v = max_step_u64<2>(v);
+  v = max_step_u64<3>(v);
+  v = max_step_u64<4>(v);
+  return max_step_u64<5>(v);
+}
+
+// Merges the (largest, second largest) pairs of lanes at butterfly step STEP.
+template <int STEP>
+__device__ __forceinline__ void top2_step(float& b1, float& b2) {
+  uint32_t a1, o1, a2, o2;
+  lane_pair<STEP>(__float_as_uint(b1), a1, o1);
+  lane_pair<STEP>(__float_as_uint(b2), a2, o2);
+  const float x1 = __uint_as_float(a1), y1 = __uint_as_float(o1);
+  const float x2 = __uint_as_float(a2), y2 = __uint_as_float(o2);
+  b2 = fmaxf(fminf(x1, y1), fmaxf(x2, y2));
+  b1 = fmaxf(x1, y1);
+}
+
+// Top-2 merge over aligned lane segments of `len` lanes (a power of two, 1..64).
+__device__ __forceinline__ void top2_segment(float& b1, float& b2, int len) {
+  if (len >= 2) top2_step<0>(b1, b2);
+  if (len >= 4) top2_step<1>(b1, b2);
+  if (len >= 8) top2_step<2>(b1, b2);
+  if (len >= 16) top2_step<3>(b1, b2);
+  if (len >= 32) top2_step<4>(b1, b2);
+  if (len >= 64) top2_step<5>(b1, b2);
+}
+
+// Selection key of an expert: the order code of its score above, the complement of its
+// index below, so a larger key is a larger score or, on equal scores, a lower index.
+__device__ __forceinline__ unsigned long long select_key(float score, int e) {
+  return ((unsigned long long)order_code(score) << 32) | (0xffffffffu - (uint32_t)e);
 }
 
 constexpr int kSelectTokens = 4;  // tokens per workgroup, one wavefront each
@@ -341,14 +410,12 @@ __global__ __launch_bounds__(256) void k_select(const double* __restrict__ parti
                                                 float* __restrict__ w_out) {
   __shared__ float lds_logit[kSelectTokens][kMaxExperts];
   __shared__ float gscore[kSelectTokens][kMaxGroups];
-  __shared__ uint32_t pick_code_s[kSelectTokens][kMaxTopK];
   __shared__ int pick_id_s[kSelectTokens][kMaxTopK];
   __shared__ float pick_val_s[kSelectTokens][kMaxTopK];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int t0 = blockIdx.x * kSelectTokens, t = t0 + wv;
   const bool token_ok = t < T;
   float* choice_lds = lds_logit[wv];
-  uint32_t* pick_code = pick_code_s[wv];
   int* pick_id = pick_id_s[wv];
   float* pick_val = pick_val_s[wv];
 
@@ -360,12 +427,12 @@ __global__ __launch_bounds__(256) void k_select(const double* __restrict__ parti
   }
 
   // Logits of the workgroup's tokens into LDS: thread i sums the splits (in split order)
-  // of entries i, i+256, ... (at most 4*VPL of them, up to kMaxSplits splits each), every
-  // load issued before the first add.
+  // of entries i, i+256, ... (kSelectTokens * E <= 256 * VPL of them, up to kMaxSplits
+  // splits each), every load issued before the first add.
   const int n_here = min(kSelectTokens, T - t0) * E;
   if (logits_in) {
 #pragma unroll
-    for (int r = 0; r < 4 * VPL; ++r) {
+    for (int r = 0; r < VPL; ++r) {
       const int i = threadIdx.x + 256 * r;
       const float v = logits_in[(size_t)t0 * E + min(i, n_here - 1)];
       if (i < n_here) lds_logit[i / E][i % E] = v;
@@ -373,9 +440,9 @@ __global__ __launch_bounds__(256) void k_select(const double* __restrict__ parti
   } else {
     const size_t stride = (size_t)T * E;
     const double* p = partial + (size_t)t0 * E;
-    constexpr int R = 4 * VPL < 8 ? 4 * VPL : 8;  // entries per round of loads
+    constexpr int R = VPL < 4 ? VPL : 4;  // entries per round of loads
 #pragma unroll
-    for (int r0 = 0; r0 < 4 * VPL; r0 += R) {
+    for (int r0 = 0; r0 < VPL; r0 += R) {
       double part[R][kMaxSplits];
 #pragma unroll
       for (int r = 0; r < R; ++r) {
@@ -416,30 +483,32 @@ __global__ __launch_bounds__(256) void k_select(const double* __restrict__ parti
       choice[j] = logit[j];
     }
   }
-  __syncthreads();  // lds_logit is reused below for the choices
-
   if (G > 1) {
-    // Group score: the sum of the two largest choices of the group (frontier.py:234).
+    // Group score: the sum of the two largest choices of the group (frontier.py:234). A
+    // group is scanned by lpg lanes (the largest power of two <= 64 / G), whose top-2
+    // pairs are then merged with shuffles inside the lane segment. Each wavefront works
+    // on its own LDS rows from here on.
     const int gs = E / G;
+    int lpg = 1;
+    while (lpg * 2 * G <= 64) lpg *= 2;
 #pragma unroll
     for (int j = 0; j < VPL; ++j)
       if (valid[j]) choice_lds[lane + 64 * j] = choice[j];
-    __syncthreads();
-    if (lane < G && token_ok) {
-      float b1 = -INFINITY, b2 = -INFINITY;
-#pragma unroll 8
-      for (int i = 0; i < gs; ++i) {
-        const float v = choice_lds[lane * gs + i];
-        if (v > b1) {
-          b2 = b1;
-          b1 = v;
-        } else if (v > b2) {
-          b2 = v;
-        }
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the choices are in LDS
+    __builtin_amdgcn_wave_barrier();
+    const int grp = lane / lpg, sub = lane % lpg;
+    float b1 = -INFINITY, b2 = -INFINITY;
+    if (grp < G && token_ok) {
+      for (int i = sub; i < gs; i += lpg) {
+        const float v = choice_lds[grp * gs + i];
+        b2 = fmaxf(b2, fminf(b1, v));
+        b1 = fmaxf(b1, v);
       }
-      gscore[wv][lane] = gs >= 2 ? b1 + b2 : b1;
     }
-    __syncthreads();
+    top2_segment(b1, b2, lpg);
+    if (grp < G && sub == 0 && token_ok) gscore[wv][grp] = gs >= 2 ? b1 + b2 : b1;
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_wave_barrier();
     // Keep the TG best groups, ties to the lower group index (frontier.py:235).
     bool keep = false;
     if (lane < G && token_ok) {
@@ -456,51 +525,33 @@ __global__ __launch_bounds__(256) void k_select(const double* __restrict__ parti
     for (int j = 0; j < VPL; ++j)
       if (valid[j] && !((kept >> ((lane + 64 * j) / gs)) & 1ull)) choice[j] = -INFINITY;
   }
-
-  uint32_t code[VPL];
+  // K rounds: the wavefront's largest remaining key is the next pick (selection order,
+  // frontier.py:236; distributed.py:174); its owner records it and drops it.
+  unsigned long long key[VPL];
 #pragma unroll
-  for (int j = 0; j < VPL; ++j) code[j] = order_code(choice[j]);
-  const unsigned pick = token_ok ? top_codes<VPL>(code, valid, K) : 0u;
-
-  // Compact the K picks into LDS, then rank them: (code desc, index asc).
-  int base = 0;
-  const unsigned long long below = lanes_below();
+  for (int j = 0; j < VPL; ++j) key[j] = valid[j] ? select_key(choice[j], lane + 64 * j) : 0ull;
+  for (int r = 0; r < K && token_ok; ++r) {
+    unsigned long long best = 0ull;
 #pragma unroll
-  for (int j = 0; j < VPL; ++j) {
-    const bool mine = (pick >> j) & 1u;
-    const unsigned long long m = __ballot(mine);
-    if (mine) {
-      const int slot = base + __popcll(m & below);
-      pick_code[slot] = code[j];
-      pick_id[slot] = lane + 64 * j;
-      pick_val[slot] = prob[j];
-    }
-    base += __popcll(m);
+    for (int j = 0; j < VPL; ++j) best = key[j] > best ? key[j] : best;
+    best = wave_max_u64(best);
+#pragma unroll
+    for (int j = 0; j < VPL; ++j)
+      if (key[j] == best) {
+        pick_id[r] = lane + 64 * j;
+        pick_val[r] = prob[j];
+        key[j] = 0ull;
+      }
   }
-  __syncthreads();
-  int my_id = 0, rank = 0;
-  float my_val = 0.0f;
-  if (lane < K && token_ok) {
-    const uint32_t c = pick_code[lane];
-    my_id = pick_id[lane];
-    my_val = pick_val[lane];
-    for (int i = 0; i < K; ++i) {
-      const uint32_t o = pick_code[i];
-      rank += (o > c) || (o == c && pick_id[i] < my_id);
-    }
-  }
-  __syncthreads();
-  if (lane < K && token_ok) {
-    pick_id[rank] = my_id;
-    pick_val[rank] = my_val;
-  }
-  __syncthreads();
+  __builtin_amdgcn_s_waitcnt(0xc07f);
+  __builtin_amdgcn_wave_barrier();
   if (!token_ok) return;
+  int my_id = 0;
+  float my_val = 0.0f;
   if (lane < K) {
     my_id = pick_id[lane];
     my_val = pick_val[lane];
   }
-
   // Weights; sums run in slot order.
   float w = 0.0f;
   if (gate == MEGAMOE_GATE_SIGMOID) {
