@@ -118,14 +118,15 @@ int megamoe_forward(const megamoe_desc* desc, const megamoe_tensors* t, void* st
 
 /* megamoe_forward with a device event between its stages; blocks until the
  * call has finished and writes the elapsed ms of each stage to stage_ms[0..4]
- * (router+quantize, select, permute, experts = gate/up + down, combine). For
+ * (router, select + x quantization, permute, experts = gate/up + down,
+ * combine). For
  * measurement; the results equal megamoe_forward's. */
 int megamoe_forward_timed(const megamoe_desc* desc, const megamoe_tensors* t, void* stream,
                           float* stage_ms);
 
 /* megamoe_forward that also records events[0..5] (hipEvent_t, created by the caller)
  * on `stream` at the stage boundaries: before the router, then after each stage
- * (router+quantize, select, permute, experts, combine). Asynchronous like
+ * (router, select + x quantization, permute, experts, combine). Asynchronous like
  * megamoe_forward; for measuring a timed loop. No reference counterpart. */
 int megamoe_forward_events(const megamoe_desc* desc, const megamoe_tensors* t, void* stream,
                            void* const* events);

@@ -15,7 +15,7 @@ LIBRARY = PACKAGE_DIR / "libmegamoe.so"
 
 OK, ERR_INVALID_ARGUMENT, ERR_SHAPE, ERR_WORKSPACE, ERR_HIP, ERR_UNSUPPORTED = range(6)
 GATE_SOFTMAX, GATE_SIGMOID = 0, 1
-STAGES = ("router_quant", "select", "permute", "experts", "combine")
+STAGES = ("router", "select_quant", "permute", "experts", "combine")
 
 # Every symbol the header declares; tests check the library exports them all.
 SYMBOLS = ("megamoe_workspace_bytes", "megamoe_forward", "megamoe_forward_events", "megamoe_forward_timed",

@@ -1,11 +1,12 @@
 // megamoe.hip — FP8 (E4M3, 128x128 block-scaled) MoE decode layer for MI355X (gfx950).
 //
 // The layer, as five stream-ordered kernel launches (one process, one GPU):
-//   k_router                  router logits on fp64 MFMA as split partials over H; its extra
-//                             workgroups quantize x (E4M3, one fp32 scale per token per 128)
+//   k_router                  router logits on fp64 MFMA as split partials over H
 //   k_select                  adds the split partials in order and rounds once to fp32, then
 //                             per token (one wavefront each): sigmoid/softmax gate,
-//                             group-limited top-k with a (value desc, index asc) total order
+//                             group-limited top-k with a (value desc, index asc) total order;
+//                             its extra workgroups quantize x (E4M3, one fp32 scale per token
+//                             per 128)
 //   k_permute                 one workgroup: expert histogram, exclusive scan, stable
 //                             (token, slot)-ordered permutation, and the expert work lists
 //                             (chunks of <= 64 rows, heaviest first)
@@ -167,121 +168,139 @@ __global__ __launch_bounds__(256) void k_quant_rows(const uint16_t* __restrict__
 
 typedef double f64x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kRouterTile = 16;   // experts and tokens per workgroup tile
+constexpr int kRouterTile = 16;   // experts per workgroup tile, tokens per accumulator tile
+constexpr int kRouterWaves = 4;   // wavefronts per router workgroup (split of its H range)
+constexpr int kMaxSplits = 16;    // router splits of H over workgroups (router_splits)
 constexpr int kQuantPerWave = 2;  // x blocks quantized per wavefront by the quantizing workgroups
-constexpr int kRouterDepth = 8;   // 16-channel steps of loads in flight per wavefront
+constexpr int kRouterDepth = 8;   // 16-channel steps per wavefront, all in flight at once
 
-// Splits of H: the largest of 4, 2, 1 whose per-wavefront quarter is a whole number of
-// 16-channel steps.
-inline int router_splits(int H) { return H % 256 == 0 ? 4 : (H % 128 == 0 ? 2 : 1); }
+// Splits of H over workgroups: the smallest power of two <= 16 that leaves each wavefront
+// at most kRouterDepth 16-channel steps (a whole number of them), else the largest that
+// divides H evenly (the wavefronts then stream their slices in rounds of kRouterDepth).
+inline int router_splits(int H) {
+  int best = 1;
+  for (int n = 1; n <= kMaxSplits; n *= 2) {
+    if (H % (n * kRouterWaves * 16)) break;
+    best = n;
+    if (H / (n * kRouterWaves * 16) <= kRouterDepth) break;
+  }
+  return best;
+}
 
 inline int router_quant_groups(int T, int H) {
   return (T * (H / kBlock) + 4 * kQuantPerWave - 1) / (4 * kQuantPerWave);
 }
 
-__global__ __launch_bounds__(256) void k_router(const uint16_t* __restrict__ x, const float* __restrict__ w,
-                                                double* __restrict__ partial, uint8_t* __restrict__ xq,
-                                                float* __restrict__ xs, int T, int H, int E, int n_et, int n_tt,
-                                                int nsplit, int pow2) {
-  __shared__ f64x4 red[3][64];
+// x quantization for the expert GEMMs, kQuantPerWave 128-blocks per wavefront; run by
+// extra workgroups of k_select (k_select is latency-bound on a few CUs, the router is not).
+__device__ __forceinline__ void quant_x_group(int group, const uint16_t* __restrict__ x, uint8_t* __restrict__ xq,
+                                              float* __restrict__ xs, int T, int H, int pow2) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const int n_router = n_et * n_tt * nsplit;
-  if ((int)blockIdx.x >= n_router) {
-    const int nbh = H / kBlock;
-    const int first = (((int)blockIdx.x - n_router) * 4 + wv) * kQuantPerWave;
+  const int nbh = H / kBlock;
+  const int first = (group * 4 + wv) * kQuantPerWave;
 #pragma unroll
-    for (int q = 0; q < kQuantPerWave; ++q) {
-      const int it = first + q;
-      if (it < T * nbh) {
-        const int t = it / nbh, cb = it % nbh;
-        const size_t o = (size_t)t * H + (size_t)cb * kBlock;
-        quant_block(x + o, xq + o, xs + (size_t)t * nbh + cb, pow2, lane);
-      }
+  for (int q = 0; q < kQuantPerWave; ++q) {
+    const int it = first + q;
+    if (it < T * nbh) {
+      const int t = it / nbh, cb = it % nbh;
+      const size_t o = (size_t)t * H + (size_t)cb * kBlock;
+      quant_block(x + o, xq + o, xs + (size_t)t * nbh + cb, pow2, lane);
     }
-    return;
   }
-  const int et = blockIdx.x % n_et, tt = (blockIdx.x / n_et) % n_tt, split = blockIdx.x / (n_et * n_tt);
-  const int span = H / nsplit / 4;  // channels per wavefront, a multiple of 16
+}
+
+// Router partials. Workgroup (expert tile et, split) of kRouterWaves wavefronts covers 16
+// experts, H range [split * H/nsplit, +H/nsplit) and every token, in passes of 16 * NTT
+// tokens: wavefront w takes the w-th of kRouterWaves equal slices of the range, keeps NTT
+// 16x16 fp64 accumulators (one per token tile) and streams its slice in 16-channel steps,
+// all of them in flight at once (at most kRouterDepth). The router weights of the slice
+// are read once per pass, x once per expert tile. The wavefronts' sums are added in
+// wavefront order through LDS and the split's partial is stored in fp64.
+template <int NTT>
+__global__ __launch_bounds__(kRouterWaves * 64) void k_router(const uint16_t* __restrict__ x,
+                                                              const float* __restrict__ w,
+                                                              double* __restrict__ partial, int T, int H, int E,
+                                                              int n_et, int nsplit) {
+  __shared__ f64x4 red[kRouterWaves - 1][NTT][64];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int et = blockIdx.x % n_et, split = blockIdx.x / n_et;
+  const int span = H / nsplit / kRouterWaves;  // channels per wavefront, a multiple of 16
   const int k0 = split * (H / nsplit) + wv * span;
   const int g = lane >> 4;
-  const int e = et * kRouterTile + (lane & 15), t = tt * kRouterTile + (lane & 15);
-  const bool e_ok = e < E, t_ok = t < T;
+  const int e = et * kRouterTile + (lane & 15);
+  const bool e_ok = e < E;
   // Rows past E or T read row 0 and are zeroed after the load: the loads themselves stay
-  // unconditional so the compiler keeps several of them in flight.
+  // unconditional so the compiler keeps all of them in flight.
   const float* wp = w + (size_t)(e_ok ? e : 0) * H + k0 + 4 * g;
-  const uint16_t* xp = x + (size_t)(t_ok ? t : 0) * H + k0 + 4 * g;
   const int steps = span / 16;
-  f64x4 acc = {0.0, 0.0, 0.0, 0.0};
-  float4 a[kRouterDepth];
-  uint2 b[kRouterDepth];
+  for (int tp = 0; tp < T; tp += 16 * NTT) {
+    const uint16_t* xp[NTT];
+    bool t_ok[NTT];
 #pragma unroll
-  for (int u = 0; u < kRouterDepth; ++u) {
-    const int k = min(u, steps - 1) * 16;
-    a[u] = *reinterpret_cast<const float4*>(wp + k);
-    b[u] = *reinterpret_cast<const uint2*>(xp + k);
-  }
-  if (steps <= kRouterDepth) {
-    // Every step is in flight already: consume them, no refills.
+    for (int i = 0; i < NTT; ++i) {
+      const int t = tp + 16 * i + (lane & 15);
+      t_ok[i] = t < T;
+      xp[i] = x + (size_t)(t_ok[i] ? t : 0) * H + k0 + 4 * g;
+    }
+    f64x4 acc[NTT];
+#pragma unroll
+    for (int i = 0; i < NTT; ++i) acc[i] = f64x4{0.0, 0.0, 0.0, 0.0};
+    for (int c0 = 0; c0 < steps; c0 += kRouterDepth) {
+    float4 a[kRouterDepth];
+    uint2 b[kRouterDepth][NTT];
 #pragma unroll
     for (int u = 0; u < kRouterDepth; ++u) {
-      const bool live = u < steps;
-      const bool ok_a = e_ok && live, ok_b = t_ok && live;
-      const float4 av = a[u];
-      const uint2 bv = b[u];
-      const double a0 = ok_a ? (double)av.x : 0.0, a1 = ok_a ? (double)av.y : 0.0;
-      const double a2 = ok_a ? (double)av.z : 0.0, a3 = ok_a ? (double)av.w : 0.0;
-      const double b0 = ok_b ? (double)bf16_bits_to_f32(bv.x & 0xffffu) : 0.0;
-      const double b1 = ok_b ? (double)bf16_bits_to_f32(bv.x >> 16) : 0.0;
-      const double b2 = ok_b ? (double)bf16_bits_to_f32(bv.y & 0xffffu) : 0.0;
-      const double b3 = ok_b ? (double)bf16_bits_to_f32(bv.y >> 16) : 0.0;
-      acc = __builtin_amdgcn_mfma_f64_16x16x4f64(a0, b0, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f64_16x16x4f64(a1, b1, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f64_16x16x4f64(a2, b2, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f64_16x16x4f64(a3, b3, acc, 0, 0, 0);
-    }
-  } else {
-    for (int s0 = 0; s0 < steps; s0 += kRouterDepth) {
+      const int k = min(c0 + u, steps - 1) * 16;
+      a[u] = *reinterpret_cast<const float4*>(wp + k);
 #pragma unroll
-      for (int u = 0; u < kRouterDepth; ++u) {
-        const float4 av = a[u];
-        const uint2 bv = b[u];
-        // Refill this slot with the step kRouterDepth ahead (clamped; the tail re-reads).
-        const int k = min(s0 + u + kRouterDepth, steps - 1) * 16;
-        a[u] = *reinterpret_cast<const float4*>(wp + k);
-        b[u] = *reinterpret_cast<const uint2*>(xp + k);
-        // Steps past the end contribute zero (their operands are zeroed, not skipped).
-        const bool live = s0 + u < steps;
-        const bool ok_a = e_ok && live, ok_b = t_ok && live;
-        const double a0 = ok_a ? (double)av.x : 0.0, a1 = ok_a ? (double)av.y : 0.0;
-        const double a2 = ok_a ? (double)av.z : 0.0, a3 = ok_a ? (double)av.w : 0.0;
-        const double b0 = ok_b ? (double)bf16_bits_to_f32(bv.x & 0xffffu) : 0.0;
-        const double b1 = ok_b ? (double)bf16_bits_to_f32(bv.x >> 16) : 0.0;
-        const double b2 = ok_b ? (double)bf16_bits_to_f32(bv.y & 0xffffu) : 0.0;
-        const double b3 = ok_b ? (double)bf16_bits_to_f32(bv.y >> 16) : 0.0;
-        acc = __builtin_amdgcn_mfma_f64_16x16x4f64(a0, b0, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f64_16x16x4f64(a1, b1, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f64_16x16x4f64(a2, b2, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f64_16x16x4f64(a3, b3, acc, 0, 0, 0);
+      for (int i = 0; i < NTT; ++i) b[u][i] = *reinterpret_cast<const uint2*>(xp[i] + k);
+    }
+#pragma unroll
+    for (int u = 0; u < kRouterDepth; ++u) {
+      const bool live = c0 + u < steps;  // steps past the end contribute zero
+      const bool ok_a = e_ok && live;
+      const float av[4] = {a[u].x, a[u].y, a[u].z, a[u].w};
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const double ac = ok_a ? (double)av[c] : 0.0;
+#pragma unroll
+        for (int i = 0; i < NTT; ++i) {
+          const uint32_t word = c < 2 ? b[u][i].x : b[u][i].y;
+          const float xv = bf16_bits_to_f32((c & 1) ? (word >> 16) : (word & 0xffffu));
+          const double bc = (t_ok[i] && live) ? (double)xv : 0.0;
+          acc[i] = __builtin_amdgcn_mfma_f64_16x16x4f64(ac, bc, acc[i], 0, 0, 0);
+        }
       }
     }
-  }
-  // Quarters of the split, added in wavefront order.
-  if (wv > 0) red[wv - 1][lane] = acc;
-  __syncthreads();
-  if (wv == 0) {
-#pragma unroll
-    for (int q = 0; q < 3; ++q) {
-      const f64x4 o = red[q][lane];
-#pragma unroll
-      for (int v = 0; v < 4; ++v) acc[v] += o[v];
     }
-    if (t_ok) {
+    // Slices of the split, added in wavefront order.
+    if (wv > 0) {
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int eo = et * kRouterTile + g + 4 * v;
-        if (eo < E) partial[((size_t)split * T + t) * E + eo] = acc[v];
+      for (int i = 0; i < NTT; ++i) red[wv - 1][i][lane] = acc[i];
+    }
+    __syncthreads();
+    if (wv == 0) {
+#pragma unroll
+      for (int q = 0; q < kRouterWaves - 1; ++q)
+#pragma unroll
+        for (int i = 0; i < NTT; ++i) {
+          const f64x4 o = red[q][i][lane];
+#pragma unroll
+          for (int v = 0; v < 4; ++v) acc[i][v] += o[v];
+        }
+#pragma unroll
+      for (int i = 0; i < NTT; ++i) {
+        const int t = tp + 16 * i + (lane & 15);
+        if (t < T) {
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const int eo = et * kRouterTile + g + 4 * v;
+            if (eo < E) partial[((size_t)split * T + t) * E + eo] = acc[i][v];
+          }
+        }
       }
     }
+    if (tp + 16 * NTT < T) __syncthreads();  // red is reused by the next pass
   }
 }
 
@@ -400,14 +419,19 @@ __device__ __forceinline__ unsigned long long select_key(float score, int e) {
 }
 
 constexpr int kSelectTokens = 4;  // tokens per workgroup, one wavefront each
-constexpr int kMaxSplits = 4;     // router splits of H (router_splits)
+
 
 template <int VPL>
 __global__ __launch_bounds__(256) void k_select(const double* __restrict__ partial, int nsplit,
                                                 const float* __restrict__ logits_in, const float* __restrict__ bias,
                                                 int T, int E, int K, int G, int TG, int gate, int renorm,
                                                 float scaling, int64_t* __restrict__ ids_out,
-                                                float* __restrict__ w_out) {
+                                                float* __restrict__ w_out, int n_sel, const uint16_t* __restrict__ x,
+                                                uint8_t* __restrict__ xq, float* __restrict__ xs, int H, int pow2) {
+  if ((int)blockIdx.x >= n_sel) {
+    quant_x_group((int)blockIdx.x - n_sel, x, xq, xs, T, H, pow2);
+    return;
+  }
   __shared__ float lds_logit[kSelectTokens][kMaxExperts];
   __shared__ float gscore[kSelectTokens][kMaxGroups];
   __shared__ int pick_id_s[kSelectTokens][kMaxTopK];
@@ -440,7 +464,7 @@ __global__ __launch_bounds__(256) void k_select(const double* __restrict__ parti
   } else {
     const size_t stride = (size_t)T * E;
     const double* p = partial + (size_t)t0 * E;
-    constexpr int R = VPL < 4 ? VPL : 4;  // entries per round of loads
+    constexpr int R = VPL < 2 ? VPL : 2;  // entries per round of loads
 #pragma unroll
     for (int r0 = 0; r0 < VPL; r0 += R) {
       double part[R][kMaxSplits];
@@ -1366,7 +1390,7 @@ __global__ __launch_bounds__(256, 2) void k_experts(ExpertArgs args) {
 // Host side
 // ---------------------------------------------------------------------------------------
 
-constexpr int kStages = 5;  // router+quantize, select, permute, experts, combine
+constexpr int kStages = 5;  // router, select + x quantization, permute, experts, combine
 constexpr size_t kAlign = 256;
 inline size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
@@ -1464,11 +1488,18 @@ int device_info(DeviceInfo* out) {
 // Router partials (and, with the extra expert tile, the quantized x) for all tokens.
 int launch_router(const megamoe_desc& d, const Layout& L, const void* x, const float* router, char* ws,
                   hipStream_t st) {
-  const int n_et = (d.experts + kRouterTile - 1) / kRouterTile, n_tt = (d.tokens + kRouterTile - 1) / kRouterTile;
-  const int n_router = n_et * n_tt * L.nsplit;
-  hipLaunchKernelGGL(k_router, dim3(n_router + router_quant_groups(d.tokens, d.hidden)), dim3(256), 0, st,
-                     (const uint16_t*)x, router, (double*)(ws + L.partial), (uint8_t*)(ws + L.xq),
-                     (float*)(ws + L.xs), d.tokens, d.hidden, d.experts, n_et, n_tt, L.nsplit, d.pow2_scales);
+  const int n_et = (d.experts + kRouterTile - 1) / kRouterTile, tiles = (d.tokens + kRouterTile - 1) / kRouterTile;
+  const dim3 grid(n_et * L.nsplit), block(kRouterWaves * 64);
+#define MEGAMOE_ROUTER(NTT)                                                                                    \
+  hipLaunchKernelGGL(k_router<NTT>, grid, block, 0, st, (const uint16_t*)x, router, (double*)(ws + L.partial),  \
+                     d.tokens, d.hidden, d.experts, n_et, L.nsplit)
+  if (tiles <= 1)
+    MEGAMOE_ROUTER(1);
+  else if (tiles <= 2)
+    MEGAMOE_ROUTER(2);
+  else
+    MEGAMOE_ROUTER(4);
+#undef MEGAMOE_ROUTER
   MEGAMOE_LAUNCH_CHECK();
   return MEGAMOE_OK;
 }
@@ -1492,13 +1523,16 @@ int launch_quant(int rows, int cols, const void* x, uint8_t* q, float* s, int po
   return MEGAMOE_OK;
 }
 
-// Routing from fp32 logits, or (logits == NULL) from the router's fp64 split partials.
+// Routing from fp32 logits, or (logits == NULL) from the router's fp64 split partials; with
+// x != NULL, extra workgroups quantize x into xq / xs.
 int launch_select(const megamoe_desc& d, const double* partial, int nsplit, const float* logits, const float* bias,
-                  int64_t* ids, float* w, hipStream_t st) {
-  const dim3 grid((d.tokens + kSelectTokens - 1) / kSelectTokens), block(256);
+                  int64_t* ids, float* w, const void* x, uint8_t* xq, float* xs, hipStream_t st) {
+  const int n_sel = (d.tokens + kSelectTokens - 1) / kSelectTokens;
+  const dim3 grid(n_sel + (x ? router_quant_groups(d.tokens, d.hidden) : 0)), block(256);
 #define MEGAMOE_SELECT(VPL)                                                                                   \
   hipLaunchKernelGGL(k_select<VPL>, grid, block, 0, st, partial, nsplit, logits, bias, d.tokens, d.experts,   \
-                     d.topk, d.groups, d.top_groups, d.gate, d.renormalize, d.routed_scaling, ids, w)
+                     d.topk, d.groups, d.top_groups, d.gate, d.renormalize, d.routed_scaling, ids, w, n_sel,   \
+                     (const uint16_t*)x, xq, xs, d.hidden, d.pow2_scales)
   if (d.experts <= 64)
     MEGAMOE_SELECT(1);
   else if (d.experts <= 128)
@@ -1544,7 +1578,7 @@ int forward_impl(const megamoe_desc* desc, const megamoe_tensors* t, hipStream_t
   if (mark(1) != hipSuccess) return MEGAMOE_ERR_HIP;
 
   if ((rc = launch_select(d, (const double*)(ws + L.partial), L.nsplit, nullptr, t->router_bias, t->expert_ids,
-                          t->expert_weights, st)))
+                          t->expert_weights, t->x, (uint8_t*)(ws + L.xq), (float*)(ws + L.xs), st)))
     return rc;
   if (mark(2) != hipSuccess) return MEGAMOE_ERR_HIP;
 
@@ -1671,7 +1705,8 @@ int megamoe_route(const megamoe_desc* desc, const float* logits, const float* bi
   if (rc) return rc;
   if (desc->tokens == 0) return MEGAMOE_OK;
   if (!logits || !expert_ids || !expert_weights) return MEGAMOE_ERR_INVALID_ARGUMENT;
-  return launch_select(*desc, nullptr, 0, logits, bias, expert_ids, expert_weights, (hipStream_t)stream);
+  return launch_select(*desc, nullptr, 0, logits, bias, expert_ids, expert_weights, nullptr, nullptr, nullptr,
+                       (hipStream_t)stream);
 }
 
 int megamoe_quantize_rows(int32_t rows, int32_t cols, const void* x, uint8_t* q, float* scales, int32_t pow2,
