@@ -674,7 +674,7 @@ struct PermuteOut {
 __device__ __forceinline__ int chunk_class(int rows) { return rows > 32 ? 0 : (rows > 16 ? 1 : 2); }
 
 __global__ __launch_bounds__(1024) void k_permute(const int64_t* __restrict__ ids, int T, int K, int E, int S,
-                                                  int nbI, int nbH, PermuteOut out) {
+                                                  int nbI, int nbH, int ks, PermuteOut out) {
   extern __shared__ int smem[];
   unsigned long long* tmp = (unsigned long long*)smem;  // 16
   int* cnt = smem + 32;                                  // E
@@ -751,7 +751,7 @@ __global__ __launch_bounds__(1024) void k_permute(const int64_t* __restrict__ id
     out.offsets[E] = total;
     out.meta[kMetaHit] = nhit;
     out.meta[kMetaUnitsGU] = (S * (s4 + s2 + s1) + t4 + t2 + t1) * nbI;
-    out.meta[kMetaUnitsDN] = (s4 + s2 + s1 + t4 + t2 + t1) * nbH;
+    out.meta[kMetaUnitsDN] = (s4 + s2 + s1 + t4 + t2 + t1) * nbH * ks;
     out.meta[kMetaQueueGU] = 0;
     out.meta[kMetaQueueDN] = 0;
     out.meta[kMetaError] = 0;
@@ -1183,74 +1183,87 @@ struct DownArgs {
   const uint8_t* hq_s; const float* hs_s;
   uint16_t* d_r;  // [T*K, H] bf16, grouped rows
   uint16_t* d_s;  // [T, H] bf16
+  float* p_r;     // ks > 1: [ks, T*K, H] fp32 partial d of each K part
+  float* p_s;     // ks > 1: [ks, T, H]
   const uint8_t* spare;  // 16 rows of the longest weight row, in the workspace
-  int T, H, I, K, S, E;
+  int T, H, I, K, S, E, ks;
 };
 
 // One down unit: rows [j*128, j*128+128) of a down matrix [H, ldk] against the chunk's
-// requantized h rows. Wave w owns rows 32w .. 32w+31.
+// requantized h rows, over K part kp of a.ks (K blocks [kp*nkb/ks, (kp+1)*nkb/ks)). Wave w
+// owns rows 32w .. 32w+31. With one part the result is d in bf16; with several, each part
+// stores its fp32 partial to pd and the combine adds the parts in order before rounding.
 template <int NCT>
 __device__ void down_unit(const DownArgs& a, const uint8_t* wd, const float* sd, int ldk, const uint8_t* hq,
-                          const float* hs, const ChunkRows& cr, int j, uint16_t* d, const ReadyWait& ready, uint8_t* ring) {
+                          const float* hs, const ChunkRows& cr, int j, int kp, uint16_t* d, float* pd,
+                          const ReadyWait& ready, uint8_t* ring) {
   const int lane = opaque_lane(), w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int kofs = 16 * (lane >> 4);
-  const int nkb = ldk / kBlock;
+  const int nkb = ldk / kBlock, nkbp = nkb / a.ks, kb0 = kp * nkbp;
   Operands<2, NCT, 1> op;
 #pragma unroll
-  for (int r = 0; r < 2; ++r) op.a[r] = wd + (size_t)(32 * w + 16 * r) * ldk;
+  for (int r = 0; r < 2; ++r) op.a[r] = wd + (size_t)(32 * w + 16 * r) * ldk + (size_t)kb0 * kBlock;
   op.lda = ldk;
   op.spare = a.spare;
-  op.sw[0] = sd;
+  op.sw[0] = sd + kb0;
 #pragma unroll
   for (int c = 0; c < NCT; ++c) {
     const int r = min(16 * c + (lane & 15), cr.n - 1);
-    op.b[c] = hq + (size_t)(cr.row0 + r) * ldk + kofs;
-    op.sx[c] = hs + (size_t)(cr.row0 + r) * scale_ld(nkb);
+    op.b[c] = hq + (size_t)(cr.row0 + r) * ldk + (size_t)kb0 * kBlock + kofs;
+    op.sx[c] = hs + (size_t)(cr.row0 + r) * scale_ld(nkb) + kb0;
   }
   f32x4 acc[2][NCT];
-  stream_gemm<2, NCT, 1, NCT == 4 ? 3 : 4>(op, nkb, ring, acc, ready);
+  stream_gemm<2, NCT, 1, NCT == 4 ? 3 : 4>(op, nkbp, ring, acc, ready);
 #pragma unroll
   for (int c = 0; c < NCT; ++c) {
     const int r = 16 * c + (lane & 15);
     if (r < cr.n) {
 #pragma unroll
       for (int p = 0; p < 2; ++p) {
-        const uint32_t lo = f32_to_bf16_bits(acc[p][c][0]) | (f32_to_bf16_bits(acc[p][c][1]) << 16);
-        const uint32_t hi = f32_to_bf16_bits(acc[p][c][2]) | (f32_to_bf16_bits(acc[p][c][3]) << 16);
-        uint16_t* dst = d + (size_t)(cr.row0 + r) * a.H + (size_t)j * kBlock + 32 * w + 16 * p + 4 * (lane >> 4);
-        *reinterpret_cast<uint2*>(dst) = make_uint2(lo, hi);
+        const size_t o = (size_t)(cr.row0 + r) * a.H + (size_t)j * kBlock + 32 * w + 16 * p + 4 * (lane >> 4);
+        if (a.ks == 1) {
+          const uint32_t lo = f32_to_bf16_bits(acc[p][c][0]) | (f32_to_bf16_bits(acc[p][c][1]) << 16);
+          const uint32_t hi = f32_to_bf16_bits(acc[p][c][2]) | (f32_to_bf16_bits(acc[p][c][3]) << 16);
+          *reinterpret_cast<uint2*>(d + o) = make_uint2(lo, hi);
+        } else {
+          *reinterpret_cast<f32x4*>(pd + o) = acc[p][c];
+        }
       }
     }
   }
 }
 
-// Down unit v of the work list: chunk v / nbH, 128-row block v % nbH of the down matrix.
+// Down unit v of the work list: chunk v / (nbH*ks), then 128-row block j of the down
+// matrix and K part kp (v % (nbH*ks) = j*ks + kp).
 __device__ void down_work(const DownArgs& a, int v, const ReadyWait& ready, uint8_t* ring) {
   const int nbH = a.H / kBlock, nbI = a.I / kBlock;
-  const int4 ch = a.chunks[v / nbH];
-  const int j = v % nbH;
+  const int4 ch = a.chunks[v / (nbH * a.ks)];
+  const int rem = v % (nbH * a.ks), j = rem / a.ks, kp = rem % a.ks;
+  const size_t TK = (size_t)a.T * a.K;
+  float* pd_s = a.p_s + (size_t)kp * a.T * a.H;
+  float* pd_r = a.p_r + (size_t)kp * TK * a.H;
   if (ch.x == a.E) {
     const int ldk = a.S * a.I;
     const ChunkRows cr{ch.z, ch.y, nullptr, a.K};
     const uint8_t* wd = a.sdown + (size_t)j * kBlock * ldk;
     const float* sd = a.sdown_scale + (size_t)j * (ldk / kBlock);
     if (cr.n <= 16)
-      down_unit<1>(a, wd, sd, ldk, a.hq_s, a.hs_s, cr, j, a.d_s, ready, ring);
+      down_unit<1>(a, wd, sd, ldk, a.hq_s, a.hs_s, cr, j, kp, a.d_s, pd_s, ready, ring);
     else if (cr.n <= 32)
-      down_unit<2>(a, wd, sd, ldk, a.hq_s, a.hs_s, cr, j, a.d_s, ready, ring);
+      down_unit<2>(a, wd, sd, ldk, a.hq_s, a.hs_s, cr, j, kp, a.d_s, pd_s, ready, ring);
     else
-      down_unit<4>(a, wd, sd, ldk, a.hq_s, a.hs_s, cr, j, a.d_s, ready, ring);
+      down_unit<4>(a, wd, sd, ldk, a.hq_s, a.hs_s, cr, j, kp, a.d_s, pd_s, ready, ring);
   } else {
     const ChunkRows cr{ch.z, a.offsets[ch.x] + ch.y, a.perm, a.K};
     const size_t rowblk = (size_t)ch.x * nbH + j;
     const uint8_t* wd = a.down + rowblk * kBlock * a.I;
     const float* sd = a.down_scale + rowblk * nbI;
     if (cr.n <= 16)
-      down_unit<1>(a, wd, sd, a.I, a.hq_r, a.hs_r, cr, j, a.d_r, ready, ring);
+      down_unit<1>(a, wd, sd, a.I, a.hq_r, a.hs_r, cr, j, kp, a.d_r, pd_r, ready, ring);
     else if (cr.n <= 32)
-      down_unit<2>(a, wd, sd, a.I, a.hq_r, a.hs_r, cr, j, a.d_r, ready, ring);
+      down_unit<2>(a, wd, sd, a.I, a.hq_r, a.hs_r, cr, j, kp, a.d_r, pd_r, ready, ring);
     else
-      down_unit<4>(a, wd, sd, a.I, a.hq_r, a.hs_r, cr, j, a.d_r, ready, ring);
+      down_unit<4>(a, wd, sd, a.I, a.hq_r, a.hs_r, cr, j, kp, a.d_r, pd_r, ready, ring);
   }
 }
 
@@ -1300,8 +1313,60 @@ __device__ __forceinline__ void combine8(const uint16_t* __restrict__ d_r, const
   *reinterpret_cast<uint4*>(y + (size_t)t * H + h0) = o;
 }
 
+// The same combine when the down GEMMs were split over ks K parts: d = bf16(sum of the
+// fp32 parts in part order) for every slot row and for the shared row, then as combine8.
+__device__ __forceinline__ void combine8_parts(const float* __restrict__ p_r, const float* __restrict__ p_s, int ks,
+                                               const int* __restrict__ inv, const float* __restrict__ wts, int T,
+                                               int H, int K, int S, int t, int h0, uint16_t* __restrict__ y) {
+  const size_t TK = (size_t)T * K;
+  float acc[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
+  for (int s = 0; s < K; ++s) {
+    const int row = inv[t * K + s];
+    const float wv = wts[t * K + s];
+    float dv[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) dv[i] = 0.0f;
+    for (int kp = 0; kp < ks; ++kp) {
+      const float* src = p_r + ((size_t)kp * TK + row) * H + h0;
+      const f32x4 lo = *reinterpret_cast<const f32x4*>(src), hi = *reinterpret_cast<const f32x4*>(src + 4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        dv[i] = __fadd_rn(dv[i], lo[i]);
+        dv[4 + i] = __fadd_rn(dv[4 + i], hi[i]);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = __fadd_rn(acc[i], __fmul_rn(round_bf16(dv[i]), wv));
+  }
+  if (S > 0) {
+    float dv[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) dv[i] = 0.0f;
+    for (int kp = 0; kp < ks; ++kp) {
+      const float* src = p_s + ((size_t)kp * T + t) * H + h0;
+      const f32x4 lo = *reinterpret_cast<const f32x4*>(src), hi = *reinterpret_cast<const f32x4*>(src + 4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        dv[i] = __fadd_rn(dv[i], lo[i]);
+        dv[4 + i] = __fadd_rn(dv[4 + i], hi[i]);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = __fadd_rn(acc[i], round_bf16(dv[i]));
+  }
+  uint4 o;
+  o.x = f32_to_bf16_bits(acc[0]) | (f32_to_bf16_bits(acc[1]) << 16);
+  o.y = f32_to_bf16_bits(acc[2]) | (f32_to_bf16_bits(acc[3]) << 16);
+  o.z = f32_to_bf16_bits(acc[4]) | (f32_to_bf16_bits(acc[5]) << 16);
+  o.w = f32_to_bf16_bits(acc[6]) | (f32_to_bf16_bits(acc[7]) << 16);
+  *reinterpret_cast<uint4*>(y + (size_t)t * H + h0) = o;
+}
+
 // If a readiness wait of the expert kernel gave up, every element of y is NaN.
 __global__ __launch_bounds__(256) void k_combine(const uint16_t* __restrict__ d_r, const uint16_t* __restrict__ d_s,
+                                                 const float* __restrict__ p_r, const float* __restrict__ p_s, int ks,
                                                  const int* __restrict__ inv, const float* __restrict__ wts, int T,
                                                  int H, int K, int S, const int* __restrict__ meta,
                                                  uint16_t* __restrict__ y) {
@@ -1311,7 +1376,10 @@ __global__ __launch_bounds__(256) void k_combine(const uint16_t* __restrict__ d_
     *reinterpret_cast<uint4*>(y + (size_t)i * 8) = make_uint4(0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u);
     return;
   }
-  combine8(d_r, d_s, inv, wts, H, K, S, i / per_row, (i % per_row) * 8, y);
+  if (ks > 1)
+    combine8_parts(p_r, p_s, ks, inv, wts, T, H, K, S, i / per_row, (i % per_row) * 8, y);
+  else
+    combine8(d_r, d_s, inv, wts, H, K, S, i / per_row, (i % per_row) * 8, y);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -1376,7 +1444,7 @@ __global__ __launch_bounds__(256, 2) void k_experts(ExpertArgs args) {
       __syncthreads();
       if (threadIdx.x == 0) atomicAdd(&a.ready[a.dn_of_gu[u / nbI]], 1);
     } else {
-      const int v = u - total_gu, c = v / nbH;
+      const int v = u - total_gu, c = v / (nbH * a.dn.ks);
       const ReadyWait ready{&a.ready[c], a.dn.chunks[c].x == a.dn.E ? a.dn.S * nbI : nbI, &meta[kMetaError]};
       down_work(a.dn, v, ready, ring);
     }
@@ -1396,8 +1464,9 @@ inline size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
 struct Layout {
   size_t partial, xq, xs, counts, offsets, meta, perm, inv, gu, dn, dn_of_gu, ready, hq_r, hs_r, hq_s, hs_s, d_r, d_s,
-      spare, total;
+      p_r, p_s, spare, total;
   int nsplit;
+  int ks;  // K parts of each down unit
 };
 
 // Upper bound of list entries: every hit expert has at most ceil(rows/64) chunks, so the
@@ -1406,6 +1475,20 @@ struct Layout {
 size_t max_chunks(const megamoe_desc& d, int copies) {
   const size_t T = d.tokens, TK = (size_t)d.tokens * d.topk, E = d.experts;
   return (E < TK ? E : TK) + TK / kChunkRows + 1 + (size_t)copies * ((T + kChunkRows - 1) / kChunkRows);
+}
+
+// K parts of each down unit: when the routing yields fewer than two down units per
+// workgroup of a reference grid (2 per CU on 256 CUs), the down GEMMs are split along K
+// into 2 or 4 parts (dividing the K blocks), so the down phase keeps every workgroup busy.
+// Depends on the geometry only, so the numerics do not depend on the device.
+int down_splits(const megamoe_desc& d) {
+  const size_t nbH = d.hidden / kBlock, nkb = d.intermediate / kBlock;
+  const size_t hit = (size_t)(d.experts < (int64_t)d.tokens * d.topk ? d.experts : (int64_t)d.tokens * d.topk);
+  const size_t units = (hit + (d.shared_experts > 0 ? 1 : 0)) * nbH;
+  const size_t target = 2 * 512;
+  int ks = 1;
+  while (ks < 4 && units * ks < target && nkb % (2 * ks) == 0) ks *= 2;
+  return ks;
 }
 
 Layout make_layout(const megamoe_desc& d) {
@@ -1436,6 +1519,9 @@ Layout make_layout(const megamoe_desc& d) {
   L.hs_s = take(T * scale_ld((int)(S * I / kBlock)) * sizeof(float));
   L.d_r = take(T * K * H * 2);
   L.d_s = take(T * H * 2);
+  L.ks = down_splits(d);
+  L.p_r = take(L.ks > 1 ? L.ks * T * K * H * sizeof(float) : 0);
+  L.p_s = take(L.ks > 1 && S ? L.ks * T * H * sizeof(float) : 0);
   L.spare = take(16 * (H > I * (S > 1 ? S : 1) ? H : I * (S > 1 ? S : 1)));
   L.total = at;
   return L;
@@ -1587,7 +1673,7 @@ int forward_impl(const megamoe_desc* desc, const megamoe_tensors* t, hipStream_t
                 (int*)(ws + L.ready)};
   const int nbI = I / kBlock, nbH = H / kBlock;
   const size_t lds = ((size_t)E * (1 + (T + 31) / 32) + 32) * 4;
-  hipLaunchKernelGGL(k_permute, dim3(1), dim3(1024), lds, st, t->expert_ids, T, K, E, S, nbI, nbH, po);
+  hipLaunchKernelGGL(k_permute, dim3(1), dim3(1024), lds, st, t->expert_ids, T, K, E, S, nbI, nbH, L.ks, po);
   MEGAMOE_LAUNCH_CHECK();
   if (mark(3) != hipSuccess) return MEGAMOE_ERR_HIP;
 
@@ -1611,12 +1697,15 @@ int forward_impl(const megamoe_desc* desc, const megamoe_tensors* t, hipStream_t
   da.hq_r = ga.hq_r; da.hs_r = ga.hs_r; da.hq_s = ga.hq_s; da.hs_s = ga.hs_s;
   da.d_r = (uint16_t*)(ws + L.d_r); da.d_s = (uint16_t*)(ws + L.d_s);
   da.spare = ga.spare;
+  da.p_r = (float*)(ws + L.p_r);
+  da.p_s = (float*)(ws + L.p_s);
+  da.ks = L.ks;
   da.T = T; da.H = H; da.I = I; da.K = K; da.S = S; da.E = E;
   ea.dn_of_gu = po.dn_of_gu;
   ea.ready = po.ready;
   // As many workgroups as fit on the device at once, and no more than the most units the
   // routing can produce.
-  const size_t units_max = max_chunks(d, S) * (size_t)nbI + max_chunks(d, S > 0 ? 1 : 0) * (size_t)nbH;
+  const size_t units_max = max_chunks(d, S) * (size_t)nbI + max_chunks(d, S > 0 ? 1 : 0) * (size_t)nbH * L.ks;
   const size_t resident = (size_t)di.cus * di.experts_per_cu;
   const unsigned grid = (unsigned)(units_max < resident ? units_max : resident);
   hipLaunchKernelGGL(k_experts, dim3(grid), dim3(256), 0, st, ea);
@@ -1625,8 +1714,8 @@ int forward_impl(const megamoe_desc* desc, const megamoe_tensors* t, hipStream_t
 
   const int rows8 = T * (H / 8);
   hipLaunchKernelGGL(k_combine, dim3((rows8 + 255) / 256), dim3(256), 0, st, (const uint16_t*)da.d_r,
-                     (const uint16_t*)da.d_s, (const int*)po.inv, (const float*)t->expert_weights, T, H, K, S,
-                     (const int*)po.meta, (uint16_t*)t->y);
+                     (const uint16_t*)da.d_s, (const float*)da.p_r, (const float*)da.p_s, L.ks, (const int*)po.inv,
+                     (const float*)t->expert_weights, T, H, K, S, (const int*)po.meta, (uint16_t*)t->y);
   MEGAMOE_LAUNCH_CHECK();
   if (mark(5) != hipSuccess) return MEGAMOE_ERR_HIP;
   return MEGAMOE_OK;
