@@ -32,6 +32,7 @@
 
 #include "megamoe.h"
 
+
 namespace {
 
 constexpr int kBlock = 128;  // quantization block edge (weights 128x128, activations 1x128)
@@ -991,6 +992,14 @@ __device__ __forceinline__ void compute_stage(uint32_t slot, const LaneTile& lt,
 // wait and the activations (which another workgroup produces) after it, so the wait's
 // round trip overlaps the first weight loads.
 //
+// The stream starts at K block `rot` and wraps around (any rot in [0, nkb); callers derive
+// it from the unit index). Units that run at the same time then read different K blocks of
+// their weight rows: with every workgroup at the same K block, the addresses in flight
+// differ only in their high bits (multiples of the row length, 4 KiB for some models), and
+// the HBM channels serve them unevenly (about 6% slower on a Mixtral-shaped layer). The
+// fp32 sum over K blocks then runs in a rotated order; it depends on the work list only,
+// so results are still the same on every call.
+//
 // The wait for stage s: a wavefront's vector memory loads (to LDS or to registers)
 // complete in issue order, and the compiler's own counters do not cover the LDS that
 // global_load_lds writes. When stage s is consumed, each of stages s+1 .. s+D-1 has been
@@ -1004,9 +1013,14 @@ __device__ __forceinline__ void compute_stage(uint32_t slot, const LaneTile& lt,
 // land before any later load into the ring (issue order). The slot a stage overwrites was
 // read (ds_read, issued in program order before the overwriting load) one stage earlier.
 template <int RT, int NCT, int SG, int D>
-__device__ __forceinline__ void stream_gemm(const Operands<RT, NCT, SG>& op, int nkb, uint8_t* ring,
+__device__ __forceinline__ void stream_gemm(const Operands<RT, NCT, SG>& op, int nkb, int rot, uint8_t* ring,
                                             f32x4 (&acc)[RT][NCT],
                                             const ReadyWait& ready = ReadyWait{nullptr, 0, nullptr}) {
+  // K block i of the stream is block (i + rot) mod nkb of the operands.
+  auto phys = [nkb, rot](int kb) {
+    const int p = kb + rot;
+    return p >= nkb ? p - nkb : p;
+  };
   constexpr int kSlot = RT * kTileBytes;
   constexpr int kAfter = (D - 1) * (2 * RT + 3 * NCT);
   static_assert(D >= 2 && D * kSlot <= kRingWave, "LDS ring");
@@ -1018,14 +1032,14 @@ __device__ __forceinline__ void stream_gemm(const Operands<RT, NCT, SG>& op, int
     for (int c = 0; c < NCT; ++c) acc[r][c] = f32x4{0.f, 0.f, 0.f, 0.f};
   Stage<NCT, SG> st[D];
 #pragma unroll
-  for (int s = 0; s < D - 1; ++s) issue_a(ring + s * kSlot, op, lt, min(s, nkb - 1), s < nkb);
+  for (int s = 0; s < D - 1; ++s) issue_a(ring + s * kSlot, op, lt, phys(min(s, nkb - 1)), s < nkb);
   wait_ready(ready);
 #pragma unroll
-  for (int s = 0; s < D - 1; ++s) load_stage_b(st[s], op, min(s, nkb - 1));
+  for (int s = 0; s < D - 1; ++s) load_stage_b(st[s], op, phys(min(s, nkb - 1)));
   for (int kb0 = 0; kb0 < nkb; kb0 += D) {
 #pragma unroll
     for (int s = 0; s < D; ++s) {
-      const int kb = kb0 + s, kn = min(kb + D - 1, nkb - 1);
+      const int kb = kb0 + s, kn = phys(min(kb + D - 1, nkb - 1));
       load_stage_b(st[(s + D - 1) % D], op, kn);
       issue_a(ring + ((s + D - 1) % D) * kSlot, op, lt, kn, kb + D - 1 < nkb);
       wait_vmem<kAfter>();
@@ -1070,7 +1084,7 @@ struct GateUpArgs {
 template <int NCT>
 __device__ void gateup_unit(const GateUpArgs& a, const uint8_t* wg, const uint8_t* wu, const float* sg,
                             const float* su, const ChunkRows& cr, int jb, uint8_t* hq, float* hs, int ldh,
-                            float (*red)[64], uint8_t* ring) {
+                            int rot, float (*red)[64], uint8_t* ring) {
   const int lane = opaque_lane(), w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int kofs = 16 * (lane >> 4);
   const int H = a.H, nkb = H / kBlock, nbh = scale_ld(ldh / kBlock);
@@ -1093,7 +1107,7 @@ __device__ void gateup_unit(const GateUpArgs& a, const uint8_t* wg, const uint8_
     op.sx[c] = a.xs + (size_t)tok * nkb;
   }
   f32x4 acc[4][NCT];
-  stream_gemm<4, NCT, 2, 2>(op, nkb, ring, acc);
+  stream_gemm<4, NCT, 2, 2>(op, nkb, rot, ring, acc);
 
   // h = bf16(silu(fp32 bf16(g)) * fp32 bf16(u)) (frontier.py:184-186,337)
   float hv[NCT][2][4];
@@ -1140,6 +1154,7 @@ __device__ void gateup_work(const GateUpArgs& a, int u, float (*red)[64], uint8_
   const int nbI = a.I / kBlock, nkb = a.H / kBlock;
   const int4 ch = a.chunks[u / nbI];
   const int j = u % nbI, jb = ch.w + j;
+  const int rot = u % nkb;  // concurrent units start at different K blocks
   const uint8_t *wg, *wu;
   const float *sg, *su;
   uint8_t* hq;
@@ -1167,11 +1182,11 @@ __device__ void gateup_work(const GateUpArgs& a, int u, float (*red)[64], uint8_
     ldh = a.I;
   }
   if (cr.n <= 16)
-    gateup_unit<1>(a, wg, wu, sg, su, cr, jb, hq, hs, ldh, red, ring);
+    gateup_unit<1>(a, wg, wu, sg, su, cr, jb, hq, hs, ldh, rot, red, ring);
   else if (cr.n <= 32)
-    gateup_unit<2>(a, wg, wu, sg, su, cr, jb, hq, hs, ldh, red, ring);
+    gateup_unit<2>(a, wg, wu, sg, su, cr, jb, hq, hs, ldh, rot, red, ring);
   else
-    gateup_unit<4>(a, wg, wu, sg, su, cr, jb, hq, hs, ldh, red, ring);
+    gateup_unit<4>(a, wg, wu, sg, su, cr, jb, hq, hs, ldh, rot, red, ring);
 }
 
 struct DownArgs {
@@ -1196,7 +1211,7 @@ struct DownArgs {
 template <int NCT>
 __device__ void down_unit(const DownArgs& a, const uint8_t* wd, const float* sd, int ldk, const uint8_t* hq,
                           const float* hs, const ChunkRows& cr, int j, int kp, uint16_t* d, float* pd,
-                          const ReadyWait& ready, uint8_t* ring) {
+                          int rot, const ReadyWait& ready, uint8_t* ring) {
   const int lane = opaque_lane(), w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int kofs = 16 * (lane >> 4);
   const int nkb = ldk / kBlock, nkbp = nkb / a.ks, kb0 = kp * nkbp;
@@ -1213,7 +1228,7 @@ __device__ void down_unit(const DownArgs& a, const uint8_t* wd, const float* sd,
     op.sx[c] = hs + (size_t)(cr.row0 + r) * scale_ld(nkb) + kb0;
   }
   f32x4 acc[2][NCT];
-  stream_gemm<2, NCT, 1, NCT == 4 ? 3 : 4>(op, nkbp, ring, acc, ready);
+  stream_gemm<2, NCT, 1, NCT == 4 ? 3 : 4>(op, nkbp, rot, ring, acc, ready);
 #pragma unroll
   for (int c = 0; c < NCT; ++c) {
     const int r = 16 * c + (lane & 15);
@@ -1239,6 +1254,7 @@ __device__ void down_work(const DownArgs& a, int v, const ReadyWait& ready, uint
   const int nbH = a.H / kBlock, nbI = a.I / kBlock;
   const int4 ch = a.chunks[v / (nbH * a.ks)];
   const int rem = v % (nbH * a.ks), j = rem / a.ks, kp = rem % a.ks;
+  const int rot = v % (nbI / a.ks);  // concurrent units start at different K blocks
   const size_t TK = (size_t)a.T * a.K;
   float* pd_s = a.p_s + (size_t)kp * a.T * a.H;
   float* pd_r = a.p_r + (size_t)kp * TK * a.H;
@@ -1248,22 +1264,22 @@ __device__ void down_work(const DownArgs& a, int v, const ReadyWait& ready, uint
     const uint8_t* wd = a.sdown + (size_t)j * kBlock * ldk;
     const float* sd = a.sdown_scale + (size_t)j * (ldk / kBlock);
     if (cr.n <= 16)
-      down_unit<1>(a, wd, sd, ldk, a.hq_s, a.hs_s, cr, j, kp, a.d_s, pd_s, ready, ring);
+      down_unit<1>(a, wd, sd, ldk, a.hq_s, a.hs_s, cr, j, kp, a.d_s, pd_s, rot, ready, ring);
     else if (cr.n <= 32)
-      down_unit<2>(a, wd, sd, ldk, a.hq_s, a.hs_s, cr, j, kp, a.d_s, pd_s, ready, ring);
+      down_unit<2>(a, wd, sd, ldk, a.hq_s, a.hs_s, cr, j, kp, a.d_s, pd_s, rot, ready, ring);
     else
-      down_unit<4>(a, wd, sd, ldk, a.hq_s, a.hs_s, cr, j, kp, a.d_s, pd_s, ready, ring);
+      down_unit<4>(a, wd, sd, ldk, a.hq_s, a.hs_s, cr, j, kp, a.d_s, pd_s, rot, ready, ring);
   } else {
     const ChunkRows cr{ch.z, a.offsets[ch.x] + ch.y, a.perm, a.K};
     const size_t rowblk = (size_t)ch.x * nbH + j;
     const uint8_t* wd = a.down + rowblk * kBlock * a.I;
     const float* sd = a.down_scale + rowblk * nbI;
     if (cr.n <= 16)
-      down_unit<1>(a, wd, sd, a.I, a.hq_r, a.hs_r, cr, j, kp, a.d_r, pd_r, ready, ring);
+      down_unit<1>(a, wd, sd, a.I, a.hq_r, a.hs_r, cr, j, kp, a.d_r, pd_r, rot, ready, ring);
     else if (cr.n <= 32)
-      down_unit<2>(a, wd, sd, a.I, a.hq_r, a.hs_r, cr, j, kp, a.d_r, pd_r, ready, ring);
+      down_unit<2>(a, wd, sd, a.I, a.hq_r, a.hs_r, cr, j, kp, a.d_r, pd_r, rot, ready, ring);
     else
-      down_unit<4>(a, wd, sd, a.I, a.hq_r, a.hs_r, cr, j, kp, a.d_r, pd_r, ready, ring);
+      down_unit<4>(a, wd, sd, a.I, a.hq_r, a.hs_r, cr, j, kp, a.d_r, pd_r, rot, ready, ring);
   }
 }
 
@@ -1477,17 +1493,18 @@ size_t max_chunks(const megamoe_desc& d, int copies) {
   return (E < TK ? E : TK) + TK / kChunkRows + 1 + (size_t)copies * ((T + kChunkRows - 1) / kChunkRows);
 }
 
-// K parts of each down unit: when the routing yields fewer than two down units per
+// K parts of each down unit: when the routing can yield fewer than four down units per
 // workgroup of a reference grid (2 per CU on 256 CUs), the down GEMMs are split along K
-// into 2 or 4 parts (dividing the K blocks), so the down phase keeps every workgroup busy.
+// into 2, 4 or 8 parts (dividing the K blocks), so the down phase keeps every workgroup
+// busy and its last units, which set the kernel's tail, are short.
 // Depends on the geometry only, so the numerics do not depend on the device.
 int down_splits(const megamoe_desc& d) {
   const size_t nbH = d.hidden / kBlock, nkb = d.intermediate / kBlock;
   const size_t hit = (size_t)(d.experts < (int64_t)d.tokens * d.topk ? d.experts : (int64_t)d.tokens * d.topk);
   const size_t units = (hit + (d.shared_experts > 0 ? 1 : 0)) * nbH;
-  const size_t target = 2 * 512;
+  const size_t target = 4 * 512;
   int ks = 1;
-  while (ks < 4 && units * ks < target && nkb % (2 * ks) == 0) ks *= 2;
+  while (ks < 8 && units * ks < target && nkb % (2 * ks) == 0) ks *= 2;
   return ks;
 }
 
