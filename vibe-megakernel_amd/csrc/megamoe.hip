@@ -974,13 +974,28 @@ __device__ __forceinline__ void compute_stage(uint32_t slot, const LaneTile& lt,
   const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
   i32x8 at[RT];
   read_slot<RT>(at, slot + lt.rd0, slot + lt.rd1);
+  // The scales pass through an empty asm first, which keeps their products where the
+  // stage is consumed: hoisted next to the loads of a later stage, a product would need
+  // those loads to have landed, and the compiler, which does not take vmcnt to count them
+  // in order once LDS DMA is in flight, would wait for vmcnt 0 there, every stage.
+  float sw[SG], sx[NCT];
+#pragma unroll
+  for (int g = 0; g < SG; ++g) {
+    sw[g] = s.sw[g];
+    asm volatile("" : "+v"(sw[g]));
+  }
+#pragma unroll
+  for (int c = 0; c < NCT; ++c) {
+    sx[c] = s.sx[c];
+    asm volatile("" : "+v"(sx[c]));
+  }
 #pragma unroll
   for (int r = 0; r < RT; ++r) {
     const i32x8& a = at[r];
 #pragma unroll
     for (int c = 0; c < NCT; ++c) {
       const f32x4 p = mfma_e4m3(a, s.b[c], zero);
-      const float k = s.sw[r * SG / RT] * s.sx[c];
+      const float k = sw[r * SG / RT] * sx[c];
 #pragma unroll
       for (int v = 0; v < 4; ++v) acc[r][c][v] = __builtin_fmaf(p[v], k, acc[r][c][v]);
     }
