@@ -143,30 +143,34 @@ def bench_case(case, steps: int, warmup: int, want_cpu: bool, cpu_budget: float)
     torch.cuda.synchronize()
     _log(f"[bench] {case.id}: inputs ready; warmup")
 
+    # Warmup runs straight into the timed region: the distinct-expert count, which needs a
+    # host round trip, is taken from the warmup outputs after the timed loops (a few ms of
+    # idle device before timing measurably slows the first timed calls).
     outs = []
     for i in range(max(warmup, n_sets)):
         outs.append(layer(sets[i % n_sets]))
-    torch.cuda.synchronize()
-    hits = [len(torch.unique(o["expert_ids"])) for o in outs[:n_sets]]
-    hit = statistics.mean(hits)
 
     _log(f"[bench] {case.id}: timing {steps} steps")
     stream = torch.cuda.current_stream(dev)
+    # The timed region: K calls back to back between two events. An event recorded between
+    # calls costs a few us of device time per step, so the per-step distribution (p50, p95)
+    # comes from a second loop of K calls, each bracketed by its own pair of events.
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    per_step = []
     torch.cuda.synchronize()
     start.record(stream)
     for i in range(steps):
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
         layer(sets[i % n_sets])
-        e1.record(stream)
-        per_step.append((e0, e1))
     end.record(stream)
     torch.cuda.synchronize()
     total_ms = start.elapsed_time(end)
-    step_ms = [a.elapsed_time(b) for a, b in per_step]
     ms = total_ms / steps
+    per_step = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    for i, (e0, e1) in enumerate(per_step):
+        e0.record(stream)
+        layer(sets[i % n_sets])
+        e1.record(stream)
+    torch.cuda.synchronize()
+    step_ms = [a.elapsed_time(b) for a, b in per_step]
 
     # Per-stage device time over a second loop of the same K steps: the library records
     # events at its stage boundaries on the stream its kernels run on.
@@ -181,6 +185,7 @@ def bench_case(case, steps: int, warmup: int, want_cpu: bool, cpu_budget: float)
     torch.cuda.synchronize()
     stage = [[row[j].elapsed_time(row[j + 1]) for j in range(nev - 1)] for row in events]
     stage_ms = [statistics.mean(s[j] for s in stage) for j in range(nev - 1)]
+    hit = statistics.mean(len(torch.unique(o["expert_ids"])) for o in outs[:n_sets])
 
     bytes_step = C.algorithmic_bytes(case, 0) + (C.algorithmic_bytes(case, 1) - C.algorithmic_bytes(case, 0)) * hit
     kb = kernel_bytes(case, hit)
