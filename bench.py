@@ -113,7 +113,8 @@ def cpu_baseline(case, values_gpu, hit: int, budget_s: float) -> dict:
     while True:
         rows = list(range(sample))
         t0 = time.perf_counter()
-        out = layer.reference(case, cpu, tokens=rows)
+        reference = layer.block_reference if (case.norm != "none" or case.residual) else layer.reference
+        out = reference(case, cpu, tokens=rows)
         dt = time.perf_counter() - t0
         sampled = len(set(out["expert_ids"].flatten().tolist()))
         if dt * 2 > budget_s or sample * 2 > case.tokens:
@@ -122,7 +123,7 @@ def cpu_baseline(case, values_gpu, hit: int, budget_s: float) -> dict:
     s = case.shared_experts
     scale = (hit + s) / max(sampled + s, 1)
     return {"value": dt * scale * 1e6, "unit": "us/step", "cores": threads, "kind": "port",
-            "sample": (f"oracle.layer.reference on tokens 0..{sample - 1} of the timed inputs "
+            "sample": (f"oracle.layer.{reference.__name__} on tokens 0..{sample - 1} of the timed inputs "
                        f"({sampled} distinct experts{' + shared' if s else ''}, {dt:.2f} s), scaled by "
                        f"{hit + s}/{sampled + s} experts; torch {torch.__version__} CPU, {threads} threads, "
                        f"{platform.processor() or platform.machine()}")}

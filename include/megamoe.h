@@ -144,6 +144,35 @@ int megamoe_router_logits(const megamoe_desc* desc, const void* x, const float* 
 int megamoe_route(const megamoe_desc* desc, const float* logits, const float* bias, int64_t* expert_ids,
                   float* expert_weights, void* stream);
 
+/* The decoder-block steps either side of the layer (frontier.py:335,354):
+ *   normalized = rms(x, norm_weight, eps, weight_in_fp32)   common.py:13-21
+ *   y          = x + bf16(layer(normalized))                frontier.py:354 (residual = 1)
+ * norm_weight is bf16 [H] (the block's ln2 gamma, frontier.py:87); NULL skips the
+ * normalization (the layer reads x). eps is 1e-6 for DeepSeek and 1e-5 otherwise in the
+ * reference (frontier.py:258), which also applies the gamma in fp32 for DeepSeek only. */
+typedef struct megamoe_block {
+  const void* norm_weight; /* bf16 [H] or NULL */
+  float eps;               /* >= 0 */
+  int32_t weight_in_fp32;  /* 1: bf16(n * w); 0: bf16(bf16(n) * w) */
+  int32_t residual;        /* 1: y = bf16(x + bf16(layer output)); 0: y = layer output */
+} megamoe_block;
+
+/* megamoe_forward for the block: RMSNorm of x (a sixth kernel, before the router; the
+ * router and the experts read the normalized rows), the layer, and the residual add in the
+ * combine. x is the block input (the residual stream). `events` is NULL or
+ * events[0..5] as for megamoe_forward_events (the normalization counts to the router
+ * stage). Workspace: megamoe_workspace_bytes(). Replaces frontier.py:335-354 from the ln2
+ * normalization to the residual add. */
+int megamoe_block_forward(const megamoe_desc* desc, const megamoe_tensors* t, const megamoe_block* block,
+                          void* stream, void* const* events);
+
+/* RMSNorm of bf16 rows [rows, cols] with a bf16 gamma [cols] into bf16 out [rows, cols]
+ * (cols a multiple of 8; rows 16-byte aligned): s = sum of x^2 in fp64, r = 1/sqrt(fp32(s/cols)
+ * + eps) with correctly rounded fp32 operations, out = bf16(x*r*w) (weight_in_fp32) or
+ * bf16(bf16(x*r)*w). Replaces common.rms (megabench/tasks/common.py:13-21). */
+int megamoe_rms_norm(int32_t rows, int32_t cols, const void* x, const void* weight, float eps,
+                     int32_t weight_in_fp32, void* out, void* stream);
+
 /* Dynamic E4M3 quantization of bf16 rows [rows, cols] with one fp32 scale
  * per row per 128 columns (the last block may be partial; padding counts as
  * zero): q e4m3fn [rows, cols], scales fp32 [rows, ceil(cols/128)].
@@ -155,7 +184,7 @@ int megamoe_quantize_rows(int32_t rows, int32_t cols, const void* x, uint8_t* q,
 /* Text for a status code (static storage). */
 const char* megamoe_status_string(int status);
 
-/* ABI version of this library: 1. */
+/* ABI version of this library: 2 (1 plus megamoe_block_forward and megamoe_rms_norm). */
 int megamoe_abi_version(void);
 
 #ifdef __cplusplus

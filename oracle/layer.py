@@ -33,6 +33,9 @@ here, and the graded bars (band rule, max-rel, cosine) do not need them.
 
 from __future__ import annotations
 
+import math
+
+import numpy as np
 import torch
 import torch.nn.functional as F
 
@@ -112,3 +115,53 @@ def reference(case, values: dict, **kw) -> dict:
 def oracle(case, values: dict, **kw) -> dict:
     """FP32 oracle: the same graph without BF16 rounding (megabench/tasks/oracle.py:51-53)."""
     return moe_layer(case, values, widen=True, **kw)
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float, weight_in_fp32: bool, *,
+             widen: bool = False) -> torch.Tensor:
+    """common.rms (megabench/tasks/common.py:13-21) for bf16 rows [T, H] and a bf16 gamma [H].
+
+    The sum of squares is taken exactly (each square of a bf16 value is exact in fp64;
+    ``math.fsum`` rounds the sum once); then, each operation rounded in fp32:
+    m = fp32(s / H), r = 1 / sqrt(m + eps), n = fp32(x) * r, and
+    out = bf16(n * w) (weight_in_fp32, the DeepSeek form) or bf16(bf16(n) * w).
+    The reference takes the fp32 mean in torch's summation order and torch.rsqrt; the
+    two differ from this by an ulp of r at most. ``widen`` drops the bf16 roundings (the
+    FP32 oracle of megabench/tasks/oracle.py) and returns fp32.
+    """
+    xf = x.cpu().float().numpy()
+    H = xf.shape[1]
+    s = np.array([math.fsum((row.astype(np.float64) ** 2).tolist()) for row in xf], dtype=np.float64)
+    m = (s / H).astype(np.float32)
+    r = (np.float32(1.0) / np.sqrt((m + np.float32(eps)).astype(np.float32))).astype(np.float32)
+    n = (xf * r[:, None]).astype(np.float32)
+    w = weight.cpu().float().numpy()
+    if widen:
+        return torch.from_numpy(n * w)
+    if not weight_in_fp32:
+        n = torch.from_numpy(n).to(torch.bfloat16).float().numpy()
+    return torch.from_numpy((n * w).astype(np.float32)).to(torch.bfloat16)
+
+
+@torch.no_grad()
+def block(case, values: dict, *, widen: bool = False, tokens=None) -> dict:
+    """The decoder-block form (frontier.py:335-354): y = x + bf16(layer(rms(x, ln2))) when
+    the case sets ``norm`` and ``residual``; ``widen`` is the FP32 oracle of the same graph."""
+    x = values["x"].cpu()
+    rows = list(range(x.shape[0])) if tokens is None else list(tokens)
+    inner = dict(values)
+    if case.norm != "none":
+        inner["x"] = rms_norm(x, values["ln2"], case.norm_eps, case.norm == "fp32_weight", widen=widen)
+    out = moe_layer(case, inner, widen=widen, tokens=tokens)
+    if case.residual:
+        res = x[rows].float() + out["y"].float()
+        out["y"] = res if widen else res.to(torch.bfloat16)
+    return out
+
+
+def block_reference(case, values: dict, **kw) -> dict:
+    return block(case, values, widen=False, **kw)
+
+
+def block_oracle(case, values: dict, **kw) -> dict:
+    return block(case, values, widen=True, **kw)

@@ -20,7 +20,8 @@ STAGES = ("router", "select_quant", "permute", "experts", "combine")
 # Every symbol the header declares; tests check the library exports them all.
 SYMBOLS = ("megamoe_workspace_bytes", "megamoe_forward", "megamoe_forward_events", "megamoe_forward_timed",
            "megamoe_router_logits", "megamoe_route", "megamoe_quantize_rows", "megamoe_status_string",
-           "megamoe_abi_version")
+           "megamoe_abi_version", "megamoe_block_forward", "megamoe_rms_norm")
+ABI_VERSION = 2
 
 
 class Desc(ctypes.Structure):
@@ -38,6 +39,11 @@ _TENSOR_FIELDS = ("x", "router", "router_bias", "gate", "gate_scale", "up", "up_
 
 class Tensors(ctypes.Structure):
     _fields_ = [(name, ctypes.c_void_p) for name in _TENSOR_FIELDS] + [("workspace_bytes", ctypes.c_size_t)]
+
+
+class Block(ctypes.Structure):
+    _fields_ = [("norm_weight", ctypes.c_void_p), ("eps", ctypes.c_float), ("weight_in_fp32", ctypes.c_int32),
+                ("residual", ctypes.c_int32)]
 
 
 class MegaMoEError(RuntimeError):
@@ -66,6 +72,9 @@ def load() -> ctypes.CDLL:
     lib.megamoe_route.argtypes = [P(Desc), c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]
     lib.megamoe_quantize_rows.argtypes = [ctypes.c_int32, ctypes.c_int32, c_void_p, c_void_p, c_void_p,
                                           ctypes.c_int32, c_void_p]
+    lib.megamoe_block_forward.argtypes = [P(Desc), P(Tensors), P(Block), c_void_p, P(c_void_p)]
+    lib.megamoe_rms_norm.argtypes = [ctypes.c_int32, ctypes.c_int32, c_void_p, c_void_p, ctypes.c_float,
+                                     ctypes.c_int32, c_void_p, c_void_p]
     lib.megamoe_status_string.argtypes = [c_int]
     lib.megamoe_status_string.restype = ctypes.c_char_p
     lib.megamoe_abi_version.argtypes = []

@@ -27,6 +27,9 @@ from dataclasses import asdict, dataclass, field, replace
 
 FAMILY = "moe_fp8_layer"
 ROUTERS = ("softmax", "sigmoid")
+# RMSNorm before the layer (the block form): none, gamma applied in fp32 before the one
+# bf16 rounding (DeepSeek), or to the rounded activation (common.py:13-21).
+NORMS = ("none", "fp32_weight", "bf16_weight")
 BIASES = ("none", "normal", "zipf")
 GATES = ("band",)
 
@@ -67,6 +70,11 @@ class Case:
     power_of_two: bool = False
     weight_std: float = 0.02
     router_std: float = 0.02
+    # The block form (frontier.py:335,354): RMSNorm of x with a bf16 gamma ~ 1 + N(0, 0.1)
+    # (frontier.py:87) before the layer, and the residual add after it.
+    norm: str = "none"
+    norm_eps: float = 1e-6
+    residual: bool = False
 
     def __post_init__(self) -> None:
         if not self.id or self.family != FAMILY or not self.model or not self.phase:
@@ -85,6 +93,8 @@ class Case:
             raise ValueError(f"invalid priority or gate in {self.id}")
         if self.router not in ROUTERS or self.bias not in BIASES:
             raise ValueError(f"invalid routing rule in {self.id}")
+        if self.norm not in NORMS or not self.norm_eps >= 0:
+            raise ValueError(f"invalid normalization in {self.id}")
         if self.router == "softmax" and self.bias != "none":
             raise ValueError(f"{self.id}: softmax routing takes no correction bias")
         groups, top = self.groups, self.top_groups
@@ -165,9 +175,20 @@ CASES: tuple[Case, ...] = (
 
 HEADLINE = "moe-fp8-deepseek-v3-t64"
 
+# Block forms (the next step outward from the layer): the DeepSeek-V3 layer with its ln2
+# RMSNorm (gamma in fp32, eps 1e-6) before it and the residual add after it, six launches.
+BLOCK_CASES: tuple[Case, ...] = (
+    replace(next(c for c in CASES if c.id == HEADLINE), id=HEADLINE + "-block", norm="fp32_weight",
+            norm_eps=1e-6, residual=True, max_gpu_launches=6,
+            note="decoder-block form: rms(x, ln2) -> layer -> x + bf16(out) (frontier.py:335-354)"),
+    replace(next(c for c in CASES if c.id == "moe-fp8-qwen3-30b-a3b-t32"), id="moe-fp8-qwen3-30b-a3b-t32-block",
+            norm="bf16_weight", norm_eps=1e-5, residual=True, max_gpu_launches=6,
+            note="decoder-block form with the Llama-style RMSNorm (gamma on the rounded activation)"),
+)
+
 
 def case(case_id: str) -> Case:
-    for c in CASES:
+    for c in CASES + BLOCK_CASES:
         if c.id == case_id:
             return c
     raise KeyError(case_id)
@@ -195,7 +216,7 @@ def development(c: Case, **params) -> Case:
 def algorithmic_bytes(c: Case, hit_experts: int) -> int:
     """HBM bytes one step must move: weights of the hit experts and the shared expert
     (E4M3 payload + fp32 128x128 scales), the fp32 router and bias, x and y in bf16,
-    ids (int64) and weights (fp32)."""
+    ids (int64) and weights (fp32); in the block form also the bf16 RMSNorm gamma."""
     T, H, E, K, I, S = c.tokens, c.hidden, c.experts, c.topk, c.intermediate, c.shared_experts
     bh, bi = math.ceil(H / 128), math.ceil(I / 128)
     per_expert = 3 * I * H + 4 * (2 * bi * bh + bh * bi)
@@ -205,7 +226,8 @@ def algorithmic_bytes(c: Case, hit_experts: int) -> int:
         bsi = math.ceil(si / 128)
         shared = 3 * si * H + 4 * (2 * bsi * bh + bh * bsi)
     bias = 4 * E if c.router == "sigmoid" else 0
-    return hit_experts * per_expert + shared + 4 * E * H + bias + 2 * T * H + 2 * T * H + 12 * T * K
+    gamma = 2 * H if c.norm != "none" else 0  # the block's ln2 (x is read once either way)
+    return hit_experts * per_expert + shared + 4 * E * H + bias + gamma + 2 * T * H + 2 * T * H + 12 * T * K
 
 
 def algorithmic_flops(c: Case) -> int:

@@ -18,7 +18,11 @@
 //                             requantization of h fused into gate/up; a down unit starts
 //                             as soon as the gate/up units of its rows are done
 //   k_combine                 slot-order fp32 sum of bf16(d)*w plus the shared expert,
-//                             rounded once to bf16
+//                             rounded once to bf16 (and, in the block form, the residual add)
+//
+// The block form (megamoe_block_forward) adds the steps either side of the layer in the
+// reference's decoder block (frontier.py:335,354): k_norm, the RMSNorm of x that the router
+// and the experts read, as a sixth launch before k_router, and the residual add in k_combine.
 //
 // Reference math (all eager PyTorch in the reference): megabench/tasks/frontier.py:180-186
 // (linear), :229-242 (route), :335-354 (MoE block); megabench/tasks/quantization.py:57-131
@@ -141,6 +145,107 @@ __global__ __launch_bounds__(256) void k_quant_rows(const uint16_t* __restrict__
     if (c < cols) dst[c] = (uint8_t)f32_to_e4m3(clamp448(v0 / s));
     if (c + 1 < cols) dst[c + 1] = (uint8_t)f32_to_e4m3(clamp448(v1 / s));
     if (lane == 0) scales[(size_t)r * nb + cb] = s;
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// RMSNorm of bf16 rows (megabench/tasks/common.py:13-21, weight_in_fp32 as there), one
+// workgroup per row:
+//   s = sum of x^2 (fp64: each square of a bf16 value is exact, and the sum of a row's
+//       squares stays exact unless its magnitudes span more than 2^37),
+//   m = fp32(s / H), r = 1 / sqrt(m + eps) (fp32, each operation correctly rounded),
+//   n = fp32(x) * r, out = bf16(n * w) (weight_in_fp32) or bf16(bf16(n) * w).
+// The reference's fp32 mean and rsqrt round in torch's order; the band absorbs the
+// difference (an ulp of r at most moves a bf16 output by one ulp).
+// ---------------------------------------------------------------------------------------
+
+constexpr int kNormChunks = 8;                     // 4-element chunks per thread and pass
+constexpr int kNormPass = 256 * 4 * kNormChunks;  // elements of a row per pass (8192)
+
+struct NormChunks {
+  uint2 x[kNormChunks], w[kNormChunks];
+};
+
+// Chunk k of a pass is elements 4 * (tid + 256 k) .. +3 from `base`; past H reads nothing.
+__device__ __forceinline__ void norm_load(NormChunks& c, const uint16_t* xr, const uint16_t* w, int base, int H,
+                                          int tid) {
+#pragma unroll
+  for (int k = 0; k < kNormChunks; ++k) {
+    const int e = base + 4 * (tid + 256 * k);
+    const bool in = e < H;
+    c.x[k] = in ? *reinterpret_cast<const uint2*>(xr + e) : make_uint2(0u, 0u);
+    c.w[k] = in ? *reinterpret_cast<const uint2*>(w + e) : make_uint2(0u, 0u);
+  }
+}
+
+__device__ __forceinline__ double norm_squares(const NormChunks& c) {
+  double s = 0.0;
+#pragma unroll
+  for (int k = 0; k < kNormChunks; ++k) {
+    const uint32_t q[2] = {c.x[k].x, c.x[k].y};
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const double a = bf16_bits_to_f32(q[i] & 0xffffu), b = bf16_bits_to_f32(q[i] >> 16);
+      s += a * a;
+      s += b * b;
+    }
+  }
+  return s;
+}
+
+__device__ __forceinline__ void norm_store(const NormChunks& c, uint16_t* orow, int base, int H, int tid, float r,
+                                           int weight_in_fp32) {
+#pragma unroll
+  for (int k = 0; k < kNormChunks; ++k) {
+    const int e = base + 4 * (tid + 256 * k);
+    const uint32_t q[2] = {c.x[k].x, c.x[k].y}, gw[2] = {c.w[k].x, c.w[k].y};
+    uint32_t o[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      float n0 = __fmul_rn(bf16_bits_to_f32(q[i] & 0xffffu), r), n1 = __fmul_rn(bf16_bits_to_f32(q[i] >> 16), r);
+      if (!weight_in_fp32) {
+        n0 = round_bf16(n0);
+        n1 = round_bf16(n1);
+      }
+      const float w0 = bf16_bits_to_f32(gw[i] & 0xffffu), w1 = bf16_bits_to_f32(gw[i] >> 16);
+      o[i] = f32_to_bf16_bits(__fmul_rn(n0, w0)) | (f32_to_bf16_bits(__fmul_rn(n1, w1)) << 16);
+    }
+    if (e < H) *reinterpret_cast<uint2*>(orow + e) = make_uint2(o[0], o[1]);
+  }
+}
+
+// Every thread issues the loads of its chunks of x and gamma at once; a row of up to
+// kNormPass elements stays in registers from the sum of squares to the output (longer rows
+// reload their later passes).
+__global__ __launch_bounds__(256) void k_norm(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+                                              int rows, int H, float eps, int weight_in_fp32,
+                                              uint16_t* __restrict__ out) {
+  __shared__ double part[4];
+  const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const uint16_t* xr = x + (size_t)row * H;
+  uint16_t* orow = out + (size_t)row * H;
+  NormChunks first;
+  norm_load(first, xr, w, 0, H, tid);
+  double s = norm_squares(first);
+  for (int base = kNormPass; base < H; base += kNormPass) {
+    NormChunks more;
+    norm_load(more, xr, w, base, H, tid);
+    s += norm_squares(more);
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
+  if (lane == 0) part[wv] = s;
+  __syncthreads();
+  s = (part[0] + part[1]) + (part[2] + part[3]);
+  const float m = (float)(s / (double)H);
+  // sqrtf and / are correctly rounded in HIP device code by default
+  // (-fhip-fp32-correctly-rounded-divide-sqrt); __fsqrt_rn is the ~1 ulp hardware sqrt.
+  const float r = 1.0f / __builtin_sqrtf(__fadd_rn(m, eps));
+  norm_store(first, orow, 0, H, tid, r, weight_in_fp32);
+  for (int base = kNormPass; base < H; base += kNormPass) {
+    NormChunks more;
+    norm_load(more, xr, w, base, H, tid);
+    norm_store(more, orow, base, H, tid, r, weight_in_fp32);
   }
 }
 
@@ -1302,8 +1407,7 @@ __device__ void down_work(const DownArgs& a, int v, const ReadyWait& ready, uint
 //                          rounded) + fp32(shared[t]) )          frontier.py:349-354
 __device__ __forceinline__ void combine8(const uint16_t* __restrict__ d_r, const uint16_t* __restrict__ d_s,
                                          const int* __restrict__ inv, const float* __restrict__ wts, int H, int K,
-                                         int S, int t, int h0, uint16_t* __restrict__ y) {
-  float acc[8];
+                                         int S, int t, int h0, float (&acc)[8]) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
   for (int s0 = 0; s0 < K; s0 += 8) {  // eight slots' loads in flight at a time
@@ -1336,21 +1440,14 @@ __device__ __forceinline__ void combine8(const uint16_t* __restrict__ d_r, const
       acc[2 * i + 1] = __fadd_rn(acc[2 * i + 1], bf16_bits_to_f32(q[i] >> 16));
     }
   }
-  uint4 o;
-  o.x = f32_to_bf16_bits(acc[0]) | (f32_to_bf16_bits(acc[1]) << 16);
-  o.y = f32_to_bf16_bits(acc[2]) | (f32_to_bf16_bits(acc[3]) << 16);
-  o.z = f32_to_bf16_bits(acc[4]) | (f32_to_bf16_bits(acc[5]) << 16);
-  o.w = f32_to_bf16_bits(acc[6]) | (f32_to_bf16_bits(acc[7]) << 16);
-  *reinterpret_cast<uint4*>(y + (size_t)t * H + h0) = o;
 }
 
 // The same combine when the down GEMMs were split over ks K parts: d = bf16(sum of the
 // fp32 parts in part order) for every slot row and for the shared row, then as combine8.
 __device__ __forceinline__ void combine8_parts(const float* __restrict__ p_r, const float* __restrict__ p_s, int ks,
                                                const int* __restrict__ inv, const float* __restrict__ wts, int T,
-                                               int H, int K, int S, int t, int h0, uint16_t* __restrict__ y) {
+                                               int H, int K, int S, int t, int h0, float (&acc)[8]) {
   const size_t TK = (size_t)T * K;
-  float acc[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
   for (int s = 0; s < K; ++s) {
@@ -1387,30 +1484,42 @@ __device__ __forceinline__ void combine8_parts(const float* __restrict__ p_r, co
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[i] = __fadd_rn(acc[i], round_bf16(dv[i]));
   }
-  uint4 o;
-  o.x = f32_to_bf16_bits(acc[0]) | (f32_to_bf16_bits(acc[1]) << 16);
-  o.y = f32_to_bf16_bits(acc[2]) | (f32_to_bf16_bits(acc[3]) << 16);
-  o.z = f32_to_bf16_bits(acc[4]) | (f32_to_bf16_bits(acc[5]) << 16);
-  o.w = f32_to_bf16_bits(acc[6]) | (f32_to_bf16_bits(acc[7]) << 16);
-  *reinterpret_cast<uint4*>(y + (size_t)t * H + h0) = o;
 }
 
-// If a readiness wait of the expert kernel gave up, every element of y is NaN.
+// If a readiness wait of the expert kernel gave up, every element of y is NaN. With a
+// residual (the block form), y = bf16(residual + bf16(layer output)) (frontier.py:354).
 __global__ __launch_bounds__(256) void k_combine(const uint16_t* __restrict__ d_r, const uint16_t* __restrict__ d_s,
                                                  const float* __restrict__ p_r, const float* __restrict__ p_s, int ks,
                                                  const int* __restrict__ inv, const float* __restrict__ wts, int T,
                                                  int H, int K, int S, const int* __restrict__ meta,
-                                                 uint16_t* __restrict__ y) {
+                                                 const uint16_t* __restrict__ residual, uint16_t* __restrict__ y) {
   const int i = blockIdx.x * 256 + threadIdx.x, per_row = H / 8;
   if (i >= T * per_row) return;
   if (meta[kMetaError]) {
     *reinterpret_cast<uint4*>(y + (size_t)i * 8) = make_uint4(0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u);
     return;
   }
+  const int t = i / per_row, h0 = (i % per_row) * 8;
+  float acc[8];
   if (ks > 1)
-    combine8_parts(p_r, p_s, ks, inv, wts, T, H, K, S, i / per_row, (i % per_row) * 8, y);
+    combine8_parts(p_r, p_s, ks, inv, wts, T, H, K, S, t, h0, acc);
   else
-    combine8(d_r, d_s, inv, wts, H, K, S, i / per_row, (i % per_row) * 8, y);
+    combine8(d_r, d_s, inv, wts, H, K, S, t, h0, acc);
+  uint32_t o[4];
+  if (residual) {
+    const uint4 v = *reinterpret_cast<const uint4*>(residual + (size_t)t * H + h0);
+    const uint32_t q[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float lo = __fadd_rn(bf16_bits_to_f32(q[j] & 0xffffu), round_bf16(acc[2 * j]));
+      const float hi = __fadd_rn(bf16_bits_to_f32(q[j] >> 16), round_bf16(acc[2 * j + 1]));
+      o[j] = f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o[j] = f32_to_bf16_bits(acc[2 * j]) | (f32_to_bf16_bits(acc[2 * j + 1]) << 16);
+  }
+  *reinterpret_cast<uint4*>(y + (size_t)t * H + h0) = make_uint4(o[0], o[1], o[2], o[3]);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -1494,7 +1603,7 @@ constexpr size_t kAlign = 256;
 inline size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
 struct Layout {
-  size_t partial, xq, xs, counts, offsets, meta, perm, inv, gu, dn, dn_of_gu, ready, hq_r, hs_r, hq_s, hs_s, d_r, d_s,
+  size_t xn, partial, xq, xs, counts, offsets, meta, perm, inv, gu, dn, dn_of_gu, ready, hq_r, hs_r, hq_s, hs_s, d_r, d_s,
       p_r, p_s, spare, total;
   int nsplit;
   int ks;  // K parts of each down unit
@@ -1533,6 +1642,7 @@ Layout make_layout(const megamoe_desc& d) {
     at += align_up(bytes > 0 ? bytes : 1);
     return o;
   };
+  L.xn = take(T * H * 2);  // normalized x of the block form
   L.partial = take((size_t)L.nsplit * T * E * sizeof(double));
   L.xq = take(T * H);
   L.xs = take(T * (H / kBlock) * sizeof(float));
@@ -1666,7 +1776,18 @@ int launch_select(const megamoe_desc& d, const double* partial, int nsplit, cons
   return MEGAMOE_OK;
 }
 
-int forward_impl(const megamoe_desc* desc, const megamoe_tensors* t, hipStream_t st, hipEvent_t* ev) {
+int launch_norm(int rows, int cols, const void* x, const void* w, float eps, int weight_in_fp32, void* out,
+                hipStream_t st) {
+  hipLaunchKernelGGL(k_norm, dim3(rows), dim3(256), 0, st,
+                     (const uint16_t*)x, (const uint16_t*)w, rows, cols, eps, weight_in_fp32, (uint16_t*)out);
+  MEGAMOE_LAUNCH_CHECK();
+  return MEGAMOE_OK;
+}
+
+// The layer; with `blk`, the block form: RMSNorm of x before the router (the layer then
+// reads the normalized rows) and the residual add in the combine.
+int forward_impl(const megamoe_desc* desc, const megamoe_tensors* t, hipStream_t st, hipEvent_t* ev,
+                 const megamoe_block* blk = nullptr) {
   int rc = validate(desc);
   if (rc) return rc;
   if (!t) return MEGAMOE_ERR_INVALID_ARGUMENT;
@@ -1692,11 +1813,16 @@ int forward_impl(const megamoe_desc* desc, const megamoe_tensors* t, hipStream_t
   const int T = d.tokens, H = d.hidden, E = d.experts, K = d.topk, I = d.intermediate, S = d.shared_experts;
 
   if (mark(0) != hipSuccess) return MEGAMOE_ERR_HIP;
-  if ((rc = launch_router(d, L, t->x, t->router, ws, st))) return rc;
+  const void* x = t->x;  // the rows the layer reads
+  if (blk && blk->norm_weight) {
+    if ((rc = launch_norm(T, H, t->x, blk->norm_weight, blk->eps, blk->weight_in_fp32, ws + L.xn, st))) return rc;
+    x = ws + L.xn;
+  }
+  if ((rc = launch_router(d, L, x, t->router, ws, st))) return rc;
   if (mark(1) != hipSuccess) return MEGAMOE_ERR_HIP;
 
   if ((rc = launch_select(d, (const double*)(ws + L.partial), L.nsplit, nullptr, t->router_bias, t->expert_ids,
-                          t->expert_weights, t->x, (uint8_t*)(ws + L.xq), (float*)(ws + L.xs), st)))
+                          t->expert_weights, x, (uint8_t*)(ws + L.xq), (float*)(ws + L.xs), st)))
     return rc;
   if (mark(2) != hipSuccess) return MEGAMOE_ERR_HIP;
 
@@ -1747,7 +1873,8 @@ int forward_impl(const megamoe_desc* desc, const megamoe_tensors* t, hipStream_t
   const int rows8 = T * (H / 8);
   hipLaunchKernelGGL(k_combine, dim3((rows8 + 255) / 256), dim3(256), 0, st, (const uint16_t*)da.d_r,
                      (const uint16_t*)da.d_s, (const float*)da.p_r, (const float*)da.p_s, L.ks, (const int*)po.inv,
-                     (const float*)t->expert_weights, T, H, K, S, (const int*)po.meta, (uint16_t*)t->y);
+                     (const float*)t->expert_weights, T, H, K, S, (const int*)po.meta,
+                     (const uint16_t*)(blk && blk->residual ? t->x : nullptr), (uint16_t*)t->y);
   MEGAMOE_LAUNCH_CHECK();
   if (mark(5) != hipSuccess) return MEGAMOE_ERR_HIP;
   return MEGAMOE_OK;
@@ -1757,7 +1884,7 @@ int forward_impl(const megamoe_desc* desc, const megamoe_tensors* t, hipStream_t
 
 extern "C" {
 
-int megamoe_abi_version(void) { return 1; }
+int megamoe_abi_version(void) { return 2; }
 
 const char* megamoe_status_string(int status) {
   switch (status) {
@@ -1828,6 +1955,29 @@ int megamoe_route(const megamoe_desc* desc, const float* logits, const float* bi
   if (!logits || !expert_ids || !expert_weights) return MEGAMOE_ERR_INVALID_ARGUMENT;
   return launch_select(*desc, nullptr, 0, logits, bias, expert_ids, expert_weights, nullptr, nullptr, nullptr,
                        (hipStream_t)stream);
+}
+
+int megamoe_block_forward(const megamoe_desc* desc, const megamoe_tensors* t, const megamoe_block* block,
+                          void* stream, void* const* events) {
+  if (!block) return MEGAMOE_ERR_INVALID_ARGUMENT;
+  if (!(block->eps >= 0.0f)) return MEGAMOE_ERR_INVALID_ARGUMENT;
+  hipEvent_t ev[kStages + 1];
+  if (events) {
+    for (int i = 0; i < kStages + 1; ++i) {
+      if (!events[i]) return MEGAMOE_ERR_INVALID_ARGUMENT;
+      ev[i] = (hipEvent_t)events[i];
+    }
+  }
+  return forward_impl(desc, t, (hipStream_t)stream, events ? ev : nullptr, block);
+}
+
+int megamoe_rms_norm(int32_t rows, int32_t cols, const void* x, const void* weight, float eps,
+                     int32_t weight_in_fp32, void* out, void* stream) {
+  if (rows < 0 || cols < 0 || !(eps >= 0.0f)) return MEGAMOE_ERR_INVALID_ARGUMENT;
+  if (cols % 8) return MEGAMOE_ERR_SHAPE;
+  if (rows == 0 || cols == 0) return MEGAMOE_OK;
+  if (!x || !weight || !out) return MEGAMOE_ERR_INVALID_ARGUMENT;
+  return launch_norm(rows, cols, x, weight, eps, weight_in_fp32, out, (hipStream_t)stream);
 }
 
 int megamoe_quantize_rows(int32_t rows, int32_t cols, const void* x, uint8_t* q, float* scales, int32_t pow2,

@@ -7,6 +7,10 @@ case's input tensors on the GPU, never mutates them, allocates its outputs and
 returns ``{"y", "expert_ids", "expert_weights"}`` with the dtypes and shapes of
 the reference outputs. All work is issued on torch's current stream through
 the C ABI of libmegamoe.so; there is no other code path.
+
+A case in the block form (``norm``/``residual`` set) takes ``x`` as the block input
+and ``ln2`` (bf16 [H]) as the RMSNorm gamma, and returns y = x + bf16(layer(rms(x)))
+(frontier.py:335-354) through megamoe_block_forward.
 """
 
 from __future__ import annotations
@@ -56,6 +60,7 @@ class MoELayer:
                    f"{case.id}: workspace size")
         self.workspace_bytes = int(size.value)
         self._workspace: dict[torch.device, torch.Tensor] = {}
+        self.block = None if case.norm == "none" and not case.residual else (case.norm, case.residual)
 
     def workspace(self, device: torch.device) -> torch.Tensor:
         ws = self._workspace.get(device)
@@ -79,6 +84,8 @@ class MoELayer:
         _expect(inputs["router"], "router", f32, (E, H), device)
         if c.bias != "none":
             _expect(inputs["router_bias"], "router_bias", f32, (E,), device)
+        if c.norm != "none":
+            _expect(inputs.get("ln2"), "ln2", torch.bfloat16, (H,), device)
         _expect(inputs["gate"], "gate", f8, (E, I, H), device)
         _expect(inputs["gate_scale"], "gate_scale", f32, (E, bi, bh), device)
         _expect(inputs["up"], "up", f8, (E, I, H), device)
@@ -113,6 +120,17 @@ class MoELayer:
                                workspace_bytes=self.workspace_bytes)
         stream = ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
         with torch.cuda.device(device):
+            if self.block is not None:
+                if timed:
+                    raise ValueError("timed() covers the layer form; use record() for the block form")
+                blk = _lib.Block(norm_weight=inputs["ln2"].data_ptr() if c.norm != "none" else None,
+                                 eps=float(c.norm_eps), weight_in_fp32=int(c.norm == "fp32_weight"),
+                                 residual=int(c.residual))
+                handles = (None if events is None else
+                           (ctypes.c_void_p * len(events))(*[e.cuda_event for e in events]))
+                _lib.check(self.lib.megamoe_block_forward(ctypes.byref(self.desc), ctypes.byref(tensors),
+                                                          ctypes.byref(blk), stream, handles), f"{c.id}: forward")
+                return {"y": y, "expert_ids": ids, "expert_weights": weights}
             if events is not None:
                 handles = (ctypes.c_void_p * len(events))(*[e.cuda_event for e in events])
                 _lib.check(self.lib.megamoe_forward_events(ctypes.byref(self.desc), ctypes.byref(tensors), stream,
@@ -195,3 +213,20 @@ def route(case: Case, logits: torch.Tensor, bias: torch.Tensor | None) -> tuple[
                                      None if bias is None else bias.contiguous().data_ptr(), ids.data_ptr(),
                                      w.data_ptr(), stream), "route")
     return ids, w
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float, weight_in_fp32: bool) -> torch.Tensor:
+    """RMSNorm of bf16 rows [rows, cols] with a bf16 gamma [cols] (common.py:13-21)."""
+    if x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16 or x.dim() != 2 or x.device.type != "cuda":
+        raise ValueError("rms_norm takes 2-D bf16 rows and a bf16 gamma on the GPU")
+    x, weight = x.contiguous(), weight.contiguous()
+    rows, cols = x.shape
+    if tuple(weight.shape) != (cols,):
+        raise ValueError(f"gamma has shape {tuple(weight.shape)}, expected ({cols},)")
+    out = torch.empty_like(x)
+    lib = _lib.load()
+    with torch.cuda.device(x.device):
+        stream = ctypes.c_void_p(torch.cuda.current_stream(x.device).cuda_stream)
+        _lib.check(lib.megamoe_rms_norm(rows, cols, x.data_ptr(), weight.data_ptr(), float(eps),
+                                        int(weight_in_fp32), out.data_ptr(), stream), "rms_norm")
+    return out

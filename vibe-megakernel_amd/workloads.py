@@ -82,6 +82,8 @@ def make_inputs(case: Case, seed: int, device="cpu") -> dict[str, torch.Tensor]:
     std, pw = case.weight_std, case.power_of_two
     values: dict[str, torch.Tensor] = {}
     values["x"] = _normal(seed, "x", (T, H), 1.0, device).to(torch.bfloat16)
+    if case.norm != "none":  # the block's ln2 gamma, 1 + N(0, 0.1) in bf16 as frontier.py:87
+        values["ln2"] = (_normal(seed, "ln2", (H,), 0.1, device) + 1.0).to(torch.bfloat16)
     values["router"] = _normal(seed, "router", (E, H), case.router_std, device)
     bias = router_bias(case, seed, device)
     if bias is not None:
@@ -97,6 +99,8 @@ def make_inputs(case: Case, seed: int, device="cpu") -> dict[str, torch.Tensor]:
 
 def input_names(case: Case) -> list[str]:
     names = ["x", "router"]
+    if case.norm != "none":
+        names.append("ln2")
     if case.bias != "none":
         names.append("router_bias")
     for n in ("gate", "up", "down"):
