@@ -53,6 +53,13 @@ def _log(msg: str) -> None:
 def kernel_bytes(case, hit: int) -> dict:
     """Algorithmic HBM bytes of the gate/up and down halves of the expert kernel for U = hit experts."""
     H, I, S, T, K = case.hidden, case.intermediate, case.shared_experts, case.tokens, case.topk
+    rows = T * K
+    if case.format == "mxfp4":
+        # E2M1 weights (half a byte) + one E8M0 byte per 32; x (E4M3 + E8M0 per 32) in; h
+        # (E4M3 + E8M0 per 32) out and in; d (bf16) out.
+        gu = hit * (2 * I * H // 2 + 2 * I * H // 32) + T * H + T * H // 32 + rows * I + rows * I // 32
+        dn = hit * (H * I // 2 + H * I // 32) + rows * I + rows * I // 32 + 2 * rows * H
+        return {"gate_up": gu, "down": dn}
     bh, bi = math.ceil(H / 128), math.ceil(I / 128)
     gu = hit * (2 * I * H + 4 * 2 * bi * bh)
     dn = hit * (H * I + 4 * bh * bi)
@@ -61,7 +68,6 @@ def kernel_bytes(case, hit: int) -> dict:
         gu += 2 * S * I * H + 4 * 2 * bs * bh
         dn += H * S * I + 4 * bh * bs
     # activations in and out: x quantized (T*H + scales) in, h (rows * I + scales) out / in, d out
-    rows = T * K
     gu += T * H + 4 * T * bh + rows * I + 4 * rows * bi + (T * S * I + 4 * T * math.ceil(S * I / 128) if S else 0)
     dn += rows * I + 4 * rows * bi + 2 * rows * H + ((T * S * I + 2 * T * H) if S else 0)
     return {"gate_up": gu, "down": dn}
@@ -104,7 +110,7 @@ def cpu_baseline(case, values_gpu, hit: int, budget_s: float) -> dict:
     expert once)."""
     import torch
 
-    from oracle import layer
+    from oracle import layer, mx
 
     threads = cpu_threads()
     torch.set_num_threads(threads)
@@ -113,17 +119,21 @@ def cpu_baseline(case, values_gpu, hit: int, budget_s: float) -> dict:
     while True:
         rows = list(range(sample))
         t0 = time.perf_counter()
-        reference = layer.block_reference if (case.norm != "none" or case.residual) else layer.reference
+        if case.format == "mxfp4":
+            reference = mx.reference
+        else:
+            reference = layer.block_reference if (case.norm != "none" or case.residual) else layer.reference
         out = reference(case, cpu, tokens=rows)
         dt = time.perf_counter() - t0
-        sampled = len(set(out["expert_ids"].flatten().tolist()))
+        ids = cpu["topk_idx"][rows] if case.format == "mxfp4" else out["expert_ids"]
+        sampled = len(set(ids.flatten().tolist()))
         if dt * 2 > budget_s or sample * 2 > case.tokens:
             break
         sample *= 2
     s = case.shared_experts
     scale = (hit + s) / max(sampled + s, 1)
     return {"value": dt * scale * 1e6, "unit": "us/step", "cores": threads, "kind": "port",
-            "sample": (f"oracle.layer.{reference.__name__} on tokens 0..{sample - 1} of the timed inputs "
+            "sample": (f"oracle.{reference.__module__.split('.')[-1]}.{reference.__name__} on tokens 0..{sample - 1} of the timed inputs "
                        f"({sampled} distinct experts{' + shared' if s else ''}, {dt:.2f} s), scaled by "
                        f"{hit + s}/{sampled + s} experts; torch {torch.__version__} CPU, {threads} threads, "
                        f"{platform.processor() or platform.machine()}")}
@@ -177,7 +187,8 @@ def bench_case(case, steps: int, warmup: int, want_cpu: bool, cpu_budget: float)
 
     # Per-stage device time over a second loop of the same K steps: the library records
     # events at its stage boundaries on the stream its kernels run on.
-    nev = len(_lib.STAGES) + 1
+    stages = layer.stages
+    nev = len(stages) + 1
     events = [[torch.cuda.Event(enable_timing=True) for _ in range(nev)] for _ in range(steps)]
     for row in events:
         for e in row:
@@ -188,11 +199,14 @@ def bench_case(case, steps: int, warmup: int, want_cpu: bool, cpu_budget: float)
     torch.cuda.synchronize()
     stage = [[row[j].elapsed_time(row[j + 1]) for j in range(nev - 1)] for row in events]
     stage_ms = [statistics.mean(s[j] for s in stage) for j in range(nev - 1)]
-    hit = statistics.mean(len(torch.unique(o["expert_ids"])) for o in outs[:n_sets])
+    if case.format == "mxfp4":
+        hit = statistics.mean(len(torch.unique(v["topk_idx"])) for v in sets)
+    else:
+        hit = statistics.mean(len(torch.unique(o["expert_ids"])) for o in outs[:n_sets])
 
     bytes_step = C.algorithmic_bytes(case, 0) + (C.algorithmic_bytes(case, 1) - C.algorithmic_bytes(case, 0)) * hit
     kb = kernel_bytes(case, hit)
-    ex_ms = stage_ms[3]
+    ex_ms = stage_ms[stages.index("experts")]
     ex_bytes = kb["gate_up"] + kb["down"]
     result = {
         "case": case.id, "ms_per_step": ms, "us_per_step": ms * 1e3,
@@ -202,7 +216,7 @@ def bench_case(case, steps: int, warmup: int, want_cpu: bool, cpu_budget: float)
         "tb_per_s": bytes_step / (ms * 1e-3) / 1e12,
         "hbm_frac": bytes_step / (ms * 1e-3) / PEAK_HBM,
         "mfma_frac": C.algorithmic_flops(case) / (ms * 1e-3) / PEAK_FP8,
-        "stage_us": {name: v * 1e3 for name, v in zip(_lib.STAGES, stage_ms)},
+        "stage_us": {name: v * 1e3 for name, v in zip(stages, stage_ms)},
         "rotation_sets": n_sets,
         "roofline": {"bound": "hbm", "achieved": ex_bytes / (ex_ms * 1e-3) / 1e9, "peak": PEAK_HBM / 1e9,
                      "unit": "GB/s", "frac": ex_bytes / (ex_ms * 1e-3) / PEAK_HBM,

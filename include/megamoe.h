@@ -173,6 +173,44 @@ int megamoe_block_forward(const megamoe_desc* desc, const megamoe_tensors* t, co
 int megamoe_rms_norm(int32_t rows, int32_t cols, const void* x, const void* weight, float eps,
                      int32_t weight_in_fp32, void* out, void* stream);
 
+/* Tensors of the MXFP4 form (megabench/tasks/megamoe.py, serial): the routed experts of a
+ * DeepSeek-V4-style layer with FP4 weights, routing given.
+ *   x            e4m3fn [T, H];  x_scales uint8 [T, H/32] (E8M0: 2^(s-127))
+ *   topk_idx     int64 [T, K] (distinct experts per token, each in [0, E));
+ *   topk_weights fp32 [T, K] (applied inside the SwiGLU)
+ *   l1_blocks    uint8 [E, 2I, H/32, 16] (E2M1 codes, two per byte, even element in the low
+ *                nibble; rows 0..I-1 gate, I..2I-1 up);  l1_scales uint8 [E, 2I, H/32]
+ *   l2_blocks    uint8 [E, H, I/32, 16];  l2_scales uint8 [E, H, I/32]
+ *   y            bf16 [T, H] (output) */
+typedef struct megamoe_mx_tensors {
+  const uint8_t* x;
+  const uint8_t* x_scales;
+  const int64_t* topk_idx;
+  const float* topk_weights;
+  const uint8_t* l1_blocks;
+  const uint8_t* l1_scales;
+  const uint8_t* l2_blocks;
+  const uint8_t* l2_scales;
+  void* y;
+  void* workspace;
+  size_t workspace_bytes;
+} megamoe_mx_tensors;
+
+/* Workspace of megamoe_mx_forward (host call). desc: tokens, hidden and intermediate
+ * (multiples of 256), experts, topk; shared_experts must be 0; the other fields are
+ * unused. No reference counterpart. */
+int megamoe_mx_workspace_bytes(const megamoe_desc* desc, size_t* bytes);
+
+/* The routed experts in MXFP4 (megamoe.py:116-182, serial mode): per (token, slot) row,
+ * l1 = bf16(x @ l1.T) on the scaled MFMA (E2M1 x E4M3 with both E8M0 scales), gate =
+ * min(gate, limit), up = clamp(up, +-limit), a = gate*sigmoid(gate)*up*w (fp32), h = E4M3 of a
+ * with E8M0 scales per 32 (quantization.py:67-109), d = bf16(h @ l2.T); y = bf16(slot-order
+ * fp32 sum of d). Out-of-range or repeated expert ids make every element of y NaN. `events`
+ * is NULL or events[0..3] (before the permute, after the permute, the experts and the
+ * combine). Replaces megamoe.reference(serial=True), megamoe.py:153-182. */
+int megamoe_mx_forward(const megamoe_desc* desc, float swiglu_limit, const megamoe_mx_tensors* t, void* stream,
+                       void* const* events);
+
 /* Dynamic E4M3 quantization of bf16 rows [rows, cols] with one fp32 scale
  * per row per 128 columns (the last block may be partial; padding counts as
  * zero): q e4m3fn [rows, cols], scales fp32 [rows, ceil(cols/128)].
@@ -184,7 +222,8 @@ int megamoe_quantize_rows(int32_t rows, int32_t cols, const void* x, uint8_t* q,
 /* Text for a status code (static storage). */
 const char* megamoe_status_string(int status);
 
-/* ABI version of this library: 2 (1 plus megamoe_block_forward and megamoe_rms_norm). */
+/* ABI version of this library: 3 (1, plus megamoe_block_forward and megamoe_rms_norm in 2,
+ * plus megamoe_mx_workspace_bytes and megamoe_mx_forward in 3). */
 int megamoe_abi_version(void);
 
 #ifdef __cplusplus

@@ -1,0 +1,103 @@
+"""GPU parity of the MXFP4 form (megamoe.py numerics, serial) against the CPU oracle,
+through the C ABI: y within max|y - y_ref| / max|y_ref| <= 1e-2 and cosine >= 0.9999 of
+the BF16 reference schedule (oracle.mx.reference) and within the band rule of
+megabench/harness/correctness.py:64-85 against the widened oracle; deterministic; inputs
+untouched; out-of-range or repeated expert ids give NaN (forced from the host: the
+kernels still run to completion)."""
+
+from __future__ import annotations
+
+import sys
+
+import pytest
+import torch
+
+from oracle import metrics, mx
+from vibe_megakernel_amd import cases as C
+from vibe_megakernel_amd import submission, workloads
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+MXCASE = "moe-mxfp4-deepseek-v4-pro-t64"
+
+
+def _log(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def _to(values, device):
+    return {k: v.to(device) for k, v in values.items()}
+
+
+def _check(case, y, want, exact):
+    check = metrics.layer_checks(y, want)
+    assert check["pass"], f"{case.id}: {check}"
+    band = metrics.band(want, y, exact, bf16_rtol=case.bf16_rtol, noise_factor=case.noise_factor)
+    assert band["pass"], f"{case.id}: band {band}"
+    return check, band
+
+
+def _dev_cases():
+    base = C.case(MXCASE)
+    return [C.development(base), C.development(base, tokens=37, experts=8, topk=4),
+            C.development(base, tokens=70, experts=4, topk=2, hidden=512, intermediate=512)]
+
+
+@pytest.mark.parametrize("case", _dev_cases(), ids=lambda c: f"T{c.tokens}-E{c.experts}-H{c.hidden}")
+def test_mx_layer_matches_oracle_on_development_geometry(case):
+    _log(f"mx parity {case.id} T={case.tokens} H={case.hidden} I={case.intermediate} E={case.experts}")
+    for seed in (104729, 104730):
+        values = workloads.make_inputs(case, seed, "cpu")
+        want, exact = mx.reference(case, values)["y"], mx.oracle(case, values)["y"]
+        got = submission.build(case.to_dict())(_to(values, DEV))["y"].cpu()
+        _check(case, got, want, exact)
+
+
+def test_mx_layer_is_deterministic_and_does_not_mutate_inputs():
+    case = C.development(C.case(MXCASE), tokens=24)
+    _log("mx determinism")
+    values = _to(workloads.make_inputs(case, 5, "cpu"), DEV)
+    before = {k: v.clone() for k, v in values.items()}
+    run = submission.build(case.to_dict())
+    a, b = run(values)["y"], run(values)["y"]
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+    u8 = (lambda t: t.view(torch.uint8) if t.dtype == torch.float8_e4m3fn else t)
+    for k, v in values.items():
+        assert torch.equal(u8(v), u8(before[k])), k
+
+
+@pytest.mark.parametrize("bad", ["out_of_range", "repeated"])
+def test_mx_invalid_ids_give_nan(bad):
+    case = C.development(C.case(MXCASE), tokens=8)
+    _log(f"mx invalid ids {bad}")
+    values = workloads.make_inputs(case, 6, "cpu")
+    ids = values["topk_idx"].clone()
+    if bad == "out_of_range":
+        ids[3, 1] = case.experts
+    else:
+        ids[2, 1] = ids[2, 0]
+    values["topk_idx"] = ids
+    y = submission.build(case.to_dict())(_to(values, DEV))["y"].cpu()
+    assert torch.isnan(y.float()).all()
+    # A valid call on the same workspace afterwards is unaffected.
+    good = workloads.make_inputs(case, 6, "cpu")
+    y2 = submission.build(case.to_dict())(_to(good, DEV))["y"].cpu()
+    assert torch.isfinite(y2.float()).all()
+
+
+def test_mx_full_size_on_sampled_tokens():
+    case = C.case(MXCASE)
+    _log(f"mx full size {case.id}")
+    values = workloads.make_inputs(case, 104729, DEV)
+    got = submission.build(case.to_dict())(values)["y"]
+    torch.cuda.synchronize()
+    cpu = {k: v.cpu() for k, v in values.items()}
+    del values
+    torch.cuda.empty_cache()
+    rows = [0, case.tokens // 2, case.tokens - 1]
+    want = mx.reference(case, cpu, tokens=rows)["y"]
+    exact = mx.oracle(case, cpu, tokens=rows)["y"]
+    check, band = _check(case, got.cpu()[rows], want, exact)
+    _log(f"  {case.id}: {check} band_rel={band['relative_error']:.3e}")

@@ -16,12 +16,14 @@ LIBRARY = PACKAGE_DIR / "libmegamoe.so"
 OK, ERR_INVALID_ARGUMENT, ERR_SHAPE, ERR_WORKSPACE, ERR_HIP, ERR_UNSUPPORTED = range(6)
 GATE_SOFTMAX, GATE_SIGMOID = 0, 1
 STAGES = ("router", "select_quant", "permute", "experts", "combine")
+STAGES_MX = ("permute", "experts", "combine")  # the MXFP4 form (routing and x are inputs)
 
 # Every symbol the header declares; tests check the library exports them all.
 SYMBOLS = ("megamoe_workspace_bytes", "megamoe_forward", "megamoe_forward_events", "megamoe_forward_timed",
            "megamoe_router_logits", "megamoe_route", "megamoe_quantize_rows", "megamoe_status_string",
-           "megamoe_abi_version", "megamoe_block_forward", "megamoe_rms_norm")
-ABI_VERSION = 2
+           "megamoe_abi_version", "megamoe_block_forward", "megamoe_rms_norm", "megamoe_mx_workspace_bytes",
+           "megamoe_mx_forward")
+ABI_VERSION = 3
 
 
 class Desc(ctypes.Structure):
@@ -44,6 +46,14 @@ class Tensors(ctypes.Structure):
 class Block(ctypes.Structure):
     _fields_ = [("norm_weight", ctypes.c_void_p), ("eps", ctypes.c_float), ("weight_in_fp32", ctypes.c_int32),
                 ("residual", ctypes.c_int32)]
+
+
+MX_TENSOR_FIELDS = ("x", "x_scales", "topk_idx", "topk_weights", "l1_blocks", "l1_scales", "l2_blocks", "l2_scales",
+                    "y", "workspace")
+
+
+class MxTensors(ctypes.Structure):
+    _fields_ = [(name, ctypes.c_void_p) for name in MX_TENSOR_FIELDS] + [("workspace_bytes", ctypes.c_size_t)]
 
 
 class MegaMoEError(RuntimeError):
@@ -75,6 +85,8 @@ def load() -> ctypes.CDLL:
     lib.megamoe_block_forward.argtypes = [P(Desc), P(Tensors), P(Block), c_void_p, P(c_void_p)]
     lib.megamoe_rms_norm.argtypes = [ctypes.c_int32, ctypes.c_int32, c_void_p, c_void_p, ctypes.c_float,
                                      ctypes.c_int32, c_void_p, c_void_p]
+    lib.megamoe_mx_workspace_bytes.argtypes = [P(Desc), P(c_size_t)]
+    lib.megamoe_mx_forward.argtypes = [P(Desc), ctypes.c_float, P(MxTensors), c_void_p, P(c_void_p)]
     lib.megamoe_status_string.argtypes = [c_int]
     lib.megamoe_status_string.restype = ctypes.c_char_p
     lib.megamoe_abi_version.argtypes = []

@@ -26,7 +26,11 @@ import math
 from dataclasses import asdict, dataclass, field, replace
 
 FAMILY = "moe_fp8_layer"
-ROUTERS = ("softmax", "sigmoid")
+ROUTERS = ("softmax", "sigmoid", "given")  # given: topk_idx / topk_weights are inputs
+# Expert formats: fp8 = E4M3 weights with fp32 128x128 scales and E4M3 activations with
+# fp32 per-128 scales (frontier.py); mxfp4 = E2M1 weights with E8M0 scales per 32 and
+# E4M3 activations with E8M0 scales per 32 (megamoe.py, quantization.py:13-116).
+FORMATS = ("fp8", "mxfp4")
 # RMSNorm before the layer (the block form): none, gamma applied in fp32 before the one
 # bf16 rounding (DeepSeek), or to the rounded activation (common.py:13-21).
 NORMS = ("none", "fp32_weight", "bf16_weight")
@@ -75,6 +79,10 @@ class Case:
     norm: str = "none"
     norm_eps: float = 1e-6
     residual: bool = False
+    # The MXFP4 form (megamoe.py numerics): expert format, and the SwiGLU clamp applied
+    # to gate (above) and up (both sides) before the activation (megamoe.py:116-122).
+    format: str = "fp8"
+    swiglu_limit: float = 0.0
 
     def __post_init__(self) -> None:
         if not self.id or self.family != FAMILY or not self.model or not self.phase:
@@ -95,6 +103,14 @@ class Case:
             raise ValueError(f"invalid routing rule in {self.id}")
         if self.norm not in NORMS or not self.norm_eps >= 0:
             raise ValueError(f"invalid normalization in {self.id}")
+        if self.format not in FORMATS:
+            raise ValueError(f"invalid expert format in {self.id}")
+        if (self.format == "mxfp4") != (self.router == "given"):
+            raise ValueError(f"{self.id}: the MXFP4 form takes its routing as an input, and only it does")
+        if self.format == "mxfp4" and (p["hidden"] % 256 or p["intermediate"] % 256 or p.get("shared_experts", 0)
+                                       or self.norm != "none" or self.residual or not self.swiglu_limit > 0):
+            raise ValueError(f"{self.id}: the MXFP4 form needs H and I multiples of 256, no shared expert "
+                             "or block steps, and a positive SwiGLU limit")
         if self.router == "softmax" and self.bias != "none":
             raise ValueError(f"{self.id}: softmax routing takes no correction bias")
         groups, top = self.groups, self.top_groups
@@ -187,8 +203,19 @@ BLOCK_CASES: tuple[Case, ...] = (
 )
 
 
+# The MXFP4 routed-expert layer of megamoe.py (DeepSeek-V4-Pro geometry: 384 experts, top-6,
+# H 7168, I 3072, SwiGLU limit 10, routed scaling 2.5; cases.py:380-387), serial, at a decode
+# batch of 64 tokens: x arrives as E4M3 with E8M0 scales per 32, routing as ids and weights.
+MX_CASES: tuple[Case, ...] = (
+    _case("moe-mxfp4-deepseek-v4-pro-t64", "deepseek-ai/DeepSeek-V4-Pro (routed experts, MXFP4)",
+          params=dict(tokens=64, hidden=7168, experts=384, topk=6, intermediate=3072),
+          router="given", format="mxfp4", swiglu_limit=10.0, routed_scaling=2.5, max_gpu_launches=3,
+          note="megamoe numerics in serial mode: E2M1 x E4M3 scaled MFMA, clamped SwiGLU, E8M0 requant"),
+)
+
+
 def case(case_id: str) -> Case:
-    for c in CASES + BLOCK_CASES:
+    for c in CASES + BLOCK_CASES + MX_CASES:
         if c.id == case_id:
             return c
     raise KeyError(case_id)
@@ -216,8 +243,13 @@ def development(c: Case, **params) -> Case:
 def algorithmic_bytes(c: Case, hit_experts: int) -> int:
     """HBM bytes one step must move: weights of the hit experts and the shared expert
     (E4M3 payload + fp32 128x128 scales), the fp32 router and bias, x and y in bf16,
-    ids (int64) and weights (fp32); in the block form also the bf16 RMSNorm gamma."""
+    ids (int64) and weights (fp32); in the block form also the bf16 RMSNorm gamma. In the
+    MXFP4 form: E2M1 payload (half a byte) + one E8M0 byte per 32 weights, x as E4M3 + E8M0
+    per 32, ids and weights, y in bf16."""
     T, H, E, K, I, S = c.tokens, c.hidden, c.experts, c.topk, c.intermediate, c.shared_experts
+    if c.format == "mxfp4":
+        per_expert = 3 * I * H // 2 + 3 * I * H // 32
+        return hit_experts * per_expert + T * H + T * H // 32 + 12 * T * K + 2 * T * H
     bh, bi = math.ceil(H / 128), math.ceil(I / 128)
     per_expert = 3 * I * H + 4 * (2 * bi * bh + bh * bi)
     shared = 0
@@ -232,6 +264,8 @@ def algorithmic_bytes(c: Case, hit_experts: int) -> int:
 
 def algorithmic_flops(c: Case) -> int:
     T, H, E, K, I, S = c.tokens, c.hidden, c.experts, c.topk, c.intermediate, c.shared_experts
+    if c.format == "mxfp4":  # no router GEMV: routing is an input
+        return 2 * T * K * 3 * I * H
     return 2 * T * E * H + 2 * T * K * 3 * I * H + 2 * T * S * 3 * I * H
 
 

@@ -763,7 +763,8 @@ __device__ unsigned long long block_exclusive_scan(unsigned long long v, unsigne
 // queue counter that every workgroup updates.
 constexpr int kMetaHit = 0, kMetaUnitsGU = 1, kMetaUnitsDN = 2, kMetaQueueGU = 3, kMetaQueueDN = 4,
               kMetaError = 32, kMetaInts = 64;
-constexpr int kChunkRows = 64;
+constexpr int kChunkRows = 64;    // rows per chunk of the fp8 form (column tiles of up to 4)
+constexpr int kChunkRowsMx = 32;  // of the MXFP4 form (up to 2)
 
 struct PermuteOut {
   int* counts;   // [E]
@@ -779,9 +780,14 @@ struct PermuteOut {
 
 __device__ __forceinline__ int chunk_class(int rows) { return rows > 32 ? 0 : (rows > 16 ? 1 : 2); }
 
+// Ids from the caller (the MXFP4 form takes its routing as an input) may be out of range or
+// repeat an expert within a token; either sets the error flag, and the permutation, the
+// work lists and every later kernel's work are skipped (the combine writes NaN).
 __global__ __launch_bounds__(1024) void k_permute(const int64_t* __restrict__ ids, int T, int K, int E, int S,
-                                                  int nbI, int nbH, int ks, PermuteOut out) {
+                                                  int nbI, int nbH, int ks, int chunk, PermuteOut out) {
   extern __shared__ int smem[];
+  __shared__ int bad_ids;
+  int* bad = &bad_ids;
   unsigned long long* tmp = (unsigned long long*)smem;  // 16
   int* cnt = smem + 32;                                  // E
   unsigned* bm = (unsigned*)(cnt + E);                   // E * words
@@ -789,16 +795,32 @@ __global__ __launch_bounds__(1024) void k_permute(const int64_t* __restrict__ id
   const int tid = threadIdx.x, n = T * K;
   for (int i = tid; i < E; i += blockDim.x) cnt[i] = 0;
   for (int i = tid; i < E * words; i += blockDim.x) bm[i] = 0u;
+  if (tid == 0) *bad = 0;
   __syncthreads();
   for (int i = tid; i < n; i += blockDim.x) {
-    const int e = (int)ids[i], t = i / K;
+    const int64_t e64 = ids[i];
+    const int t = i / K;
+    if (e64 < 0 || e64 >= E) {
+      *bad = 1;
+      continue;
+    }
+    const int e = (int)e64;
     atomicAdd(&cnt[e], 1);
-    atomicOr(&bm[e * words + (t >> 5)], 1u << (t & 31));
+    if (atomicOr(&bm[e * words + (t >> 5)], 1u << (t & 31)) & (1u << (t & 31))) *bad = 1;
   }
   __syncthreads();
+  if (*bad) {
+    if (tid == 0) {
+      out.meta[kMetaUnitsGU] = 0;
+      out.meta[kMetaUnitsDN] = 0;
+      out.meta[kMetaQueueGU] = 0;
+      out.meta[kMetaError] = 1;
+    }
+    return;
+  }
   // E <= 1024 = blockDim: one expert per thread.
   const int c = tid < E ? cnt[tid] : 0;
-  const int full = c / kChunkRows, rem = c % kChunkRows;
+  const int full = c / chunk, rem = c % chunk;
   const int a4 = full + (rem > 32 ? 1 : 0), a2 = (rem > 16 && rem <= 32) ? 1 : 0, a1 = (rem > 0 && rem <= 16) ? 1 : 0;
   const int nhit = __syncthreads_count(c > 0);
   unsigned long long tot = 0;
@@ -810,7 +832,7 @@ __global__ __launch_bounds__(1024) void k_permute(const int64_t* __restrict__ id
   const int total = (int)(tot & 0x1fffffu), t4 = (int)((tot >> 21) & 0x7fffu), t2 = (int)((tot >> 36) & 0x7ffu),
             t1 = (int)((tot >> 47) & 0x7ffu);
   // Shared expert chunks of T rows.
-  const int sf = T / kChunkRows, sr = T % kChunkRows;
+  const int sf = T / chunk, sr = T % chunk;
   const int s4 = S ? sf + (sr > 32 ? 1 : 0) : 0, s2 = S ? ((sr > 16 && sr <= 32) ? 1 : 0) : 0,
             s1 = S ? ((sr > 0 && sr <= 16) ? 1 : 0) : 0;
   // gate/up list: [S*s4 | t4 | S*s2 | t2 | S*s1 | t1]; down list: [s4 | t4 | s2 | t2 | s1 | t1]
@@ -822,19 +844,19 @@ __global__ __launch_bounds__(1024) void k_permute(const int64_t* __restrict__ id
     out.counts[tid] = c;
     out.offsets[tid] = off;
     for (int i = 0; i < a4; ++i) {
-      const int4 ch = make_int4(tid, kChunkRows * i, min(kChunkRows, c - kChunkRows * i), 0);
+      const int4 ch = make_int4(tid, chunk * i, min(chunk, c - chunk * i), 0);
       out.gu[gbase[0] + gshared[0] + p4 + i] = ch;
       out.dn[dbase[0] + dshared[0] + p4 + i] = ch;
       out.dn_of_gu[gbase[0] + gshared[0] + p4 + i] = dbase[0] + dshared[0] + p4 + i;
     }
     if (a2) {
-      const int4 ch = make_int4(tid, kChunkRows * full, rem, 0);
+      const int4 ch = make_int4(tid, chunk * full, rem, 0);
       out.gu[gbase[1] + gshared[1] + p2] = ch;
       out.dn[dbase[1] + dshared[1] + p2] = ch;
       out.dn_of_gu[gbase[1] + gshared[1] + p2] = dbase[1] + dshared[1] + p2;
     }
     if (a1) {
-      const int4 ch = make_int4(tid, kChunkRows * full, rem, 0);
+      const int4 ch = make_int4(tid, chunk * full, rem, 0);
       out.gu[gbase[2] + gshared[2] + p1] = ch;
       out.dn[dbase[2] + dshared[2] + p1] = ch;
       out.dn_of_gu[gbase[2] + gshared[2] + p1] = dbase[2] + dshared[2] + p1;
@@ -842,16 +864,16 @@ __global__ __launch_bounds__(1024) void k_permute(const int64_t* __restrict__ id
   }
   if (tid == 0) {
     if (S > 0) {
-      for (int i = 0; i * kChunkRows < T; ++i) {
-        const int rows = min(kChunkRows, T - kChunkRows * i);
+      for (int i = 0; i * chunk < T; ++i) {
+        const int rows = min(chunk, T - chunk * i);
         const int cls = chunk_class(rows);
         const int idx = cls == 0 ? i : 0;        // index within the shared part of the class
         const int per_copy = cls == 0 ? s4 : 1;  // shared chunks of this class per copy
         for (int s = 0; s < S; ++s) {
-          out.gu[gbase[cls] + s * per_copy + idx] = make_int4(E, kChunkRows * i, rows, s * nbI);
+          out.gu[gbase[cls] + s * per_copy + idx] = make_int4(E, chunk * i, rows, s * nbI);
           out.dn_of_gu[gbase[cls] + s * per_copy + idx] = dbase[cls] + idx;
         }
-        out.dn[dbase[cls] + idx] = make_int4(E, kChunkRows * i, rows, 0);
+        out.dn[dbase[cls] + idx] = make_int4(E, chunk * i, rows, 0);
       }
     }
     out.offsets[E] = total;
@@ -883,9 +905,10 @@ __global__ __launch_bounds__(1024) void k_permute(const int64_t* __restrict__ id
 // atomic stores, which write through the XCD's L2 to memory), so publishing them takes
 // only a wait for the stores to complete, not a writeback of the whole L2. Readers use
 // ordinary loads, which cannot return a stale line: every cache is coherent when the
-// kernel starts (kernel-boundary acquire), each 128-byte line of h and of the padded
-// scale rows is written by exactly one unit, and no workgroup reads a line before the
-// count of its writer has landed, so no cache can hold an old copy of it.
+// kernel starts (kernel-boundary acquire); each 128-byte line of h is written by exactly
+// one unit, and each padded scale row (one line) by the gate/up units of its chunk, each
+// storing only its own 4 bytes; and no workgroup reads a line before the counts of all its
+// writers have landed, so no cache holds a copy of a line from before its last write.
 // ---------------------------------------------------------------------------------------
 
 __device__ __forceinline__ void store_coherent(uint32_t* p, uint32_t v) {
@@ -1417,7 +1440,7 @@ __device__ __forceinline__ void combine8(const uint16_t* __restrict__ d_r, const
     for (int u = 0; u < 8; ++u) {
       const int s = min(s0 + u, K - 1);  // clamped, unconditional loads
       v[u] = *reinterpret_cast<const uint4*>(d_r + (size_t)inv[t * K + s] * H + h0);
-      wv[u] = wts[t * K + s];
+      wv[u] = wts ? wts[t * K + s] : 1.0f;  // no weights: already applied (the MXFP4 form)
     }
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
@@ -1452,7 +1475,7 @@ __device__ __forceinline__ void combine8_parts(const float* __restrict__ p_r, co
   for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
   for (int s = 0; s < K; ++s) {
     const int row = inv[t * K + s];
-    const float wv = wts[t * K + s];
+    const float wv = wts ? wts[t * K + s] : 1.0f;
     float dv[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) dv[i] = 0.0f;
@@ -1594,6 +1617,389 @@ __global__ __launch_bounds__(256, 2) void k_experts(ExpertArgs args) {
   }
 }
 
+// =======================================================================================
+// The MXFP4 form (megamoe.py:116-182, serial): E2M1 expert weights with one E8M0 scale per
+// 32 input channels, activations in E4M3 with E8M0 scales per 32, routing as an input.
+// gfx950's scaled MFMA takes both formats and both scales natively: in
+// v_mfma_scale_f32_16x16x128_f8f6f4 with an E2M1 A operand, lane r + 16g holds row r and
+// K elements [32g, 32g+32) in 16 bytes (the even element in the low nibble), so one lane's
+// operand is one stored 32-block; the E4M3 B operand keeps the layout of the fp8 form; and
+// the E8M0 byte of lane r + 16g scales row (or column) r over K elements [32g, 32g+32)
+// (layouts measured on gfx950). Products and power-of-two scales are exact and the MFMA
+// sums in fp32, so no scale multiplies follow it.
+//
+// A ring stage covers 256 K elements: one 128-byte line of each weight row, two MFMAs per
+// tile (the first and second 16 bytes of each 32-byte LDS read). The scale bytes of a stage
+// come with one 8-byte load per lane and operand row, shifted to the lane's block.
+// =======================================================================================
+
+constexpr int kMxStageK = 256;
+
+__device__ __forceinline__ f32x4 mfma_e2m1_e4m3(const i32x4& a, const i32x8& b, f32x4 c, int sa, int sb) {
+  const i32x8 a8 = {a[0], a[1], a[2], a[3], 0, 0, 0, 0};
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a8, b, c, 4, 0, 0, sa, 0, sb);
+}
+
+// Biased E8M0 exponent that maps `amax` (>= 0) into E4M3: the fp32 exponent, one up where
+// the mantissa exceeds 1.75's, less 448's exponent (8), floored at 2^-22 (1e-4 / 448);
+// quantization.py:67-78.
+__device__ __forceinline__ uint32_t e8m0_exponent(float amax) {
+  const int r = (int)((__float_as_uint(amax) + (0x7FFFFFu - 0x600000u)) >> 23);
+  return (uint32_t)(max(r, 105 + 8) - 8);
+}
+
+template <int RT, int NCT>
+struct StageMx {
+  i32x8 b[NCT][2];  // activations of the stage's two 128-K steps
+  uint2 sb[NCT];    // activation E8M0 bytes [8p, 8p+8) of the lane's token row
+  uint2 sa[RT];     // weight E8M0 bytes [8p, 8p+8) of the lane's row in each tile
+};
+
+template <int RT, int NCT>
+struct OperandsMx {
+  const uint8_t* a[RT];    // row 0 of each 16-row weight tile (E2M1, lda bytes per row)
+  int lda;
+  const uint8_t* spare;    // 16 * lda bytes that loads past the last stage read instead
+  const uint8_t* sa[RT];   // lane's weight scale row in each tile
+  const uint8_t* b[NCT];   // lane's activation row at its K byte offset
+  const uint8_t* sb[NCT];  // lane's activation scale row
+};
+
+template <int RT, int NCT>
+__device__ __forceinline__ void issue_a_mx(uint8_t* slot, const OperandsMx<RT, NCT>& op, const LaneTile& lt, int p,
+                                           bool live) {
+#pragma unroll
+  for (int t = 0; t < RT; ++t) {
+    const uint8_t* base = live ? op.a[t] + (size_t)p * kBlock : op.spare;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(base +
+                                                                                     (uint32_t)(lt.dma + 8 * i * op.lda)),
+                                       (__attribute__((address_space(3))) void*)(slot + t * kTileBytes + i * 1024),
+                                       16, 0, kNonTemporal);
+  }
+}
+
+// 5*NCT + RT vector loads.
+template <int RT, int NCT>
+__device__ __forceinline__ void load_stage_mx(StageMx<RT, NCT>& s, const OperandsMx<RT, NCT>& op, int p) {
+  const size_t o = (size_t)p * kMxStageK;
+#pragma unroll
+  for (int c = 0; c < NCT; ++c) {
+    s.b[c][0] = load_k32(op.b[c] + o);
+    s.b[c][1] = load_k32(op.b[c] + o + 128);
+  }
+#pragma unroll
+  for (int c = 0; c < NCT; ++c) s.sb[c] = *reinterpret_cast<const uint2*>(op.sb[c] + 8 * p);
+#pragma unroll
+  for (int t = 0; t < RT; ++t) s.sa[t] = *reinterpret_cast<const uint2*>(op.sa[t] + 8 * p);
+}
+
+template <int RT>
+__device__ __forceinline__ void read_slot_mx(i32x4 (&lo)[RT], i32x4 (&hi)[RT], uint32_t p0, uint32_t p1) {
+#pragma unroll
+  for (int r = 0; r < RT; ++r)
+    asm volatile("ds_read_b128 %0, %2\n\tds_read_b128 %1, %3"
+                 : "=&v"(lo[r]), "=&v"(hi[r])
+                 : "v"(p0 + r * kTileBytes), "v"(p1 + r * kTileBytes)
+                 : "memory");
+  if constexpr (RT == 2) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(lo[0]), "+v"(hi[0]), "+v"(lo[1]), "+v"(hi[1]));
+  } else {
+    static_assert(RT == 4, "two or four row tiles");
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(lo[0]), "+v"(hi[0]), "+v"(lo[1]), "+v"(hi[1]), "+v"(lo[2]), "+v"(hi[2]), "+v"(lo[3]),
+                   "+v"(hi[3]));
+  }
+}
+
+// `shift` = 8 * (lane / 16): the lane's byte in each scale word. The scale bytes pass an
+// empty asm (as in mfma_stage) so their extraction stays after the stage's wait.
+template <int RT, int NCT>
+__device__ __forceinline__ void mfma_stage_mx(const i32x4 (&lo)[RT], const i32x4 (&hi)[RT], const StageMx<RT, NCT>& s,
+                                              int shift, f32x4 (&acc)[RT][NCT]) {
+  int sa0[RT], sa1[RT], sb0[NCT], sb1[NCT];
+#pragma unroll
+  for (int r = 0; r < RT; ++r) {
+    uint2 w = s.sa[r];
+    asm volatile("" : "+v"(w.x), "+v"(w.y));
+    sa0[r] = (int)((w.x >> shift) & 0xffu);
+    sa1[r] = (int)((w.y >> shift) & 0xffu);
+  }
+#pragma unroll
+  for (int c = 0; c < NCT; ++c) {
+    uint2 w = s.sb[c];
+    asm volatile("" : "+v"(w.x), "+v"(w.y));
+    sb0[c] = (int)((w.x >> shift) & 0xffu);
+    sb1[c] = (int)((w.y >> shift) & 0xffu);
+  }
+#pragma unroll
+  for (int r = 0; r < RT; ++r)
+#pragma unroll
+    for (int c = 0; c < NCT; ++c) acc[r][c] = mfma_e2m1_e4m3(lo[r], s.b[c][0], acc[r][c], sa0[r], sb0[c]);
+#pragma unroll
+  for (int r = 0; r < RT; ++r)
+#pragma unroll
+    for (int c = 0; c < NCT; ++c) acc[r][c] = mfma_e2m1_e4m3(hi[r], s.b[c][1], acc[r][c], sa1[r], sb1[c]);
+}
+
+// The fp8 form's stream (D slots, loads in issue order, the spare region for loads past
+// the end, a rotated start) over nst stages of 256 K elements.
+template <int RT, int NCT, int D>
+__device__ __forceinline__ void stream_gemm_mx(const OperandsMx<RT, NCT>& op, int nst, int rot, uint8_t* ring,
+                                               f32x4 (&acc)[RT][NCT],
+                                               const ReadyWait& ready = ReadyWait{nullptr, 0, nullptr}) {
+  constexpr int kSlot = RT * kTileBytes;
+  constexpr int kAfter = (D - 1) * (3 * RT + 5 * NCT);
+  static_assert(D >= 2 && D * kSlot <= kRingWave && kAfter <= 63, "LDS ring and vmcnt range");
+  auto phys = [nst, rot](int p) {
+    const int q = p + rot;
+    return q >= nst ? q - nst : q;
+  };
+  const LaneTile lt = lane_tile(op.lda);
+  const uint32_t ring_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)ring;
+  const int shift = 8 * (opaque_lane() >> 4);
+#pragma unroll
+  for (int r = 0; r < RT; ++r)
+#pragma unroll
+    for (int c = 0; c < NCT; ++c) acc[r][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+  StageMx<RT, NCT> st[D];
+#pragma unroll
+  for (int s = 0; s < D - 1; ++s) issue_a_mx(ring + s * kSlot, op, lt, phys(min(s, nst - 1)), s < nst);
+  wait_ready(ready);
+#pragma unroll
+  for (int s = 0; s < D - 1; ++s) load_stage_mx(st[s], op, phys(min(s, nst - 1)));
+  for (int p0 = 0; p0 < nst; p0 += D) {
+#pragma unroll
+    for (int s = 0; s < D; ++s) {
+      const int p = p0 + s, pn = phys(min(p + D - 1, nst - 1));
+      load_stage_mx(st[(s + D - 1) % D], op, pn);
+      issue_a_mx(ring + ((s + D - 1) % D) * kSlot, op, lt, pn, p + D - 1 < nst);
+      wait_vmem<kAfter>();
+      if (p < nst) {
+        i32x4 lo[RT], hi[RT];
+        read_slot_mx<RT>(lo, hi, ring_lds + s * kSlot + lt.rd0, ring_lds + s * kSlot + lt.rd1);
+        mfma_stage_mx(lo, hi, st[s], shift, acc);
+      }
+    }
+  }
+}
+
+struct GateUpMxArgs {
+  const uint8_t* x;    // [T, H] e4m3
+  const uint8_t* xs;   // [T, H/32] e8m0
+  const float* wts;    // [T*K] routing weights
+  const uint8_t* l1;   // [E, 2I, H/2] e2m1 (rows 0..I-1 gate, I..2I-1 up)
+  const uint8_t* l1s;  // [E, 2I, H/32] e8m0
+  const int* offsets; const int* perm; const int4* chunks;
+  int* meta;
+  uint8_t* hq;         // [T*K, I] e4m3, grouped rows
+  uint8_t* hs;         // [T*K, hs_ld] e8m0 (one 128-byte line per row)
+  const uint8_t* spare;
+  int T, H, I, K, E, hs_ld;
+  float limit;
+};
+
+// Gate/up unit: rows [jb*128, +128) of the expert's gate and up matrices. Wave w owns
+// gate rows 32w .. 32w+31 and the same up rows, i.e. one 32-channel block of h: its E8M0
+// requantization needs no reduction across wavefronts.
+//   gate, up = bf16(l1); gate = min(gate, limit); up = clamp(up, +-limit)
+//   a = gate / (1 + exp(-gate)) * up * w_slot (fp32, megamoe.py:116-122)
+//   h = E4M3(a * 2^(127-e)), e = E8M0 exponent of the block's amax (megamoe.py:125-128)
+template <int NCT>
+__device__ void gateup_mx_unit(const GateUpMxArgs& a, int e, int jb, const ChunkRows& cr, int rot, uint8_t (*red8)[64],
+                               uint8_t* ring) {
+  const int lane = opaque_lane(), w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lr = lane & 15;
+  const int H = a.H, lda = H / 2, sld = H / 32;
+  const size_t gate0 = (size_t)e * 2 * a.I + (size_t)jb * kBlock + 32 * w, up0 = gate0 + a.I;
+  OperandsMx<4, NCT> op;
+  op.lda = lda;
+  op.spare = a.spare;
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    op.a[r] = a.l1 + (gate0 + 16 * r) * lda;
+    op.a[r + 2] = a.l1 + (up0 + 16 * r) * lda;
+    op.sa[r] = a.l1s + (gate0 + 16 * r + lr) * sld;
+    op.sa[r + 2] = a.l1s + (up0 + 16 * r + lr) * sld;
+  }
+#pragma unroll
+  for (int c = 0; c < NCT; ++c) {
+    const int tok = row_token(cr, min(16 * c + lr, cr.n - 1));
+    op.b[c] = a.x + (size_t)tok * H + 16 * (lane >> 4);
+    op.sb[c] = a.xs + (size_t)tok * sld;
+  }
+  f32x4 acc[4][NCT];
+  stream_gemm_mx<4, NCT, 2>(op, H / kMxStageK, rot, ring, acc);
+
+  const float L = a.limit;
+#pragma unroll
+  for (int c = 0; c < NCT; ++c) {
+    const int col = 16 * c + lr;
+    const float wrow = a.wts[cr.perm[cr.row0 + min(col, cr.n - 1)]];
+    float hv[2][4];
+    float amax = 0.0f;
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const float g = fminf(round_bf16(acc[p][c][v]), L);
+        const float u = fminf(fmaxf(round_bf16(acc[p + 2][c][v]), -L), L);
+        const float act = __fmul_rn(__fmul_rn(g / __fadd_rn(1.0f, expf(-g)), u), wrow);
+        hv[p][v] = act;
+        amax = fmaxf(amax, fabsf(act));
+      }
+    amax = fmaxf(amax, __shfl_xor(amax, 16));
+    amax = fmaxf(amax, __shfl_xor(amax, 32));
+    const uint32_t ex = e8m0_exponent(amax);
+    const float inv = __uint_as_float((254u - ex) << 23);
+    if (col < cr.n) {
+      uint8_t* dst = a.hq + (size_t)(cr.row0 + col) * a.I + (size_t)jb * kBlock + 32 * w + 4 * (lane >> 4);
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        uint32_t packed = 0;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) packed |= f32_to_e4m3(clamp448(__fmul_rn(hv[p][v], inv))) << (8 * v);
+        store_coherent(reinterpret_cast<uint32_t*>(dst + 16 * p), packed);
+      }
+      if (lane < 16) red8[w][col] = (uint8_t)ex;
+    }
+  }
+  __syncthreads();
+  if (w == 0) {
+    for (int col = lane; col < 16 * NCT && col < cr.n; col += 64) {
+      const uint32_t word = red8[0][col] | (red8[1][col] << 8) | (red8[2][col] << 16) | (red8[3][col] << 24);
+      store_coherent(reinterpret_cast<uint32_t*>(a.hs + (size_t)(cr.row0 + col) * a.hs_ld + 4 * jb), word);
+    }
+  }
+}
+
+__device__ void gateup_mx_work(const GateUpMxArgs& a, int u, uint8_t (*red8)[64], uint8_t* ring) {
+  const int nbI = a.I / kBlock;
+  const int4 ch = a.chunks[u / nbI];
+  const int jb = u % nbI;
+  const ChunkRows cr{ch.z, a.offsets[ch.x] + ch.y, a.perm, a.K};
+  const int rot = u % (a.H / kMxStageK);
+  if (cr.n <= 16)
+    gateup_mx_unit<1>(a, ch.x, jb, cr, rot, red8, ring);
+  else
+    gateup_mx_unit<2>(a, ch.x, jb, cr, rot, red8, ring);
+}
+
+struct DownMxArgs {
+  const uint8_t* l2;   // [E, H, I/2] e2m1
+  const uint8_t* l2s;  // [E, H, I/32] e8m0
+  const int* offsets; const int* perm; const int4* chunks;
+  int* meta;
+  const uint8_t* hq; const uint8_t* hs;
+  uint16_t* d;  // [T*K, H] bf16, grouped rows
+  float* pd;    // ks > 1: [ks, T*K, H] fp32 partial d of each K part
+  const uint8_t* spare;
+  int T, H, I, K, E, hs_ld, ks;
+};
+
+// Down unit: rows [j*128, +128) of the expert's down matrix over K part kp of ks.
+template <int NCT>
+__device__ void down_mx_unit(const DownMxArgs& a, int e, int j, int kp, const ChunkRows& cr, int rot,
+                             const ReadyWait& ready, uint8_t* ring) {
+  const int lane = opaque_lane(), w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lr = lane & 15;
+  const int I = a.I, lda = I / 2, sld = I / 32, nstp = I / kMxStageK / a.ks, p0 = kp * nstp;
+  OperandsMx<2, NCT> op;
+  op.lda = lda;
+  op.spare = a.spare;
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const size_t row = (size_t)e * a.H + (size_t)j * kBlock + 32 * w + 16 * r;
+    op.a[r] = a.l2 + row * lda + (size_t)p0 * kBlock;
+    op.sa[r] = a.l2s + (row + lr) * sld + 8 * p0;
+  }
+#pragma unroll
+  for (int c = 0; c < NCT; ++c) {
+    const int rr = cr.row0 + min(16 * c + lr, cr.n - 1);
+    op.b[c] = a.hq + (size_t)rr * I + (size_t)p0 * kMxStageK + 16 * (lane >> 4);
+    op.sb[c] = a.hs + (size_t)rr * a.hs_ld + 8 * p0;
+  }
+  f32x4 acc[2][NCT];
+  stream_gemm_mx<2, NCT, NCT == 2 ? 3 : 4>(op, nstp, rot, ring, acc, ready);
+  float* pd = a.pd + (size_t)kp * a.T * a.K * a.H;
+#pragma unroll
+  for (int c = 0; c < NCT; ++c) {
+    const int r = 16 * c + lr;
+    if (r < cr.n) {
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        const size_t o = (size_t)(cr.row0 + r) * a.H + (size_t)j * kBlock + 32 * w + 16 * p + 4 * (lane >> 4);
+        if (a.ks == 1) {
+          const uint32_t lo = f32_to_bf16_bits(acc[p][c][0]) | (f32_to_bf16_bits(acc[p][c][1]) << 16);
+          const uint32_t hi = f32_to_bf16_bits(acc[p][c][2]) | (f32_to_bf16_bits(acc[p][c][3]) << 16);
+          *reinterpret_cast<uint2*>(a.d + o) = make_uint2(lo, hi);
+        } else {
+          *reinterpret_cast<f32x4*>(pd + o) = acc[p][c];
+        }
+      }
+    }
+  }
+}
+
+__device__ void down_mx_work(const DownMxArgs& a, int v, const ReadyWait& ready, uint8_t* ring) {
+  const int nbH = a.H / kBlock;
+  const int4 ch = a.chunks[v / (nbH * a.ks)];
+  const int rem = v % (nbH * a.ks), j = rem / a.ks, kp = rem % a.ks;
+  const ChunkRows cr{ch.z, a.offsets[ch.x] + ch.y, a.perm, a.K};
+  const int rot = v % (a.I / kMxStageK / a.ks);
+  if (cr.n <= 16)
+    down_mx_unit<1>(a, ch.x, j, kp, cr, rot, ready, ring);
+  else
+    down_mx_unit<2>(a, ch.x, j, kp, cr, rot, ready, ring);
+}
+
+struct ExpertMxArgs {
+  GateUpMxArgs gu;
+  DownMxArgs dn;
+  const int* dn_of_gu;
+  int* ready;
+};
+
+// The persistent expert kernel of the MXFP4 form: the queue, claims and readiness waits
+// of k_experts, with the MXFP4 units.
+__global__ __launch_bounds__(256, 2) void k_experts_mx(ExpertMxArgs args) {
+  typedef const __attribute__((address_space(4))) ExpertMxArgs* ArgsPtr;
+  __shared__ uint8_t red8[4][64];
+  __shared__ __attribute__((aligned(16))) uint8_t rings[4 * kRingWave];
+  __shared__ int slot;
+  static_assert(sizeof(ExpertMxArgs) % 8 == 0, "argument segment layout");
+  int* meta = args.gu.meta;
+  const int total_gu = meta[kMetaUnitsGU];
+  const int total = total_gu + meta[kMetaUnitsDN];
+  if (threadIdx.x == 0) slot = atomicAdd(&meta[kMetaQueueGU], 1);
+  __syncthreads();
+  int u = slot, next = 0;
+  while (u < total) {
+    ArgsPtr ap = (ArgsPtr)__builtin_amdgcn_kernarg_segment_ptr();
+    asm volatile("" : "+s"(ap));
+    ExpertMxArgs a;
+    __builtin_memcpy(&a, (const ExpertMxArgs*)ap, sizeof(a));
+    const int nbI = a.gu.I / kBlock, nbH = a.dn.H / kBlock;
+    uint8_t* ring = rings + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) * kRingWave;
+    __syncthreads();
+    if (threadIdx.x == 0) next = atomicAdd(&meta[kMetaQueueGU], 1);
+    if (u < total_gu) {
+      gateup_mx_work(a.gu, u, red8, ring);
+      publish_fence();
+      __syncthreads();
+      if (threadIdx.x == 0) atomicAdd(&a.ready[a.dn_of_gu[u / nbI]], 1);
+    } else {
+      const int v = u - total_gu, c = v / (nbH * a.dn.ks);
+      const ReadyWait ready{&a.ready[c], nbI, &meta[kMetaError]};
+      down_mx_work(a.dn, v, ready, ring);
+    }
+    if (threadIdx.x == 0) slot = next;
+    __syncthreads();
+    u = slot;
+  }
+}
+
 // ---------------------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------------------
@@ -1612,9 +2018,9 @@ struct Layout {
 // Upper bound of list entries: every hit expert has at most ceil(rows/64) chunks, so the
 // routed chunks number at most min(E, T*K) + T*K/64; the shared expert adds ceil(T/64)
 // per copy.
-size_t max_chunks(const megamoe_desc& d, int copies) {
+size_t max_chunks(const megamoe_desc& d, int copies, int chunk = kChunkRows) {
   const size_t T = d.tokens, TK = (size_t)d.tokens * d.topk, E = d.experts;
-  return (E < TK ? E : TK) + TK / kChunkRows + 1 + (size_t)copies * ((T + kChunkRows - 1) / kChunkRows);
+  return (E < TK ? E : TK) + TK / chunk + 1 + (size_t)copies * ((T + chunk - 1) / chunk);
 }
 
 // K parts of each down unit: when the routing can yield fewer than four down units per
@@ -1689,7 +2095,8 @@ int validate(const megamoe_desc* d) {
 
 struct DeviceInfo {
   int cus = 0;
-  int experts_per_cu = 0;  // resident k_experts workgroups per CU
+  int experts_per_cu = 0;     // resident k_experts workgroups per CU
+  int experts_mx_per_cu = 0;  // resident k_experts_mx workgroups per CU
 };
 
 int device_info(DeviceInfo* out) {
@@ -1702,6 +2109,9 @@ int device_info(DeviceInfo* out) {
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return MEGAMOE_ERR_HIP;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_experts, 256, 0) != hipSuccess) return MEGAMOE_ERR_HIP;
     di.experts_per_cu = per_cu > 0 ? per_cu : 1;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_experts_mx, 256, 0) != hipSuccess)
+      return MEGAMOE_ERR_HIP;
+    di.experts_mx_per_cu = per_cu > 0 ? per_cu : 1;
     di.cus = cus > 0 ? cus : 1;
   }
   *out = di;
@@ -1831,7 +2241,8 @@ int forward_impl(const megamoe_desc* desc, const megamoe_tensors* t, hipStream_t
                 (int*)(ws + L.ready)};
   const int nbI = I / kBlock, nbH = H / kBlock;
   const size_t lds = ((size_t)E * (1 + (T + 31) / 32) + 32) * 4;
-  hipLaunchKernelGGL(k_permute, dim3(1), dim3(1024), lds, st, t->expert_ids, T, K, E, S, nbI, nbH, L.ks, po);
+  hipLaunchKernelGGL(k_permute, dim3(1), dim3(1024), lds, st, t->expert_ids, T, K, E, S, nbI, nbH, L.ks, kChunkRows,
+                     po);
   MEGAMOE_LAUNCH_CHECK();
   if (mark(3) != hipSuccess) return MEGAMOE_ERR_HIP;
 
@@ -1880,11 +2291,140 @@ int forward_impl(const megamoe_desc* desc, const megamoe_tensors* t, hipStream_t
   return MEGAMOE_OK;
 }
 
+// -- The MXFP4 form ----------------------------------------------------------------------
+
+constexpr int kStagesMx = 3;  // permute, experts, combine
+
+int validate_mx(const megamoe_desc* d) {
+  if (!d) return MEGAMOE_ERR_INVALID_ARGUMENT;
+  if (d->tokens < 0 || d->hidden <= 0 || d->experts <= 0 || d->topk <= 0 || d->intermediate <= 0 ||
+      d->shared_experts != 0)
+    return MEGAMOE_ERR_SHAPE;
+  if (d->hidden % kMxStageK || d->intermediate % kMxStageK || d->topk > d->experts) return MEGAMOE_ERR_SHAPE;
+  if (d->experts > kMaxExperts || d->topk > kMaxTopK) return MEGAMOE_ERR_UNSUPPORTED;
+  const size_t words = ((size_t)d->tokens + 31) / 32;
+  if (((size_t)d->experts * (1 + words) + 32) * 4 > 64 * 1024) return MEGAMOE_ERR_UNSUPPORTED;
+  if ((size_t)d->tokens * d->topk >= ((size_t)1 << 21) - kMaxExperts * 64) return MEGAMOE_ERR_UNSUPPORTED;
+  return MEGAMOE_OK;
+}
+
+struct LayoutMx {
+  size_t counts, offsets, meta, perm, inv, gu, dn, dn_of_gu, ready, hq, hs, d, p, spare, total;
+  int ks, hs_ld;
+};
+
+// K parts of the down units, as down_splits for the fp8 form, over stages of 256.
+int down_splits_mx(const megamoe_desc& d) {
+  const size_t nbH = d.hidden / kBlock, nst = d.intermediate / kMxStageK;
+  const size_t hit = (size_t)(d.experts < (int64_t)d.tokens * d.topk ? d.experts : (int64_t)d.tokens * d.topk);
+  const size_t units = hit * nbH, target = 4 * 512;
+  int ks = 1;
+  while (ks < 8 && units * ks < target && nst % (2 * ks) == 0) ks *= 2;
+  return ks;
+}
+
+LayoutMx make_layout_mx(const megamoe_desc& d) {
+  LayoutMx L{};
+  const size_t T = d.tokens, H = d.hidden, E = d.experts, K = d.topk, I = d.intermediate;
+  size_t at = 0;
+  auto take = [&](size_t bytes) {
+    const size_t o = at;
+    at += align_up(bytes > 0 ? bytes : 1);
+    return o;
+  };
+  const size_t chunks = max_chunks(d, 0, kChunkRowsMx);
+  L.counts = take(E * sizeof(int));
+  L.offsets = take((E + 1) * sizeof(int));
+  L.meta = take(kMetaInts * sizeof(int));
+  L.perm = take(T * K * sizeof(int));
+  L.inv = take(T * K * sizeof(int));
+  L.gu = take(chunks * sizeof(int4));
+  L.dn = take(chunks * sizeof(int4));
+  L.dn_of_gu = take(chunks * sizeof(int));
+  L.ready = take(chunks * sizeof(int));
+  L.hq = take(T * K * I);
+  L.hs_ld = (int)((I / 32 + 127) / 128 * 128);  // each row's scale bytes on lines of their own
+  L.hs = take(T * K * (size_t)L.hs_ld);
+  L.d = take(T * K * H * 2);
+  L.ks = down_splits_mx(d);
+  L.p = take(L.ks > 1 ? L.ks * T * K * H * sizeof(float) : 0);
+  L.spare = take(16 * (H > I ? H : I) / 2);
+  L.total = at;
+  return L;
+}
+
+int forward_mx_impl(const megamoe_desc* desc, float limit, const megamoe_mx_tensors* t, hipStream_t st,
+                    hipEvent_t* ev) {
+  int rc = validate_mx(desc);
+  if (rc) return rc;
+  if (!t || !(limit > 0.0f)) return MEGAMOE_ERR_INVALID_ARGUMENT;
+  const megamoe_desc& d = *desc;
+  auto mark = [&](int i) { return ev ? hipEventRecord(ev[i], st) : hipSuccess; };
+  if (d.tokens == 0) {
+    for (int i = 0; i < kStagesMx + 1; ++i)
+      if (mark(i) != hipSuccess) return MEGAMOE_ERR_HIP;
+    return MEGAMOE_OK;
+  }
+  if (!t->x || !t->x_scales || !t->topk_idx || !t->topk_weights || !t->l1_blocks || !t->l1_scales ||
+      !t->l2_blocks || !t->l2_scales || !t->y || !t->workspace)
+    return MEGAMOE_ERR_INVALID_ARGUMENT;
+  const LayoutMx L = make_layout_mx(d);
+  if (t->workspace_bytes < L.total) return MEGAMOE_ERR_WORKSPACE;
+  DeviceInfo di;
+  if ((rc = device_info(&di))) return rc;
+  char* ws = (char*)t->workspace;
+  const int T = d.tokens, H = d.hidden, E = d.experts, K = d.topk, I = d.intermediate;
+  const int nbI = I / kBlock, nbH = H / kBlock;
+
+  if (mark(0) != hipSuccess) return MEGAMOE_ERR_HIP;
+  PermuteOut po{(int*)(ws + L.counts), (int*)(ws + L.offsets), (int*)(ws + L.meta), (int*)(ws + L.perm),
+                (int*)(ws + L.inv),    (int4*)(ws + L.gu),     (int4*)(ws + L.dn),  (int*)(ws + L.dn_of_gu),
+                (int*)(ws + L.ready)};
+  const size_t lds = ((size_t)E * (1 + (T + 31) / 32) + 32) * 4;
+  hipLaunchKernelGGL(k_permute, dim3(1), dim3(1024), lds, st, t->topk_idx, T, K, E, 0, nbI, nbH, L.ks, kChunkRowsMx,
+                     po);
+  MEGAMOE_LAUNCH_CHECK();
+  if (mark(1) != hipSuccess) return MEGAMOE_ERR_HIP;
+
+  ExpertMxArgs ea;
+  GateUpMxArgs& ga = ea.gu;
+  ga.x = t->x; ga.xs = t->x_scales; ga.wts = t->topk_weights;
+  ga.l1 = t->l1_blocks; ga.l1s = t->l1_scales;
+  ga.offsets = po.offsets; ga.perm = po.perm; ga.chunks = po.gu; ga.meta = po.meta;
+  ga.hq = (uint8_t*)(ws + L.hq); ga.hs = (uint8_t*)(ws + L.hs);
+  ga.spare = (const uint8_t*)(ws + L.spare);
+  ga.T = T; ga.H = H; ga.I = I; ga.K = K; ga.E = E; ga.hs_ld = L.hs_ld; ga.limit = limit;
+  DownMxArgs& da = ea.dn;
+  da.l2 = t->l2_blocks; da.l2s = t->l2_scales;
+  da.offsets = po.offsets; da.perm = po.perm; da.chunks = po.dn; da.meta = po.meta;
+  da.hq = ga.hq; da.hs = ga.hs;
+  da.d = (uint16_t*)(ws + L.d); da.pd = (float*)(ws + L.p);
+  da.spare = ga.spare;
+  da.T = T; da.H = H; da.I = I; da.K = K; da.E = E; da.hs_ld = L.hs_ld; da.ks = L.ks;
+  ea.dn_of_gu = po.dn_of_gu;
+  ea.ready = po.ready;
+  const size_t chunks = max_chunks(d, 0, kChunkRowsMx);
+  const size_t units_max = chunks * (size_t)nbI + chunks * (size_t)nbH * L.ks;
+  const size_t resident = (size_t)di.cus * di.experts_mx_per_cu;
+  hipLaunchKernelGGL(k_experts_mx, dim3((unsigned)(units_max < resident ? units_max : resident)), dim3(256), 0, st,
+                     ea);
+  MEGAMOE_LAUNCH_CHECK();
+  if (mark(2) != hipSuccess) return MEGAMOE_ERR_HIP;
+
+  const int rows8 = T * (H / 8);
+  hipLaunchKernelGGL(k_combine, dim3((rows8 + 255) / 256), dim3(256), 0, st, (const uint16_t*)da.d,
+                     (const uint16_t*)nullptr, (const float*)da.pd, (const float*)nullptr, L.ks, (const int*)po.inv,
+                     (const float*)nullptr, T, H, K, 0, (const int*)po.meta, (const uint16_t*)nullptr, (uint16_t*)t->y);
+  MEGAMOE_LAUNCH_CHECK();
+  if (mark(3) != hipSuccess) return MEGAMOE_ERR_HIP;
+  return MEGAMOE_OK;
+}
+
 }  // namespace
 
 extern "C" {
 
-int megamoe_abi_version(void) { return 2; }
+int megamoe_abi_version(void) { return 3; }
 
 const char* megamoe_status_string(int status) {
   switch (status) {
@@ -1969,6 +2509,26 @@ int megamoe_block_forward(const megamoe_desc* desc, const megamoe_tensors* t, co
     }
   }
   return forward_impl(desc, t, (hipStream_t)stream, events ? ev : nullptr, block);
+}
+
+int megamoe_mx_workspace_bytes(const megamoe_desc* desc, size_t* bytes) {
+  if (!bytes) return MEGAMOE_ERR_INVALID_ARGUMENT;
+  const int rc = validate_mx(desc);
+  if (rc) return rc;
+  *bytes = make_layout_mx(*desc).total;
+  return MEGAMOE_OK;
+}
+
+int megamoe_mx_forward(const megamoe_desc* desc, float swiglu_limit, const megamoe_mx_tensors* t, void* stream,
+                       void* const* events) {
+  hipEvent_t ev[kStagesMx + 1];
+  if (events) {
+    for (int i = 0; i < kStagesMx + 1; ++i) {
+      if (!events[i]) return MEGAMOE_ERR_INVALID_ARGUMENT;
+      ev[i] = (hipEvent_t)events[i];
+    }
+  }
+  return forward_mx_impl(desc, swiglu_limit, t, (hipStream_t)stream, events ? ev : nullptr);
 }
 
 int megamoe_rms_norm(int32_t rows, int32_t cols, const void* x, const void* weight, float eps,

@@ -8,6 +8,11 @@ returns ``{"y", "expert_ids", "expert_weights"}`` with the dtypes and shapes of
 the reference outputs. All work is issued on torch's current stream through
 the C ABI of libmegamoe.so; there is no other code path.
 
+A case in the MXFP4 form (``format="mxfp4"``, megamoe.py numerics) takes ``x`` (E4M3),
+``x_scales`` (E8M0 per 32), ``topk_idx``, ``topk_weights`` and the MXFP4 expert stacks
+``l1_blocks``/``l1_scales``/``l2_blocks``/``l2_scales`` and returns ``{"y"}`` as
+megamoe.reference does, through megamoe_mx_forward.
+
 A case in the block form (``norm``/``residual`` set) takes ``x`` as the block input
 and ``ln2`` (bf16 [H]) as the RMSNorm gamma, and returns y = x + bf16(layer(rms(x)))
 (frontier.py:335-354) through megamoe_block_forward.
@@ -55,9 +60,11 @@ class MoELayer:
         self.case = case
         self.lib = _lib.load()
         self.desc = make_desc(case)
+        self.mx = case.format == "mxfp4"
+        self.stages = _lib.STAGES_MX if self.mx else _lib.STAGES
         size = ctypes.c_size_t(0)
-        _lib.check(self.lib.megamoe_workspace_bytes(ctypes.byref(self.desc), ctypes.byref(size)),
-                   f"{case.id}: workspace size")
+        sizer = self.lib.megamoe_mx_workspace_bytes if self.mx else self.lib.megamoe_workspace_bytes
+        _lib.check(sizer(ctypes.byref(self.desc), ctypes.byref(size)), f"{case.id}: workspace size")
         self.workspace_bytes = int(size.value)
         self._workspace: dict[torch.device, torch.Tensor] = {}
         self.block = None if case.norm == "none" and not case.residual else (case.norm, case.residual)
@@ -68,6 +75,40 @@ class MoELayer:
             ws = torch.empty(self.workspace_bytes, dtype=torch.uint8, device=device)
             self._workspace[device] = ws
         return ws
+
+    def check_mx_inputs(self, inputs: dict) -> torch.device:
+        c = self.case
+        T, H, E, K, I = c.tokens, c.hidden, c.experts, c.topk, c.intermediate
+        x = inputs.get("x")
+        if not isinstance(x, torch.Tensor):
+            raise ValueError("inputs must hold 'x'")
+        device = x.device
+        if device.type != "cuda":
+            raise RuntimeError(f"the HIP layer runs on a GPU; inputs are on {device}")
+        u8 = torch.uint8
+        _expect(x, "x", torch.float8_e4m3fn, (T, H), device)
+        _expect(inputs.get("x_scales"), "x_scales", u8, (T, H // 32), device)
+        _expect(inputs.get("topk_idx"), "topk_idx", torch.int64, (T, K), device)
+        _expect(inputs.get("topk_weights"), "topk_weights", torch.float32, (T, K), device)
+        _expect(inputs.get("l1_blocks"), "l1_blocks", u8, (E, 2 * I, H // 32, 16), device)
+        _expect(inputs.get("l1_scales"), "l1_scales", u8, (E, 2 * I, H // 32), device)
+        _expect(inputs.get("l2_blocks"), "l2_blocks", u8, (E, H, I // 32, 16), device)
+        _expect(inputs.get("l2_scales"), "l2_scales", u8, (E, H, I // 32), device)
+        return device
+
+    def _call_mx(self, inputs: dict, events=None) -> dict:
+        device = self.check_mx_inputs(inputs)
+        c = self.case
+        y = torch.empty((c.tokens, c.hidden), dtype=torch.bfloat16, device=device)
+        ws = self.workspace(device)
+        ptr = {name: inputs[name].data_ptr() for name in _lib.MX_TENSOR_FIELDS if name not in ("y", "workspace")}
+        tensors = _lib.MxTensors(**ptr, y=y.data_ptr(), workspace=ws.data_ptr(), workspace_bytes=self.workspace_bytes)
+        stream = ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+        handles = None if events is None else (ctypes.c_void_p * len(events))(*[e.cuda_event for e in events])
+        with torch.cuda.device(device):
+            _lib.check(self.lib.megamoe_mx_forward(ctypes.byref(self.desc), float(c.swiglu_limit),
+                                                   ctypes.byref(tensors), stream, handles), f"{c.id}: forward")
+        return {"y": y}
 
     def check_inputs(self, inputs: dict) -> torch.device:
         c = self.case
@@ -103,6 +144,10 @@ class MoELayer:
         return device
 
     def _call(self, inputs: dict, timed: bool, events=None):
+        if self.mx:
+            if timed:
+                raise ValueError("timed() covers the fp8 layer form; use record() for the MXFP4 form")
+            return self._call_mx(inputs, events)
         device = self.check_inputs(inputs)
         c = self.case
         y = torch.empty((c.tokens, c.hidden), dtype=torch.bfloat16, device=device)
@@ -155,8 +200,8 @@ class MoELayer:
     def record(self, inputs: dict, events) -> dict:
         """One asynchronous call that records ``events`` (len(STAGES) + 1 torch.cuda.Event
         objects, each recorded once before so its HIP event exists) at the stage boundaries."""
-        if len(events) != len(_lib.STAGES) + 1 or not all(e.cuda_event for e in events):
-            raise ValueError("record() takes len(STAGES) + 1 created events")
+        if len(events) != len(self.stages) + 1 or not all(e.cuda_event for e in events):
+            raise ValueError("record() takes len(self.stages) + 1 created events")
         return self._call(inputs, timed=False, events=events)
 
 

@@ -77,7 +77,72 @@ def router_bias(case: Case, seed: int, device) -> torch.Tensor | None:
     return (case.zipf_c * ranks.pow(-case.zipf_s)).float().to(device)
 
 
+# -- MXFP4 form (megamoe.py numerics) ---------------------------------------------------
+
+MX = 32       # E8M0 block of the MXFP4 weights and of the E4M3 activations
+L1_GAIN = 4   # gate/up outputs of std ~4, so ~1% of them reach the SwiGLU clamp of 10 (megamoe.py:41)
+
+
+def pack_mxfp4(m: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """E2M1 codes packed two per byte (even element in the low nibble) [..., n/32, 16] and
+    E8M0 scales [..., n/32] of an fp32 matrix (the format of quantization.py:13-40): scale
+    exponent ceil(log2(amax/6)) clamped to [-126, 127], codes rounded to nearest with ties
+    to the even code. The rounding runs per binade of the E2M1 grid: steps of 1/2 below 2,
+    of 1 up to 4, of 2 up to 6, each a half-to-even round of the scaled magnitude."""
+    g = m.float().unflatten(-1, (-1, MX))
+    amax = g.abs().amax(-1)
+    e = torch.ceil(torch.log2((amax / 6.0).clamp_min(2.0 ** -126))).clamp(-126, 127).to(torch.int32)
+    n = torch.ldexp(g, -e[..., None].float())
+    a = n.abs()
+    mag = torch.where(a < 2.0, torch.round(a * 2.0) / 2.0,
+                      torch.where(a < 4.0, torch.round(a), torch.round(a / 2.0) * 2.0))
+    # magnitude -> code: 0, .5, 1, 1.5, 2 -> 0..4; 3 -> 5; 4 -> 6; 6 -> 7
+    code = torch.where(mag <= 2.0, mag * 2.0, torch.where(mag == 3.0, 5.0, torch.where(mag == 4.0, 6.0, 7.0)))
+    code = code.to(torch.uint8) | ((n < 0).to(torch.uint8) << 3)
+    return (code[..., 0::2] | (code[..., 1::2] << 4)).contiguous(), (e + 127).to(torch.uint8)
+
+
+def pack_e4m3_e8m0(v: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """E4M3 payload and E8M0 scale exponents per row per 32 columns (quantization.py:67-109,
+    scale_format='e8m0'): the exponent comes from the fp32 bits of the block amax, raised by
+    one where its mantissa exceeds 1.75's, less 448's exponent, floored at 1e-4/448's."""
+    g = v.float().unflatten(-1, (-1, MX))
+    bits = g.abs().amax(-1).contiguous().view(torch.int32).to(torch.int64)
+    e = (((bits + (0x7FFFFF - 0x600000)) >> 23).clamp_min(105 + 8) - 8).to(torch.int32)
+    inv = ((254 - e) << 23).view(torch.float32)
+    return (g * inv[..., None]).to(torch.float8_e4m3fn).flatten(-2).contiguous(), e.to(torch.uint8)
+
+
+def mx_routing(case: Case, seed: int, device) -> tuple[torch.Tensor, torch.Tensor]:
+    """Distinct experts per token from a log-normal popularity plus Gumbel noise (top-k),
+    weights sqrt(softplus(N(0,1))) normalized to the routed scaling (the scheme of
+    megamoe.py:59-73, with this build's own seeded streams)."""
+    T, E, K = case.tokens, case.experts, case.topk
+    pop = _normal(seed, "expert_popularity", (E,), 0.4, device)
+    gen = torch.Generator(device=device).manual_seed(seed_for(seed, "route_noise"))
+    u = torch.rand((T, E), generator=gen, device=device).clamp(1e-12, 1 - 1e-7)
+    idx = (pop + (-torch.log(-torch.log(u)))).topk(K, -1).indices
+    score = torch.nn.functional.softplus(_normal(seed, "route_logits", (T, K), 1.0, device)).sqrt()
+    return idx.to(torch.int64).contiguous(), (score / score.sum(-1, keepdim=True) * case.routed_scaling).contiguous()
+
+
+def make_mx_inputs(case: Case, seed: int, device="cpu") -> dict[str, torch.Tensor]:
+    T, H, E, I = case.tokens, case.hidden, case.experts, case.intermediate
+    values = {}
+    values["x"], values["x_scales"] = pack_e4m3_e8m0(_normal(seed, "x", (T, H), 1.0, device))
+    values["topk_idx"], values["topk_weights"] = mx_routing(case, seed, device)
+    for name, rows, cols, std in (("l1", 2 * I, H, L1_GAIN / H ** 0.5), ("l2", H, I, 1.0 / I ** 0.5)):
+        blocks = torch.empty((E, rows, cols // MX, MX // 2), dtype=torch.uint8, device=device)
+        scales = torch.empty((E, rows, cols // MX), dtype=torch.uint8, device=device)
+        for e in range(E):
+            blocks[e], scales[e] = pack_mxfp4(_normal(seed, f"{name}:{e}", (rows, cols), std, device))
+        values[name + "_blocks"], values[name + "_scales"] = blocks, scales
+    return values
+
+
 def make_inputs(case: Case, seed: int, device="cpu") -> dict[str, torch.Tensor]:
+    if case.format == "mxfp4":
+        return make_mx_inputs(case, seed, device)
     T, H, E, I, S = case.tokens, case.hidden, case.experts, case.intermediate, case.shared_experts
     std, pw = case.weight_std, case.power_of_two
     values: dict[str, torch.Tensor] = {}
@@ -98,6 +163,8 @@ def make_inputs(case: Case, seed: int, device="cpu") -> dict[str, torch.Tensor]:
 
 
 def input_names(case: Case) -> list[str]:
+    if case.format == "mxfp4":
+        return ["x", "x_scales", "topk_idx", "topk_weights", "l1_blocks", "l1_scales", "l2_blocks", "l2_scales"]
     names = ["x", "router"]
     if case.norm != "none":
         names.append("ln2")
