@@ -31,6 +31,7 @@
 
 #include <hip/hip_runtime.h>
 #include <math.h>
+#include <type_traits>
 #include <stdint.h>
 #include <string.h>
 
@@ -1635,6 +1636,16 @@ __global__ __launch_bounds__(256, 2) void k_experts(ExpertArgs args) {
 
 constexpr int kMxStageK = 256;
 
+// Calls f(std::integral_constant<int, I>{}) for I = B .. E-1 (a loop whose index is a
+// compile-time constant in the body).
+template <int B, int E, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
+
 __device__ __forceinline__ f32x4 mfma_e2m1_e4m3(const i32x4& a, const i32x8& b, f32x4 c, int sa, int sb) {
   const i32x8 a8 = {a[0], a[1], a[2], a[3], 0, 0, 0, 0};
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a8, b, c, 4, 0, 0, sa, 0, sb);
@@ -1652,7 +1663,7 @@ template <int RT, int NCT>
 struct StageMx {
   i32x8 b[NCT][2];  // activations of the stage's two 128-K steps
   uint2 sb[NCT];    // activation E8M0 bytes [8p, 8p+8) of the lane's token row
-  uint2 sa[RT];     // weight E8M0 bytes [8p, 8p+8) of the lane's row in each tile
+  uint2 sa[RT];     // weight E8M0 bytes [8p, 8p+8) of the lane's row in each tile (per-stage loads)
 };
 
 template <int RT, int NCT>
@@ -1680,8 +1691,8 @@ __device__ __forceinline__ void issue_a_mx(uint8_t* slot, const OperandsMx<RT, N
   }
 }
 
-// 5*NCT + RT vector loads.
-template <int RT, int NCT>
+// 4*NCT vector loads, plus NCT + RT for the scales of stage p when SCALES.
+template <bool SCALES, int RT, int NCT>
 __device__ __forceinline__ void load_stage_mx(StageMx<RT, NCT>& s, const OperandsMx<RT, NCT>& op, int p) {
   const size_t o = (size_t)p * kMxStageK;
 #pragma unroll
@@ -1689,10 +1700,28 @@ __device__ __forceinline__ void load_stage_mx(StageMx<RT, NCT>& s, const Operand
     s.b[c][0] = load_k32(op.b[c] + o);
     s.b[c][1] = load_k32(op.b[c] + o + 128);
   }
+  if constexpr (SCALES) {
 #pragma unroll
-  for (int c = 0; c < NCT; ++c) s.sb[c] = *reinterpret_cast<const uint2*>(op.sb[c] + 8 * p);
+    for (int c = 0; c < NCT; ++c) s.sb[c] = *reinterpret_cast<const uint2*>(op.sb[c] + 8 * p);
 #pragma unroll
-  for (int t = 0; t < RT; ++t) s.sa[t] = *reinterpret_cast<const uint2*>(op.sa[t] + 8 * p);
+    for (int t = 0; t < RT; ++t) s.sa[t] = *reinterpret_cast<const uint2*>(op.sa[t] + 8 * p);
+  }
+}
+
+// The weight and activation scales of the stage pair starting at the even stage pa
+// (RT + NCT vector loads).
+template <int RT, int NCT>
+struct PairMx {
+  uint4 sa[RT];
+  uint4 sb[NCT];
+};
+
+template <int RT, int NCT>
+__device__ __forceinline__ void load_pair_mx(PairMx<RT, NCT>& q, const OperandsMx<RT, NCT>& op, int pa) {
+#pragma unroll
+  for (int c = 0; c < NCT; ++c) q.sb[c] = *reinterpret_cast<const uint4*>(op.sb[c] + 8 * pa);
+#pragma unroll
+  for (int t = 0; t < RT; ++t) q.sa[t] = *reinterpret_cast<const uint4*>(op.sa[t] + 8 * pa);
 }
 
 template <int RT>
@@ -1713,22 +1742,24 @@ __device__ __forceinline__ void read_slot_mx(i32x4 (&lo)[RT], i32x4 (&hi)[RT], u
   }
 }
 
-// `shift` = 8 * (lane / 16): the lane's byte in each scale word. The scale bytes pass an
-// empty asm (as in mfma_stage) so their extraction stays after the stage's wait.
+// `shift` = 8 * (lane / 16): the lane's byte in each scale word; `saw` and `sbw` hold the
+// weight and activation scale words of the stage. The scale bytes pass an empty asm (as in mfma_stage) so their
+// extraction stays after the stage's wait.
 template <int RT, int NCT>
 __device__ __forceinline__ void mfma_stage_mx(const i32x4 (&lo)[RT], const i32x4 (&hi)[RT], const StageMx<RT, NCT>& s,
-                                              int shift, f32x4 (&acc)[RT][NCT]) {
+                                              const uint2 (&saw)[RT], const uint2 (&sbw)[NCT], int shift,
+                                              f32x4 (&acc)[RT][NCT]) {
   int sa0[RT], sa1[RT], sb0[NCT], sb1[NCT];
 #pragma unroll
   for (int r = 0; r < RT; ++r) {
-    uint2 w = s.sa[r];
+    uint2 w = saw[r];
     asm volatile("" : "+v"(w.x), "+v"(w.y));
     sa0[r] = (int)((w.x >> shift) & 0xffu);
     sa1[r] = (int)((w.y >> shift) & 0xffu);
   }
 #pragma unroll
   for (int c = 0; c < NCT; ++c) {
-    uint2 w = s.sb[c];
+    uint2 w = sbw[c];
     asm volatile("" : "+v"(w.x), "+v"(w.y));
     sb0[c] = (int)((w.x >> shift) & 0xffu);
     sb1[c] = (int)((w.y >> shift) & 0xffu);
@@ -1744,14 +1775,21 @@ __device__ __forceinline__ void mfma_stage_mx(const i32x4 (&lo)[RT], const i32x4
 }
 
 // The fp8 form's stream (D slots, loads in issue order, the spare region for loads past
-// the end, a rotated start) over nst stages of 256 K elements.
-template <int RT, int NCT, int D>
+// the end, a rotated start) over nst stages of 256 K elements. The per-lane scale loads
+// touch one line per row (or token) and tile per stage; with PAIR (nst and rot even,
+// D = 2) one 16-byte load per lane and tile brings the scales of a stage pair, issued
+// with the even stage's loads into one of two pair buffers (stage p reads buffer (p / 2) % 2, so the
+// loop is unrolled by four and no register copy crosses the back edge: a copy of loaded
+// registers there makes the compiler wait for vmcnt 0).
+template <int RT, int NCT, int D, bool PAIR>
 __device__ __forceinline__ void stream_gemm_mx(const OperandsMx<RT, NCT>& op, int nst, int rot, uint8_t* ring,
                                                f32x4 (&acc)[RT][NCT],
                                                const ReadyWait& ready = ReadyWait{nullptr, 0, nullptr}) {
   constexpr int kSlot = RT * kTileBytes;
-  constexpr int kAfter = (D - 1) * (3 * RT + 5 * NCT);
+  constexpr int U = PAIR ? 4 : D;  // stages per loop trip
+  constexpr int kAfter = PAIR ? (D - 1) * (2 * RT + 4 * NCT) : (D - 1) * (3 * RT + 5 * NCT);
   static_assert(D >= 2 && D * kSlot <= kRingWave && kAfter <= 63, "LDS ring and vmcnt range");
+  static_assert(!PAIR || D == 2, "paired scale loads use two pair buffers and a two-slot ring");
   auto phys = [nst, rot](int p) {
     const int q = p + rot;
     return q >= nst ? q - nst : q;
@@ -1764,24 +1802,55 @@ __device__ __forceinline__ void stream_gemm_mx(const OperandsMx<RT, NCT>& op, in
 #pragma unroll
     for (int c = 0; c < NCT; ++c) acc[r][c] = f32x4{0.f, 0.f, 0.f, 0.f};
   StageMx<RT, NCT> st[D];
+  PairMx<RT, NCT> pair[2];
+  // The loads of stage i (logical index; its parity is a compile-time fact at each call).
+  // The pair load's address stays inside the rows: its even stage is at most nst - 2.
+  auto load = [&](auto ic, int i) {
+    constexpr int c = decltype(ic)::value;  // i modulo U
+    const int pi = phys(min(i, nst - 1));
+    load_stage_mx<!PAIR>(st[c % D], op, pi);
+    if constexpr (PAIR && c % 2 == 0) load_pair_mx(pair[(c / 2) % 2], op, phys(min(i, nst - 2)));
+  };
+  auto half = [](const uint4& q, auto odd) {
+    return decltype(odd)::value ? make_uint2(q.z, q.w) : make_uint2(q.x, q.y);
+  };
+  auto scales = [&](auto sc, uint2 (&saw)[RT], uint2 (&sbw)[NCT]) {
+    constexpr int c = decltype(sc)::value;
+    const std::integral_constant<bool, c % 2 == 1> odd{};
+#pragma unroll
+    for (int r = 0; r < RT; ++r) {
+      if constexpr (!PAIR)
+        saw[r] = st[c % D].sa[r];
+      else
+        saw[r] = half(pair[(c / 2) % 2].sa[r], odd);
+    }
+#pragma unroll
+    for (int k = 0; k < NCT; ++k) {
+      if constexpr (!PAIR)
+        sbw[k] = st[c % D].sb[k];
+      else
+        sbw[k] = half(pair[(c / 2) % 2].sb[k], odd);
+    }
+  };
 #pragma unroll
   for (int s = 0; s < D - 1; ++s) issue_a_mx(ring + s * kSlot, op, lt, phys(min(s, nst - 1)), s < nst);
   wait_ready(ready);
-#pragma unroll
-  for (int s = 0; s < D - 1; ++s) load_stage_mx(st[s], op, phys(min(s, nst - 1)));
-  for (int p0 = 0; p0 < nst; p0 += D) {
-#pragma unroll
-    for (int s = 0; s < D; ++s) {
-      const int p = p0 + s, pn = phys(min(p + D - 1, nst - 1));
-      load_stage_mx(st[(s + D - 1) % D], op, pn);
-      issue_a_mx(ring + ((s + D - 1) % D) * kSlot, op, lt, pn, p + D - 1 < nst);
+  static_for<0, D - 1>([&](auto si) { load(si, (int)decltype(si)::value); });
+  for (int p0 = 0; p0 < nst; p0 += U) {
+    static_for<0, U>([&](auto si) {
+      constexpr int s = decltype(si)::value;
+      const int p = p0 + s;
+      load(std::integral_constant<int, (s + D - 1) % U>{}, p + D - 1);
+      issue_a_mx(ring + ((s + D - 1) % D) * kSlot, op, lt, phys(min(p + D - 1, nst - 1)), p + D - 1 < nst);
       wait_vmem<kAfter>();
       if (p < nst) {
         i32x4 lo[RT], hi[RT];
-        read_slot_mx<RT>(lo, hi, ring_lds + s * kSlot + lt.rd0, ring_lds + s * kSlot + lt.rd1);
-        mfma_stage_mx(lo, hi, st[s], shift, acc);
+        uint2 saw[RT], sbw[NCT];
+        read_slot_mx<RT>(lo, hi, ring_lds + (s % D) * kSlot + lt.rd0, ring_lds + (s % D) * kSlot + lt.rd1);
+        scales(si, saw, sbw);
+        mfma_stage_mx(lo, hi, st[s % D], saw, sbw, shift, acc);
       }
-    }
+    });
   }
 }
 
@@ -1806,7 +1875,7 @@ struct GateUpMxArgs {
 //   gate, up = bf16(l1); gate = min(gate, limit); up = clamp(up, +-limit)
 //   a = gate / (1 + exp(-gate)) * up * w_slot (fp32, megamoe.py:116-122)
 //   h = E4M3(a * 2^(127-e)), e = E8M0 exponent of the block's amax (megamoe.py:125-128)
-template <int NCT>
+template <int NCT, bool PAIR>
 __device__ void gateup_mx_unit(const GateUpMxArgs& a, int e, int jb, const ChunkRows& cr, int rot, uint8_t (*red8)[64],
                                uint8_t* ring) {
   const int lane = opaque_lane(), w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1830,7 +1899,7 @@ __device__ void gateup_mx_unit(const GateUpMxArgs& a, int e, int jb, const Chunk
     op.sb[c] = a.xs + (size_t)tok * sld;
   }
   f32x4 acc[4][NCT];
-  stream_gemm_mx<4, NCT, 2>(op, H / kMxStageK, rot, ring, acc);
+  stream_gemm_mx<4, NCT, 2, PAIR>(op, H / kMxStageK, rot, ring, acc);
 
   const float L = a.limit;
 #pragma unroll
@@ -1879,11 +1948,20 @@ __device__ void gateup_mx_work(const GateUpMxArgs& a, int u, uint8_t (*red8)[64]
   const int4 ch = a.chunks[u / nbI];
   const int jb = u % nbI;
   const ChunkRows cr{ch.z, a.offsets[ch.x] + ch.y, a.perm, a.K};
-  const int rot = u % (a.H / kMxStageK);
-  if (cr.n <= 16)
-    gateup_mx_unit<1>(a, ch.x, jb, cr, rot, red8, ring);
-  else
-    gateup_mx_unit<2>(a, ch.x, jb, cr, rot, red8, ring);
+  const int nst = a.H / kMxStageK;
+  if (nst % 2 == 0) {  // paired scale loads: an even rotation keeps the pairs aligned
+    const int rot = 2 * (u % (nst / 2));
+    if (cr.n <= 16)
+      gateup_mx_unit<1, true>(a, ch.x, jb, cr, rot, red8, ring);
+    else
+      gateup_mx_unit<2, true>(a, ch.x, jb, cr, rot, red8, ring);
+  } else {
+    const int rot = u % nst;
+    if (cr.n <= 16)
+      gateup_mx_unit<1, false>(a, ch.x, jb, cr, rot, red8, ring);
+    else
+      gateup_mx_unit<2, false>(a, ch.x, jb, cr, rot, red8, ring);
+  }
 }
 
 struct DownMxArgs {
@@ -1899,7 +1977,7 @@ struct DownMxArgs {
 };
 
 // Down unit: rows [j*128, +128) of the expert's down matrix over K part kp of ks.
-template <int NCT>
+template <int NCT, bool PAIR>
 __device__ void down_mx_unit(const DownMxArgs& a, int e, int j, int kp, const ChunkRows& cr, int rot,
                              const ReadyWait& ready, uint8_t* ring) {
   const int lane = opaque_lane(), w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1921,7 +1999,7 @@ __device__ void down_mx_unit(const DownMxArgs& a, int e, int j, int kp, const Ch
     op.sb[c] = a.hs + (size_t)rr * a.hs_ld + 8 * p0;
   }
   f32x4 acc[2][NCT];
-  stream_gemm_mx<2, NCT, NCT == 2 ? 3 : 4>(op, nstp, rot, ring, acc, ready);
+  stream_gemm_mx<2, NCT, PAIR ? 2 : (NCT == 2 ? 3 : 4), PAIR>(op, nstp, rot, ring, acc, ready);
   float* pd = a.pd + (size_t)kp * a.T * a.K * a.H;
 #pragma unroll
   for (int c = 0; c < NCT; ++c) {
@@ -1947,11 +2025,20 @@ __device__ void down_mx_work(const DownMxArgs& a, int v, const ReadyWait& ready,
   const int4 ch = a.chunks[v / (nbH * a.ks)];
   const int rem = v % (nbH * a.ks), j = rem / a.ks, kp = rem % a.ks;
   const ChunkRows cr{ch.z, a.offsets[ch.x] + ch.y, a.perm, a.K};
-  const int rot = v % (a.I / kMxStageK / a.ks);
-  if (cr.n <= 16)
-    down_mx_unit<1>(a, ch.x, j, kp, cr, rot, ready, ring);
-  else
-    down_mx_unit<2>(a, ch.x, j, kp, cr, rot, ready, ring);
+  const int nstp = a.I / kMxStageK / a.ks;
+  if (nstp % 2 == 0) {
+    const int rot = 2 * (v % (nstp / 2));
+    if (cr.n <= 16)
+      down_mx_unit<1, true>(a, ch.x, j, kp, cr, rot, ready, ring);
+    else
+      down_mx_unit<2, true>(a, ch.x, j, kp, cr, rot, ready, ring);
+  } else {
+    const int rot = v % nstp;
+    if (cr.n <= 16)
+      down_mx_unit<1, false>(a, ch.x, j, kp, cr, rot, ready, ring);
+    else
+      down_mx_unit<2, false>(a, ch.x, j, kp, cr, rot, ready, ring);
+  }
 }
 
 struct ExpertMxArgs {
