@@ -221,12 +221,155 @@ def bench_case(case, steps: int, warmup: int, want_cpu: bool, cpu_budget: float)
         "roofline": {"bound": "hbm", "achieved": ex_bytes / (ex_ms * 1e-3) / 1e9, "peak": PEAK_HBM / 1e9,
                      "unit": "GB/s", "frac": ex_bytes / (ex_ms * 1e-3) / PEAK_HBM,
                      "traffic": measured_traffic(case),
-                     "kernel": "k_experts", "kernel_us": ex_ms * 1e3, "bytes_per_launch": ex_bytes},
+                     "kernel": "k_experts_mx" if case.format == "mxfp4" else "k_experts",
+                     "kernel_us": ex_ms * 1e3, "bytes_per_launch": ex_bytes},
+        "dtype": ("e2m1xe4m3->fp32 (E8M0 scales per 32; bf16 out)" if case.format == "mxfp4"
+                  else "e4m3xe4m3->fp32 (bf16 in/out)"),
     }
     if want_cpu:
         _log(f"[bench] {case.id}: CPU oracle baseline")
         result["cpu_baseline"] = cpu_baseline(case, sets[0], round(hit), cpu_budget)
     del sets
+    torch.cuda.empty_cache()
+    return result
+
+
+def cpu_baseline_ep(case, experts_cpu: dict, received: dict, hit: int, budget_s: float) -> dict:
+    """The CPU oracle of the local experts (oracle.ep.experts, BF16 schedule) on the rows of
+    the first local experts, doubling until the budget, scaled by the hit local experts."""
+    import torch
+
+    from oracle import ep as OE
+
+    threads = cpu_threads()
+    torch.set_num_threads(threads)
+    ids = received["ids"]
+    n = 1
+    while True:
+        sel = (ids < n).nonzero().flatten()
+        t0 = time.perf_counter()
+        OE.experts(case, {k: v[:n] for k, v in experts_cpu.items()}, received["rows"][sel],
+                   received["row_scales"][sel], ids[sel], received["weights"][sel], 0)
+        dt = time.perf_counter() - t0
+        sampled = len(set(ids[sel].tolist()))
+        if dt * 2 > budget_s or n * 2 > case.experts // case.ep:
+            break
+        n *= 2
+    return {"value": dt * hit / max(sampled, 1) * 1e6, "unit": "us/step", "cores": threads, "kind": "port",
+            "sample": (f"oracle.ep.experts on the received rows of local experts 0..{n - 1} ({sampled} hit, "
+                       f"{sel.numel()} rows, {dt:.2f} s), scaled by {hit}/{sampled} experts; dispatch and combine "
+                       f"not included; torch {torch.__version__} CPU, {threads} threads, "
+                       f"{platform.processor() or platform.machine()}")}
+
+
+def bench_ep_share(case, steps: int, warmup: int, want_cpu: bool, cpu_budget: float) -> dict:
+    """Rank 0's share of an EP case: its dispatch (order + pack), its local experts over the
+    rows all ranks send it, and its combine, issued back to back on one stream. The rows it
+    receives are built before timing from every rank's dispatch (the exchange is a
+    collective, not part of the share); the rows it gets back are synthetic bf16 of the
+    returned shape (the combine's cost does not depend on their values)."""
+    import dataclasses
+
+    import numpy as np
+    import torch
+
+    __graft_entry__.load_package()
+    from vibe_megakernel_amd import cases as C
+    from vibe_megakernel_amd import ep as EP
+    from vibe_megakernel_amd import workloads
+
+    dev = torch.device("cuda:0")
+    T, K, H, ep = case.tokens, case.topk, case.hidden, case.ep
+    local = case.experts // ep
+    _log(f"[bench] {case.id}: generating rank 0's share on the GPU")
+    v = workloads.make_ep_inputs(case, 7301, dev, rank=0)
+    routing = ("x", "x_scales", "topk_idx", "topk_weights")
+    sends = [EP.dispatch(*(v[k][r * T:(r + 1) * T] for k in routing), case.experts, ep) for r in range(ep)]
+    counts = [EP.send_counts(s_) for s_ in sends]
+    received = {name: torch.cat([getattr(s_, name)[:c[0]] for s_, c in zip(sends, counts)])
+                for name in ("rows", "row_scales", "ids", "weights")}
+    R = received["rows"].shape[0]
+    mine = [v[k][:T] for k in routing]
+    del sends
+    weights = ("l1_blocks", "l1_scales", "l2_blocks", "l2_scales")
+    experts = EP.Experts(*(v[k] for k in weights), 0, case.swiglu_limit)
+    ws = torch.empty(experts.workspace_bytes(R), dtype=torch.uint8, device=dev)
+    returned = torch.randn((T * K, H), device=dev).to(torch.bfloat16)
+    args = (received["rows"], received["row_scales"], received["ids"], received["weights"])
+    torch.cuda.synchronize()
+    _log(f"[bench] {case.id}: rank 0 sends {counts[0]} rows, receives {R}; warmup")
+
+    def step(events=None):
+        send = EP.dispatch(*mine, case.experts, ep)
+        if events is not None:
+            events[0].record(stream)
+        out = experts(*args, workspace=ws, events=None if events is None else events[1:5])
+        y = EP.combine(returned, send.slot_rows)
+        if events is not None:
+            events[5].record(stream)
+        return out, y
+
+    stream = torch.cuda.current_stream(dev)
+    for _ in range(warmup):
+        step()
+    _log(f"[bench] {case.id}: timing {steps} steps")
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for _ in range(steps):
+        step()
+    end.record(stream)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    per_step = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    for e0, e1 in per_step:
+        e0.record(stream)
+        step()
+        e1.record(stream)
+    torch.cuda.synchronize()
+    step_ms = [a.elapsed_time(b) for a, b in per_step]
+    # Stage boundaries: before the dispatch's first kernel is not marked (its launch comes
+    # first); events[0] follows the dispatch, the library marks the experts' three stages,
+    # events[5] follows the combine.
+    names = ("dispatch", "permute", "experts", "row_copy", "combine")
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(7)] for _ in range(steps)]
+    for row in events:
+        for e in row:
+            e.record(stream)
+    torch.cuda.synchronize()
+    for row in events:
+        row[0].record(stream)
+        step(row[1:])
+    torch.cuda.synchronize()
+    stage = [[row[j].elapsed_time(row[j + 1]) for j in range(6)] for row in events]
+    stage_ms = [statistics.mean(st[j] for st in stage) for j in range(6)]
+    # row[1] is recorded after the dispatch and row[2] by the library before its permute
+    stage_ms = [stage_ms[0] + stage_ms[1]] + stage_ms[2:]
+    hit = len(torch.unique(received["ids"]))
+    bytes_step = C.algorithmic_bytes(case, hit)
+    rows_case = dataclasses.replace(case, gpus=1, ep=1, params=dict(case.params, tokens=R, topk=1, experts=local))
+    kb = kernel_bytes(rows_case, hit)
+    ex_ms = stage_ms[names.index("experts")]
+    ex_bytes = kb["gate_up"] + kb["down"]
+    result = {
+        "case": case.id, "ms_per_step": ms, "us_per_step": ms * 1e3,
+        "p50_us": statistics.median(step_ms) * 1e3,
+        "p95_us": sorted(step_ms)[min(len(step_ms) - 1, int(0.95 * (len(step_ms) - 1) + 0.5))] * 1e3,
+        "hit_experts": hit, "bytes_per_step": bytes_step,
+        "tb_per_s": bytes_step / (ms * 1e-3) / 1e12, "hbm_frac": bytes_step / (ms * 1e-3) / PEAK_HBM,
+        "mfma_frac": 2 * R * 3 * case.intermediate * H / (ms * 1e-3) / PEAK_FP8,
+        "stage_us": {name: x * 1e3 for name, x in zip(names, stage_ms)},
+        "rotation_sets": 1, "received_rows": R, "sent_rows": T * K,
+        "roofline": {"bound": "hbm", "achieved": ex_bytes / (ex_ms * 1e-3) / 1e9, "peak": PEAK_HBM / 1e9,
+                     "unit": "GB/s", "frac": ex_bytes / (ex_ms * 1e-3) / PEAK_HBM, "traffic": None,
+                     "kernel": "k_experts_mx", "kernel_us": ex_ms * 1e3, "bytes_per_launch": ex_bytes},
+        "dtype": "e2m1xe4m3->fp32 (E8M0 scales per 32; bf16 out)",
+    }
+    if want_cpu:
+        _log(f"[bench] {case.id}: CPU oracle baseline")
+        result["cpu_baseline"] = cpu_baseline_ep(case, {k: v[k].cpu() for k in weights},
+                                                 {k: x.cpu() for k, x in received.items()}, hit, cpu_budget)
+    del v, received
     torch.cuda.empty_cache()
     return result
 
@@ -260,7 +403,8 @@ def main() -> int:
         copy_probe(args.copy_probe_mib)
     head = C.case(args.case or C.HEADLINE)
     others = [c for c in C.CASES if c.id != head.id] if args.all else []
-    r = bench_case(head, args.steps, args.warmup, not args.no_cpu_baseline, args.cpu_budget)
+    run = bench_ep_share if head.ep > 1 else bench_case
+    r = run(head, args.steps, args.warmup, not args.no_cpu_baseline, args.cpu_budget)
     # Each other config runs in a child process of its own, on a fresh device heap: after a
     # config's inputs (up to 17 GB) are allocated and freed in this process, the next
     # config's weights land in fragmented memory and its expert kernel measures a few
@@ -279,11 +423,12 @@ def main() -> int:
                    f"MoE decode layer \u00b5s/step + achieved HBM TB/s (% of peak), {head.id}, 1 GPU"),
         "value": r["us_per_step"], "unit": "us/step", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": r["ms_per_step"], "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
-        "dtype": "e4m3xe4m3->fp32 (bf16 in/out)", "data": "synthetic (seeded, generated on the GPU)",
+        "dtype": r["dtype"], "data": "synthetic (seeded, generated on the GPU)",
         "config": {"workload": head.id, "tokens": head.tokens, "hidden": head.hidden, "experts": head.experts,
                    "shared_experts": head.shared_experts, "topk": head.topk, "intermediate": head.intermediate,
                    "router": head.router, "groups": head.groups, "top_groups": head.top_groups,
-                   "parallelism": "single GPU"},
+                   "parallelism": (f"rank 0 of ep{head.ep} (its dispatch, local experts and combine; the "
+                                   "exchanges are not run)" if head.ep > 1 else "single GPU")},
         "achieved_tb_per_s": r["tb_per_s"], "hbm_frac": r["hbm_frac"], "p50_us": r["p50_us"], "p95_us": r["p95_us"],
         "hit_experts": r["hit_experts"], "bytes_per_step": r["bytes_per_step"], "stage_us": r["stage_us"],
         "mfma_frac": r["mfma_frac"],

@@ -211,6 +211,53 @@ int megamoe_mx_workspace_bytes(const megamoe_desc* desc, size_t* bytes);
 int megamoe_mx_forward(const megamoe_desc* desc, float swiglu_limit, const megamoe_mx_tensors* t, void* stream,
                        void* const* events);
 
+/* Expert parallelism, one rank's share (megamoe.py:153-182 with ep ranks): expert e belongs
+ * to rank e / (E/ep). A rank sends each (token, slot) row to the owner of the slot's expert,
+ * runs its local experts over the rows it receives, and sums the outputs that come back.
+ * The two exchanges between these calls (all_to_all_single, parallel.py:52-68) are the
+ * caller's collectives.
+ *
+ * The send buffers of megamoe_ep_dispatch, for this rank's T tokens (T*K rows):
+ *   rows        uint8 [T*K, H] (E4M3 bytes);  row_scales uint8 [T*K, H/32] (E8M0)
+ *   ids         int64 [T*K] (global expert ids);  weights fp32 [T*K]
+ *   counts      int64 [ep] rows per destination rank, in rank order
+ *   slot_rows   int32 [T*K] send row of (token t, slot k) at t*K + k */
+typedef struct megamoe_ep_send {
+  uint8_t* rows;
+  uint8_t* row_scales;
+  int64_t* ids;
+  float* weights;
+  int64_t* counts;
+  int32_t* slot_rows;
+} megamoe_ep_send;
+
+/* Dispatch (megamoe.py:160-171, and the send counts of parallel.py:59-68): the rows in a
+ * stable order by owner rank, so each destination receives this rank's rows in (token,
+ * slot) order. desc: tokens, hidden (a multiple of 256), experts (divisible by ep), topk;
+ * t: x, x_scales, topk_idx, topk_weights (16- and 8-byte aligned x and x_scales, as the send
+ * rows and row scales). An id outside [0, E) makes every count -1 and every slot row -1, and
+ * nothing is packed. */
+int megamoe_ep_dispatch(const megamoe_desc* desc, int32_t ep, const megamoe_mx_tensors* t,
+                        const megamoe_ep_send* send, void* stream);
+
+/* The local experts over the received rows (megamoe.py:131-150): desc.tokens = R received
+ * rows, desc.topk = 1, desc.experts = E/ep local experts; t->x, x_scales are the received
+ * rows and scales, topk_idx their global ids (int64 [R], each in [expert_base, expert_base +
+ * E/ep)), topk_weights [R]; l1/l2 hold the local experts only; y = bf16 [R, H], each row's
+ * weighted expert output (the returned payload). Rows are computed exactly as in
+ * megamoe_mx_forward, whose result for a row depends only on the row, its expert's weights
+ * and the layer's down-projection split, so a rank's rows equal the serial layer's bit for
+ * bit when the splits agree (they do whenever both have at least 2048 down units of 128
+ * rows). Workspace: megamoe_mx_workspace_bytes(desc). Bad ids make every element NaN. */
+int megamoe_ep_experts(const megamoe_desc* desc, float swiglu_limit, int64_t expert_base, const megamoe_mx_tensors* t,
+                       void* stream, void* const* events);
+
+/* Combine at the source (megamoe.py:176-182): returned = bf16 [T*K, H], the outputs of this
+ * rank's send rows in send order; y[t] = bf16(fp32 sum over slots k in order of
+ * returned[slot_rows[t*K + k]]). A slot row of -1 makes the token's row NaN. */
+int megamoe_ep_combine(int32_t tokens, int32_t hidden, int32_t topk, const void* returned, const int32_t* slot_rows,
+                       void* y, void* stream);
+
 /* Dynamic E4M3 quantization of bf16 rows [rows, cols] with one fp32 scale
  * per row per 128 columns (the last block may be partial; padding counts as
  * zero): q e4m3fn [rows, cols], scales fp32 [rows, ceil(cols/128)].
@@ -222,8 +269,9 @@ int megamoe_quantize_rows(int32_t rows, int32_t cols, const void* x, uint8_t* q,
 /* Text for a status code (static storage). */
 const char* megamoe_status_string(int status);
 
-/* ABI version of this library: 3 (1, plus megamoe_block_forward and megamoe_rms_norm in 2,
- * plus megamoe_mx_workspace_bytes and megamoe_mx_forward in 3). */
+/* ABI version of this library: 4 (1, plus megamoe_block_forward and megamoe_rms_norm in 2,
+ * plus megamoe_mx_workspace_bytes and megamoe_mx_forward in 3, plus megamoe_ep_dispatch,
+ * megamoe_ep_experts and megamoe_ep_combine in 4). */
 int megamoe_abi_version(void);
 
 #ifdef __cplusplus

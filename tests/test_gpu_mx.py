@@ -40,8 +40,11 @@ def _check(case, y, want, exact):
 
 def _dev_cases():
     base = C.case(MXCASE)
+    # 1-30 rows per expert (narrow units), about 35 (wide, one tile per wave) and about 150
+    # (a wide chunk of 128 rows with two tiles per wave, plus a narrow remainder).
     return [C.development(base), C.development(base, tokens=37, experts=8, topk=4),
-            C.development(base, tokens=70, experts=4, topk=2, hidden=512, intermediate=512)]
+            C.development(base, tokens=70, experts=4, topk=2, hidden=512, intermediate=512),
+            C.development(base, tokens=300, experts=4, topk=2)]
 
 
 @pytest.mark.parametrize("case", _dev_cases(), ids=lambda c: f"T{c.tokens}-E{c.experts}-H{c.hidden}")

@@ -22,8 +22,8 @@ STAGES_MX = ("permute", "experts", "combine")  # the MXFP4 form (routing and x a
 SYMBOLS = ("megamoe_workspace_bytes", "megamoe_forward", "megamoe_forward_events", "megamoe_forward_timed",
            "megamoe_router_logits", "megamoe_route", "megamoe_quantize_rows", "megamoe_status_string",
            "megamoe_abi_version", "megamoe_block_forward", "megamoe_rms_norm", "megamoe_mx_workspace_bytes",
-           "megamoe_mx_forward")
-ABI_VERSION = 3
+           "megamoe_mx_forward", "megamoe_ep_dispatch", "megamoe_ep_experts", "megamoe_ep_combine")
+ABI_VERSION = 4
 
 
 class Desc(ctypes.Structure):
@@ -54,6 +54,13 @@ MX_TENSOR_FIELDS = ("x", "x_scales", "topk_idx", "topk_weights", "l1_blocks", "l
 
 class MxTensors(ctypes.Structure):
     _fields_ = [(name, ctypes.c_void_p) for name in MX_TENSOR_FIELDS] + [("workspace_bytes", ctypes.c_size_t)]
+
+
+EP_SEND_FIELDS = ("rows", "row_scales", "ids", "weights", "counts", "slot_rows")
+
+
+class EpSend(ctypes.Structure):
+    _fields_ = [(name, ctypes.c_void_p) for name in EP_SEND_FIELDS]
 
 
 class MegaMoEError(RuntimeError):
@@ -87,6 +94,10 @@ def load() -> ctypes.CDLL:
                                      ctypes.c_int32, c_void_p, c_void_p]
     lib.megamoe_mx_workspace_bytes.argtypes = [P(Desc), P(c_size_t)]
     lib.megamoe_mx_forward.argtypes = [P(Desc), ctypes.c_float, P(MxTensors), c_void_p, P(c_void_p)]
+    lib.megamoe_ep_dispatch.argtypes = [P(Desc), ctypes.c_int32, P(MxTensors), P(EpSend), c_void_p]
+    lib.megamoe_ep_experts.argtypes = [P(Desc), ctypes.c_float, ctypes.c_int64, P(MxTensors), c_void_p, P(c_void_p)]
+    lib.megamoe_ep_combine.argtypes = [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, c_void_p, c_void_p, c_void_p,
+                                       c_void_p]
     lib.megamoe_status_string.argtypes = [c_int]
     lib.megamoe_status_string.restype = ctypes.c_char_p
     lib.megamoe_abi_version.argtypes = []

@@ -111,6 +111,9 @@ class Case:
                                        or self.norm != "none" or self.residual or not self.swiglu_limit > 0):
             raise ValueError(f"{self.id}: the MXFP4 form needs H and I multiples of 256, no shared expert "
                              "or block steps, and a positive SwiGLU limit")
+        if self.ep > 1 and (self.format != "mxfp4" or p["experts"] % self.ep or self.gpus != self.ep):
+            raise ValueError(f"{self.id}: expert parallelism is defined for the MXFP4 form, over all ranks, "
+                             "with ep dividing the experts")
         if self.router == "softmax" and self.bias != "none":
             raise ValueError(f"{self.id}: softmax routing takes no correction bias")
         groups, top = self.groups, self.top_groups
@@ -214,8 +217,21 @@ MX_CASES: tuple[Case, ...] = (
 )
 
 
+# One rank's share of the expert-parallel MXFP4 layer at the reference's catalog geometry
+# (megabench/cases.py:380-388: 512 tokens per rank, 8 ranks, 48 local experts each). On one
+# GPU the share is the rank's dispatch, its local experts over the rows it receives and its
+# combine (megamoe.py:153-182); the exchanges between them are collectives, not built here.
+EP_CASES: tuple[Case, ...] = (
+    _case("megamoe-layer-deepseek-v4-pro-ep8-t512", "deepseek-ai/DeepSeek-V4-Pro (routed experts, MXFP4, EP8)",
+          params=dict(tokens=512, hidden=7168, experts=384, topk=6, intermediate=3072),
+          router="given", format="mxfp4", swiglu_limit=10.0, routed_scaling=2.5, gpus=8, ep=8,
+          max_gpu_launches=6,
+          note="one rank's share: dispatch (order + pack), local experts (permute, experts, row copy), combine"),
+)
+
+
 def case(case_id: str) -> Case:
-    for c in CASES + BLOCK_CASES + MX_CASES:
+    for c in CASES + BLOCK_CASES + MX_CASES + EP_CASES:
         if c.id == case_id:
             return c
     raise KeyError(case_id)
@@ -247,7 +263,8 @@ def algorithmic_bytes(c: Case, hit_experts: int) -> int:
     MXFP4 form: E2M1 payload (half a byte) + one E8M0 byte per 32 weights, x as E4M3 + E8M0
     per 32, ids and weights, y in bf16."""
     T, H, E, K, I, S = c.tokens, c.hidden, c.experts, c.topk, c.intermediate, c.shared_experts
-    if c.format == "mxfp4":
+    if c.format == "mxfp4":  # also one rank's share under EP, hit_experts counting local experts
+        # (the HBM terms of megabench/sol.py:160-183)
         per_expert = 3 * I * H // 2 + 3 * I * H // 32
         return hit_experts * per_expert + T * H + T * H // 32 + 12 * T * K + 2 * T * H
     bh, bi = math.ceil(H / 128), math.ceil(I / 128)

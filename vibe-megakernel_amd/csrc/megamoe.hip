@@ -763,9 +763,9 @@ __device__ unsigned long long block_exclusive_scan(unsigned long long v, unsigne
 // Ints of the meta block. The error flag has a 128-byte line of its own, apart from the
 // queue counter that every workgroup updates.
 constexpr int kMetaHit = 0, kMetaUnitsGU = 1, kMetaUnitsDN = 2, kMetaQueueGU = 3, kMetaQueueDN = 4,
-              kMetaError = 32, kMetaInts = 64;
-constexpr int kChunkRows = 64;    // rows per chunk of the fp8 form (column tiles of up to 4)
-constexpr int kChunkRowsMx = 32;  // of the MXFP4 form (up to 2)
+              kMetaWide = 5, kMetaError = 32, kMetaInts = 64;
+constexpr int kChunkRows = 64;     // rows per chunk of the fp8 form (column tiles of up to 4)
+constexpr int kChunkRowsMx = 128;  // of the MXFP4 form: wide units over 33-128 rows, narrow up to 32
 
 struct PermuteOut {
   int* counts;   // [E]
@@ -783,9 +783,15 @@ __device__ __forceinline__ int chunk_class(int rows) { return rows > 32 ? 0 : (r
 
 // Ids from the caller (the MXFP4 form takes its routing as an input) may be out of range or
 // repeat an expert within a token; either sets the error flag, and the permutation, the
-// work lists and every later kernel's work are skipped (the combine writes NaN).
-__global__ __launch_bounds__(1024) void k_permute(const int64_t* __restrict__ ids, int T, int K, int E, int S,
-                                                  int nbI, int nbH, int ks, int chunk, PermuteOut out) {
+// work lists and every later kernel's work are skipped (the combine writes NaN). Expert
+// e here is id e + base (a rank's local experts under expert parallelism).
+//
+// With `wide` (the MXFP4 form, no shared expert), a chunk of more than 32 rows is worked by
+// wide units, 4 per 128-channel block of gate/up and 2 per 128-row block of down (times
+// the K parts); those chunks lead the lists, and meta[kMetaWide] counts them.
+__global__ __launch_bounds__(1024) void k_permute(const int64_t* __restrict__ ids, int64_t base, int T, int K, int E,
+                                                  int S, int nbI, int nbH, int ks, int chunk, int wide,
+                                                  PermuteOut out) {
   extern __shared__ int smem[];
   __shared__ int bad_ids;
   int* bad = &bad_ids;
@@ -799,7 +805,7 @@ __global__ __launch_bounds__(1024) void k_permute(const int64_t* __restrict__ id
   if (tid == 0) *bad = 0;
   __syncthreads();
   for (int i = tid; i < n; i += blockDim.x) {
-    const int64_t e64 = ids[i];
+    const int64_t e64 = ids[i] - base;
     const int t = i / K;
     if (e64 < 0 || e64 >= E) {
       *bad = 1;
@@ -879,8 +885,10 @@ __global__ __launch_bounds__(1024) void k_permute(const int64_t* __restrict__ id
     }
     out.offsets[E] = total;
     out.meta[kMetaHit] = nhit;
-    out.meta[kMetaUnitsGU] = (S * (s4 + s2 + s1) + t4 + t2 + t1) * nbI;
-    out.meta[kMetaUnitsDN] = (s4 + s2 + s1 + t4 + t2 + t1) * nbH * ks;
+    const int wf = wide ? 4 : 1, wfd = wide ? 2 : 1;  // units per block of a chunk of over 32 rows
+    out.meta[kMetaUnitsGU] = (S * (s4 + s2 + s1) + wf * t4 + t2 + t1) * nbI;
+    out.meta[kMetaUnitsDN] = (s4 + s2 + s1 + wfd * t4 + t2 + t1) * nbH * ks;
+    out.meta[kMetaWide] = wide ? t4 : 0;
     out.meta[kMetaQueueGU] = 0;
     out.meta[kMetaQueueDN] = 0;
     out.meta[kMetaError] = 0;
@@ -890,7 +898,7 @@ __global__ __launch_bounds__(1024) void k_permute(const int64_t* __restrict__ id
   if (tid < E) cnt[tid] = off;  // reuse as offsets (every thread read its count above)
   __syncthreads();
   for (int i = tid; i < n; i += blockDim.x) {
-    const int e = (int)ids[i], t = i / K;
+    const int e = (int)(ids[i] - base), t = i / K;
     const unsigned* row = bm + e * words;
     int rank = __popc(row[t >> 5] & ((1u << (t & 31)) - 1u));
     for (int q = 0; q < (t >> 5); ++q) rank += __popc(row[q]);
@@ -1676,7 +1684,7 @@ struct OperandsMx {
   const uint8_t* sb[NCT];  // lane's activation scale row
 };
 
-template <int RT, int NCT>
+template <int CPOL, int RT, int NCT>
 __device__ __forceinline__ void issue_a_mx(uint8_t* slot, const OperandsMx<RT, NCT>& op, const LaneTile& lt, int p,
                                            bool live) {
 #pragma unroll
@@ -1687,7 +1695,7 @@ __device__ __forceinline__ void issue_a_mx(uint8_t* slot, const OperandsMx<RT, N
       __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(base +
                                                                                      (uint32_t)(lt.dma + 8 * i * op.lda)),
                                        (__attribute__((address_space(3))) void*)(slot + t * kTileBytes + i * 1024),
-                                       16, 0, kNonTemporal);
+                                       16, 0, CPOL);
   }
 }
 
@@ -1780,8 +1788,10 @@ __device__ __forceinline__ void mfma_stage_mx(const i32x4 (&lo)[RT], const i32x4
 // D = 2) one 16-byte load per lane and tile brings the scales of a stage pair, issued
 // with the even stage's loads into one of two pair buffers (stage p reads buffer (p / 2) % 2, so the
 // loop is unrolled by four and no register copy crosses the back edge: a copy of loaded
-// registers there makes the compiler wait for vmcnt 0).
-template <int RT, int NCT, int D, bool PAIR>
+// registers there makes the compiler wait for vmcnt 0). CPOL is the weight loads' cache
+// policy: non-temporal where each line is read once, cached where the four wavefronts of a
+// wide unit request the same lines.
+template <int RT, int NCT, int D, bool PAIR, int CPOL = kNonTemporal>
 __device__ __forceinline__ void stream_gemm_mx(const OperandsMx<RT, NCT>& op, int nst, int rot, uint8_t* ring,
                                                f32x4 (&acc)[RT][NCT],
                                                const ReadyWait& ready = ReadyWait{nullptr, 0, nullptr}) {
@@ -1833,7 +1843,7 @@ __device__ __forceinline__ void stream_gemm_mx(const OperandsMx<RT, NCT>& op, in
     }
   };
 #pragma unroll
-  for (int s = 0; s < D - 1; ++s) issue_a_mx(ring + s * kSlot, op, lt, phys(min(s, nst - 1)), s < nst);
+  for (int s = 0; s < D - 1; ++s) issue_a_mx<CPOL>(ring + s * kSlot, op, lt, phys(min(s, nst - 1)), s < nst);
   wait_ready(ready);
   static_for<0, D - 1>([&](auto si) { load(si, (int)decltype(si)::value); });
   for (int p0 = 0; p0 < nst; p0 += U) {
@@ -1841,7 +1851,7 @@ __device__ __forceinline__ void stream_gemm_mx(const OperandsMx<RT, NCT>& op, in
       constexpr int s = decltype(si)::value;
       const int p = p0 + s;
       load(std::integral_constant<int, (s + D - 1) % U>{}, p + D - 1);
-      issue_a_mx(ring + ((s + D - 1) % D) * kSlot, op, lt, phys(min(p + D - 1, nst - 1)), p + D - 1 < nst);
+      issue_a_mx<CPOL>(ring + ((s + D - 1) % D) * kSlot, op, lt, phys(min(p + D - 1, nst - 1)), p + D - 1 < nst);
       wait_vmem<kAfter>();
       if (p < nst) {
         i32x4 lo[RT], hi[RT];
@@ -1866,6 +1876,7 @@ struct GateUpMxArgs {
   uint8_t* hs;         // [T*K, hs_ld] e8m0 (one 128-byte line per row)
   const uint8_t* spare;
   int T, H, I, K, E, hs_ld;
+  int ebase;  // id of expert 0 (a rank's first local expert)
   float limit;
 };
 
@@ -1943,25 +1954,127 @@ __device__ void gateup_mx_unit(const GateUpMxArgs& a, int e, int jb, const Chunk
   }
 }
 
-__device__ void gateup_mx_work(const GateUpMxArgs& a, int u, uint8_t (*red8)[64], uint8_t* ring) {
+__device__ __forceinline__ void store_coherent_byte(uint8_t* p, uint8_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Wide gate/up unit, for a chunk of 33-128 rows: gate rows [32 blk, +32) and the same up
+// rows (one 32-channel block of h) for every row of the chunk; wave w takes column tiles
+// [w NCT, w NCT + NCT). Every wave streams the same 64 weight rows into its own ring, with
+// cached loads so that L2 can serve the four requests for a line; the LDS-DMA requests
+// themselves are four times the weight bytes, which bounds these units below the HBM rate.
+// A wave past the chunk's last tile streams a copy of it and stores nothing (all waves take
+// the same path and barriers).
+template <int NCT, bool PAIR>
+__device__ void gateup_mx_wide(const GateUpMxArgs& a, int e, int blk, const ChunkRows& cr, int rot, uint8_t* ring) {
+  const int lane = opaque_lane(), w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lr = lane & 15;
+  const int H = a.H, lda = H / 2, sld = H / 32;
+  const size_t gate0 = (size_t)e * 2 * a.I + (size_t)blk * 32, up0 = gate0 + a.I;
+  OperandsMx<4, NCT> op;
+  op.lda = lda;
+  op.spare = a.spare;
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    op.a[r] = a.l1 + (gate0 + 16 * r) * lda;
+    op.a[r + 2] = a.l1 + (up0 + 16 * r) * lda;
+    op.sa[r] = a.l1s + (gate0 + 16 * r + lr) * sld;
+    op.sa[r + 2] = a.l1s + (up0 + 16 * r + lr) * sld;
+  }
+#pragma unroll
+  for (int c = 0; c < NCT; ++c) {
+    const int tok = row_token(cr, min(16 * (w * NCT + c) + lr, cr.n - 1));
+    op.b[c] = a.x + (size_t)tok * H + 16 * (lane >> 4);
+    op.sb[c] = a.xs + (size_t)tok * sld;
+  }
+  f32x4 acc[4][NCT];
+  stream_gemm_mx<4, NCT, 2, PAIR, 0>(op, H / kMxStageK, rot, ring, acc);
+
+  const float L = a.limit;
+#pragma unroll
+  for (int c = 0; c < NCT; ++c) {
+    const int col = 16 * (w * NCT + c) + lr;
+    const float wrow = a.wts[cr.perm[cr.row0 + min(col, cr.n - 1)]];
+    float hv[2][4];
+    float amax = 0.0f;
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const float g = fminf(round_bf16(acc[p][c][v]), L);
+        const float u = fminf(fmaxf(round_bf16(acc[p + 2][c][v]), -L), L);
+        const float act = __fmul_rn(__fmul_rn(g / __fadd_rn(1.0f, expf(-g)), u), wrow);
+        hv[p][v] = act;
+        amax = fmaxf(amax, fabsf(act));
+      }
+    amax = fmaxf(amax, __shfl_xor(amax, 16));
+    amax = fmaxf(amax, __shfl_xor(amax, 32));
+    const uint32_t ex = e8m0_exponent(amax);
+    const float inv = __uint_as_float((254u - ex) << 23);
+    if (col < cr.n) {
+      uint8_t* dst = a.hq + (size_t)(cr.row0 + col) * a.I + (size_t)blk * 32 + 4 * (lane >> 4);
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        uint32_t packed = 0;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) packed |= f32_to_e4m3(clamp448(__fmul_rn(hv[p][v], inv))) << (8 * v);
+        store_coherent(reinterpret_cast<uint32_t*>(dst + 16 * p), packed);
+      }
+      if (lane < 16) store_coherent_byte(a.hs + (size_t)(cr.row0 + col) * a.hs_ld + blk, (uint8_t)ex);
+    }
+  }
+}
+
+// Gate/up units: `nwide` wide chunks first (4 nbI units each, one per 32-channel block),
+// then narrow chunks (nbI units each). Returns the unit's chunk.
+__device__ int gateup_mx_work(const GateUpMxArgs& a, int u, int nwide, uint8_t (*red8)[64], uint8_t* ring) {
   const int nbI = a.I / kBlock;
-  const int4 ch = a.chunks[u / nbI];
+  const int nst = a.H / kMxStageK;
+  if (u < nwide * 4 * nbI) {
+    const int c = u / (4 * nbI), blk = u % (4 * nbI);
+    const int4 ch = a.chunks[c];
+    const ChunkRows cr{ch.z, a.offsets[ch.x] + ch.y, a.perm, a.K};
+    const int key = (ch.x + a.ebase) * nbI + blk / 4;  // as the narrow unit of the same 128 channels
+    const bool two = cr.n > 64;
+    if (nst % 2 == 0) {
+      const int rot = 2 * (key % (nst / 2));
+      if (two)
+        gateup_mx_wide<2, true>(a, ch.x, blk, cr, rot, ring);
+      else
+        gateup_mx_wide<1, true>(a, ch.x, blk, cr, rot, ring);
+    } else {
+      const int rot = key % nst;
+      if (two)
+        gateup_mx_wide<2, false>(a, ch.x, blk, cr, rot, ring);
+      else
+        gateup_mx_wide<1, false>(a, ch.x, blk, cr, rot, ring);
+    }
+    return c;
+  }
+  u -= nwide * 4 * nbI;
+  const int c = nwide + u / nbI;
+  const int4 ch = a.chunks[c];
   const int jb = u % nbI;
   const ChunkRows cr{ch.z, a.offsets[ch.x] + ch.y, a.perm, a.K};
-  const int nst = a.H / kMxStageK;
+  // The rotation (the first of the nst stages, which sets the fp32 accumulation order)
+  // follows the global expert and the 128-channel block, not the unit's place in the queue
+  // or its kind, so a row's result does not depend on which other rows share its chunk or
+  // rank.
+  const int key = (ch.x + a.ebase) * nbI + jb;
   if (nst % 2 == 0) {  // paired scale loads: an even rotation keeps the pairs aligned
-    const int rot = 2 * (u % (nst / 2));
+    const int rot = 2 * (key % (nst / 2));
     if (cr.n <= 16)
       gateup_mx_unit<1, true>(a, ch.x, jb, cr, rot, red8, ring);
     else
       gateup_mx_unit<2, true>(a, ch.x, jb, cr, rot, red8, ring);
   } else {
-    const int rot = u % nst;
+    const int rot = key % nst;
     if (cr.n <= 16)
       gateup_mx_unit<1, false>(a, ch.x, jb, cr, rot, red8, ring);
     else
       gateup_mx_unit<2, false>(a, ch.x, jb, cr, rot, red8, ring);
   }
+  return c;
 }
 
 struct DownMxArgs {
@@ -1974,6 +2087,7 @@ struct DownMxArgs {
   float* pd;    // ks > 1: [ks, T*K, H] fp32 partial d of each K part
   const uint8_t* spare;
   int T, H, I, K, E, hs_ld, ks;
+  int ebase;
 };
 
 // Down unit: rows [j*128, +128) of the expert's down matrix over K part kp of ks.
@@ -2020,20 +2134,96 @@ __device__ void down_mx_unit(const DownMxArgs& a, int e, int j, int kp, const Ch
   }
 }
 
-__device__ void down_mx_work(const DownMxArgs& a, int v, const ReadyWait& ready, uint8_t* ring) {
-  const int nbH = a.H / kBlock;
-  const int4 ch = a.chunks[v / (nbH * a.ks)];
+// Wide down unit, for a chunk of 33-128 rows: down rows [64 j64, +64) over K part kp, for
+// every row of the chunk; wave w takes column tiles [w NCT, w NCT + NCT), every wave
+// streaming the same weight rows (as gateup_mx_wide).
+template <int NCT, bool PAIR>
+__device__ void down_mx_wide(const DownMxArgs& a, int e, int j64, int kp, const ChunkRows& cr, int rot,
+                             const ReadyWait& ready, uint8_t* ring) {
+  const int lane = opaque_lane(), w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lr = lane & 15;
+  const int I = a.I, lda = I / 2, sld = I / 32, nstp = I / kMxStageK / a.ks, p0 = kp * nstp;
+  OperandsMx<4, NCT> op;
+  op.lda = lda;
+  op.spare = a.spare;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const size_t row = (size_t)e * a.H + (size_t)j64 * 64 + 16 * r;
+    op.a[r] = a.l2 + row * lda + (size_t)p0 * kBlock;
+    op.sa[r] = a.l2s + (row + lr) * sld + 8 * p0;
+  }
+#pragma unroll
+  for (int c = 0; c < NCT; ++c) {
+    const int rr = cr.row0 + min(16 * (w * NCT + c) + lr, cr.n - 1);
+    op.b[c] = a.hq + (size_t)rr * I + (size_t)p0 * kMxStageK + 16 * (lane >> 4);
+    op.sb[c] = a.hs + (size_t)rr * a.hs_ld + 8 * p0;
+  }
+  f32x4 acc[4][NCT];
+  stream_gemm_mx<4, NCT, 2, PAIR, 0>(op, nstp, rot, ring, acc, ready);
+  float* pd = a.pd + (size_t)kp * a.T * a.K * a.H;
+#pragma unroll
+  for (int c = 0; c < NCT; ++c) {
+    const int r = 16 * (w * NCT + c) + lr;
+    if (r < cr.n) {
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        const size_t o = (size_t)(cr.row0 + r) * a.H + (size_t)j64 * 64 + 16 * p + 4 * (lane >> 4);
+        if (a.ks == 1) {
+          const uint32_t lo = f32_to_bf16_bits(acc[p][c][0]) | (f32_to_bf16_bits(acc[p][c][1]) << 16);
+          const uint32_t hi = f32_to_bf16_bits(acc[p][c][2]) | (f32_to_bf16_bits(acc[p][c][3]) << 16);
+          *reinterpret_cast<uint2*>(a.d + o) = make_uint2(lo, hi);
+        } else {
+          *reinterpret_cast<f32x4*>(pd + o) = acc[p][c];
+        }
+      }
+    }
+  }
+}
+
+// Down units: `nwide` wide chunks first (2 nbH ks units each), then narrow chunks (nbH ks
+// each). A unit waits for every gate/up unit of its chunk: 4 nbI for a wide chunk, nbI
+// for a narrow one.
+__device__ void down_mx_work(const DownMxArgs& a, int v, int nwide, int* ready_counts, int* error,
+                             uint8_t* ring) {
+  const int nbH = a.H / kBlock, nbI = a.I / kBlock;
+  const int nstp = a.I / kMxStageK / a.ks;
+  if (v < nwide * 2 * nbH * a.ks) {
+    const int c = v / (2 * nbH * a.ks), rem = v % (2 * nbH * a.ks), j64 = rem / a.ks, kp = rem % a.ks;
+    const int4 ch = a.chunks[c];
+    const ChunkRows cr{ch.z, a.offsets[ch.x] + ch.y, a.perm, a.K};
+    const ReadyWait ready{&ready_counts[c], 4 * nbI, error};
+    const int key = ((ch.x + a.ebase) * nbH + j64 / 2) * a.ks + kp;  // as the narrow unit of the same rows
+    const bool two = cr.n > 64;
+    if (nstp % 2 == 0) {
+      const int rot = 2 * (key % (nstp / 2));
+      if (two)
+        down_mx_wide<2, true>(a, ch.x, j64, kp, cr, rot, ready, ring);
+      else
+        down_mx_wide<1, true>(a, ch.x, j64, kp, cr, rot, ready, ring);
+    } else {
+      const int rot = key % nstp;
+      if (two)
+        down_mx_wide<2, false>(a, ch.x, j64, kp, cr, rot, ready, ring);
+      else
+        down_mx_wide<1, false>(a, ch.x, j64, kp, cr, rot, ready, ring);
+    }
+    return;
+  }
+  v -= nwide * 2 * nbH * a.ks;
+  const int c = nwide + v / (nbH * a.ks);
+  const int4 ch = a.chunks[c];
   const int rem = v % (nbH * a.ks), j = rem / a.ks, kp = rem % a.ks;
   const ChunkRows cr{ch.z, a.offsets[ch.x] + ch.y, a.perm, a.K};
-  const int nstp = a.I / kMxStageK / a.ks;
+  const ReadyWait ready{&ready_counts[c], nbI, error};
+  const int key = ((ch.x + a.ebase) * nbH + j) * a.ks + kp;
   if (nstp % 2 == 0) {
-    const int rot = 2 * (v % (nstp / 2));
+    const int rot = 2 * (key % (nstp / 2));
     if (cr.n <= 16)
       down_mx_unit<1, true>(a, ch.x, j, kp, cr, rot, ready, ring);
     else
       down_mx_unit<2, true>(a, ch.x, j, kp, cr, rot, ready, ring);
   } else {
-    const int rot = v % nstp;
+    const int rot = key % nstp;
     if (cr.n <= 16)
       down_mx_unit<1, false>(a, ch.x, j, kp, cr, rot, ready, ring);
     else
@@ -2059,6 +2249,7 @@ __global__ __launch_bounds__(256, 2) void k_experts_mx(ExpertMxArgs args) {
   int* meta = args.gu.meta;
   const int total_gu = meta[kMetaUnitsGU];
   const int total = total_gu + meta[kMetaUnitsDN];
+  const int nwide = meta[kMetaWide];
   if (threadIdx.x == 0) slot = atomicAdd(&meta[kMetaQueueGU], 1);
   __syncthreads();
   int u = slot, next = 0;
@@ -2067,19 +2258,16 @@ __global__ __launch_bounds__(256, 2) void k_experts_mx(ExpertMxArgs args) {
     asm volatile("" : "+s"(ap));
     ExpertMxArgs a;
     __builtin_memcpy(&a, (const ExpertMxArgs*)ap, sizeof(a));
-    const int nbI = a.gu.I / kBlock, nbH = a.dn.H / kBlock;
     uint8_t* ring = rings + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) * kRingWave;
     __syncthreads();
     if (threadIdx.x == 0) next = atomicAdd(&meta[kMetaQueueGU], 1);
     if (u < total_gu) {
-      gateup_mx_work(a.gu, u, red8, ring);
+      const int c = gateup_mx_work(a.gu, u, nwide, red8, ring);
       publish_fence();
       __syncthreads();
-      if (threadIdx.x == 0) atomicAdd(&a.ready[a.dn_of_gu[u / nbI]], 1);
+      if (threadIdx.x == 0) atomicAdd(&a.ready[a.dn_of_gu[c]], 1);
     } else {
-      const int v = u - total_gu, c = v / (nbH * a.dn.ks);
-      const ReadyWait ready{&a.ready[c], nbI, &meta[kMetaError]};
-      down_mx_work(a.dn, v, ready, ring);
+      down_mx_work(a.dn, u - total_gu, nwide, a.ready, &meta[kMetaError], ring);
     }
     if (threadIdx.x == 0) slot = next;
     __syncthreads();
@@ -2328,8 +2516,8 @@ int forward_impl(const megamoe_desc* desc, const megamoe_tensors* t, hipStream_t
                 (int*)(ws + L.ready)};
   const int nbI = I / kBlock, nbH = H / kBlock;
   const size_t lds = ((size_t)E * (1 + (T + 31) / 32) + 32) * 4;
-  hipLaunchKernelGGL(k_permute, dim3(1), dim3(1024), lds, st, t->expert_ids, T, K, E, S, nbI, nbH, L.ks, kChunkRows,
-                     po);
+  hipLaunchKernelGGL(k_permute, dim3(1), dim3(1024), lds, st, t->expert_ids, (int64_t)0, T, K, E, S, nbI, nbH, L.ks,
+                     kChunkRows, 0, po);
   MEGAMOE_LAUNCH_CHECK();
   if (mark(3) != hipSuccess) return MEGAMOE_ERR_HIP;
 
@@ -2441,7 +2629,7 @@ LayoutMx make_layout_mx(const megamoe_desc& d) {
 }
 
 int forward_mx_impl(const megamoe_desc* desc, float limit, const megamoe_mx_tensors* t, hipStream_t st,
-                    hipEvent_t* ev) {
+                    hipEvent_t* ev, int64_t base = 0) {
   int rc = validate_mx(desc);
   if (rc) return rc;
   if (!t || !(limit > 0.0f)) return MEGAMOE_ERR_INVALID_ARGUMENT;
@@ -2468,8 +2656,8 @@ int forward_mx_impl(const megamoe_desc* desc, float limit, const megamoe_mx_tens
                 (int*)(ws + L.inv),    (int4*)(ws + L.gu),     (int4*)(ws + L.dn),  (int*)(ws + L.dn_of_gu),
                 (int*)(ws + L.ready)};
   const size_t lds = ((size_t)E * (1 + (T + 31) / 32) + 32) * 4;
-  hipLaunchKernelGGL(k_permute, dim3(1), dim3(1024), lds, st, t->topk_idx, T, K, E, 0, nbI, nbH, L.ks, kChunkRowsMx,
-                     po);
+  hipLaunchKernelGGL(k_permute, dim3(1), dim3(1024), lds, st, t->topk_idx, base, T, K, E, 0, nbI, nbH, L.ks,
+                     kChunkRowsMx, 1, po);
   MEGAMOE_LAUNCH_CHECK();
   if (mark(1) != hipSuccess) return MEGAMOE_ERR_HIP;
 
@@ -2481,6 +2669,7 @@ int forward_mx_impl(const megamoe_desc* desc, float limit, const megamoe_mx_tens
   ga.hq = (uint8_t*)(ws + L.hq); ga.hs = (uint8_t*)(ws + L.hs);
   ga.spare = (const uint8_t*)(ws + L.spare);
   ga.T = T; ga.H = H; ga.I = I; ga.K = K; ga.E = E; ga.hs_ld = L.hs_ld; ga.limit = limit;
+  ga.ebase = (int)base;
   DownMxArgs& da = ea.dn;
   da.l2 = t->l2_blocks; da.l2s = t->l2_scales;
   da.offsets = po.offsets; da.perm = po.perm; da.chunks = po.dn; da.meta = po.meta;
@@ -2488,10 +2677,11 @@ int forward_mx_impl(const megamoe_desc* desc, float limit, const megamoe_mx_tens
   da.d = (uint16_t*)(ws + L.d); da.pd = (float*)(ws + L.p);
   da.spare = ga.spare;
   da.T = T; da.H = H; da.I = I; da.K = K; da.E = E; da.hs_ld = L.hs_ld; da.ks = L.ks;
+  da.ebase = (int)base;
   ea.dn_of_gu = po.dn_of_gu;
   ea.ready = po.ready;
   const size_t chunks = max_chunks(d, 0, kChunkRowsMx);
-  const size_t units_max = chunks * (size_t)nbI + chunks * (size_t)nbH * L.ks;
+  const size_t units_max = chunks * 4 * (size_t)nbI + chunks * 2 * (size_t)nbH * L.ks;
   const size_t resident = (size_t)di.cus * di.experts_mx_per_cu;
   hipLaunchKernelGGL(k_experts_mx, dim3((unsigned)(units_max < resident ? units_max : resident)), dim3(256), 0, st,
                      ea);
@@ -2507,11 +2697,113 @@ int forward_mx_impl(const megamoe_desc* desc, float limit, const megamoe_mx_tens
   return MEGAMOE_OK;
 }
 
+
+// -- Expert parallelism: one rank's share ---------------------------------------------------
+//
+// Under EP (megamoe.py:153-182) expert e belongs to rank e / (E/ep). A rank sends each of its
+// (token, slot) rows to the owner of the slot's expert, in a stable order by owner
+// (megamoe.py:160-171; the per-destination counts are those of parallel.py:59-68), runs its
+// local experts over the rows it receives (megamoe.py:131-150: the MXFP4 form with one slot
+// per row) and, once the outputs have come back in send order, sums each token's slots in
+// slot order (megamoe.py:176-182). The exchanges in between are collectives of the caller.
+
+constexpr int kMaxRanks = 1024;
+
+// Send row of every (token, slot): a stable counting sort by owner rank, one workgroup. Each
+// thread owns a contiguous run of entries; per owner, an exclusive scan of the runs' counts
+// places each run after the earlier ones. An id outside [0, E) makes every count -1 and
+// every send row -1 (nothing is packed).
+__global__ __launch_bounds__(1024) void k_ep_order(const int64_t* __restrict__ ids, int n, int E, int local, int ep,
+                                                   int64_t* __restrict__ counts, int32_t* __restrict__ slot_rows) {
+  __shared__ unsigned long long tmp[16];
+  __shared__ int bad;
+  const int tid = threadIdx.x, per = (n + 1023) / 1024;
+  const int lo = min(n, tid * per), hi = min(n, lo + per);
+  if (tid == 0) bad = 0;
+  __syncthreads();
+  for (int i = lo; i < hi; ++i) {
+    const int64_t e = ids[i];
+    if (e < 0 || e >= E) bad = 1;
+  }
+  __syncthreads();
+  if (bad) {
+    for (int i = tid; i < n; i += 1024) slot_rows[i] = -1;
+    for (int o = tid; o < ep; o += 1024) counts[o] = -1;
+    return;
+  }
+  int base = 0;
+  for (int o = 0; o < ep; ++o) {
+    int c = 0;
+    for (int i = lo; i < hi; ++i) c += (int)ids[i] / local == o;
+    unsigned long long total;
+    int pos = base + (int)block_exclusive_scan((unsigned long long)c, tmp, &total);
+    for (int i = lo; i < hi; ++i)
+      if ((int)ids[i] / local == o) slot_rows[i] = pos++;
+    if (tid == 0) counts[o] = (int64_t)total;
+    base += (int)total;
+    __syncthreads();  // tmp is rewritten by the next owner's scan
+  }
+}
+
+// The send payload: row slot_rows[i] of each buffer gets (token i / K)'s E4M3 row and E8M0
+// scales and slot i's expert id and weight. One workgroup per (token, slot).
+__global__ __launch_bounds__(256) void k_ep_pack(const uint8_t* __restrict__ x, const uint8_t* __restrict__ xs,
+                                                 const int64_t* __restrict__ ids, const float* __restrict__ wts,
+                                                 const int32_t* __restrict__ slot_rows, int K, int H,
+                                                 uint8_t* __restrict__ rows, uint8_t* __restrict__ row_scales,
+                                                 int64_t* __restrict__ out_ids, float* __restrict__ out_wts) {
+  const int i = blockIdx.x, t = i / K, p = slot_rows[i];
+  if (p < 0) return;
+  const uint4* src = reinterpret_cast<const uint4*>(x + (size_t)t * H);
+  uint4* dst = reinterpret_cast<uint4*>(rows + (size_t)p * H);
+  for (int c = threadIdx.x; c < H / 16; c += 256) dst[c] = src[c];
+  const uint2* ssrc = reinterpret_cast<const uint2*>(xs + (size_t)t * (H / 32));
+  uint2* sdst = reinterpret_cast<uint2*>(row_scales + (size_t)p * (H / 32));
+  for (int c = threadIdx.x; c < H / 256; c += 256) sdst[c] = ssrc[c];
+  if (threadIdx.x == 0) {
+    out_ids[p] = ids[i];
+    out_wts[p] = wts[i];
+  }
+}
+
+// y[t] = bf16 of the slot-order fp32 sum of the returned rows of token t's slots; a slot
+// without a send row (bad ids at the dispatch) makes the token's row NaN.
+__global__ __launch_bounds__(256) void k_ep_combine(const uint16_t* __restrict__ returned,
+                                                    const int32_t* __restrict__ slot_rows, int T, int H, int K,
+                                                    uint16_t* __restrict__ y) {
+  const int i = blockIdx.x * 256 + threadIdx.x, per_row = H / 8;
+  if (i >= T * per_row) return;
+  const int t = i / per_row, h0 = (i % per_row) * 8;
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  bool bad = false;
+  for (int k = 0; k < K; ++k) {
+    const int r = slot_rows[(size_t)t * K + k];
+    if (r < 0) {
+      bad = true;
+      continue;
+    }
+    const uint4 v = *reinterpret_cast<const uint4*>(returned + (size_t)r * H + h0);
+    const uint32_t q[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      acc[2 * j] = __fadd_rn(acc[2 * j], bf16_bits_to_f32(q[j] & 0xffffu));
+      acc[2 * j + 1] = __fadd_rn(acc[2 * j + 1], bf16_bits_to_f32(q[j] >> 16));
+    }
+  }
+  uint32_t o[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    o[j] = bad ? 0x7fc07fc0u : (f32_to_bf16_bits(acc[2 * j]) | (f32_to_bf16_bits(acc[2 * j + 1]) << 16));
+  *reinterpret_cast<uint4*>(y + (size_t)t * H + h0) = make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
 }  // namespace
 
 extern "C" {
 
-int megamoe_abi_version(void) { return 3; }
+int megamoe_abi_version(void) { return 4; }
 
 const char* megamoe_status_string(int status) {
   switch (status) {
@@ -2616,6 +2908,65 @@ int megamoe_mx_forward(const megamoe_desc* desc, float swiglu_limit, const megam
     }
   }
   return forward_mx_impl(desc, swiglu_limit, t, (hipStream_t)stream, events ? ev : nullptr);
+}
+
+int megamoe_ep_dispatch(const megamoe_desc* desc, int32_t ep, const megamoe_mx_tensors* t,
+                        const megamoe_ep_send* send, void* stream) {
+  if (!desc || !t || !send) return MEGAMOE_ERR_INVALID_ARGUMENT;
+  const int64_t T = desc->tokens, H = desc->hidden, E = desc->experts, K = desc->topk;
+  if (T < 0 || H <= 0 || E <= 0 || K <= 0 || K > E || H % kMxStageK || ep <= 0 || E % ep) return MEGAMOE_ERR_SHAPE;
+  if (ep > kMaxRanks || T * K >= ((int64_t)1 << 30)) return MEGAMOE_ERR_UNSUPPORTED;
+  if (!send->counts) return MEGAMOE_ERR_INVALID_ARGUMENT;
+  hipStream_t st = (hipStream_t)stream;
+  const int n = (int)(T * K);
+  if (n == 0) {  // zero counts, written by the order kernel (no memset, so the call may be captured)
+    hipLaunchKernelGGL(k_ep_order, dim3(1), dim3(1024), 0, st, (const int64_t*)nullptr, 0, (int)E, (int)(E / ep),
+                       (int)ep, send->counts, (int32_t*)nullptr);
+    MEGAMOE_LAUNCH_CHECK();
+    return MEGAMOE_OK;
+  }
+  if (!t->x || !t->x_scales || !t->topk_idx || !t->topk_weights || !send->rows || !send->row_scales || !send->ids ||
+      !send->weights || !send->slot_rows)
+    return MEGAMOE_ERR_INVALID_ARGUMENT;
+  if (!aligned16(t->x) || !aligned16(send->rows) || ((uintptr_t)t->x_scales & 7) || ((uintptr_t)send->row_scales & 7))
+    return MEGAMOE_ERR_INVALID_ARGUMENT;
+  hipLaunchKernelGGL(k_ep_order, dim3(1), dim3(1024), 0, st, t->topk_idx, n, (int)E, (int)(E / ep), (int)ep,
+                     send->counts, send->slot_rows);
+  MEGAMOE_LAUNCH_CHECK();
+  hipLaunchKernelGGL(k_ep_pack, dim3(n), dim3(256), 0, st, t->x, t->x_scales, t->topk_idx, t->topk_weights,
+                     (const int32_t*)send->slot_rows, (int)K, (int)H, send->rows, send->row_scales, send->ids,
+                     send->weights);
+  MEGAMOE_LAUNCH_CHECK();
+  return MEGAMOE_OK;
+}
+
+int megamoe_ep_experts(const megamoe_desc* desc, float swiglu_limit, int64_t expert_base, const megamoe_mx_tensors* t,
+                       void* stream, void* const* events) {
+  if (!desc) return MEGAMOE_ERR_INVALID_ARGUMENT;
+  if (desc->topk != 1) return MEGAMOE_ERR_SHAPE;
+  if (expert_base < 0 || expert_base > ((int64_t)1 << 30)) return MEGAMOE_ERR_SHAPE;
+  hipEvent_t ev[kStagesMx + 1];
+  if (events) {
+    for (int i = 0; i < kStagesMx + 1; ++i) {
+      if (!events[i]) return MEGAMOE_ERR_INVALID_ARGUMENT;
+      ev[i] = (hipEvent_t)events[i];
+    }
+  }
+  return forward_mx_impl(desc, swiglu_limit, t, (hipStream_t)stream, events ? ev : nullptr, expert_base);
+}
+
+int megamoe_ep_combine(int32_t tokens, int32_t hidden, int32_t topk, const void* returned, const int32_t* slot_rows,
+                       void* y, void* stream) {
+  if (tokens < 0 || hidden <= 0 || topk <= 0 || hidden % 8) return MEGAMOE_ERR_SHAPE;
+  if (tokens == 0) return MEGAMOE_OK;
+  if (!returned || !slot_rows || !y) return MEGAMOE_ERR_INVALID_ARGUMENT;
+  if (!aligned16(returned) || !aligned16(y)) return MEGAMOE_ERR_INVALID_ARGUMENT;
+  const int64_t work = (int64_t)tokens * (hidden / 8);
+  if (work >= ((int64_t)1 << 31)) return MEGAMOE_ERR_UNSUPPORTED;
+  hipLaunchKernelGGL(k_ep_combine, dim3((unsigned)((work + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                     (const uint16_t*)returned, slot_rows, tokens, hidden, topk, (uint16_t*)y);
+  MEGAMOE_LAUNCH_CHECK();
+  return MEGAMOE_OK;
 }
 
 int megamoe_rms_norm(int32_t rows, int32_t cols, const void* x, const void* weight, float eps,

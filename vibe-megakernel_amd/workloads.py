@@ -21,6 +21,7 @@ scale, +-448)) (the rule of megabench/tasks/quantization.py:57-59,119-126).
 from __future__ import annotations
 
 import hashlib
+from dataclasses import replace
 
 import torch
 
@@ -126,17 +127,46 @@ def mx_routing(case: Case, seed: int, device) -> tuple[torch.Tensor, torch.Tenso
     return idx.to(torch.int64).contiguous(), (score / score.sum(-1, keepdim=True) * case.routed_scaling).contiguous()
 
 
+def _mx_experts(case: Case, seed: int, first: int, count: int, device) -> dict[str, torch.Tensor]:
+    """MXFP4 weights of experts [first, first + count), each from its own global id's stream."""
+    H, I = case.hidden, case.intermediate
+    values = {}
+    for name, rows, cols, std in (("l1", 2 * I, H, L1_GAIN / H ** 0.5), ("l2", H, I, 1.0 / I ** 0.5)):
+        blocks = torch.empty((count, rows, cols // MX, MX // 2), dtype=torch.uint8, device=device)
+        scales = torch.empty((count, rows, cols // MX), dtype=torch.uint8, device=device)
+        for e in range(count):
+            blocks[e], scales[e] = pack_mxfp4(_normal(seed, f"{name}:{first + e}", (rows, cols), std, device))
+        values[name + "_blocks"], values[name + "_scales"] = blocks, scales
+    return values
+
+
 def make_mx_inputs(case: Case, seed: int, device="cpu") -> dict[str, torch.Tensor]:
-    T, H, E, I = case.tokens, case.hidden, case.experts, case.intermediate
+    T, H, E = case.tokens, case.hidden, case.experts
     values = {}
     values["x"], values["x_scales"] = pack_e4m3_e8m0(_normal(seed, "x", (T, H), 1.0, device))
     values["topk_idx"], values["topk_weights"] = mx_routing(case, seed, device)
-    for name, rows, cols, std in (("l1", 2 * I, H, L1_GAIN / H ** 0.5), ("l2", H, I, 1.0 / I ** 0.5)):
-        blocks = torch.empty((E, rows, cols // MX, MX // 2), dtype=torch.uint8, device=device)
-        scales = torch.empty((E, rows, cols // MX), dtype=torch.uint8, device=device)
-        for e in range(E):
-            blocks[e], scales[e] = pack_mxfp4(_normal(seed, f"{name}:{e}", (rows, cols), std, device))
-        values[name + "_blocks"], values[name + "_scales"] = blocks, scales
+    values.update(_mx_experts(case, seed, 0, E, device))
+    return values
+
+
+def serial_case(case: Case) -> Case:
+    """The single-rank problem of an EP case: every rank's tokens, every expert
+    (megabench/verify_megamoe.py:39-40)."""
+    return replace(case, gpus=1, ep=1, params=dict(case.params, tokens=case.tokens * case.ep))
+
+
+def make_ep_inputs(case: Case, seed: int, device="cpu", rank: int = 0) -> dict[str, torch.Tensor]:
+    """Inputs of rank ``rank``'s share: x, x_scales, topk_idx and topk_weights of the serial
+    problem (all ep * T tokens; rank r's own are rows [r*T, (r+1)*T)) and the MXFP4 weights
+    of the rank's local experts [rank*E/ep, (rank+1)*E/ep) only. Every rank's tokens and
+    weights are the serial problem's (make_mx_inputs of serial_case), as the reference's rank
+    inputs are (megabench/tests/test_megamoe.py:150-158)."""
+    serial = serial_case(case)
+    local = case.experts // case.ep
+    values = {}
+    values["x"], values["x_scales"] = pack_e4m3_e8m0(_normal(seed, "x", (serial.tokens, case.hidden), 1.0, device))
+    values["topk_idx"], values["topk_weights"] = mx_routing(serial, seed, device)
+    values.update(_mx_experts(case, seed, rank * local, local, device))
     return values
 
 
