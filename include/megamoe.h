@@ -173,6 +173,36 @@ int megamoe_block_forward(const megamoe_desc* desc, const megamoe_tensors* t, co
 int megamoe_rms_norm(int32_t rows, int32_t cols, const void* x, const void* weight, float eps,
                      int32_t weight_in_fp32, void* out, void* stream);
 
+/* Epilogue variants of the FP8 layer's experts (routed and shared alike). With g, u the
+ * bf16 gate and up outputs:
+ *   swiglu 0: h = bf16(silu(fp32 g) * fp32 u), rounded once (frontier.py:337, DeepSeek/TileRT);
+ *   swiglu 1: h = bf16(bf16(silu(g)) * u), silu rounded to bf16 first (F.silu(gate)*up on
+ *             bf16, frontier.py:338 and glm53.py:174-175);
+ *   swiglu_limit > 0: g = min(g, limit) and u = clamp(u, -limit, limit) before either form
+ *             (glm53.py:175, SWIGLU_LIMIT = 10); 0 clamps nothing. */
+typedef struct megamoe_epilogue {
+  int32_t swiglu;
+  float swiglu_limit;
+} megamoe_epilogue;
+
+/* megamoe_forward with optional block steps and epilogue variant: `block` NULL runs the
+ * layer alone (as megamoe_forward), else as megamoe_block_forward; `epilogue` NULL is
+ * {0, 0} (the DeepSeek form). `events` is NULL or events[0..5] as megamoe_forward_events
+ * (asynchronous: recorded, not waited for). Replaces the MoE step of the frontier decoders
+ * that use these forms: frontier.py:335-354 (sigmoid routing, shared expert) with
+ * glm53.py:263-274 for GLM-5.3-Flash. */
+int megamoe_forward_ex(const megamoe_desc* desc, const megamoe_tensors* t, const megamoe_block* block,
+                       const megamoe_epilogue* epilogue, void* stream, void* const* events);
+
+/* GPT-OSS's combine (gptoss.py:112-124): per token t, its K expert outputs (bf16
+ * expert_out [T*K, H], row t*K + k for slot k) accumulate in ascending expert id order
+ * (expert_ids int64 [T*K], distinct within a token; a repeated id counts once), in bf16:
+ * o = bf16(o + bf16(p * e)) from o = 0 with the slot's bf16 weight p (weights bf16 [T*K]);
+ * y = bf16(residual + o) when residual (bf16 [T, H]) is given, else y = o. */
+int megamoe_combine_by_expert_id(int32_t tokens, int32_t hidden, int32_t topk, const void* expert_out,
+                                 const int64_t* expert_ids, const void* weights, const void* residual, void* y,
+                                 void* stream);
+
 /* Tensors of the MXFP4 form (megabench/tasks/megamoe.py, serial): the routed experts of a
  * DeepSeek-V4-style layer with FP4 weights, routing given.
  *   x            e4m3fn [T, H];  x_scales uint8 [T, H/32] (E8M0: 2^(s-127))
@@ -269,9 +299,10 @@ int megamoe_quantize_rows(int32_t rows, int32_t cols, const void* x, uint8_t* q,
 /* Text for a status code (static storage). */
 const char* megamoe_status_string(int status);
 
-/* ABI version of this library: 4 (1, plus megamoe_block_forward and megamoe_rms_norm in 2,
+/* ABI version of this library: 5 (1, plus megamoe_block_forward and megamoe_rms_norm in 2,
  * plus megamoe_mx_workspace_bytes and megamoe_mx_forward in 3, plus megamoe_ep_dispatch,
- * megamoe_ep_experts and megamoe_ep_combine in 4). */
+ * megamoe_ep_experts and megamoe_ep_combine in 4, plus megamoe_forward_ex and
+ * megamoe_combine_by_expert_id in 5). */
 int megamoe_abi_version(void);
 
 #ifdef __cplusplus

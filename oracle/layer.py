@@ -8,6 +8,8 @@ Per token t (megabench/tasks/frontier.py:343-354, with ``linear`` of :180-186):
         xq, xs  = E4M3 per 128 of x[t]                             quantization.py:87-109
         g, u    = bf16(deq(W_gate[e]) @ deq(xq, xs)), same for up  frontier.py:184-186
         h       = bf16(silu(fp32 g) * fp32 u)                      frontier.py:337
+                  (case.swiglu "bf16": bf16(bf16(silu(g)) * u), frontier.py:338 and
+                  glm53.py:174; case.swiglu_limit > 0: g, u clamped first, glm53.py:175)
         d       = bf16(deq(W_down[e]) @ deq(E4M3 per 128 of h))
         acc     = acc + fp32(d) * w[slot]                          frontier.py:349-350
     acc = acc + fp32(shared expert output)                          frontier.py:352
@@ -49,7 +51,16 @@ def _linear(w_deq: torch.Tensor, act: torch.Tensor, power_of_two: bool, out_dtyp
     return (w_deq @ formats.unpack_activation(payload, scales)).to(out_dtype)
 
 
-def _swiglu(g: torch.Tensor, u: torch.Tensor, out_dtype) -> torch.Tensor:
+def _swiglu(case, g: torch.Tensor, u: torch.Tensor, out_dtype) -> torch.Tensor:
+    """g, u in out_dtype (bf16, or fp32 widened). With a limit, gate.clamp(max=L) and
+    up.clamp(-L, L) first (glm53.py:175); then the "fp32" form rounds silu(g) * u once
+    (frontier.py:337) and the "bf16" form is F.silu(gate) * up on the dtype itself, silu
+    rounded before the product (frontier.py:338, glm53.py:174)."""
+    limit = getattr(case, "swiglu_limit", 0.0)
+    if limit > 0:
+        g, u = g.clamp(max=limit), u.clamp(-limit, limit)
+    if getattr(case, "swiglu", "fp32") == "bf16":
+        return (F.silu(g) * u).to(out_dtype)
     return (F.silu(g.float()) * u.float()).to(out_dtype)
 
 
@@ -87,13 +98,13 @@ def moe_layer(case, values: dict, *, widen: bool = False, tokens=None) -> dict:
         wg, wu, wd = _expert(cpu, "gate", e), _expert(cpu, "up", e), _expert(cpu, "down", e)
         for r, t in enumerate(rows):
             for slot in (ids_t[r] == e).nonzero().flatten().tolist():
-                h = _swiglu(_linear(wg, act[t], pw, bf), _linear(wu, act[t], pw, bf), bf)
+                h = _swiglu(case, _linear(wg, act[t], pw, bf), _linear(wu, act[t], pw, bf), bf)
                 down[(r, slot)] = _linear(wd, h, pw, bf)
     shared = {}
     if case.shared_experts:
         wg, wu, wd = _expert(cpu, "shared_gate"), _expert(cpu, "shared_up"), _expert(cpu, "shared_down")
         for r, t in enumerate(rows):
-            h = _swiglu(_linear(wg, act[t], pw, bf), _linear(wu, act[t], pw, bf), bf)
+            h = _swiglu(case, _linear(wg, act[t], pw, bf), _linear(wu, act[t], pw, bf), bf)
             shared[r] = _linear(wd, h, pw, bf)
 
     y = torch.empty((len(rows), H), dtype=bf)

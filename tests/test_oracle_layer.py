@@ -122,7 +122,7 @@ class _Planted:
             orig = layer._expert
             layer._expert = lambda v, n, i=None: orig(v, n, i) * (0.0 if n == "shared_down" else 1.0)
         elif self.kind == "silu_sign":
-            layer._swiglu = lambda g, u, dt: (torch.nn.functional.silu(-g.float()) * u.float()).to(dt)
+            layer._swiglu = lambda case, g, u, dt: (torch.nn.functional.silu(-g.float()) * u.float()).to(dt)
         elif self.kind == "drop_slot":
             orig = layer.route
 

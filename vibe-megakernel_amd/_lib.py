@@ -22,8 +22,9 @@ STAGES_MX = ("permute", "experts", "combine")  # the MXFP4 form (routing and x a
 SYMBOLS = ("megamoe_workspace_bytes", "megamoe_forward", "megamoe_forward_events", "megamoe_forward_timed",
            "megamoe_router_logits", "megamoe_route", "megamoe_quantize_rows", "megamoe_status_string",
            "megamoe_abi_version", "megamoe_block_forward", "megamoe_rms_norm", "megamoe_mx_workspace_bytes",
-           "megamoe_mx_forward", "megamoe_ep_dispatch", "megamoe_ep_experts", "megamoe_ep_combine")
-ABI_VERSION = 4
+           "megamoe_mx_forward", "megamoe_ep_dispatch", "megamoe_ep_experts", "megamoe_ep_combine",
+           "megamoe_forward_ex", "megamoe_combine_by_expert_id")
+ABI_VERSION = 5
 
 
 class Desc(ctypes.Structure):
@@ -46,6 +47,10 @@ class Tensors(ctypes.Structure):
 class Block(ctypes.Structure):
     _fields_ = [("norm_weight", ctypes.c_void_p), ("eps", ctypes.c_float), ("weight_in_fp32", ctypes.c_int32),
                 ("residual", ctypes.c_int32)]
+
+
+class Epilogue(ctypes.Structure):
+    _fields_ = [("swiglu", ctypes.c_int32), ("swiglu_limit", ctypes.c_float)]
 
 
 MX_TENSOR_FIELDS = ("x", "x_scales", "topk_idx", "topk_weights", "l1_blocks", "l1_scales", "l2_blocks", "l2_scales",
@@ -98,6 +103,9 @@ def load() -> ctypes.CDLL:
     lib.megamoe_ep_experts.argtypes = [P(Desc), ctypes.c_float, ctypes.c_int64, P(MxTensors), c_void_p, P(c_void_p)]
     lib.megamoe_ep_combine.argtypes = [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, c_void_p, c_void_p, c_void_p,
                                        c_void_p]
+    lib.megamoe_forward_ex.argtypes = [P(Desc), P(Tensors), P(Block), P(Epilogue), c_void_p, P(c_void_p)]
+    lib.megamoe_combine_by_expert_id.argtypes = [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, c_void_p, c_void_p,
+                                                 c_void_p, c_void_p, c_void_p, c_void_p]
     lib.megamoe_status_string.argtypes = [c_int]
     lib.megamoe_status_string.restype = ctypes.c_char_p
     lib.megamoe_abi_version.argtypes = []

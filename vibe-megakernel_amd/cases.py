@@ -31,6 +31,7 @@ ROUTERS = ("softmax", "sigmoid", "given")  # given: topk_idx / topk_weights are 
 # fp32 per-128 scales (frontier.py); mxfp4 = E2M1 weights with E8M0 scales per 32 and
 # E4M3 activations with E8M0 scales per 32 (megamoe.py, quantization.py:13-116).
 FORMATS = ("fp8", "mxfp4")
+SWIGLUS = ("fp32", "bf16")
 # RMSNorm before the layer (the block form): none, gamma applied in fp32 before the one
 # bf16 rounding (DeepSeek), or to the rounded activation (common.py:13-21).
 NORMS = ("none", "fp32_weight", "bf16_weight")
@@ -83,6 +84,10 @@ class Case:
     # to gate (above) and up (both sides) before the activation (megamoe.py:116-122).
     format: str = "fp8"
     swiglu_limit: float = 0.0
+    # The SwiGLU form of the fp8 experts: "fp32" h = bf16(silu(g) * u) rounded once
+    # (frontier.py:337, DeepSeek), "bf16" h = bf16(bf16(silu(g)) * u) (frontier.py:338,
+    # glm53.py:174-175); swiglu_limit > 0 clamps g and u first in either form.
+    swiglu: str = "fp32"
 
     def __post_init__(self) -> None:
         if not self.id or self.family != FAMILY or not self.model or not self.phase:
@@ -103,6 +108,8 @@ class Case:
             raise ValueError(f"invalid routing rule in {self.id}")
         if self.norm not in NORMS or not self.norm_eps >= 0:
             raise ValueError(f"invalid normalization in {self.id}")
+        if self.swiglu not in SWIGLUS or not self.swiglu_limit >= 0 or (self.format == "mxfp4" and self.swiglu != "fp32"):
+            raise ValueError(f"invalid SwiGLU form in {self.id}")
         if self.format not in FORMATS:
             raise ValueError(f"invalid expert format in {self.id}")
         if (self.format == "mxfp4") != (self.router == "given"):
@@ -230,8 +237,22 @@ EP_CASES: tuple[Case, ...] = (
 )
 
 
+# Epilogue variants of the fp8 layer: GLM-5.3-Flash's MoE (glm53.py:263-274): sigmoid
+# routing with the correction bias and no groups (frontier.route(..., 1, 1), scaling 2.5),
+# one shared expert, and SwiGLU in bf16 with the clamp at 10 (glm53.py:30,174-175); the
+# geometry of its catalog entry (megabench/cases.py:304-313), 64 tokens as the other
+# decode configs.
+VARIANT_CASES: tuple[Case, ...] = (
+    _case("moe-fp8-glm-5.3-flash-t64", "zai-org/GLM-5.3-Flash (MoE shape, clamped bf16 SwiGLU)",
+          params=dict(tokens=64, hidden=4096, experts=288, topk=8, intermediate=2048, shared_experts=1,
+                      router_groups=1, router_top_groups=1),
+          router="sigmoid", renormalize=True, routed_scaling=2.5, bias="normal", bias_std=0.1,
+          swiglu="bf16", swiglu_limit=10.0),
+)
+
+
 def case(case_id: str) -> Case:
-    for c in CASES + BLOCK_CASES + MX_CASES + EP_CASES:
+    for c in CASES + BLOCK_CASES + MX_CASES + EP_CASES + VARIANT_CASES:
         if c.id == case_id:
             return c
     raise KeyError(case_id)

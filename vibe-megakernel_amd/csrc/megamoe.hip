@@ -1227,6 +1227,8 @@ struct GateUpArgs {
   uint8_t* hq_s; float* hs_s;   // shared rows [T, S*I], [T, S*I/128]
   const uint8_t* spare;         // 16 rows of the longest weight row, in the workspace
   int T, H, I, K, S, E, pow2;
+  int swiglu;                   // 0: fp32 product rounded once; 1: bf16 silu, bf16 product
+  float limit;                  // > 0: SwiGLU clamp (gate above, up both sides)
 };
 
 // One gate/up unit: rows [jb*128, jb*128+128) of gate and of up against the chunk's
@@ -1261,7 +1263,11 @@ __device__ void gateup_unit(const GateUpArgs& a, const uint8_t* wg, const uint8_
   f32x4 acc[4][NCT];
   stream_gemm<4, NCT, 2, 2>(op, nkb, rot, ring, acc);
 
-  // h = bf16(silu(fp32 bf16(g)) * fp32 bf16(u)) (frontier.py:184-186,337)
+  // g, u = bf16 (frontier.py:184-186), clamped at the SwiGLU limit if one is set
+  // (glm53.py:175); h = bf16(silu(fp32 g) * fp32 u) (frontier.py:337, DeepSeek) or
+  // bf16(bf16(silu(g)) * u) (frontier.py:338, glm53.py:174-175).
+  const bool bf16_silu = a.swiglu != 0;
+  const float L = a.limit > 0.0f ? a.limit : INFINITY;
   float hv[NCT][2][4];
 #pragma unroll
   for (int c = 0; c < NCT; ++c) {
@@ -1270,9 +1276,9 @@ __device__ void gateup_unit(const GateUpArgs& a, const uint8_t* wg, const uint8_
     for (int p = 0; p < 2; ++p)
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        const float g = round_bf16(acc[p][c][v]);
-        const float u = round_bf16(acc[p + 2][c][v]);
-        const float h = round_bf16(silu(g) * u);
+        const float g = fminf(round_bf16(acc[p][c][v]), L);
+        const float u = fminf(fmaxf(round_bf16(acc[p + 2][c][v]), -L), L);
+        const float h = bf16_silu ? round_bf16(round_bf16(silu(g)) * u) : round_bf16(silu(g) * u);
         hv[c][p][v] = h;
         amax = fmaxf(amax, fabsf(h));
       }
@@ -2472,7 +2478,7 @@ int launch_norm(int rows, int cols, const void* x, const void* w, float eps, int
 // The layer; with `blk`, the block form: RMSNorm of x before the router (the layer then
 // reads the normalized rows) and the residual add in the combine.
 int forward_impl(const megamoe_desc* desc, const megamoe_tensors* t, hipStream_t st, hipEvent_t* ev,
-                 const megamoe_block* blk = nullptr) {
+                 const megamoe_block* blk = nullptr, const megamoe_epilogue* epi = nullptr) {
   int rc = validate(desc);
   if (rc) return rc;
   if (!t) return MEGAMOE_ERR_INVALID_ARGUMENT;
@@ -2534,6 +2540,8 @@ int forward_impl(const megamoe_desc* desc, const megamoe_tensors* t, hipStream_t
   ga.hq_s = (uint8_t*)(ws + L.hq_s); ga.hs_s = (float*)(ws + L.hs_s);
   ga.spare = (const uint8_t*)(ws + L.spare);
   ga.T = T; ga.H = H; ga.I = I; ga.K = K; ga.S = S; ga.E = E; ga.pow2 = d.pow2_scales;
+  ga.swiglu = epi ? epi->swiglu : 0;
+  ga.limit = epi ? epi->swiglu_limit : 0.0f;
   DownArgs& da = ea.dn;
   da.down = t->down; da.down_scale = t->down_scale;
   da.sdown = t->shared_down; da.sdown_scale = t->shared_down_scale;
@@ -2797,13 +2805,64 @@ __global__ __launch_bounds__(256) void k_ep_combine(const uint16_t* __restrict__
   *reinterpret_cast<uint4*>(y + (size_t)t * H + h0) = make_uint4(o[0], o[1], o[2], o[3]);
 }
 
+// GPT-OSS's combine (gptoss.py:112-124): a token's expert outputs accumulate in ascending
+// expert id order, independent of the router's rank order, in bf16: o = bf16(o + bf16(p * e))
+// from o = 0, with bf16 weights p; then y = bf16(x + o) with a residual x, else y = o.
+__global__ __launch_bounds__(256) void k_combine_id_order(const uint16_t* __restrict__ out,
+                                                          const int64_t* __restrict__ ids,
+                                                          const uint16_t* __restrict__ wts,
+                                                          const uint16_t* __restrict__ residual, int T, int H, int K,
+                                                          uint16_t* __restrict__ y) {
+  const int i = blockIdx.x * 256 + threadIdx.x, per_row = H / 8;
+  if (i >= T * per_row) return;
+  const int t = i / per_row, h0 = (i % per_row) * 8;
+  const int64_t* row_ids = ids + (size_t)t * K;
+  float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  int64_t last = INT64_MIN;
+  for (int n = 0; n < K; ++n) {
+    // The slot with the smallest id above the previous one (ids of a token are distinct).
+    int k = -1;
+    int64_t best = INT64_MAX;
+    for (int j = 0; j < K; ++j) {
+      const int64_t e = row_ids[j];
+      if (e > last && e <= best) {
+        best = e;
+        k = j;
+      }
+    }
+    if (k < 0) break;
+    last = best;
+    const float p = bf16_bits_to_f32(wts[(size_t)t * K + k]);
+    const uint4 v = *reinterpret_cast<const uint4*>(out + ((size_t)t * K + k) * H + h0);
+    const uint32_t q[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      o[2 * j] = round_bf16(__fadd_rn(o[2 * j], round_bf16(__fmul_rn(p, bf16_bits_to_f32(q[j] & 0xffffu)))));
+      o[2 * j + 1] = round_bf16(__fadd_rn(o[2 * j + 1], round_bf16(__fmul_rn(p, bf16_bits_to_f32(q[j] >> 16)))));
+    }
+  }
+  uint32_t r[4];
+  if (residual) {
+    const uint4 v = *reinterpret_cast<const uint4*>(residual + (size_t)t * H + h0);
+    const uint32_t q[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      r[j] = f32_to_bf16_bits(__fadd_rn(bf16_bits_to_f32(q[j] & 0xffffu), o[2 * j])) |
+             (f32_to_bf16_bits(__fadd_rn(bf16_bits_to_f32(q[j] >> 16), o[2 * j + 1])) << 16);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) r[j] = f32_to_bf16_bits(o[2 * j]) | (f32_to_bf16_bits(o[2 * j + 1]) << 16);
+  }
+  *reinterpret_cast<uint4*>(y + (size_t)t * H + h0) = make_uint4(r[0], r[1], r[2], r[3]);
+}
+
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 }  // namespace
 
 extern "C" {
 
-int megamoe_abi_version(void) { return 4; }
+int megamoe_abi_version(void) { return 5; }
 
 const char* megamoe_status_string(int status) {
   switch (status) {
@@ -2888,6 +2947,38 @@ int megamoe_block_forward(const megamoe_desc* desc, const megamoe_tensors* t, co
     }
   }
   return forward_impl(desc, t, (hipStream_t)stream, events ? ev : nullptr, block);
+}
+
+int megamoe_forward_ex(const megamoe_desc* desc, const megamoe_tensors* t, const megamoe_block* block,
+                       const megamoe_epilogue* epilogue, void* stream, void* const* events) {
+  if (block && !(block->eps >= 0.0f)) return MEGAMOE_ERR_INVALID_ARGUMENT;
+  if (epilogue && ((epilogue->swiglu != 0 && epilogue->swiglu != 1) || !(epilogue->swiglu_limit >= 0.0f)))
+    return MEGAMOE_ERR_INVALID_ARGUMENT;
+  hipEvent_t ev[kStages + 1];
+  if (events) {
+    for (int i = 0; i < kStages + 1; ++i) {
+      if (!events[i]) return MEGAMOE_ERR_INVALID_ARGUMENT;
+      ev[i] = (hipEvent_t)events[i];
+    }
+  }
+  return forward_impl(desc, t, (hipStream_t)stream, events ? ev : nullptr, block, epilogue);
+}
+
+int megamoe_combine_by_expert_id(int32_t tokens, int32_t hidden, int32_t topk, const void* expert_out,
+                                 const int64_t* expert_ids, const void* weights, const void* residual, void* y,
+                                 void* stream) {
+  if (tokens < 0 || hidden <= 0 || topk <= 0 || hidden % 8) return MEGAMOE_ERR_SHAPE;
+  if (topk > kMaxTopK) return MEGAMOE_ERR_UNSUPPORTED;
+  if (tokens == 0) return MEGAMOE_OK;
+  if (!expert_out || !expert_ids || !weights || !y) return MEGAMOE_ERR_INVALID_ARGUMENT;
+  if (!aligned16(expert_out) || !aligned16(y) || (residual && !aligned16(residual))) return MEGAMOE_ERR_INVALID_ARGUMENT;
+  const int64_t work = (int64_t)tokens * (hidden / 8);
+  if (work >= ((int64_t)1 << 31)) return MEGAMOE_ERR_UNSUPPORTED;
+  hipLaunchKernelGGL(k_combine_id_order, dim3((unsigned)((work + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                     (const uint16_t*)expert_out, expert_ids, (const uint16_t*)weights, (const uint16_t*)residual,
+                     tokens, hidden, topk, (uint16_t*)y);
+  MEGAMOE_LAUNCH_CHECK();
+  return MEGAMOE_OK;
 }
 
 int megamoe_mx_workspace_bytes(const megamoe_desc* desc, size_t* bytes) {

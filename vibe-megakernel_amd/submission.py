@@ -68,6 +68,9 @@ class MoELayer:
         self.workspace_bytes = int(size.value)
         self._workspace: dict[torch.device, torch.Tensor] = {}
         self.block = None if case.norm == "none" and not case.residual else (case.norm, case.residual)
+        # The epilogue variant of the fp8 form (megamoe_forward_ex): None is the DeepSeek form.
+        self.epilogue = (None if self.mx or (case.swiglu == "fp32" and case.swiglu_limit == 0) else
+                         _lib.Epilogue(swiglu=int(case.swiglu == "bf16"), swiglu_limit=float(case.swiglu_limit)))
 
     def workspace(self, device: torch.device) -> torch.Tensor:
         ws = self._workspace.get(device)
@@ -165,16 +168,20 @@ class MoELayer:
                                workspace_bytes=self.workspace_bytes)
         stream = ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
         with torch.cuda.device(device):
-            if self.block is not None:
+            if self.block is not None or self.epilogue is not None:
                 if timed:
-                    raise ValueError("timed() covers the layer form; use record() for the block form")
-                blk = _lib.Block(norm_weight=inputs["ln2"].data_ptr() if c.norm != "none" else None,
-                                 eps=float(c.norm_eps), weight_in_fp32=int(c.norm == "fp32_weight"),
-                                 residual=int(c.residual))
+                    raise ValueError("timed() covers the plain layer form; use record() for the block form and "
+                                     "the epilogue variants")
+                blk = None
+                if self.block is not None:
+                    blk = ctypes.byref(_lib.Block(norm_weight=inputs["ln2"].data_ptr() if c.norm != "none" else None,
+                                                  eps=float(c.norm_eps), weight_in_fp32=int(c.norm == "fp32_weight"),
+                                                  residual=int(c.residual)))
+                epi = None if self.epilogue is None else ctypes.byref(self.epilogue)
                 handles = (None if events is None else
                            (ctypes.c_void_p * len(events))(*[e.cuda_event for e in events]))
-                _lib.check(self.lib.megamoe_block_forward(ctypes.byref(self.desc), ctypes.byref(tensors),
-                                                          ctypes.byref(blk), stream, handles), f"{c.id}: forward")
+                _lib.check(self.lib.megamoe_forward_ex(ctypes.byref(self.desc), ctypes.byref(tensors), blk, epi,
+                                                       stream, handles), f"{c.id}: forward")
                 return {"y": y, "expert_ids": ids, "expert_weights": weights}
             if events is not None:
                 handles = (ctypes.c_void_p * len(events))(*[e.cuda_event for e in events])
@@ -258,6 +265,26 @@ def route(case: Case, logits: torch.Tensor, bias: torch.Tensor | None) -> tuple[
                                      None if bias is None else bias.contiguous().data_ptr(), ids.data_ptr(),
                                      w.data_ptr(), stream), "route")
     return ids, w
+
+
+def combine_by_expert_id(expert_out: torch.Tensor, expert_ids: torch.Tensor, weights: torch.Tensor,
+                         residual: torch.Tensor | None = None) -> torch.Tensor:
+    """GPT-OSS's combine (gptoss.py:112-124) through megamoe_combine_by_expert_id: expert_out
+    bf16 [T, K, H], expert_ids int64 [T, K], weights bf16 [T, K], residual bf16 [T, H] or None."""
+    T, K, H = expert_out.shape
+    device = expert_out.device
+    _expect(expert_out, "expert_out", torch.bfloat16, (T, K, H), device)
+    _expect(expert_ids, "expert_ids", torch.int64, (T, K), device)
+    _expect(weights, "weights", torch.bfloat16, (T, K), device)
+    if residual is not None:
+        _expect(residual, "residual", torch.bfloat16, (T, H), device)
+    y = torch.empty((T, H), dtype=torch.bfloat16, device=device)
+    stream = ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+    with torch.cuda.device(device):
+        _lib.check(_lib.load().megamoe_combine_by_expert_id(
+            T, H, K, expert_out.data_ptr(), expert_ids.data_ptr(), weights.data_ptr(),
+            None if residual is None else residual.data_ptr(), y.data_ptr(), stream), "combine by expert id")
+    return y
 
 
 def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float, weight_in_fp32: bool) -> torch.Tensor:
