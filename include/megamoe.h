@@ -266,7 +266,7 @@ typedef struct megamoe_ep_send {
  * slot) order. desc: tokens, hidden (a multiple of 256), experts (divisible by ep), topk;
  * t: x, x_scales, topk_idx, topk_weights (16- and 8-byte aligned x and x_scales, as the send
  * rows and row scales). An id outside [0, E) makes every count -1 and every slot row -1, and
- * nothing is packed. */
+ * nothing is packed. Limits: ep <= 256, T*K <= 49152 (MEGAMOE_ERR_UNSUPPORTED beyond). */
 int megamoe_ep_dispatch(const megamoe_desc* desc, int32_t ep, const megamoe_mx_tensors* t,
                         const megamoe_ep_send* send, void* stream);
 

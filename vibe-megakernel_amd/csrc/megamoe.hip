@@ -2091,10 +2091,17 @@ struct DownMxArgs {
   const uint8_t* hq; const uint8_t* hs;
   uint16_t* d;  // [T*K, H] bf16, grouped rows
   float* pd;    // ks > 1: [ks, T*K, H] fp32 partial d of each K part
+  uint16_t* y;  // K == 1 and ks == 1: d straight into the output, row perm[r] (token order)
   const uint8_t* spare;
   int T, H, I, K, E, hs_ld, ks;
   int ebase;
 };
+
+// Where a down unit's bf16 d row goes: grouped row r of the workspace, or with one slot per
+// token and no K split, the token's output row (y = bf16(fp32(d)) = d needs no combine).
+__device__ __forceinline__ uint16_t* down_row_mx(const DownMxArgs& a, const ChunkRows& cr, int r) {
+  return a.y ? a.y + (size_t)cr.perm[cr.row0 + r] * a.H : a.d + (size_t)(cr.row0 + r) * a.H;
+}
 
 // Down unit: rows [j*128, +128) of the expert's down matrix over K part kp of ks.
 template <int NCT, bool PAIR>
@@ -2127,13 +2134,13 @@ __device__ void down_mx_unit(const DownMxArgs& a, int e, int j, int kp, const Ch
     if (r < cr.n) {
 #pragma unroll
       for (int p = 0; p < 2; ++p) {
-        const size_t o = (size_t)(cr.row0 + r) * a.H + (size_t)j * kBlock + 32 * w + 16 * p + 4 * (lane >> 4);
+        const size_t col = (size_t)j * kBlock + 32 * w + 16 * p + 4 * (lane >> 4);
         if (a.ks == 1) {
           const uint32_t lo = f32_to_bf16_bits(acc[p][c][0]) | (f32_to_bf16_bits(acc[p][c][1]) << 16);
           const uint32_t hi = f32_to_bf16_bits(acc[p][c][2]) | (f32_to_bf16_bits(acc[p][c][3]) << 16);
-          *reinterpret_cast<uint2*>(a.d + o) = make_uint2(lo, hi);
+          *reinterpret_cast<uint2*>(down_row_mx(a, cr, r) + col) = make_uint2(lo, hi);
         } else {
-          *reinterpret_cast<f32x4*>(pd + o) = acc[p][c];
+          *reinterpret_cast<f32x4*>(pd + (size_t)(cr.row0 + r) * a.H + col) = acc[p][c];
         }
       }
     }
@@ -2173,13 +2180,13 @@ __device__ void down_mx_wide(const DownMxArgs& a, int e, int j64, int kp, const 
     if (r < cr.n) {
 #pragma unroll
       for (int p = 0; p < 4; ++p) {
-        const size_t o = (size_t)(cr.row0 + r) * a.H + (size_t)j64 * 64 + 16 * p + 4 * (lane >> 4);
+        const size_t col = (size_t)j64 * 64 + 16 * p + 4 * (lane >> 4);
         if (a.ks == 1) {
           const uint32_t lo = f32_to_bf16_bits(acc[p][c][0]) | (f32_to_bf16_bits(acc[p][c][1]) << 16);
           const uint32_t hi = f32_to_bf16_bits(acc[p][c][2]) | (f32_to_bf16_bits(acc[p][c][3]) << 16);
-          *reinterpret_cast<uint2*>(a.d + o) = make_uint2(lo, hi);
+          *reinterpret_cast<uint2*>(down_row_mx(a, cr, r) + col) = make_uint2(lo, hi);
         } else {
-          *reinterpret_cast<f32x4*>(pd + o) = acc[p][c];
+          *reinterpret_cast<f32x4*>(pd + (size_t)(cr.row0 + r) * a.H + col) = acc[p][c];
         }
       }
     }
@@ -2576,6 +2583,14 @@ int forward_impl(const megamoe_desc* desc, const megamoe_tensors* t, hipStream_t
 
 // -- The MXFP4 form ----------------------------------------------------------------------
 
+// With the output written by the down units (one slot per token, no K split), this stands
+// in for the combine: if the permute flagged bad ids, every element of y is NaN.
+__global__ __launch_bounds__(256) void k_error_fill(const int* __restrict__ meta, size_t n8, uint16_t* __restrict__ y) {
+  if (!meta[kMetaError]) return;
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n8; i += (size_t)gridDim.x * 256)
+    *reinterpret_cast<uint4*>(y + i * 8) = make_uint4(0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u);
+}
+
 constexpr int kStagesMx = 3;  // permute, experts, combine
 
 int validate_mx(const megamoe_desc* d) {
@@ -2683,6 +2698,8 @@ int forward_mx_impl(const megamoe_desc* desc, float limit, const megamoe_mx_tens
   da.offsets = po.offsets; da.perm = po.perm; da.chunks = po.dn; da.meta = po.meta;
   da.hq = ga.hq; da.hs = ga.hs;
   da.d = (uint16_t*)(ws + L.d); da.pd = (float*)(ws + L.p);
+  const bool direct = K == 1 && L.ks == 1;  // the down units write y; no combine
+  da.y = direct ? (uint16_t*)t->y : nullptr;
   da.spare = ga.spare;
   da.T = T; da.H = H; da.I = I; da.K = K; da.E = E; da.hs_ld = L.hs_ld; da.ks = L.ks;
   da.ebase = (int)base;
@@ -2697,9 +2714,14 @@ int forward_mx_impl(const megamoe_desc* desc, float limit, const megamoe_mx_tens
   if (mark(2) != hipSuccess) return MEGAMOE_ERR_HIP;
 
   const int rows8 = T * (H / 8);
-  hipLaunchKernelGGL(k_combine, dim3((rows8 + 255) / 256), dim3(256), 0, st, (const uint16_t*)da.d,
-                     (const uint16_t*)nullptr, (const float*)da.pd, (const float*)nullptr, L.ks, (const int*)po.inv,
-                     (const float*)nullptr, T, H, K, 0, (const int*)po.meta, (const uint16_t*)nullptr, (uint16_t*)t->y);
+  if (direct)
+    hipLaunchKernelGGL(k_error_fill, dim3((unsigned)((rows8 + 255) / 256 < 1024 ? (rows8 + 255) / 256 : 1024)),
+                       dim3(256), 0, st, (const int*)po.meta, (size_t)rows8, (uint16_t*)t->y);
+  else
+    hipLaunchKernelGGL(k_combine, dim3((rows8 + 255) / 256), dim3(256), 0, st, (const uint16_t*)da.d,
+                       (const uint16_t*)nullptr, (const float*)da.pd, (const float*)nullptr, L.ks,
+                       (const int*)po.inv, (const float*)nullptr, T, H, K, 0, (const int*)po.meta,
+                       (const uint16_t*)nullptr, (uint16_t*)t->y);
   MEGAMOE_LAUNCH_CHECK();
   if (mark(3) != hipSuccess) return MEGAMOE_ERR_HIP;
   return MEGAMOE_OK;
@@ -2715,23 +2737,29 @@ int forward_mx_impl(const megamoe_desc* desc, float limit, const megamoe_mx_tens
 // per row) and, once the outputs have come back in send order, sums each token's slots in
 // slot order (megamoe.py:176-182). The exchanges in between are collectives of the caller.
 
-constexpr int kMaxRanks = 1024;
+constexpr int kMaxRanks = 256;              // owner ranks are held as bytes
+constexpr int kMaxDispatch = 48 * 1024;     // (token, slot) entries of one dispatch (LDS bytes)
 
-// Send row of every (token, slot): a stable counting sort by owner rank, one workgroup. Each
-// thread owns a contiguous run of entries; per owner, an exclusive scan of the runs' counts
-// places each run after the earlier ones. An id outside [0, E) makes every count -1 and
-// every send row -1 (nothing is packed).
+// Send row of every (token, slot): a stable counting sort by owner rank, one workgroup. The
+// owners are read once (coalesced) into LDS; each thread then owns a contiguous run of
+// entries, and per owner an exclusive scan of the runs' counts places each run after the
+// earlier ones. An id outside [0, E) makes every count -1 and every send row -1 (nothing is
+// packed).
 __global__ __launch_bounds__(1024) void k_ep_order(const int64_t* __restrict__ ids, int n, int E, int local, int ep,
                                                    int64_t* __restrict__ counts, int32_t* __restrict__ slot_rows) {
+  extern __shared__ uint8_t owner[];  // n bytes
   __shared__ unsigned long long tmp[16];
   __shared__ int bad;
   const int tid = threadIdx.x, per = (n + 1023) / 1024;
   const int lo = min(n, tid * per), hi = min(n, lo + per);
   if (tid == 0) bad = 0;
   __syncthreads();
-  for (int i = lo; i < hi; ++i) {
+  for (int i = tid; i < n; i += 1024) {
     const int64_t e = ids[i];
-    if (e < 0 || e >= E) bad = 1;
+    if (e < 0 || e >= E)
+      bad = 1;
+    else
+      owner[i] = (uint8_t)(e / local);
   }
   __syncthreads();
   if (bad) {
@@ -2742,11 +2770,11 @@ __global__ __launch_bounds__(1024) void k_ep_order(const int64_t* __restrict__ i
   int base = 0;
   for (int o = 0; o < ep; ++o) {
     int c = 0;
-    for (int i = lo; i < hi; ++i) c += (int)ids[i] / local == o;
+    for (int i = lo; i < hi; ++i) c += owner[i] == o;
     unsigned long long total;
     int pos = base + (int)block_exclusive_scan((unsigned long long)c, tmp, &total);
     for (int i = lo; i < hi; ++i)
-      if ((int)ids[i] / local == o) slot_rows[i] = pos++;
+      if (owner[i] == o) slot_rows[i] = pos++;
     if (tid == 0) counts[o] = (int64_t)total;
     base += (int)total;
     __syncthreads();  // tmp is rewritten by the next owner's scan
@@ -3006,12 +3034,12 @@ int megamoe_ep_dispatch(const megamoe_desc* desc, int32_t ep, const megamoe_mx_t
   if (!desc || !t || !send) return MEGAMOE_ERR_INVALID_ARGUMENT;
   const int64_t T = desc->tokens, H = desc->hidden, E = desc->experts, K = desc->topk;
   if (T < 0 || H <= 0 || E <= 0 || K <= 0 || K > E || H % kMxStageK || ep <= 0 || E % ep) return MEGAMOE_ERR_SHAPE;
-  if (ep > kMaxRanks || T * K >= ((int64_t)1 << 30)) return MEGAMOE_ERR_UNSUPPORTED;
+  if (ep > kMaxRanks || T * K > kMaxDispatch) return MEGAMOE_ERR_UNSUPPORTED;
   if (!send->counts) return MEGAMOE_ERR_INVALID_ARGUMENT;
   hipStream_t st = (hipStream_t)stream;
   const int n = (int)(T * K);
   if (n == 0) {  // zero counts, written by the order kernel (no memset, so the call may be captured)
-    hipLaunchKernelGGL(k_ep_order, dim3(1), dim3(1024), 0, st, (const int64_t*)nullptr, 0, (int)E, (int)(E / ep),
+    hipLaunchKernelGGL(k_ep_order, dim3(1), dim3(1024), 16, st, (const int64_t*)nullptr, 0, (int)E, (int)(E / ep),
                        (int)ep, send->counts, (int32_t*)nullptr);
     MEGAMOE_LAUNCH_CHECK();
     return MEGAMOE_OK;
@@ -3021,8 +3049,8 @@ int megamoe_ep_dispatch(const megamoe_desc* desc, int32_t ep, const megamoe_mx_t
     return MEGAMOE_ERR_INVALID_ARGUMENT;
   if (!aligned16(t->x) || !aligned16(send->rows) || ((uintptr_t)t->x_scales & 7) || ((uintptr_t)send->row_scales & 7))
     return MEGAMOE_ERR_INVALID_ARGUMENT;
-  hipLaunchKernelGGL(k_ep_order, dim3(1), dim3(1024), 0, st, t->topk_idx, n, (int)E, (int)(E / ep), (int)ep,
-                     send->counts, send->slot_rows);
+  hipLaunchKernelGGL(k_ep_order, dim3(1), dim3(1024), (size_t)n, st, t->topk_idx, n, (int)E, (int)(E / ep),
+                     (int)ep, send->counts, send->slot_rows);
   MEGAMOE_LAUNCH_CHECK();
   hipLaunchKernelGGL(k_ep_pack, dim3(n), dim3(256), 0, st, t->x, t->x_scales, t->topk_idx, t->topk_weights,
                      (const int32_t*)send->slot_rows, (int)K, (int)H, send->rows, send->row_scales, send->ids,
