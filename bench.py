@@ -11,8 +11,11 @@ Infinity Cache cannot hold a step's weights.
 
 Printed: one JSON line (rank 0) with the headline metric of the DeepSeek-V3
 shape (or --case), the roofline of the dominant kernel (k_experts: gate/up +
-SwiGLU + down) and the CPU oracle timed on a bounded sample. --all adds one
-line per config to stderr.
+SwiGLU + down; k_experts_mx for the MXFP4 forms) and the CPU oracle timed on a
+bounded sample. --all measures every other config and form (the block forms, the
+MXFP4 layer, rank 0's EP share, the epilogue variants), each in a child process,
+prints each child's line to stderr and summarizes them under "configs". For an EP
+case a step is rank 0's dispatch, local experts and combine (bench_ep_share).
 
 The kernel's duration comes from a second loop of K steps in which the library
 records HIP events at its stage boundaries on the stream its kernels run on
@@ -380,7 +383,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--case", default=None)
-    ap.add_argument("--all", action="store_true", help="also measure the other four configs")
+    ap.add_argument("--all", action="store_true",
+                    help="also measure the other configs and forms (block, MXFP4, EP share, epilogue variants)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU oracle work")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
@@ -402,7 +406,8 @@ def main() -> int:
     if args.copy_probe_mib > 0:
         copy_probe(args.copy_probe_mib)
     head = C.case(args.case or C.HEADLINE)
-    others = [c for c in C.CASES if c.id != head.id] if args.all else []
+    every = C.CASES + C.BLOCK_CASES + C.MX_CASES + C.EP_CASES + C.VARIANT_CASES
+    others = [c for c in every if c.id != head.id] if args.all else []
     run = bench_ep_share if head.ep > 1 else bench_case
     r = run(head, args.steps, args.warmup, not args.no_cpu_baseline, args.cpu_budget)
     # Each other config runs in a child process of its own, on a fresh device heap: after a
@@ -436,7 +441,8 @@ def main() -> int:
         "cpu_baseline": r.get("cpu_baseline"),
         "configs": {cid: {"us_per_step": v["value"], "p50_us": v["p50_us"], "tb_per_s": v["achieved_tb_per_s"],
                           "hbm_frac": v["hbm_frac"], "hit_experts": v["hit_experts"],
-                          "experts_frac": v["roofline"]["frac"], "stage_us": v["stage_us"]}
+                          "kernel": v["roofline"]["kernel"], "kernel_frac": v["roofline"]["frac"],
+                          "stage_us": v["stage_us"]}
                     for cid, v in results.items()},
     }
     print(json.dumps(line), flush=True)

@@ -104,3 +104,21 @@ def test_mx_full_size_on_sampled_tokens():
     exact = mx.oracle(case, cpu, tokens=rows)["y"]
     check, band = _check(case, got.cpu()[rows], want, exact)
     _log(f"  {case.id}: {check} band_rel={band['relative_error']:.3e}")
+
+
+def test_rows_do_not_depend_on_the_kernel_mode():
+    """A row's result depends only on the row and its expert: the same 8 tokens give the same
+    bits in a call of 8 tokens (decode units, 16 rows per expert at most) and as the first 8
+    of 200 tokens (100 rows per expert on average: batch units, chunks of 64 rows)."""
+    base = C.case(MXCASE)
+    small = C.development(base, tokens=8, experts=4, topk=2, hidden=512, intermediate=512)
+    large = C.development(base, tokens=200, experts=4, topk=2, hidden=512, intermediate=512)
+    _log("mx mode independence")
+    values = workloads.make_inputs(large, 31, "cpu")
+    head = {k: (v[:8] if k in ("x", "x_scales", "topk_idx", "topk_weights") else v) for k, v in values.items()}
+    y_small = submission.build(small.to_dict())(_to(head, DEV))["y"]
+    y_large = submission.build(large.to_dict())(_to(values, DEV))["y"]
+    torch.cuda.synchronize()
+    assert torch.equal(y_small, y_large[:8])
+    want, exact = mx.reference(large, values)["y"], mx.oracle(large, values)["y"]
+    _check(large, y_large.cpu(), want, exact)

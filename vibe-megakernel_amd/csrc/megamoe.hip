@@ -1892,6 +1892,10 @@ struct GateUpMxArgs {
 //   gate, up = bf16(l1); gate = min(gate, limit); up = clamp(up, +-limit)
 //   a = gate / (1 + exp(-gate)) * up * w_slot (fp32, megamoe.py:116-122)
 //   h = E4M3(a * 2^(127-e)), e = E8M0 exponent of the block's amax (megamoe.py:125-128)
+template <int NCT>
+__device__ void gateup_mx_epilogue(const GateUpMxArgs& a, int jb, const ChunkRows& cr, const f32x4 (&acc)[4][NCT],
+                                   uint8_t (*red8)[64]);
+
 template <int NCT, bool PAIR>
 __device__ void gateup_mx_unit(const GateUpMxArgs& a, int e, int jb, const ChunkRows& cr, int rot, uint8_t (*red8)[64],
                                uint8_t* ring) {
@@ -1917,7 +1921,18 @@ __device__ void gateup_mx_unit(const GateUpMxArgs& a, int e, int jb, const Chunk
   }
   f32x4 acc[4][NCT];
   stream_gemm_mx<4, NCT, 2, PAIR>(op, H / kMxStageK, rot, ring, acc);
+  gateup_mx_epilogue<NCT>(a, jb, cr, acc, red8);
+}
 
+// The epilogue of a 128-channel gate/up unit whose wave w holds gate and up channels
+// [32w, 32w + 32) of block jb for column tiles 0 .. NCT-1: SwiGLU, the E8M0 scale of each
+// row's 32 channels (within the wavefront), E4M3 h, and the four waves' scale bytes of a
+// row gathered into one dword.
+template <int NCT>
+__device__ void gateup_mx_epilogue(const GateUpMxArgs& a, int jb, const ChunkRows& cr, const f32x4 (&acc)[4][NCT],
+                                   uint8_t (*red8)[64]) {
+  const int lane = opaque_lane(), w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lr = lane & 15;
   const float L = a.limit;
 #pragma unroll
   for (int c = 0; c < NCT; ++c) {
@@ -2205,7 +2220,7 @@ __device__ void down_mx_work(const DownMxArgs& a, int v, int nwide, int* ready_c
     const int4 ch = a.chunks[c];
     const ChunkRows cr{ch.z, a.offsets[ch.x] + ch.y, a.perm, a.K};
     const ReadyWait ready{&ready_counts[c], 4 * nbI, error};
-    const int key = ((ch.x + a.ebase) * nbH + j64 / 2) * a.ks + kp;  // as the narrow unit of the same rows
+    const int key = ((ch.x + a.ebase) * (nbH / 2) + j64 / 4) * a.ks + kp;  // as every unit of these rows
     const bool two = cr.n > 64;
     if (nstp % 2 == 0) {
       const int rot = 2 * (key % (nstp / 2));
@@ -2228,7 +2243,8 @@ __device__ void down_mx_work(const DownMxArgs& a, int v, int nwide, int* ready_c
   const int rem = v % (nbH * a.ks), j = rem / a.ks, kp = rem % a.ks;
   const ChunkRows cr{ch.z, a.offsets[ch.x] + ch.y, a.perm, a.K};
   const ReadyWait ready{&ready_counts[c], nbI, error};
-  const int key = ((ch.x + a.ebase) * nbH + j) * a.ks + kp;
+  // Keyed by 256-row block, as the batch units (k_experts_mx_batch) of the same rows.
+  const int key = ((ch.x + a.ebase) * (nbH / 2) + j / 2) * a.ks + kp;
   if (nstp % 2 == 0) {
     const int rot = 2 * (key % (nstp / 2));
     if (cr.n <= 16)
@@ -2242,6 +2258,250 @@ __device__ void down_mx_work(const DownMxArgs& a, int v, int nwide, int* ready_c
     else
       down_mx_unit<2, false>(a, ch.x, j, kp, cr, rot, ready, ring);
   }
+}
+
+
+// ---------------------------------------------------------------------------------------
+// Batch mode of the MXFP4 experts (tens of rows per expert, e.g. a rank's share under
+// expert parallelism): one workgroup per CU, every operand through LDS DMA.
+//   * weights: wave w streams its own 4 tiles (gate/up: 32 gate + 32 up rows of a
+//     128-channel block; down: 64 rows of a 256-row block) into a private ring of
+//     kBatchSlots stages, and their E8M0 scale rows (4-byte DMA) beside them;
+//   * activations: the chunk's (up to) 64 rows in 4 tiles of 16, tile w requested by wave w
+//     into a slot shared by the workgroup, with their E8M0 scale rows; each wave multiplies
+//     its weight tiles by all four tiles (64 MFMA accumulators);
+//   * one barrier per stage: after it every tile of the stage is in LDS and every wave has
+//     read the previous stage's slots, which the stage kBatchSlots - 1 ahead then refills.
+// No register load is in flight across the loop, so the compiler's wait counting cannot
+// force a drain; the LDS reads are inline asm, ordered by their own lgkmcnt wait. The K
+// rotation and the MFMA sequence of every output are the decode units', so a row's result
+// does not depend on the mode either.
+// ---------------------------------------------------------------------------------------
+
+constexpr int kBatchSlots = 3;
+constexpr int kBatchA = 4 * kTileBytes;      // a wave's four weight tiles of one stage (8 KB)
+constexpr int kBatchAs = 512;                // their scale rows: 64 rows x 8 bytes
+constexpr int kBatchB = 4 * 2 * kTileBytes;  // four 16-row activation tiles x 256 bytes (16 KB)
+constexpr int kBatchBs = 4 * 256;            // their scale rows: 16 rows x 8 bytes in each 256
+constexpr int kBatchRows = 64;               // rows per chunk
+constexpr int kBatchMinRows = 24;            // average rows per expert from which batch mode runs
+
+struct BatchLds {
+  uint8_t a[4][kBatchSlots][kBatchA];
+  uint8_t as[4][kBatchSlots][kBatchAs];
+  uint8_t b[kBatchSlots][kBatchB];
+  uint8_t bs[kBatchSlots][kBatchBs];
+};
+
+// The per-lane addresses of one wave's loads, at stage 0 of the unit's K range.
+struct BatchOps {
+  OperandsMx<4, 1> w;        // weight tiles (a[], lda, spare); sa/b/sb unused
+  const uint8_t* as[2];      // scale DMA j: this lane's dword of tile 2j + lane/32, row (lane/2)%16
+  const uint8_t* b[2];       // activation rows 8i + lane/8 of this wave's tile, at its swizzled chunk
+  const uint8_t* bs;         // this lane's scale dword of tile row (lane/2)%16
+  int bstage;                // activation bytes per stage (256)
+};
+
+// One LDS DMA instruction: SIZE bytes per lane from src into dst + lane * SIZE (cached).
+template <int SIZE>
+__device__ __forceinline__ void lds_dma(const uint8_t* src, uint8_t* dst) {
+  static_assert(SIZE == 4 || SIZE == 16, "dword or dwordx4");
+  if constexpr (SIZE == 16)
+    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                     (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
+  else
+    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                     (__attribute__((address_space(3))) void*)dst, 4, 0, 0);
+}
+
+// The weight half of stage pp (this wave's four tiles and their scale rows: 10 DMA
+// instructions) into weight slot s, and the activation half (this wave's token tile and its
+// scale rows: 5) into activation slot s.
+__device__ __forceinline__ void batch_issue_w(BatchLds& L, const BatchOps& o, const LaneTile& lt, int w, int s, int pp,
+                                              bool live) {
+  issue_a_mx<kNonTemporal>(L.a[w][s], o.w, lt, pp, live);
+#pragma unroll
+  for (int j = 0; j < 2; ++j) lds_dma<4>(o.as[j] + 8 * pp, L.as[w][s] + 256 * j);
+}
+
+__device__ __forceinline__ void batch_issue_x(BatchLds& L, const BatchOps& o, int w, int s, int pp) {
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+      lds_dma<16>(o.b[q] + (size_t)pp * o.bstage + 128 * h, L.b[s] + w * 2 * kTileBytes + h * kTileBytes + q * 1024);
+  lds_dma<4>(o.bs + 8 * pp, L.bs[s] + 256 * w);
+}
+
+// Weights run three stages ahead and activations two, in rings of three slots. Iteration p:
+// wait for stage p; barrier (every wave's activation tile of stage p is in LDS and every
+// wave has read the activation slot of stage p - 1); request activations p + 2 into that
+// slot; read stage p; request weights p + 3 into the weight slot just read; the MFMAs.
+// The loads go out in the order x(p+2), w(p+3), so the ones issued after x(p) are w(p+1),
+// x(p+1), w(p+2): 25 instructions (5 and 15 at p = 0 and 1, after the prologue's
+// w0 w1 w2 x0 x1), and waiting for x(p) also completes w(p), issued before it.
+__device__ __forceinline__ void stream_gemm_mx_batch(BatchLds& L, const BatchOps& o, int nst, int rot,
+                                                     f32x4 (&acc)[4][4],
+                                                     const ReadyWait& ready = ReadyWait{nullptr, 0, nullptr}) {
+  constexpr int S = kBatchSlots;
+  static_assert(S == 3, "three-slot rings: weights three stages ahead, activations two");
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = opaque_lane(), r = lane & 15;
+  auto phys = [nst, rot](int p) {
+    const int q = p + rot;
+    return q >= nst ? q - nst : q;
+  };
+  const LaneTile lt = lane_tile(o.w.lda);
+  const int shift = 8 * (lane >> 4);
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) acc[t][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // Weights (and their scales) first: they do not depend on the readiness wait.
+#pragma unroll
+  for (int i = 0; i < 3; ++i) batch_issue_w(L, o, lt, w, i, phys(min(i, nst - 1)), i < nst);
+  wait_ready(ready);
+#pragma unroll
+  for (int i = 0; i < 2; ++i) batch_issue_x(L, o, w, i, phys(min(i, nst - 1)));
+  const uint32_t a_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)&L.a[w][0][0];
+  const uint32_t as_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)&L.as[w][0][0];
+  const uint32_t b_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)&L.b[0][0];
+  const uint32_t bs_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)&L.bs[0][0];
+  const int rr = r & 7, g = lane >> 4;
+  const uint32_t brow = (uint32_t)((r >> 3) * 1024 + rr * kBlock);
+  const uint32_t c0 = (uint32_t)((g ^ rr) << 4), c1 = (uint32_t)(((g + 4) ^ rr) << 4);
+  for (int p0 = 0; p0 < nst; p0 += S) {
+    static_for<0, S>([&](auto si) {
+      constexpr int s = decltype(si)::value;
+      const int p = p0 + s;
+      if (p >= 2)
+        wait_vmem<25>();
+      else if (p == 1)
+        wait_vmem<15>();
+      else
+        wait_vmem<5>();
+      __builtin_amdgcn_s_barrier();
+      batch_issue_x(L, o, w, (s + 2) % S, phys(min(p + 2, nst - 1)));
+      i32x4 lo[4], hi[4];
+      uint2 saw[4], sbw[4];
+      StageMx<4, 4> st;
+      if (p < nst) {
+        read_slot_mx<4>(lo, hi, a_lds + s * kBatchA + lt.rd0, a_lds + s * kBatchA + lt.rd1);
+        const uint32_t asb = as_lds + s * kBatchAs + 8 * r, bsb = bs_lds + s * kBatchBs + 8 * r;
+        const uint32_t bb = b_lds + s * kBatchB + brow;
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          asm volatile("ds_read_b64 %0, %1" : "=v"(saw[t]) : "v"(asb + (t >> 1) * 256 + (t & 1) * 128) : "memory");
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          asm volatile("ds_read_b64 %0, %1" : "=v"(sbw[c]) : "v"(bsb + 256 * c) : "memory");
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            i32x4 x0, x1;
+            const uint32_t base = bb + c * 2 * kTileBytes + h * kTileBytes;
+            asm volatile("ds_read_b128 %0, %2\n\tds_read_b128 %1, %3"
+                         : "=&v"(x0), "=&v"(x1)
+                         : "v"(base + c0), "v"(base + c1)
+                         : "memory");
+            st.b[c][h] = __builtin_shufflevector(x0, x1, 0, 1, 2, 3, 4, 5, 6, 7);
+          }
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)"
+                     : "+v"(saw[0]), "+v"(saw[1]), "+v"(saw[2]), "+v"(saw[3]), "+v"(sbw[0]), "+v"(sbw[1]),
+                       "+v"(sbw[2]), "+v"(sbw[3]));
+#pragma unroll
+        for (int c = 0; c < 4; ++c) asm volatile("" : "+v"(st.b[c][0]), "+v"(st.b[c][1]));
+      }
+      // The weight slot of stage p is read (its lgkmcnt wait is above): refill it.
+      batch_issue_w(L, o, lt, w, s, phys(min(p + 3, nst - 1)), p + 3 < nst);
+      if (p < nst) mfma_stage_mx(lo, hi, st, saw, sbw, shift, acc);
+    });
+  }
+}
+
+// Batch gate/up unit: 128-channel block jb of gate and up for the chunk's rows (at most 64):
+// wave w holds gate and up channels [32w, 32w + 32), as the decode unit.
+__device__ void gateup_mx_batch(const GateUpMxArgs& a, int e, int jb, const ChunkRows& cr, int rot, BatchLds& L,
+                                uint8_t (*red8)[64]) {
+  const int lane = opaque_lane(), w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int H = a.H, lda = H / 2, sld = H / 32;
+  const size_t gate0 = (size_t)e * 2 * a.I + (size_t)jb * kBlock + 32 * w, up0 = gate0 + a.I;
+  BatchOps o;
+  o.w.lda = lda;
+  o.w.spare = a.spare;
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    o.w.a[r] = a.l1 + (gate0 + 16 * r) * lda;
+    o.w.a[r + 2] = a.l1 + (up0 + 16 * r) * lda;
+  }
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int t = 2 * j + (lane >> 5);
+    const size_t row = (t < 2 ? gate0 + 16 * t : up0 + 16 * (t - 2)) + ((lane >> 1) & 15);
+    o.as[j] = a.l1s + row * sld + 4 * (lane & 1);
+  }
+  const int chunk16 = ((lane & 7) ^ (lane >> 3)) << 4;
+#pragma unroll
+  for (int q = 0; q < 2; ++q)
+    o.b[q] = a.x + (size_t)row_token(cr, min(16 * w + 8 * q + (lane >> 3), cr.n - 1)) * H + chunk16;
+  o.bs = a.xs + (size_t)row_token(cr, min(16 * w + ((lane >> 1) & 15), cr.n - 1)) * sld + 4 * (lane & 1);
+  o.bstage = kMxStageK;
+  f32x4 acc[4][4];
+  stream_gemm_mx_batch(L, o, H / kMxStageK, rot, acc);
+  gateup_mx_epilogue<4>(a, jb, cr, acc, red8);
+}
+
+// Batch down unit: down rows [256 j2, +256) over K part kp for the chunk's rows; wave w
+// holds rows 64w .. 64w+63 of the block.
+__device__ void down_mx_batch(const DownMxArgs& a, int e, int j2, int kp, const ChunkRows& cr, int rot,
+                              const ReadyWait& ready, BatchLds& L) {
+  const int lane = opaque_lane(), w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lr = lane & 15;
+  const int I = a.I, lda = I / 2, sld = I / 32, nstp = I / kMxStageK / a.ks, p0 = kp * nstp;
+  const size_t row0 = (size_t)e * a.H + (size_t)j2 * 256 + 64 * w;
+  BatchOps o;
+  o.w.lda = lda;
+  o.w.spare = a.spare;
+#pragma unroll
+  for (int t = 0; t < 4; ++t) o.w.a[t] = a.l2 + (row0 + 16 * t) * lda + (size_t)p0 * kBlock;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int t = 2 * j + (lane >> 5);
+    o.as[j] = a.l2s + (row0 + 16 * t + ((lane >> 1) & 15)) * sld + 8 * p0 + 4 * (lane & 1);
+  }
+  const int chunk16 = ((lane & 7) ^ (lane >> 3)) << 4;
+#pragma unroll
+  for (int q = 0; q < 2; ++q)
+    o.b[q] = a.hq + (size_t)(cr.row0 + min(16 * w + 8 * q + (lane >> 3), cr.n - 1)) * I + (size_t)p0 * kMxStageK +
+             chunk16;
+  o.bs = a.hs + (size_t)(cr.row0 + min(16 * w + ((lane >> 1) & 15), cr.n - 1)) * a.hs_ld + 8 * p0 + 4 * (lane & 1);
+  o.bstage = kMxStageK;
+  f32x4 acc[4][4];
+  stream_gemm_mx_batch(L, o, nstp, rot, acc, ready);
+  float* pd = a.pd + (size_t)kp * a.T * a.K * a.H;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const int col = 16 * c + lr;
+    if (col < cr.n) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const size_t h0 = (size_t)j2 * 256 + 64 * w + 16 * t + 4 * (lane >> 4);
+        if (a.ks == 1) {
+          const uint32_t lo = f32_to_bf16_bits(acc[t][c][0]) | (f32_to_bf16_bits(acc[t][c][1]) << 16);
+          const uint32_t hi = f32_to_bf16_bits(acc[t][c][2]) | (f32_to_bf16_bits(acc[t][c][3]) << 16);
+          *reinterpret_cast<uint2*>(down_row_mx(a, cr, col) + h0) = make_uint2(lo, hi);
+        } else {
+          *reinterpret_cast<f32x4*>(pd + (size_t)(cr.row0 + col) * a.H + h0) = acc[t][c];
+        }
+      }
+    }
+  }
+}
+
+// The rotation of the decode units of the same block (their paired scale loads keep it
+// even when the stage count is).
+__device__ __forceinline__ int mx_rotation(int key, int nst) {
+  return nst % 2 == 0 ? 2 * (key % (nst / 2)) : key % nst;
 }
 
 struct ExpertMxArgs {
@@ -2281,6 +2541,53 @@ __global__ __launch_bounds__(256, 2) void k_experts_mx(ExpertMxArgs args) {
       if (threadIdx.x == 0) atomicAdd(&a.ready[a.dn_of_gu[c]], 1);
     } else {
       down_mx_work(a.dn, u - total_gu, nwide, a.ready, &meta[kMetaError], ring);
+    }
+    if (threadIdx.x == 0) slot = next;
+    __syncthreads();
+    u = slot;
+  }
+}
+
+
+// The batch-mode expert kernel: the queue, claims and readiness waits of k_experts_mx, one
+// workgroup per CU, with the batch units (chunks of at most 64 rows; down units of 256 rows).
+__global__ __launch_bounds__(256, 1) void k_experts_mx_batch(ExpertMxArgs args) {
+  typedef const __attribute__((address_space(4))) ExpertMxArgs* ArgsPtr;
+  __shared__ uint8_t red8[4][64];
+  __shared__ __attribute__((aligned(16))) BatchLds lds;
+  __shared__ int slot;
+  int* meta = args.gu.meta;
+  const int total_gu = meta[kMetaUnitsGU];
+  const int total = total_gu + meta[kMetaUnitsDN];
+  if (threadIdx.x == 0) slot = atomicAdd(&meta[kMetaQueueGU], 1);
+  __syncthreads();
+  int u = slot, next = 0;
+  while (u < total) {
+    ArgsPtr ap = (ArgsPtr)__builtin_amdgcn_kernarg_segment_ptr();
+    asm volatile("" : "+s"(ap));
+    ExpertMxArgs a;
+    __builtin_memcpy(&a, (const ExpertMxArgs*)ap, sizeof(a));
+    const int nbI = a.gu.I / kBlock, nbH2 = a.dn.H / 256;
+    __syncthreads();
+    if (threadIdx.x == 0) next = atomicAdd(&meta[kMetaQueueGU], 1);
+    if (u < total_gu) {
+      const int c = u / nbI, jb = u % nbI;
+      const int4 ch = a.gu.chunks[c];
+      const ChunkRows cr{ch.z, a.gu.offsets[ch.x] + ch.y, a.gu.perm, a.gu.K};
+      const int nst = a.gu.H / kMxStageK;
+      gateup_mx_batch(a.gu, ch.x, jb, cr, mx_rotation((ch.x + a.gu.ebase) * nbI + jb, nst), lds, red8);
+      publish_fence();
+      __syncthreads();
+      if (threadIdx.x == 0) atomicAdd(&a.ready[a.dn_of_gu[c]], 1);
+    } else {
+      const int v = u - total_gu, ks = a.dn.ks;
+      const int c = v / (nbH2 * ks), rem = v % (nbH2 * ks), j2 = rem / ks, kp = rem % ks;
+      const int4 ch = a.dn.chunks[c];
+      const ChunkRows cr{ch.z, a.dn.offsets[ch.x] + ch.y, a.dn.perm, a.dn.K};
+      const ReadyWait ready{&a.ready[c], nbI, &meta[kMetaError]};
+      const int nstp = a.dn.I / kMxStageK / ks;
+      down_mx_batch(a.dn, ch.x, j2, kp, cr, mx_rotation(((ch.x + a.dn.ebase) * nbH2 + j2) * ks + kp, nstp), ready,
+                    lds);
     }
     if (threadIdx.x == 0) slot = next;
     __syncthreads();
@@ -2385,6 +2692,7 @@ struct DeviceInfo {
   int cus = 0;
   int experts_per_cu = 0;     // resident k_experts workgroups per CU
   int experts_mx_per_cu = 0;  // resident k_experts_mx workgroups per CU
+  int batch_mx_per_cu = 0;    // resident k_experts_mx_batch workgroups per CU
 };
 
 int device_info(DeviceInfo* out) {
@@ -2400,6 +2708,9 @@ int device_info(DeviceInfo* out) {
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_experts_mx, 256, 0) != hipSuccess)
       return MEGAMOE_ERR_HIP;
     di.experts_mx_per_cu = per_cu > 0 ? per_cu : 1;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_experts_mx_batch, 256, 0) != hipSuccess)
+      return MEGAMOE_ERR_HIP;
+    di.batch_mx_per_cu = per_cu > 0 ? per_cu : 1;
     di.cus = cus > 0 ? cus : 1;
   }
   *out = di;
@@ -2630,7 +2941,7 @@ LayoutMx make_layout_mx(const megamoe_desc& d) {
     at += align_up(bytes > 0 ? bytes : 1);
     return o;
   };
-  const size_t chunks = max_chunks(d, 0, kChunkRowsMx);
+  const size_t chunks = max_chunks(d, 0, kBatchRows < kChunkRowsMx ? kBatchRows : kChunkRowsMx);
   L.counts = take(E * sizeof(int));
   L.offsets = take((E + 1) * sizeof(int));
   L.meta = take(kMetaInts * sizeof(int));
@@ -2678,9 +2989,12 @@ int forward_mx_impl(const megamoe_desc* desc, float limit, const megamoe_mx_tens
   PermuteOut po{(int*)(ws + L.counts), (int*)(ws + L.offsets), (int*)(ws + L.meta), (int*)(ws + L.perm),
                 (int*)(ws + L.inv),    (int4*)(ws + L.gu),     (int4*)(ws + L.dn),  (int*)(ws + L.dn_of_gu),
                 (int*)(ws + L.ready)};
+  // Batch mode (k_experts_mx_batch) when the rows per expert average kBatchMinRows or more:
+  // chunks of up to 64 rows, down units of 256 rows, no wide units.
+  const bool batch = (int64_t)T * K >= (int64_t)kBatchMinRows * E;
   const size_t lds = ((size_t)E * (1 + (T + 31) / 32) + 32) * 4;
-  hipLaunchKernelGGL(k_permute, dim3(1), dim3(1024), lds, st, t->topk_idx, base, T, K, E, 0, nbI, nbH, L.ks,
-                     kChunkRowsMx, 1, po);
+  hipLaunchKernelGGL(k_permute, dim3(1), dim3(1024), lds, st, t->topk_idx, base, T, K, E, 0, nbI,
+                     batch ? nbH / 2 : nbH, L.ks, batch ? kBatchRows : kChunkRowsMx, batch ? 0 : 1, po);
   MEGAMOE_LAUNCH_CHECK();
   if (mark(1) != hipSuccess) return MEGAMOE_ERR_HIP;
 
@@ -2705,11 +3019,19 @@ int forward_mx_impl(const megamoe_desc* desc, float limit, const megamoe_mx_tens
   da.ebase = (int)base;
   ea.dn_of_gu = po.dn_of_gu;
   ea.ready = po.ready;
-  const size_t chunks = max_chunks(d, 0, kChunkRowsMx);
-  const size_t units_max = chunks * 4 * (size_t)nbI + chunks * 2 * (size_t)nbH * L.ks;
-  const size_t resident = (size_t)di.cus * di.experts_mx_per_cu;
-  hipLaunchKernelGGL(k_experts_mx, dim3((unsigned)(units_max < resident ? units_max : resident)), dim3(256), 0, st,
-                     ea);
+  if (batch) {
+    const size_t chunks = max_chunks(d, 0, kBatchRows);
+    const size_t units_max = chunks * (size_t)nbI + chunks * (size_t)(nbH / 2) * L.ks;
+    const size_t resident = (size_t)di.cus * di.batch_mx_per_cu;
+    hipLaunchKernelGGL(k_experts_mx_batch, dim3((unsigned)(units_max < resident ? units_max : resident)), dim3(256),
+                       0, st, ea);
+  } else {
+    const size_t chunks = max_chunks(d, 0, kChunkRowsMx);
+    const size_t units_max = chunks * 4 * (size_t)nbI + chunks * 2 * (size_t)nbH * L.ks;
+    const size_t resident = (size_t)di.cus * di.experts_mx_per_cu;
+    hipLaunchKernelGGL(k_experts_mx, dim3((unsigned)(units_max < resident ? units_max : resident)), dim3(256), 0,
+                       st, ea);
+  }
   MEGAMOE_LAUNCH_CHECK();
   if (mark(2) != hipSuccess) return MEGAMOE_ERR_HIP;
 
