@@ -76,6 +76,12 @@ def kernel_bytes(case, hit: int) -> dict:
     return {"gate_up": gu, "down": dn}
 
 
+def mx_kernel(rows: int, experts: int) -> str:
+    """The MXFP4 expert kernel the library runs: batch mode from 24 rows per expert on
+    average (kBatchMinRows in the library), the decode kernel below."""
+    return "k_experts_mx_batch" if rows >= 24 * experts else "k_experts_mx"
+
+
 def measured_traffic(case) -> float | None:
     """HBM bytes per k_experts launch from profiles/k_experts_<case>_counters.md: the line
     ``traffic_bytes_per_launch: <number>`` (FETCH_SIZE + WRITE_SIZE, calibrated on a copy)."""
@@ -224,7 +230,8 @@ def bench_case(case, steps: int, warmup: int, want_cpu: bool, cpu_budget: float)
         "roofline": {"bound": "hbm", "achieved": ex_bytes / (ex_ms * 1e-3) / 1e9, "peak": PEAK_HBM / 1e9,
                      "unit": "GB/s", "frac": ex_bytes / (ex_ms * 1e-3) / PEAK_HBM,
                      "traffic": measured_traffic(case),
-                     "kernel": "k_experts_mx" if case.format == "mxfp4" else "k_experts",
+                     "kernel": (mx_kernel(case.tokens * case.topk, case.experts) if case.format == "mxfp4"
+                                else "k_experts"),
                      "kernel_us": ex_ms * 1e3, "bytes_per_launch": ex_bytes},
         "dtype": ("e2m1xe4m3->fp32 (E8M0 scales per 32; bf16 out)" if case.format == "mxfp4"
                   else "e4m3xe4m3->fp32 (bf16 in/out)"),
@@ -365,7 +372,7 @@ def bench_ep_share(case, steps: int, warmup: int, want_cpu: bool, cpu_budget: fl
         "rotation_sets": 1, "received_rows": R, "sent_rows": T * K,
         "roofline": {"bound": "hbm", "achieved": ex_bytes / (ex_ms * 1e-3) / 1e9, "peak": PEAK_HBM / 1e9,
                      "unit": "GB/s", "frac": ex_bytes / (ex_ms * 1e-3) / PEAK_HBM, "traffic": None,
-                     "kernel": "k_experts_mx", "kernel_us": ex_ms * 1e3, "bytes_per_launch": ex_bytes},
+                     "kernel": mx_kernel(R, local), "kernel_us": ex_ms * 1e3, "bytes_per_launch": ex_bytes},
         "dtype": "e2m1xe4m3->fp32 (E8M0 scales per 32; bf16 out)",
     }
     if want_cpu:
