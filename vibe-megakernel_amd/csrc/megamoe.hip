@@ -2280,9 +2280,9 @@ __device__ void down_mx_work(const DownMxArgs& a, int v, int nwide, int* ready_c
 
 constexpr int kBatchSlots = 3;
 constexpr int kBatchA = 4 * kTileBytes;      // a wave's four weight tiles of one stage (8 KB)
-constexpr int kBatchAs = 512;                // their scale rows: 64 rows x 8 bytes
+constexpr int kBatchAs = 1024;               // their scale rows for a stage pair: 64 rows x 16 bytes
 constexpr int kBatchB = 4 * 2 * kTileBytes;  // four 16-row activation tiles x 256 bytes (16 KB)
-constexpr int kBatchBs = 4 * 256;            // their scale rows: 16 rows x 8 bytes in each 256
+constexpr int kBatchBs = 1024;               // their scale rows for a stage pair: 64 rows x 16 bytes
 constexpr int kBatchRows = 64;               // rows per chunk
 constexpr int kBatchMinRows = 24;            // average rows per expert from which batch mode runs
 
@@ -2296,9 +2296,9 @@ struct BatchLds {
 // The per-lane addresses of one wave's loads, at stage 0 of the unit's K range.
 struct BatchOps {
   OperandsMx<4, 1> w;        // weight tiles (a[], lda, spare); sa/b/sb unused
-  const uint8_t* as[2];      // scale DMA j: this lane's dword of tile 2j + lane/32, row (lane/2)%16
+  const uint8_t* as;         // scale row of tile lane/16, row lane%16 (16 bytes: a stage pair)
   const uint8_t* b[2];       // activation rows 8i + lane/8 of this wave's tile, at its swizzled chunk
-  const uint8_t* bs;         // this lane's scale dword of tile row (lane/2)%16
+  const uint8_t* bs;         // lanes 0-15: scale row of this wave's tile row lane (a stage pair)
   int bstage;                // activation bytes per stage (256)
 };
 
@@ -2314,36 +2314,44 @@ __device__ __forceinline__ void lds_dma(const uint8_t* src, uint8_t* dst) {
                                      (__attribute__((address_space(3))) void*)dst, 4, 0, 0);
 }
 
-// The weight half of stage pp (this wave's four tiles and their scale rows: 10 DMA
-// instructions) into weight slot s, and the activation half (this wave's token tile and its
-// scale rows: 5) into activation slot s.
+// The weight tiles of stage pp (8 DMA instructions) into weight slot s; with `scales`, also
+// the E8M0 rows of the stage pair starting at the even stage pq (one 16-byte DMA: lane l
+// fetches row l % 16 of tile l / 16) into scale slot ss.
 __device__ __forceinline__ void batch_issue_w(BatchLds& L, const BatchOps& o, const LaneTile& lt, int w, int s, int pp,
-                                              bool live) {
+                                              bool live, bool scales, int ss, int pq) {
   issue_a_mx<kNonTemporal>(L.a[w][s], o.w, lt, pp, live);
-#pragma unroll
-  for (int j = 0; j < 2; ++j) lds_dma<4>(o.as[j] + 8 * pp, L.as[w][s] + 256 * j);
+  if (scales) lds_dma<16>(o.as + 8 * pq, L.as[w][ss]);
 }
 
-__device__ __forceinline__ void batch_issue_x(BatchLds& L, const BatchOps& o, int w, int s, int pp) {
+// This wave's activation tile of stage pp (4 DMA instructions) into activation slot s;
+// with `scales`, also its tile's E8M0 rows for the stage pair at pq (lanes 0-15 only, each
+// 16 bytes) into scale slot ss.
+__device__ __forceinline__ void batch_issue_x(BatchLds& L, const BatchOps& o, int w, int s, int pp, bool scales, int ss,
+                                              int pq) {
 #pragma unroll
   for (int h = 0; h < 2; ++h)
 #pragma unroll
     for (int q = 0; q < 2; ++q)
       lds_dma<16>(o.b[q] + (size_t)pp * o.bstage + 128 * h, L.b[s] + w * 2 * kTileBytes + h * kTileBytes + q * 1024);
-  lds_dma<4>(o.bs + 8 * pp, L.bs[s] + 256 * w);
+  if (scales && opaque_lane() < 16) lds_dma<16>(o.bs + 8 * pq, L.bs[ss] + 256 * w);
 }
 
-// Weights run three stages ahead and activations two, in rings of three slots. Iteration p:
-// wait for stage p; barrier (every wave's activation tile of stage p is in LDS and every
-// wave has read the activation slot of stage p - 1); request activations p + 2 into that
-// slot; read stage p; request weights p + 3 into the weight slot just read; the MFMAs.
-// The loads go out in the order x(p+2), w(p+3), so the ones issued after x(p) are w(p+1),
-// x(p+1), w(p+2): 25 instructions (5 and 15 at p = 0 and 1, after the prologue's
-// w0 w1 w2 x0 x1), and waiting for x(p) also completes w(p), issued before it.
+// Weights run three stages ahead and activations two, in rings of three slots; the E8M0
+// rows of both come per stage pair (one 16-byte DMA per row and pair, halving the
+// scattered scale requests), in rings of three pairs, issued with the pair's even stage.
+// Iteration p: wait for stage p; barrier (every wave's activation tile of stage p is in LDS
+// and every wave has read the activation slot of stage p - 1); request activations p + 2
+// into that slot; read stage p; request weights p + 3 into the weight slot just read; the
+// MFMAs. The loads go out in the order x(p+2), w(p+3) and those issued after x(p) are w(p+1),
+// x(p+1), w(p+2): 21 instructions for even p and 22 for odd p (a pair's scales ride with its
+// even stage), 4 and 13 at p = 0 and 1 after the prologue's w0 w1 w2 x0 x1. Waiting for x(p)
+// also completes w(p) and both scale pairs of stage p, issued before it. The unroll of six
+// keeps every slot index a compile-time constant. The stage count and the rotation are even
+// (the host runs batch mode only then), so a pair never wraps.
 __device__ __forceinline__ void stream_gemm_mx_batch(BatchLds& L, const BatchOps& o, int nst, int rot,
                                                      f32x4 (&acc)[4][4],
                                                      const ReadyWait& ready = ReadyWait{nullptr, 0, nullptr}) {
-  constexpr int S = kBatchSlots;
+  constexpr int S = kBatchSlots, U = 6;
   static_assert(S == 3, "three-slot rings: weights three stages ahead, activations two");
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = opaque_lane(), r = lane & 15;
@@ -2351,6 +2359,9 @@ __device__ __forceinline__ void stream_gemm_mx_batch(BatchLds& L, const BatchOps
     const int q = p + rot;
     return q >= nst ? q - nst : q;
   };
+  // First stage of the pair holding stage q, clamped into the range (loads past the end
+  // re-read the last pair).
+  auto pair_of = [&](int q) { return phys(2 * min(q / 2, nst / 2 - 1)); };
   const LaneTile lt = lane_tile(o.w.lda);
   const int shift = 8 * (lane >> 4);
 #pragma unroll
@@ -2359,10 +2370,11 @@ __device__ __forceinline__ void stream_gemm_mx_batch(BatchLds& L, const BatchOps
     for (int c = 0; c < 4; ++c) acc[t][c] = f32x4{0.f, 0.f, 0.f, 0.f};
   // Weights (and their scales) first: they do not depend on the readiness wait.
 #pragma unroll
-  for (int i = 0; i < 3; ++i) batch_issue_w(L, o, lt, w, i, phys(min(i, nst - 1)), i < nst);
+  for (int i = 0; i < 3; ++i)
+    batch_issue_w(L, o, lt, w, i, phys(min(i, nst - 1)), i < nst, i % 2 == 0, (i / 2) % S, pair_of(i));
   wait_ready(ready);
 #pragma unroll
-  for (int i = 0; i < 2; ++i) batch_issue_x(L, o, w, i, phys(min(i, nst - 1)));
+  for (int i = 0; i < 2; ++i) batch_issue_x(L, o, w, i, phys(min(i, nst - 1)), i % 2 == 0, (i / 2) % S, pair_of(i));
   const uint32_t a_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)&L.a[w][0][0];
   const uint32_t as_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)&L.as[w][0][0];
   const uint32_t b_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)&L.b[0][0];
@@ -2370,28 +2382,34 @@ __device__ __forceinline__ void stream_gemm_mx_batch(BatchLds& L, const BatchOps
   const int rr = r & 7, g = lane >> 4;
   const uint32_t brow = (uint32_t)((r >> 3) * 1024 + rr * kBlock);
   const uint32_t c0 = (uint32_t)((g ^ rr) << 4), c1 = (uint32_t)(((g + 4) ^ rr) << 4);
-  for (int p0 = 0; p0 < nst; p0 += S) {
-    static_for<0, S>([&](auto si) {
+  for (int p0 = 0; p0 < nst; p0 += U) {
+    static_for<0, U>([&](auto si) {
       constexpr int s = decltype(si)::value;
       const int p = p0 + s;
-      if (p >= 2)
-        wait_vmem<25>();
-      else if (p == 1)
-        wait_vmem<15>();
-      else
-        wait_vmem<5>();
+      if (p >= 2) {
+        if constexpr (s % 2 == 0)
+          wait_vmem<21>();
+        else
+          wait_vmem<22>();
+      } else if (p == 1) {
+        wait_vmem<13>();
+      } else {
+        wait_vmem<4>();
+      }
       __builtin_amdgcn_s_barrier();
-      batch_issue_x(L, o, w, (s + 2) % S, phys(min(p + 2, nst - 1)));
+      batch_issue_x(L, o, w, (s + 2) % S, phys(min(p + 2, nst - 1)), s % 2 == 0, ((s + 2) / 2) % S, pair_of(p + 2));
       i32x4 lo[4], hi[4];
       uint2 saw[4], sbw[4];
       StageMx<4, 4> st;
       if (p < nst) {
-        read_slot_mx<4>(lo, hi, a_lds + s * kBatchA + lt.rd0, a_lds + s * kBatchA + lt.rd1);
-        const uint32_t asb = as_lds + s * kBatchAs + 8 * r, bsb = bs_lds + s * kBatchBs + 8 * r;
-        const uint32_t bb = b_lds + s * kBatchB + brow;
+        read_slot_mx<4>(lo, hi, a_lds + (s % S) * kBatchA + lt.rd0, a_lds + (s % S) * kBatchA + lt.rd1);
+        const uint32_t half = 8 * (s % 2);
+        const uint32_t asb = as_lds + ((s / 2) % S) * kBatchAs + 16 * r + half;
+        const uint32_t bsb = bs_lds + ((s / 2) % S) * kBatchBs + 16 * r + half;
+        const uint32_t bb = b_lds + (s % S) * kBatchB + brow;
 #pragma unroll
         for (int t = 0; t < 4; ++t)
-          asm volatile("ds_read_b64 %0, %1" : "=v"(saw[t]) : "v"(asb + (t >> 1) * 256 + (t & 1) * 128) : "memory");
+          asm volatile("ds_read_b64 %0, %1" : "=v"(saw[t]) : "v"(asb + 256 * t) : "memory");
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
           asm volatile("ds_read_b64 %0, %1" : "=v"(sbw[c]) : "v"(bsb + 256 * c) : "memory");
@@ -2413,7 +2431,8 @@ __device__ __forceinline__ void stream_gemm_mx_batch(BatchLds& L, const BatchOps
         for (int c = 0; c < 4; ++c) asm volatile("" : "+v"(st.b[c][0]), "+v"(st.b[c][1]));
       }
       // The weight slot of stage p is read (its lgkmcnt wait is above): refill it.
-      batch_issue_w(L, o, lt, w, s, phys(min(p + 3, nst - 1)), p + 3 < nst);
+      batch_issue_w(L, o, lt, w, s % S, phys(min(p + 3, nst - 1)), p + 3 < nst, (s + 3) % 2 == 0, ((s + 3) / 2) % S,
+                    pair_of(p + 3));
       if (p < nst) mfma_stage_mx(lo, hi, st, saw, sbw, shift, acc);
     });
   }
@@ -2434,17 +2453,16 @@ __device__ void gateup_mx_batch(const GateUpMxArgs& a, int e, int jb, const Chun
     o.w.a[r] = a.l1 + (gate0 + 16 * r) * lda;
     o.w.a[r + 2] = a.l1 + (up0 + 16 * r) * lda;
   }
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int t = 2 * j + (lane >> 5);
-    const size_t row = (t < 2 ? gate0 + 16 * t : up0 + 16 * (t - 2)) + ((lane >> 1) & 15);
-    o.as[j] = a.l1s + row * sld + 4 * (lane & 1);
+  {
+    const int t = lane >> 4;
+    const size_t row = (t < 2 ? gate0 + 16 * t : up0 + 16 * (t - 2)) + (lane & 15);
+    o.as = a.l1s + row * sld;
   }
   const int chunk16 = ((lane & 7) ^ (lane >> 3)) << 4;
 #pragma unroll
   for (int q = 0; q < 2; ++q)
     o.b[q] = a.x + (size_t)row_token(cr, min(16 * w + 8 * q + (lane >> 3), cr.n - 1)) * H + chunk16;
-  o.bs = a.xs + (size_t)row_token(cr, min(16 * w + ((lane >> 1) & 15), cr.n - 1)) * sld + 4 * (lane & 1);
+  o.bs = a.xs + (size_t)row_token(cr, min(16 * w + (lane & 15), cr.n - 1)) * sld;
   o.bstage = kMxStageK;
   f32x4 acc[4][4];
   stream_gemm_mx_batch(L, o, H / kMxStageK, rot, acc);
@@ -2464,17 +2482,13 @@ __device__ void down_mx_batch(const DownMxArgs& a, int e, int j2, int kp, const 
   o.w.spare = a.spare;
 #pragma unroll
   for (int t = 0; t < 4; ++t) o.w.a[t] = a.l2 + (row0 + 16 * t) * lda + (size_t)p0 * kBlock;
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int t = 2 * j + (lane >> 5);
-    o.as[j] = a.l2s + (row0 + 16 * t + ((lane >> 1) & 15)) * sld + 8 * p0 + 4 * (lane & 1);
-  }
+  o.as = a.l2s + (row0 + 16 * (lane >> 4) + (lane & 15)) * sld + 8 * p0;
   const int chunk16 = ((lane & 7) ^ (lane >> 3)) << 4;
 #pragma unroll
   for (int q = 0; q < 2; ++q)
     o.b[q] = a.hq + (size_t)(cr.row0 + min(16 * w + 8 * q + (lane >> 3), cr.n - 1)) * I + (size_t)p0 * kMxStageK +
              chunk16;
-  o.bs = a.hs + (size_t)(cr.row0 + min(16 * w + ((lane >> 1) & 15), cr.n - 1)) * a.hs_ld + 8 * p0 + 4 * (lane & 1);
+  o.bs = a.hs + (size_t)(cr.row0 + min(16 * w + (lane & 15), cr.n - 1)) * a.hs_ld + 8 * p0;
   o.bstage = kMxStageK;
   f32x4 acc[4][4];
   stream_gemm_mx_batch(L, o, nstp, rot, acc, ready);
@@ -2991,7 +3005,8 @@ int forward_mx_impl(const megamoe_desc* desc, float limit, const megamoe_mx_tens
                 (int*)(ws + L.ready)};
   // Batch mode (k_experts_mx_batch) when the rows per expert average kBatchMinRows or more:
   // chunks of up to 64 rows, down units of 256 rows, no wide units.
-  const bool batch = (int64_t)T * K >= (int64_t)kBatchMinRows * E;
+  const bool batch = (int64_t)T * K >= (int64_t)kBatchMinRows * E && (H / kMxStageK) % 2 == 0 &&
+                     (I / kMxStageK / L.ks) % 2 == 0;
   const size_t lds = ((size_t)E * (1 + (T + 31) / 32) + 32) * 4;
   hipLaunchKernelGGL(k_permute, dim3(1), dim3(1024), lds, st, t->topk_idx, base, T, K, E, 0, nbI,
                      batch ? nbH / 2 : nbH, L.ks, batch ? kBatchRows : kChunkRowsMx, batch ? 0 : 1, po);
