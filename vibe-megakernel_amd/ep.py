@@ -53,8 +53,9 @@ class Send:
 
 
 def dispatch(x: torch.Tensor, x_scales: torch.Tensor, topk_idx: torch.Tensor, topk_weights: torch.Tensor,
-             experts: int, ep: int) -> Send:
-    """megamoe.py:160-168 and parallel.py:59-68 (the send half) for this rank's tokens."""
+             experts: int, ep: int, send: Send | None = None) -> Send:
+    """megamoe.py:160-168 and parallel.py:59-68 (the send half) for this rank's tokens.
+    ``send`` (from an earlier call of the same shape) is reused instead of allocating."""
     T, H = x.shape
     K = topk_idx.shape[1] if topk_idx.dim() == 2 else 0
     device = x.device
@@ -67,12 +68,20 @@ def dispatch(x: torch.Tensor, x_scales: torch.Tensor, topk_idx: torch.Tensor, to
     _check(topk_idx, "topk_idx", torch.int64, (T, K), device)
     _check(topk_weights, "topk_weights", torch.float32, (T, K), device)
     n = T * K
-    send = Send(rows=torch.empty((n, H), dtype=torch.float8_e4m3fn, device=device),
-                row_scales=torch.empty((n, H // 32), dtype=torch.uint8, device=device),
-                ids=torch.empty(n, dtype=torch.int64, device=device),
-                weights=torch.empty(n, dtype=torch.float32, device=device),
-                counts=torch.empty(ep, dtype=torch.int64, device=device),
-                slot_rows=torch.empty((T, K), dtype=torch.int32, device=device))
+    if send is None:
+        send = Send(rows=torch.empty((n, H), dtype=torch.float8_e4m3fn, device=device),
+                    row_scales=torch.empty((n, H // 32), dtype=torch.uint8, device=device),
+                    ids=torch.empty(n, dtype=torch.int64, device=device),
+                    weights=torch.empty(n, dtype=torch.float32, device=device),
+                    counts=torch.empty(ep, dtype=torch.int64, device=device),
+                    slot_rows=torch.empty((T, K), dtype=torch.int32, device=device))
+    else:
+        _check(send.rows, "send.rows", torch.float8_e4m3fn, (n, H), device)
+        _check(send.row_scales, "send.row_scales", torch.uint8, (n, H // 32), device)
+        _check(send.ids, "send.ids", torch.int64, (n,), device)
+        _check(send.weights, "send.weights", torch.float32, (n,), device)
+        _check(send.counts, "send.counts", torch.int64, (ep,), device)
+        _check(send.slot_rows, "send.slot_rows", torch.int32, (T, K), device)
     lib = _lib.load()
     desc = _lib.Desc(tokens=T, hidden=H, experts=experts, topk=K)
     src = _lib.MxTensors(x=x.data_ptr(), x_scales=x_scales.data_ptr(), topk_idx=topk_idx.data_ptr(),
@@ -109,19 +118,24 @@ class Experts:
         self.weights = (l1_blocks, l1_scales, l2_blocks, l2_scales)
         self.expert_base, self.limit = int(expert_base), float(swiglu_limit)
         self.lib = _lib.load()
+        self._ws_bytes: dict[int, int] = {}
 
     def desc(self, rows: int) -> _lib.Desc:
         return _lib.Desc(tokens=rows, hidden=self.hidden, experts=self.local, topk=1, intermediate=self.inter)
 
     def workspace_bytes(self, rows: int) -> int:
-        size = ctypes.c_size_t(0)
-        _lib.check(self.lib.megamoe_mx_workspace_bytes(ctypes.byref(self.desc(rows)), ctypes.byref(size)),
-                   "ep experts: workspace size")
-        return int(size.value)
+        if rows not in self._ws_bytes:
+            size = ctypes.c_size_t(0)
+            _lib.check(self.lib.megamoe_mx_workspace_bytes(ctypes.byref(self.desc(rows)), ctypes.byref(size)),
+                       "ep experts: workspace size")
+            self._ws_bytes[rows] = int(size.value)
+        return self._ws_bytes[rows]
 
     def __call__(self, rows: torch.Tensor, row_scales: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor,
-                 *, workspace: torch.Tensor | None = None, events=None) -> torch.Tensor:
-        """bf16 [R, H]: each received row's weighted expert output (the returned payload)."""
+                 *, workspace: torch.Tensor | None = None, out: torch.Tensor | None = None,
+                 events=None) -> torch.Tensor:
+        """bf16 [R, H]: each received row's weighted expert output (the returned payload),
+        into ``out`` when given."""
         R, H = rows.shape[0], self.hidden
         device = rows.device
         _check(rows, "rows", torch.float8_e4m3fn, (R, H), device)
@@ -134,7 +148,10 @@ class Experts:
             workspace = torch.empty(need, dtype=torch.uint8, device=device)
         elif workspace.numel() < need:
             raise ValueError(f"ep experts: workspace of {workspace.numel()} bytes, {need} needed")
-        out = torch.empty((R, H), dtype=torch.bfloat16, device=device)
+        if out is None:
+            out = torch.empty((R, H), dtype=torch.bfloat16, device=device)
+        else:
+            _check(out, "out", torch.bfloat16, (R, H), device)
         l1, l1s, l2, l2s = self.weights
         t = _lib.MxTensors(x=rows.data_ptr(), x_scales=row_scales.data_ptr(), topk_idx=ids.data_ptr(),
                            topk_weights=weights.data_ptr(), l1_blocks=l1.data_ptr(), l1_scales=l1s.data_ptr(),
@@ -147,14 +164,18 @@ class Experts:
         return out
 
 
-def combine(returned: torch.Tensor, slot_rows: torch.Tensor) -> torch.Tensor:
-    """megamoe.py:176-182: y[t] = bf16(sum over slots in order of fp32(returned[slot_rows[t, k]]))."""
+def combine(returned: torch.Tensor, slot_rows: torch.Tensor, y: torch.Tensor | None = None) -> torch.Tensor:
+    """megamoe.py:176-182: y[t] = bf16(sum over slots in order of fp32(returned[slot_rows[t, k]])),
+    into ``y`` when given."""
     T, K = slot_rows.shape
     H = returned.shape[1]
     device = returned.device
     _check(returned, "returned", torch.bfloat16, (T * K, H), device)
     _check(slot_rows, "slot_rows", torch.int32, (T, K), device)
-    y = torch.empty((T, H), dtype=torch.bfloat16, device=device)
+    if y is None:
+        y = torch.empty((T, H), dtype=torch.bfloat16, device=device)
+    else:
+        _check(y, "y", torch.bfloat16, (T, H), device)
     with torch.cuda.device(device):
         _lib.check(_lib.load().megamoe_ep_combine(T, H, K, returned.data_ptr(), slot_rows.data_ptr(), y.data_ptr(),
                                                   _stream(device)), "ep combine")
