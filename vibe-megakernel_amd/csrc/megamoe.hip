@@ -3076,66 +3076,82 @@ int forward_mx_impl(const megamoe_desc* desc, float limit, const megamoe_mx_tens
 
 constexpr int kMaxRanks = 256;              // owner ranks are held as bytes
 constexpr int kMaxDispatch = 48 * 1024;     // (token, slot) entries of one dispatch (LDS bytes)
+constexpr int kDispatchList = 1024;         // entries one workgroup packs at most
 
-// Send row of every (token, slot): a stable counting sort by owner rank, one workgroup. The
-// owners are read once (coalesced) into LDS; each thread then owns a contiguous run of
-// entries, and per owner an exclusive scan of the runs' counts places each run after the
-// earlier ones. An id outside [0, E) makes every count -1 and every send row -1 (nothing is
-// packed).
-__global__ __launch_bounds__(1024) void k_ep_order(const int64_t* __restrict__ ids, int n, int E, int local, int ep,
-                                                   int64_t* __restrict__ counts, int32_t* __restrict__ slot_rows) {
+// The dispatch in one kernel: a stable counting sort by owner rank and the payload gather.
+// Workgroup (o, j) of ep x m: every workgroup reads all owners into LDS (coalesced; an id
+// outside [0, E) makes every count and send row -1); each thread owns a contiguous run of
+// entries; a reduction of the runs' counts below o and a scan of their counts of o give the
+// send row of every entry of owner o (owner o's rows start after all rows of lower owners and
+// keep (token, slot) order). Workgroup j packs the entries of owner o whose rank falls in
+// its j-th share, the whole workgroup copying one row (E4M3 bytes and E8M0 scales) at a
+// time; workgroup (o, 0) writes owner o's count.
+__global__ __launch_bounds__(256) void k_ep_dispatch(const int64_t* __restrict__ ids, const uint8_t* __restrict__ x,
+                                                     const uint8_t* __restrict__ xs, const float* __restrict__ wts,
+                                                     int n, int K, int H, int E, int local, int m,
+                                                     int64_t* __restrict__ counts, int32_t* __restrict__ slot_rows,
+                                                     uint8_t* __restrict__ rows, uint8_t* __restrict__ row_scales,
+                                                     int64_t* __restrict__ out_ids, float* __restrict__ out_wts) {
   extern __shared__ uint8_t owner[];  // n bytes
-  __shared__ unsigned long long tmp[16];
-  __shared__ int bad;
-  const int tid = threadIdx.x, per = (n + 1023) / 1024;
-  const int lo = min(n, tid * per), hi = min(n, lo + per);
-  if (tid == 0) bad = 0;
+  __shared__ unsigned long long tmp[4];
+  __shared__ int2 list[kDispatchList];
+  __shared__ int bad, nlist, below;
+  const int o = blockIdx.x / m, j = blockIdx.x % m, tid = threadIdx.x;
+  if (tid == 0) {
+    bad = 0;
+    nlist = 0;
+    below = 0;
+  }
   __syncthreads();
-  for (int i = tid; i < n; i += 1024) {
+  for (int i = tid; i < n; i += 256) {
     const int64_t e = ids[i];
     if (e < 0 || e >= E)
       bad = 1;
     else
-      owner[i] = (uint8_t)(e / local);
+      owner[i] = (uint8_t)((int)e / local);
   }
   __syncthreads();
   if (bad) {
-    for (int i = tid; i < n; i += 1024) slot_rows[i] = -1;
-    for (int o = tid; o < ep; o += 1024) counts[o] = -1;
+    for (int i = blockIdx.x * 256 + tid; i < n; i += gridDim.x * 256) slot_rows[i] = -1;
+    if (j == 0 && tid == 0) counts[o] = -1;
     return;
   }
-  int base = 0;
-  for (int o = 0; o < ep; ++o) {
-    int c = 0;
-    for (int i = lo; i < hi; ++i) c += owner[i] == o;
-    unsigned long long total;
-    int pos = base + (int)block_exclusive_scan((unsigned long long)c, tmp, &total);
-    for (int i = lo; i < hi; ++i)
-      if (owner[i] == o) slot_rows[i] = pos++;
-    if (tid == 0) counts[o] = (int64_t)total;
-    base += (int)total;
-    __syncthreads();  // tmp is rewritten by the next owner's scan
+  const int per = (n + 255) / 256, lo = min(n, tid * per), hi = min(n, lo + per);
+  int c_lt = 0, c_eq = 0;
+  for (int i = lo; i < hi; ++i) {
+    c_lt += owner[i] < o;
+    c_eq += owner[i] == o;
   }
-}
-
-// The send payload: row slot_rows[i] of each buffer gets (token i / K)'s E4M3 row and E8M0
-// scales and slot i's expert id and weight. One workgroup per (token, slot).
-__global__ __launch_bounds__(256) void k_ep_pack(const uint8_t* __restrict__ x, const uint8_t* __restrict__ xs,
-                                                 const int64_t* __restrict__ ids, const float* __restrict__ wts,
-                                                 const int32_t* __restrict__ slot_rows, int K, int H,
-                                                 uint8_t* __restrict__ rows, uint8_t* __restrict__ row_scales,
-                                                 int64_t* __restrict__ out_ids, float* __restrict__ out_wts) {
-  const int i = blockIdx.x, t = i / K, p = slot_rows[i];
-  if (p < 0) return;
-  const uint4* src = reinterpret_cast<const uint4*>(x + (size_t)t * H);
-  uint4* dst = reinterpret_cast<uint4*>(rows + (size_t)p * H);
-  for (int c = threadIdx.x; c < H / 16; c += 256) dst[c] = src[c];
-  const uint2* ssrc = reinterpret_cast<const uint2*>(xs + (size_t)t * (H / 32));
-  uint2* sdst = reinterpret_cast<uint2*>(row_scales + (size_t)p * (H / 32));
-  for (int c = threadIdx.x; c < H / 256; c += 256) sdst[c] = ssrc[c];
-  if (threadIdx.x == 0) {
-    out_ids[p] = ids[i];
-    out_wts[p] = wts[i];
+  if (c_lt) atomicAdd(&below, c_lt);
+  unsigned long long total;
+  const int first = (int)block_exclusive_scan((unsigned long long)c_eq, tmp, &total);
+  __syncthreads();  // `below` complete
+  const int base = below, n_o = (int)total;
+  if (j == 0 && tid == 0) counts[o] = n_o;
+  const int r0 = (int)((int64_t)n_o * j / m), r1 = (int)((int64_t)n_o * (j + 1) / m);
+  for (int i = lo, rank = first; i < hi; ++i) {
+    if (owner[i] != o) continue;
+    if (rank >= r0 && rank < r1) {
+      const int at = atomicAdd(&nlist, 1);
+      list[at] = make_int2(i, base + rank);
+    }
+    ++rank;
+  }
+  __syncthreads();
+  const int cnt = nlist;
+  for (int q = 0; q < cnt; ++q) {
+    const int i = list[q].x, pos = list[q].y, t = i / K;
+    const uint4* src = reinterpret_cast<const uint4*>(x + (size_t)t * H);
+    uint4* dst = reinterpret_cast<uint4*>(rows + (size_t)pos * H);
+    for (int c = tid; c < H / 16; c += 256) dst[c] = src[c];
+    const uint2* ssrc = reinterpret_cast<const uint2*>(xs + (size_t)t * (H / 32));
+    uint2* sdst = reinterpret_cast<uint2*>(row_scales + (size_t)pos * (H / 32));
+    for (int c = tid; c < H / 256; c += 256) sdst[c] = ssrc[c];
+    if (tid == 0) {
+      out_ids[pos] = ids[i];
+      out_wts[pos] = wts[i];
+      slot_rows[i] = pos;
+    }
   }
 }
 
@@ -3375,9 +3391,15 @@ int megamoe_ep_dispatch(const megamoe_desc* desc, int32_t ep, const megamoe_mx_t
   if (!send->counts) return MEGAMOE_ERR_INVALID_ARGUMENT;
   hipStream_t st = (hipStream_t)stream;
   const int n = (int)(T * K);
-  if (n == 0) {  // zero counts, written by the order kernel (no memset, so the call may be captured)
-    hipLaunchKernelGGL(k_ep_order, dim3(1), dim3(1024), 16, st, (const int64_t*)nullptr, 0, (int)E, (int)(E / ep),
-                       (int)ep, send->counts, (int32_t*)nullptr);
+  // Workgroups per owner: about 512 in all, each packing at most kDispatchList entries.
+  int m = 512 / ep;
+  if (m < 1) m = 1;
+  while ((int64_t)m * kDispatchList < n) ++m;
+  if (n == 0) {  // zero counts, written by the kernel (no memset, so the call may be captured)
+    hipLaunchKernelGGL(k_ep_dispatch, dim3((unsigned)ep), dim3(256), 16, st, (const int64_t*)nullptr,
+                       (const uint8_t*)nullptr, (const uint8_t*)nullptr, (const float*)nullptr, 0, (int)K, (int)H,
+                       (int)E, (int)(E / ep), 1, send->counts, (int32_t*)nullptr, (uint8_t*)nullptr,
+                       (uint8_t*)nullptr, (int64_t*)nullptr, (float*)nullptr);
     MEGAMOE_LAUNCH_CHECK();
     return MEGAMOE_OK;
   }
@@ -3386,12 +3408,9 @@ int megamoe_ep_dispatch(const megamoe_desc* desc, int32_t ep, const megamoe_mx_t
     return MEGAMOE_ERR_INVALID_ARGUMENT;
   if (!aligned16(t->x) || !aligned16(send->rows) || ((uintptr_t)t->x_scales & 7) || ((uintptr_t)send->row_scales & 7))
     return MEGAMOE_ERR_INVALID_ARGUMENT;
-  hipLaunchKernelGGL(k_ep_order, dim3(1), dim3(1024), (size_t)n, st, t->topk_idx, n, (int)E, (int)(E / ep),
-                     (int)ep, send->counts, send->slot_rows);
-  MEGAMOE_LAUNCH_CHECK();
-  hipLaunchKernelGGL(k_ep_pack, dim3(n), dim3(256), 0, st, t->x, t->x_scales, t->topk_idx, t->topk_weights,
-                     (const int32_t*)send->slot_rows, (int)K, (int)H, send->rows, send->row_scales, send->ids,
-                     send->weights);
+  hipLaunchKernelGGL(k_ep_dispatch, dim3((unsigned)(ep * m)), dim3(256), (size_t)n, st, t->topk_idx, t->x,
+                     t->x_scales, t->topk_weights, n, (int)K, (int)H, (int)E, (int)(E / ep), m, send->counts,
+                     send->slot_rows, send->rows, send->row_scales, send->ids, send->weights);
   MEGAMOE_LAUNCH_CHECK();
   return MEGAMOE_OK;
 }
