@@ -3103,12 +3103,20 @@ __global__ __launch_bounds__(256) void k_ep_dispatch(const int64_t* __restrict__
     below = 0;
   }
   __syncthreads();
-  for (int i = tid; i < n; i += 256) {
-    const int64_t e = ids[i];
-    if (e < 0 || e >= E)
-      bad = 1;
-    else
-      owner[i] = (uint8_t)((int)e / local);
+  for (int i0 = tid; i0 < n; i0 += 256 * 8) {  // eight id loads in flight per thread
+    int64_t e[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) e[u] = i0 + 256 * u < n ? ids[i0 + 256 * u] : 0;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int i = i0 + 256 * u;
+      if (i < n) {
+        if (e[u] < 0 || e[u] >= E)
+          bad = 1;
+        else
+          owner[i] = (uint8_t)((int)e[u] / local);
+      }
+    }
   }
   __syncthreads();
   if (bad) {
@@ -3138,20 +3146,38 @@ __global__ __launch_bounds__(256) void k_ep_dispatch(const int64_t* __restrict__
     ++rank;
   }
   __syncthreads();
-  const int cnt = nlist;
-  for (int q = 0; q < cnt; ++q) {
-    const int i = list[q].x, pos = list[q].y, t = i / K;
-    const uint4* src = reinterpret_cast<const uint4*>(x + (size_t)t * H);
-    uint4* dst = reinterpret_cast<uint4*>(rows + (size_t)pos * H);
-    for (int c = tid; c < H / 16; c += 256) dst[c] = src[c];
-    const uint2* ssrc = reinterpret_cast<const uint2*>(xs + (size_t)t * (H / 32));
-    uint2* sdst = reinterpret_cast<uint2*>(row_scales + (size_t)pos * (H / 32));
-    for (int c = tid; c < H / 256; c += 256) sdst[c] = ssrc[c];
-    if (tid == 0) {
-      out_ids[pos] = ids[i];
-      out_wts[pos] = wts[i];
-      slot_rows[i] = pos;
+  // The rows as one flat list of 16-byte chunks, eight loads in flight per thread.
+  const int cnt = nlist, nch = H / 16, total_ch = cnt * nch;
+  for (int k0 = tid; k0 < total_ch; k0 += 256 * 8) {
+    uint4 v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int k = k0 + 256 * u;
+      if (k < total_ch) {
+        const int q = k / nch;
+        v[u] = reinterpret_cast<const uint4*>(x + (size_t)(list[q].x / K) * H)[k - q * nch];
+      }
     }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int k = k0 + 256 * u;
+      if (k < total_ch) {
+        const int q = k / nch;
+        reinterpret_cast<uint4*>(rows + (size_t)list[q].y * H)[k - q * nch] = v[u];
+      }
+    }
+  }
+  const int nsc = H / 256;  // 8-byte scale words per row
+  for (int k = tid; k < cnt * nsc; k += 256) {
+    const int q = k / nsc;
+    reinterpret_cast<uint2*>(row_scales + (size_t)list[q].y * (H / 32))[k - q * nsc] =
+        reinterpret_cast<const uint2*>(xs + (size_t)(list[q].x / K) * (H / 32))[k - q * nsc];
+  }
+  for (int q = tid; q < cnt; q += 256) {
+    const int i = list[q].x, pos = list[q].y;
+    out_ids[pos] = ids[i];
+    out_wts[pos] = wts[i];
+    slot_rows[i] = pos;
   }
 }
 
