@@ -125,3 +125,66 @@ def test_python_errors_follow_the_reference_behaviour():
         _lib.check(_lib.ERR_SHAPE, "probe")
     with pytest.raises(_lib.MegaMoEError):
         _lib.check(_lib.ERR_HIP, "probe")
+
+
+def test_ep_and_variant_entry_points_check_arguments_before_any_gpu_call():
+    lib = _lib.load()
+    P = ctypes.byref
+    desc = _lib.Desc(tokens=64, hidden=7168, experts=384, topk=6, intermediate=3072)
+    t, send = _lib.MxTensors(), _lib.EpSend()
+    # Dispatch: geometry, limits, pointers.
+    assert lib.megamoe_ep_dispatch(None, 8, P(t), P(send), None) == _lib.ERR_INVALID_ARGUMENT
+    assert lib.megamoe_ep_dispatch(P(desc), 7, P(t), P(send), None) == _lib.ERR_SHAPE  # 7 does not divide 384
+    assert lib.megamoe_ep_dispatch(P(desc), 0, P(t), P(send), None) == _lib.ERR_SHAPE
+    assert lib.megamoe_ep_dispatch(P(desc), 384, P(t), P(send), None) == _lib.ERR_UNSUPPORTED  # > 256 ranks
+    big = _lib.Desc(tokens=10000, hidden=7168, experts=384, topk=6, intermediate=3072)
+    assert lib.megamoe_ep_dispatch(P(big), 8, P(t), P(send), None) == _lib.ERR_UNSUPPORTED  # T*K > 49152
+    assert lib.megamoe_ep_dispatch(P(desc), 8, P(t), P(send), None) == _lib.ERR_INVALID_ARGUMENT  # no counts
+    fake = _lib.EpSend(**{name: 256 for name in _lib.EP_SEND_FIELDS})
+    assert lib.megamoe_ep_dispatch(P(desc), 8, P(t), P(fake), None) == _lib.ERR_INVALID_ARGUMENT  # no x
+    odd = _lib.MxTensors(x=257, x_scales=256, topk_idx=256, topk_weights=256)
+    assert lib.megamoe_ep_dispatch(P(desc), 8, P(odd), P(fake), None) == _lib.ERR_INVALID_ARGUMENT  # x unaligned
+    # Local experts: one slot per row, a valid base.
+    assert lib.megamoe_ep_experts(P(desc), 10.0, 0, P(t), None, None) == _lib.ERR_SHAPE  # topk 6
+    one = _lib.Desc(tokens=100, hidden=7168, experts=48, topk=1, intermediate=3072)
+    assert lib.megamoe_ep_experts(P(one), 10.0, -1, P(t), None, None) == _lib.ERR_SHAPE
+    assert lib.megamoe_ep_experts(P(one), 10.0, 48, P(t), None, None) == _lib.ERR_INVALID_ARGUMENT  # no pointers
+    assert lib.megamoe_ep_experts(P(one), 0.0, 48, P(t), None, None) == _lib.ERR_INVALID_ARGUMENT  # limit 0
+    # Combine at the source.
+    assert lib.megamoe_ep_combine(4, 100, 2, None, None, None, None) == _lib.ERR_SHAPE  # H % 8
+    assert lib.megamoe_ep_combine(0, 7168, 6, None, None, None, None) == _lib.OK
+    assert lib.megamoe_ep_combine(4, 7168, 6, None, None, None, None) == _lib.ERR_INVALID_ARGUMENT
+    assert lib.megamoe_ep_combine(4, 7168, 6, 257, 256, 256, None) == _lib.ERR_INVALID_ARGUMENT  # unaligned
+    # GPT-OSS combine.
+    assert lib.megamoe_combine_by_expert_id(4, 2880, 33, None, None, None, None, None, None) == \
+        _lib.ERR_UNSUPPORTED  # K > 32
+    assert lib.megamoe_combine_by_expert_id(0, 2880, 4, None, None, None, None, None, None) == _lib.OK
+    assert lib.megamoe_combine_by_expert_id(4, 2880, 4, None, None, None, None, None, None) == \
+        _lib.ERR_INVALID_ARGUMENT
+    # Epilogue variants: the form and the limit are checked.
+    d8 = submission.make_desc(C.case(C.HEADLINE))
+    ft = _lib.Tensors()
+    for bad in (_lib.Epilogue(swiglu=2, swiglu_limit=0.0), _lib.Epilogue(swiglu=1, swiglu_limit=-1.0),
+                _lib.Epilogue(swiglu=0, swiglu_limit=float("nan"))):
+        assert lib.megamoe_forward_ex(P(d8), P(ft), None, P(bad), None, None) == _lib.ERR_INVALID_ARGUMENT
+    ok = _lib.Epilogue(swiglu=1, swiglu_limit=10.0)
+    assert lib.megamoe_forward_ex(P(d8), P(ft), None, P(ok), None, None) == _lib.ERR_INVALID_ARGUMENT  # no tensors
+    d8.tokens = 0
+    assert lib.megamoe_forward_ex(P(d8), P(ft), None, P(ok), None, None) == _lib.OK
+
+
+def test_case_table_of_the_forms():
+    """Every form's case builds its layer (workspace sizing on the CPU) and the catalog
+    geometry of the EP share, the MXFP4 and GLM cases is the reference's."""
+    for c in C.BLOCK_CASES + C.MX_CASES + C.VARIANT_CASES:
+        layer = submission.MoELayer(c)
+        assert layer.workspace_bytes > 0 and layer.workspace_bytes % 256 == 0
+    glm = C.case("moe-fp8-glm-5.3-flash-t64")
+    assert (glm.hidden, glm.experts, glm.topk, glm.intermediate, glm.shared_experts) == (4096, 288, 8, 2048, 1)
+    assert (glm.swiglu, glm.swiglu_limit, glm.router, glm.groups) == ("bf16", 10.0, "sigmoid", 1)
+    with pytest.raises(ValueError):
+        C.Case.from_dict({**glm.to_dict(), "swiglu": "fp16"})
+    with pytest.raises(ValueError):
+        C.Case.from_dict({**C.case("moe-mxfp4-deepseek-v4-pro-t64").to_dict(), "swiglu": "bf16"})
+    with pytest.raises(ValueError):  # expert parallelism is defined for the MXFP4 form
+        C.Case.from_dict({**C.case(C.HEADLINE).to_dict(), "gpus": 8, "ep": 8})
