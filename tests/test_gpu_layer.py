@@ -36,6 +36,10 @@ def _dev_cases():
         out.append(C.development(c))
     out.append(C.development(C.case(C.HEADLINE), tokens=37))  # ragged token count, multi-row experts
     out.append(C.development(C.case("moe-fp8-kimi-k2-t128"), tokens=70, experts=8, topk=4))  # hot experts > 16 rows
+    # Rows of 32 K blocks and few gate/up blocks: the expert kernel works gate and up of each
+    # block as separate units (with and without a shared expert).
+    out.append(C.development(C.case("moe-fp8-mixtral-t16"), hidden=4096, intermediate=512))
+    out.append(C.development(C.case(C.HEADLINE), hidden=4096, tokens=40))
     return out
 
 

@@ -777,6 +777,7 @@ struct PermuteOut {
   int4* dn;      // down chunks
   int* dn_of_gu; // gate/up chunk -> down chunk of the same rows
   int* ready;    // [down chunks] zeroed here, counted by the expert kernel
+  int* pairs;    // [gate/up chunks * nbI] zeroed here (NULL: none), counted by the expert kernel
 };
 
 __device__ __forceinline__ int chunk_class(int rows) { return rows > 32 ? 0 : (rows > 16 ? 1 : 2); }
@@ -895,6 +896,8 @@ __global__ __launch_bounds__(1024) void k_permute(const int64_t* __restrict__ id
   }
   const int dtot = s4 + s2 + s1 + t4 + t2 + t1;
   for (int i = tid; i < dtot; i += blockDim.x) out.ready[i] = 0;
+  if (out.pairs)
+    for (int i = tid; i < (S * (s4 + s2 + s1) + t4 + t2 + t1) * nbI; i += blockDim.x) out.pairs[i] = 0;
   if (tid < E) cnt[tid] = off;  // reuse as offsets (every thread read its count above)
   __syncthreads();
   for (int i = tid; i < n; i += blockDim.x) {
@@ -1225,6 +1228,9 @@ struct GateUpArgs {
   int* meta;
   uint8_t* hq_r; float* hs_r;   // routed rows [T*K, I], [T*K, I/128]
   uint8_t* hq_s; float* hs_s;   // shared rows [T, S*I], [T, S*I/128]
+  uint16_t* st_r;               // bf16 gate and up outputs of routed rows, [2][T*K, I]
+  uint16_t* st_s;               // of shared rows, [2][T, S*I]
+  int* pairs;                   // per (gate/up chunk, 128-row block): halves finished
   const uint8_t* spare;         // 16 rows of the longest weight row, in the workspace
   int T, H, I, K, S, E, pow2;
   int swiglu;                   // 0: fp32 product rounded once; 1: bf16 silu, bf16 product
@@ -1345,6 +1351,171 @@ __device__ void gateup_work(const GateUpArgs& a, int u, float (*red)[64], uint8_
     gateup_unit<2>(a, wg, wu, sg, su, cr, jb, hq, hs, ldh, rot, red, ring);
   else
     gateup_unit<4>(a, wg, wu, sg, su, cr, jb, hq, hs, ldh, rot, red, ring);
+}
+
+// One half of a gate/up block: rows [jb*128, jb*128+128) of gate (half 0) or of up (half 1)
+// against the chunk's activation rows (at most 16*NCT). Wave w owns rows 32w .. 32w+31 of
+// the block. The half rounds its outputs to bf16 (frontier.py:184-186), clamps them at the
+// SwiGLU limit if one is set (glm53.py:175: gate above, up on both sides) and stores them
+// to the staging rows with device-coherent stores; then it counts itself in the block's
+// pair counter. The half that finishes second reads the other half's values back (the same
+// elements its own lanes hold), forms h = bf16(silu(fp32 g) * fp32 u) (frontier.py:337,
+// DeepSeek) or bf16(bf16(silu(g)) * u) (frontier.py:338, glm53.py:174-175), reduces the
+// per-row amax over the 128-block across the four wavefronts through LDS and requantizes h
+// to E4M3 per 128. Returns true for that half (the block of h is complete).
+//
+// Staging hand-over: every staged line is written by exactly one half, read only by the
+// other half of its block after the counter has shown the writer done (the writer's
+// stores complete before its increment), and never read earlier in the kernel, so no
+// cache can hold a stale copy of it.
+template <int NCT>
+__device__ bool gateup_half(const GateUpArgs& a, const uint8_t* wt, const float* sc, const ChunkRows& cr, int jb,
+                            int half, uint8_t* hq, float* hs, uint16_t* st_mine, const uint16_t* st_other, int ldh,
+                            int* pair, int rot, float (*red)[64], int* flag, uint8_t* ring) {
+  const int lane = opaque_lane(), w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int kofs = 16 * (lane >> 4);
+  const int H = a.H, nkb = H / kBlock, nbh = scale_ld(ldh / kBlock);
+  Operands<2, NCT, 1> op;
+  op.lda = H;
+  op.spare = a.spare;
+#pragma unroll
+  for (int r = 0; r < 2; ++r) op.a[r] = wt + (size_t)(32 * w + 16 * r) * H;
+  op.sw[0] = sc;
+#pragma unroll
+  for (int c = 0; c < NCT; ++c) {
+    const int r = min(16 * c + (lane & 15), cr.n - 1);  // padding columns repeat a valid row
+    const int tok = row_token(cr, r);
+    op.b[c] = a.xq + (size_t)tok * H + kofs;
+    op.sx[c] = a.xs + (size_t)tok * nkb;
+  }
+  f32x4 acc[2][NCT];
+  stream_gemm<2, NCT, 1, NCT == 4 ? 3 : 4>(op, nkb, rot, ring, acc);
+
+  const float L = a.limit > 0.0f ? a.limit : INFINITY;
+  const float lo = half ? -L : -INFINITY;  // up is clamped on both sides, gate above only
+  float mine[NCT][2][4];
+  // Lane element (c, p, v): output channel jb*128 + 32w + 16p + 4*(lane/16) + v of token
+  // row 16c + lane%16; four consecutive channels per lane go out as one 8-byte store.
+#pragma unroll
+  for (int c = 0; c < NCT; ++c) {
+    const int col = 16 * c + (lane & 15);
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      uint32_t bits[4];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const float x = fminf(fmaxf(round_bf16(acc[p][c][v]), lo), L);
+        mine[c][p][v] = x;
+        bits[v] = f32_to_bf16_bits(x);
+      }
+      if (col < cr.n) {
+        uint16_t* dst = st_mine + (size_t)(cr.row0 + col) * ldh + (size_t)jb * kBlock + 32 * w + 16 * p +
+                        4 * (lane >> 4);
+        store_coherent(reinterpret_cast<uint64_t*>(dst),
+                       (uint64_t)(bits[0] | (bits[1] << 16)) | ((uint64_t)(bits[2] | (bits[3] << 16)) << 32));
+      }
+    }
+  }
+  publish_fence();
+  __syncthreads();
+  if (threadIdx.x == 0) *flag = atomicAdd(pair, 1);
+  __syncthreads();
+  if (*flag == 0) return false;  // the other half finishes the block
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+
+  const bool bf16_silu = a.swiglu != 0;
+  float hv[NCT][2][4];
+#pragma unroll
+  for (int c = 0; c < NCT; ++c) {
+    const int col = 16 * c + (lane & 15);
+    const int rr = min(col, cr.n - 1);
+    float amax = 0.0f;
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      const uint2 o = *reinterpret_cast<const uint2*>(st_other + (size_t)(cr.row0 + rr) * ldh +
+                                                      (size_t)jb * kBlock + 32 * w + 16 * p + 4 * (lane >> 4));
+      const float ov[4] = {bf16_bits_to_f32(o.x & 0xffffu), bf16_bits_to_f32(o.x >> 16),
+                           bf16_bits_to_f32(o.y & 0xffffu), bf16_bits_to_f32(o.y >> 16)};
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const float g = half ? ov[v] : mine[c][p][v];
+        const float u = half ? mine[c][p][v] : ov[v];
+        const float h = bf16_silu ? round_bf16(round_bf16(silu(g)) * u) : round_bf16(silu(g) * u);
+        hv[c][p][v] = h;
+        amax = fmaxf(amax, fabsf(h));
+      }
+    }
+    amax = fmaxf(amax, __shfl_xor(amax, 16));
+    amax = fmaxf(amax, __shfl_xor(amax, 32));
+    if (lane < 16) red[w][16 * c + lane] = amax;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int c = 0; c < NCT; ++c) {
+    const int col = 16 * c + (lane & 15);
+    const float amax = fmaxf(fmaxf(red[0][col], red[1][col]), fmaxf(red[2][col], red[3][col]));
+    const float s = act_scale(amax, a.pow2);
+    if (col < cr.n) {
+      uint8_t* dst = hq + (size_t)(cr.row0 + col) * ldh + (size_t)jb * kBlock + 32 * w + 4 * (lane >> 4);
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        uint32_t packed = 0;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) packed |= f32_to_e4m3(clamp448(hv[c][p][v] / s)) << (8 * v);
+        store_coherent(reinterpret_cast<uint32_t*>(dst + 16 * p), packed);
+      }
+      if (w == 0 && lane < 16) store_coherent(hs + (size_t)(cr.row0 + col) * nbh + jb, s);
+    }
+  }
+  return true;
+}
+
+// Gate/up unit u of the work list: block pair u / 2 (chunk (u/2) / nbI, 128-row block
+// (u/2) % nbI of the chunk's expert, plus the slice offset of a shared-expert copy), half
+// u % 2 (gate, then up). Returns true if this unit completed the block of h.
+__device__ bool gateup_work_split(const GateUpArgs& a, int u, float (*red)[64], int* flag, uint8_t* ring) {
+  const int nbI = a.I / kBlock, nkb = a.H / kBlock;
+  const int pair = u >> 1, half = u & 1;
+  const int4 ch = a.chunks[pair / nbI];
+  const int j = pair % nbI, jb = ch.w + j;
+  const int rot = pair % nkb;  // concurrent units start at different K blocks
+  const uint8_t* wt;
+  const float* sc;
+  uint8_t* hq;
+  float* hs;
+  uint16_t* st;
+  int ldh;
+  size_t st_half;
+  ChunkRows cr;
+  if (ch.x == a.E) {  // shared expert: rows of its S*I-row gate/up matrices
+    wt = (half ? a.sup : a.sgate) + (size_t)jb * kBlock * a.H;
+    sc = (half ? a.sup_scale : a.sgate_scale) + (size_t)jb * nkb;
+    cr = ChunkRows{ch.z, ch.y, nullptr, a.K};
+    hq = a.hq_s;
+    hs = a.hs_s;
+    ldh = a.S * a.I;
+    st = a.st_s;
+    st_half = (size_t)a.T * ldh;
+  } else {
+    const size_t rowblk = (size_t)ch.x * nbI + jb;
+    wt = (half ? a.up : a.gate) + rowblk * kBlock * a.H;
+    sc = (half ? a.up_scale : a.gate_scale) + rowblk * nkb;
+    cr = ChunkRows{ch.z, a.offsets[ch.x] + ch.y, a.perm, a.K};
+    hq = a.hq_r;
+    hs = a.hs_r;
+    ldh = a.I;
+    st = a.st_r;
+    st_half = (size_t)a.T * a.K * ldh;
+  }
+  uint16_t* mine = st + (half ? st_half : 0);
+  const uint16_t* other = st + (half ? 0 : st_half);
+  int* ctr = a.pairs + pair;
+  if (cr.n <= 16)
+    return gateup_half<1>(a, wt, sc, cr, jb, half, hq, hs, mine, other, ldh, ctr, rot, red, flag, ring);
+  else if (cr.n <= 32)
+    return gateup_half<2>(a, wt, sc, cr, jb, half, hq, hs, mine, other, ldh, ctr, rot, red, flag, ring);
+  else
+    return gateup_half<4>(a, wt, sc, cr, jb, half, hq, hs, mine, other, ldh, ctr, rot, red, flag, ring);
 }
 
 struct DownArgs {
@@ -1584,14 +1755,18 @@ struct ExpertArgs {
   int* ready;           // [down chunks] finished gate/up units
 };
 
+// SPLIT: each 128-row block of gate/up is worked as two units, gate and up, and the one
+// that finishes second forms h (gateup_half); otherwise one unit multiplies both
+// (gateup_unit). The two give the same bits; the host picks one from the geometry.
+template <bool SPLIT>
 __global__ __launch_bounds__(256, 2) void k_experts(ExpertArgs args) {
   typedef const __attribute__((address_space(4))) ExpertArgs* ArgsPtr;
   __shared__ float red[4][64];
   __shared__ __attribute__((aligned(16))) uint8_t rings[4 * kRingWave];  // one weight ring per wavefront
-  __shared__ int slot;
+  __shared__ int slot, flag;
   static_assert(sizeof(ExpertArgs) % 8 == 0, "argument segment layout");
   int* meta = args.gu.meta;
-  const int total_gu = meta[kMetaUnitsGU];
+  const int total_gu = (SPLIT ? 2 : 1) * meta[kMetaUnitsGU];
   const int total = total_gu + meta[kMetaUnitsDN];
   // Every unit, the first included, is claimed from the queue: a unit that a down unit
   // waits for is then always held by a running workgroup (one that has not started yet
@@ -1617,10 +1792,16 @@ __global__ __launch_bounds__(256, 2) void k_experts(ExpertArgs args) {
     // unit waits behind a waiting workgroup.
     if (threadIdx.x == 0) next = atomicAdd(&meta[kMetaQueueGU], 1);
     if (u < total_gu) {
-      gateup_work(a.gu, u, red, ring);
-      publish_fence();
-      __syncthreads();
-      if (threadIdx.x == 0) atomicAdd(&a.ready[a.dn_of_gu[u / nbI]], 1);
+      bool done = true;
+      if constexpr (SPLIT)
+        done = gateup_work_split(a.gu, u, red, &flag, ring);
+      else
+        gateup_work(a.gu, u, red, ring);
+      if (done) {
+        publish_fence();
+        __syncthreads();
+        if (threadIdx.x == 0) atomicAdd(&a.ready[a.dn_of_gu[(SPLIT ? u >> 1 : u) / nbI]], 1);
+      }
     } else {
       const int v = u - total_gu, c = v / (nbH * a.dn.ks);
       const ReadyWait ready{&a.ready[c], a.dn.chunks[c].x == a.dn.E ? a.dn.S * nbI : nbI, &meta[kMetaError]};
@@ -2618,8 +2799,8 @@ constexpr size_t kAlign = 256;
 inline size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
 struct Layout {
-  size_t xn, partial, xq, xs, counts, offsets, meta, perm, inv, gu, dn, dn_of_gu, ready, hq_r, hs_r, hq_s, hs_s, d_r, d_s,
-      p_r, p_s, spare, total;
+  size_t xn, partial, xq, xs, counts, offsets, meta, perm, inv, gu, dn, dn_of_gu, ready, pairs, hq_r, hs_r, hq_s, hs_s,
+      st_r, st_s, d_r, d_s, p_r, p_s, spare, total;
   int nsplit;
   int ks;  // K parts of each down unit
 };
@@ -2647,6 +2828,20 @@ int down_splits(const megamoe_desc& d) {
   return ks;
 }
 
+// Whether the expert kernel works gate and up of each 128-row block as separate units
+// (k_experts<true>). Worth it when the whole-block units cannot fill two rounds of a
+// reference grid (2 per CU on 256 CUs) even if every expert is hit, so the last blocks of
+// each expert (which its down units wait for) land late, and the rows are long enough (32
+// or more K blocks) for the hand-over between the halves to be cheap next to the stream:
+// a Mixtral-shaped layer (8 experts of 112 blocks, H 4096) ran 6% faster split, and the
+// DeepSeek-V3, Kimi-K2 and Qwen3-30B-A3B shapes 3-7% slower. Depends on the geometry
+// only; both forms give the same bits.
+bool split_gate_up(const megamoe_desc& d) {
+  const size_t hit = (size_t)(d.experts < (int64_t)d.tokens * d.topk ? d.experts : (int64_t)d.tokens * d.topk);
+  const size_t units = (hit + (size_t)d.shared_experts) * (size_t)(d.intermediate / kBlock);
+  return units < 2 * 512 && d.hidden / kBlock >= 32;
+}
+
 Layout make_layout(const megamoe_desc& d) {
   Layout L{};
   const size_t T = d.tokens, H = d.hidden, E = d.experts, K = d.topk, I = d.intermediate, S = d.shared_experts;
@@ -2670,10 +2865,14 @@ Layout make_layout(const megamoe_desc& d) {
   L.dn = take(max_chunks(d, S > 0 ? 1 : 0) * sizeof(int4));
   L.dn_of_gu = take(max_chunks(d, (int)S) * sizeof(int));
   L.ready = take(max_chunks(d, S > 0 ? 1 : 0) * sizeof(int));
+  L.pairs = take(max_chunks(d, (int)S) * (I / kBlock) * sizeof(int));
   L.hq_r = take(T * K * I);
   L.hs_r = take(T * K * scale_ld((int)(I / kBlock)) * sizeof(float));
   L.hq_s = take(T * S * I);
   L.hs_s = take(T * scale_ld((int)(S * I / kBlock)) * sizeof(float));
+  const bool split = split_gate_up(d);  // staging of the separate gate and up units
+  L.st_r = take(split ? 2 * T * K * I * 2 : 0);
+  L.st_s = take(split ? 2 * T * S * I * 2 : 0);
   L.d_r = take(T * K * H * 2);
   L.d_s = take(T * H * 2);
   L.ks = down_splits(d);
@@ -2717,7 +2916,11 @@ int device_info(DeviceInfo* out) {
   if (di.cus == 0) {
     int cus = 0, per_cu = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return MEGAMOE_ERR_HIP;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_experts, 256, 0) != hipSuccess) return MEGAMOE_ERR_HIP;
+    int per_cu_split = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_experts<false>, 256, 0) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu_split, k_experts<true>, 256, 0) != hipSuccess)
+      return MEGAMOE_ERR_HIP;
+    per_cu = per_cu_split < per_cu ? per_cu_split : per_cu;
     di.experts_per_cu = per_cu > 0 ? per_cu : 1;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_experts_mx, 256, 0) != hipSuccess)
       return MEGAMOE_ERR_HIP;
@@ -2851,7 +3054,7 @@ int forward_impl(const megamoe_desc* desc, const megamoe_tensors* t, hipStream_t
 
   PermuteOut po{(int*)(ws + L.counts), (int*)(ws + L.offsets), (int*)(ws + L.meta), (int*)(ws + L.perm),
                 (int*)(ws + L.inv),    (int4*)(ws + L.gu),     (int4*)(ws + L.dn),  (int*)(ws + L.dn_of_gu),
-                (int*)(ws + L.ready)};
+                (int*)(ws + L.ready),  (int*)(ws + L.pairs)};
   const int nbI = I / kBlock, nbH = H / kBlock;
   const size_t lds = ((size_t)E * (1 + (T + 31) / 32) + 32) * 4;
   hipLaunchKernelGGL(k_permute, dim3(1), dim3(1024), lds, st, t->expert_ids, (int64_t)0, T, K, E, S, nbI, nbH, L.ks,
@@ -2870,6 +3073,8 @@ int forward_impl(const megamoe_desc* desc, const megamoe_tensors* t, hipStream_t
   ga.offsets = po.offsets; ga.perm = po.perm; ga.chunks = po.gu; ga.meta = po.meta;
   ga.hq_r = (uint8_t*)(ws + L.hq_r); ga.hs_r = (float*)(ws + L.hs_r);
   ga.hq_s = (uint8_t*)(ws + L.hq_s); ga.hs_s = (float*)(ws + L.hs_s);
+  ga.st_r = (uint16_t*)(ws + L.st_r); ga.st_s = (uint16_t*)(ws + L.st_s);
+  ga.pairs = po.pairs;
   ga.spare = (const uint8_t*)(ws + L.spare);
   ga.T = T; ga.H = H; ga.I = I; ga.K = K; ga.S = S; ga.E = E; ga.pow2 = d.pow2_scales;
   ga.swiglu = epi ? epi->swiglu : 0;
@@ -2889,10 +3094,15 @@ int forward_impl(const megamoe_desc* desc, const megamoe_tensors* t, hipStream_t
   ea.ready = po.ready;
   // As many workgroups as fit on the device at once, and no more than the most units the
   // routing can produce.
-  const size_t units_max = max_chunks(d, S) * (size_t)nbI + max_chunks(d, S > 0 ? 1 : 0) * (size_t)nbH * L.ks;
+  const bool split = split_gate_up(d);
+  const size_t units_max =
+      (split ? 2 : 1) * max_chunks(d, S) * (size_t)nbI + max_chunks(d, S > 0 ? 1 : 0) * (size_t)nbH * L.ks;
   const size_t resident = (size_t)di.cus * di.experts_per_cu;
   const unsigned grid = (unsigned)(units_max < resident ? units_max : resident);
-  hipLaunchKernelGGL(k_experts, dim3(grid), dim3(256), 0, st, ea);
+  if (split)
+    hipLaunchKernelGGL(k_experts<true>, dim3(grid), dim3(256), 0, st, ea);
+  else
+    hipLaunchKernelGGL(k_experts<false>, dim3(grid), dim3(256), 0, st, ea);
   MEGAMOE_LAUNCH_CHECK();
   if (mark(4) != hipSuccess) return MEGAMOE_ERR_HIP;
 
