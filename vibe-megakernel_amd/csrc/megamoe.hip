@@ -316,13 +316,15 @@ __device__ __forceinline__ void quant_x_group(int group, const uint16_t* __restr
   }
 }
 
-// Router partials. Workgroup (expert tile et, split) of kRouterWaves wavefronts covers 16
-// experts, H range [split * H/nsplit, +H/nsplit) and every token, in passes of 16 * NTT
-// tokens: wavefront w takes the w-th of kRouterWaves equal slices of the range, keeps NTT
-// 16x16 fp64 accumulators (one per token tile) and streams its slice in 16-channel steps,
-// all of them in flight at once (at most kRouterDepth). The router weights of the slice
-// are read once per pass, x once per expert tile. The wavefronts' sums are added in
-// wavefront order through LDS and the split's partial is stored in fp64.
+// Router partials. Workgroup (expert tile et, split, pass) of kRouterWaves wavefronts
+// covers 16 experts, H range [split * H/nsplit, +H/nsplit) and tokens [pass * 16 * NTT,
+// +16 * NTT): wavefront w takes the w-th of kRouterWaves equal slices of the range, keeps
+// NTT 16x16 fp64 accumulators (one per token tile) and streams its slice in 16-channel
+// steps, all of them in flight at once (at most kRouterDepth). The router weights of the
+// slice are read once per pass, x once per expert tile. The wavefronts' sums are added in
+// wavefront order through LDS and the split's partial is stored in fp64. Passes are
+// workgroups of their own, so every workgroup does the same work and the grid spreads
+// evenly over the CUs.
 template <int NTT>
 __global__ __launch_bounds__(kRouterWaves * 64) void k_router(const uint16_t* __restrict__ x,
                                                               const float* __restrict__ w,
@@ -330,7 +332,7 @@ __global__ __launch_bounds__(kRouterWaves * 64) void k_router(const uint16_t* __
                                                               int n_et, int nsplit) {
   __shared__ f64x4 red[kRouterWaves - 1][NTT][64];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const int et = blockIdx.x % n_et, split = blockIdx.x / n_et;
+  const int et = blockIdx.x % n_et, split = (blockIdx.x / n_et) % nsplit, pass = blockIdx.x / (n_et * nsplit);
   const int span = H / nsplit / kRouterWaves;  // channels per wavefront, a multiple of 16
   const int k0 = split * (H / nsplit) + wv * span;
   const int g = lane >> 4;
@@ -340,7 +342,8 @@ __global__ __launch_bounds__(kRouterWaves * 64) void k_router(const uint16_t* __
   // unconditional so the compiler keeps all of them in flight.
   const float* wp = w + (size_t)(e_ok ? e : 0) * H + k0 + 4 * g;
   const int steps = span / 16;
-  for (int tp = 0; tp < T; tp += 16 * NTT) {
+  {
+    const int tp = pass * 16 * NTT;
     const uint16_t* xp[NTT];
     bool t_ok[NTT];
 #pragma unroll
@@ -407,7 +410,6 @@ __global__ __launch_bounds__(kRouterWaves * 64) void k_router(const uint16_t* __
         }
       }
     }
-    if (tp + 16 * NTT < T) __syncthreads();  // red is reused by the next pass
   }
 }
 
@@ -479,22 +481,20 @@ __device__ __forceinline__ void lane_pair(uint32_t v, uint32_t& a, uint32_t& b) 
 }
 
 template <int STEP>
-__device__ __forceinline__ unsigned long long max_step_u64(unsigned long long v) {
-  uint32_t la, lb, ha, hb;
-  lane_pair<STEP>((uint32_t)v, la, lb);
-  lane_pair<STEP>((uint32_t)(v >> 32), ha, hb);
-  const unsigned long long a = ((unsigned long long)ha << 32) | la, b = ((unsigned long long)hb << 32) | lb;
+__device__ __forceinline__ uint32_t max_step_u32(uint32_t v) {
+  uint32_t a, b;
+  lane_pair<STEP>(v, a, b);
   return a > b ? a : b;
 }
 
-// Largest 64-bit value over the wavefront (every lane gets it).
-__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v) {
-  v = max_step_u64<0>(v);
-  v = max_step_u64<1>(v);
-  v = max_step_u64<2>(v);
-  v = max_step_u64<3>(v);
-  v = max_step_u64<4>(v);
-  return max_step_u64<5>(v);
+// Largest 32-bit value over the wavefront (every lane gets it).
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = max_step_u32<0>(v);
+  v = max_step_u32<1>(v);
+  v = max_step_u32<2>(v);
+  v = max_step_u32<3>(v);
+  v = max_step_u32<4>(v);
+  return max_step_u32<5>(v);
 }
 
 // Merges the (largest, second largest) pairs of lanes at butterfly step STEP.
@@ -525,7 +525,10 @@ __device__ __forceinline__ unsigned long long select_key(float score, int e) {
   return ((unsigned long long)order_code(score) << 32) | (0xffffffffu - (uint32_t)e);
 }
 
-constexpr int kSelectTokens = 4;  // tokens per workgroup, one wavefront each
+// Tokens per workgroup: one. Its four wavefronts load and sum the split partials of the
+// token's logits (one entry, all splits, per thread for up to 256 experts), then
+// wavefront 0 routes the token.
+constexpr int kSelectTokens = 1;
 
 
 template <int VPL>
@@ -546,9 +549,10 @@ __global__ __launch_bounds__(256) void k_select(const double* __restrict__ parti
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int t0 = blockIdx.x * kSelectTokens, t = t0 + wv;
   const bool token_ok = t < T;
-  float* choice_lds = lds_logit[wv];
-  int* pick_id = pick_id_s[wv];
-  float* pick_val = pick_val_s[wv];
+  const int ws = wv < kSelectTokens ? wv : 0;  // the wavefronts past kSelectTokens only load
+  float* choice_lds = lds_logit[ws];
+  int* pick_id = pick_id_s[ws];
+  float* pick_val = pick_val_s[ws];
 
   float bias_v[VPL];
 #pragma unroll
@@ -558,12 +562,12 @@ __global__ __launch_bounds__(256) void k_select(const double* __restrict__ parti
   }
 
   // Logits of the workgroup's tokens into LDS: thread i sums the splits (in split order)
-  // of entries i, i+256, ... (kSelectTokens * E <= 256 * VPL of them, up to kMaxSplits
+  // of entries i, i+256, ... (kSelectTokens * E <= 64 * VPL of them, up to kMaxSplits
   // splits each), every load issued before the first add.
   const int n_here = min(kSelectTokens, T - t0) * E;
   if (logits_in) {
 #pragma unroll
-    for (int r = 0; r < VPL; ++r) {
+    for (int r = 0; r < (kSelectTokens * 64 * VPL + 255) / 256; ++r) {
       const int i = threadIdx.x + 256 * r;
       const float v = logits_in[(size_t)t0 * E + min(i, n_here - 1)];
       if (i < n_here) lds_logit[i / E][i % E] = v;
@@ -571,9 +575,10 @@ __global__ __launch_bounds__(256) void k_select(const double* __restrict__ parti
   } else {
     const size_t stride = (size_t)T * E;
     const double* p = partial + (size_t)t0 * E;
-    constexpr int R = VPL < 2 ? VPL : 2;  // entries per round of loads
+    constexpr int NE = (kSelectTokens * 64 * VPL + 255) / 256;  // entries per thread
+    constexpr int R = NE < 2 ? NE : 2;                           // entries per round of loads
 #pragma unroll
-    for (int r0 = 0; r0 < VPL; r0 += R) {
+    for (int r0 = 0; r0 < NE; r0 += R) {
       double part[R][kMaxSplits];
 #pragma unroll
       for (int r = 0; r < R; ++r) {
@@ -597,6 +602,7 @@ __global__ __launch_bounds__(256) void k_select(const double* __restrict__ parti
     }
   }
   __syncthreads();
+  if (wv >= kSelectTokens) return;  // no barrier follows
 
   float logit[VPL], prob[VPL], choice[VPL];
   bool valid[VPL];
@@ -657,7 +663,9 @@ __global__ __launch_bounds__(256) void k_select(const double* __restrict__ parti
       if (valid[j] && !((kept >> ((lane + 64 * j) / gs)) & 1ull)) choice[j] = -INFINITY;
   }
   // K rounds: the wavefront's largest remaining key is the next pick (selection order,
-  // frontier.py:236; distributed.py:174); its owner records it and drops it.
+  // frontier.py:236; distributed.py:174); its owner records it and drops it. The maximum
+  // is taken over the score codes (the keys' upper halves) first; only when several lanes
+  // hold that code does a second maximum over their index parts pick the lowest index.
   unsigned long long key[VPL];
 #pragma unroll
   for (int j = 0; j < VPL; ++j) key[j] = valid[j] ? select_key(choice[j], lane + 64 * j) : 0ull;
@@ -665,14 +673,22 @@ __global__ __launch_bounds__(256) void k_select(const double* __restrict__ parti
     unsigned long long best = 0ull;
 #pragma unroll
     for (int j = 0; j < VPL; ++j) best = key[j] > best ? key[j] : best;
-    best = wave_max_u64(best);
+    const uint32_t hi = (uint32_t)(best >> 32), lo = (uint32_t)best;
+    const uint32_t top = wave_max_u32(hi);
+    unsigned long long owner = __ballot(hi == top);
+    if (__popcll(owner) > 1) {
+      const uint32_t top_lo = wave_max_u32(hi == top ? lo : 0u);
+      owner = __ballot(hi == top && lo == top_lo);
+    }
+    if (lane == __ffsll((long long)owner) - 1) {
 #pragma unroll
-    for (int j = 0; j < VPL; ++j)
-      if (key[j] == best) {
-        pick_id[r] = lane + 64 * j;
-        pick_val[r] = prob[j];
-        key[j] = 0ull;
-      }
+      for (int j = 0; j < VPL; ++j)
+        if (key[j] == best) {
+          pick_id[r] = lane + 64 * j;
+          pick_val[r] = prob[j];
+          key[j] = 0ull;
+        }
+    }
   }
   __builtin_amdgcn_s_waitcnt(0xc07f);
   __builtin_amdgcn_wave_barrier();
@@ -2943,7 +2959,8 @@ int device_info(DeviceInfo* out) {
 int launch_router(const megamoe_desc& d, const Layout& L, const void* x, const float* router, char* ws,
                   hipStream_t st) {
   const int n_et = (d.experts + kRouterTile - 1) / kRouterTile, tiles = (d.tokens + kRouterTile - 1) / kRouterTile;
-  const dim3 grid(n_et * L.nsplit), block(kRouterWaves * 64);
+  const int ntt = tiles <= 1 ? 1 : (tiles <= 2 ? 2 : 4), passes = (tiles + ntt - 1) / ntt;
+  const dim3 grid(n_et * L.nsplit * passes), block(kRouterWaves * 64);
 #define MEGAMOE_ROUTER(NTT)                                                                                    \
   hipLaunchKernelGGL(k_router<NTT>, grid, block, 0, st, (const uint16_t*)x, router, (double*)(ws + L.partial),  \
                      d.tokens, d.hidden, d.experts, n_et, L.nsplit)
