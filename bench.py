@@ -10,8 +10,8 @@ independent input sets as it takes to move >= 1 GB per rotation, so the 256 MB
 Infinity Cache cannot hold a step's weights.
 
 Printed: one JSON line (rank 0) with the headline metric of the DeepSeek-V3
-shape (or --case), the roofline of the dominant kernel (k_experts: gate/up +
-SwiGLU + down; k_experts_mx for the MXFP4 forms) and the CPU oracle timed on a
+shape (or --case), the roofline of the dominant kernel (k_experts<false|true>:
+gate/up + SwiGLU + down; k_experts_mx for the MXFP4 forms) and the CPU oracle timed on a
 bounded sample. --all measures every other config and form (the block forms, the
 MXFP4 layer, rank 0's EP share, the epilogue variants), each in a child process,
 prints each child's line to stderr and summarizes them under "configs". For an EP
@@ -80,6 +80,15 @@ def mx_kernel(rows: int, experts: int) -> str:
     """The MXFP4 expert kernel the library runs: batch mode from 24 rows per expert on
     average (kBatchMinRows in the library), the decode kernel below."""
     return "k_experts_mx_batch" if rows >= 24 * experts else "k_experts_mx"
+
+
+def fp8_kernel(case) -> str:
+    """The FP8 expert kernel the library runs: the split gate/up form when the whole-block
+    gate/up units cannot fill two rounds of a 512-workgroup grid with every expert hit and
+    the rows have 32 or more K blocks (split_gate_up in csrc/megamoe.hip)."""
+    hit = min(case.experts, case.tokens * case.topk) + case.shared_experts
+    split = hit * (case.intermediate // 128) < 2 * 512 and case.hidden // 128 >= 32
+    return "k_experts<true>" if split else "k_experts<false>"
 
 
 def measured_traffic(case) -> float | None:
@@ -231,7 +240,7 @@ def bench_case(case, steps: int, warmup: int, want_cpu: bool, cpu_budget: float)
                      "unit": "GB/s", "frac": ex_bytes / (ex_ms * 1e-3) / PEAK_HBM,
                      "traffic": measured_traffic(case),
                      "kernel": (mx_kernel(case.tokens * case.topk, case.experts) if case.format == "mxfp4"
-                                else "k_experts"),
+                                else fp8_kernel(case)),
                      "kernel_us": ex_ms * 1e3, "bytes_per_launch": ex_bytes},
         "dtype": ("e2m1xe4m3->fp32 (E8M0 scales per 32; bf16 out)" if case.format == "mxfp4"
                   else "e4m3xe4m3->fp32 (bf16 in/out)"),
