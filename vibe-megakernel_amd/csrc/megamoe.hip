@@ -1219,6 +1219,117 @@ __device__ __forceinline__ void stream_gemm(const Operands<RT, NCT, SG>& op, int
   }
 }
 
+// The stream of a down unit over 33-64 activation rows (four column tiles), with the
+// activation tiles shared by the workgroup's four wavefronts: wave w moves only column
+// tile w of each stage, HBM/L2 -> LDS by DMA (two 1 KB instructions, the weight tiles'
+// swizzle), into one of two slots; a barrier per stage makes all four tiles visible, and
+// every wave reads them from LDS. Each wave so moves a quarter of stream_gemm's
+// activation bytes through the vector L1. The slots are the last 4 KB of the four waves'
+// rings (a three-slot weight ring of 4 KB leaves them free): tiles 0-1 of slot q in wave
+// 2q's ring, tiles 2-3 in wave 2q+1's. Weights run two stages ahead (as stream_gemm with
+// D = 3), activations and scales one: iteration kb waits for its activation tile (issued
+// after the barrier of stage kb - 1) with only the weights of stage kb + 1 issued after
+// it, passes the barrier, requests the tile of stage kb + 1 into the other slot (read by
+// every wave before this barrier), reads stage kb and requests the weights of kb + 2.
+struct StageShared {
+  float sx[4];
+  float sw;
+};
+
+__device__ __forceinline__ void issue_shared(uint32_t slot_tile, const uint8_t* const (&xrow)[2], int kb,
+                                             StageShared& st, const Operands<2, 4, 1>& op) {
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(xrow[i] + (size_t)kb * kBlock),
+                                     (__attribute__((address_space(3))) void*)(uintptr_t)(slot_tile + i * 1024), 16, 0,
+                                     0);
+#pragma unroll
+  for (int c = 0; c < 4; ++c) st.sx[c] = op.sx[c][kb];
+  st.sw = op.sw[0][kb];
+}
+
+// xrow[i]: this lane's DMA source row for rows 8i .. 8i+7 of column tile w (clamped to
+// the chunk), at its swizzled 16-byte chunk of a K block, K part start included.
+__device__ __forceinline__ void stream_gemm_shared(const Operands<2, 4, 1>& op, const uint8_t* const (&xrow)[2],
+                                                   int nkb, int rot, uint8_t* ring, f32x4 (&acc)[2][4],
+                                                   const ReadyWait& ready) {
+  constexpr int RT = 2, NCT = 4, D = 3;
+  constexpr int kSlot = RT * kTileBytes;
+  static_assert(D * kSlot + 2 * kTileBytes <= kRingWave, "LDS ring and activation slots");
+  auto phys = [nkb, rot](int kb) {
+    const int p = kb + rot;
+    return p >= nkb ? p - nkb : p;
+  };
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const LaneTile lt = lane_tile(op.lda);
+  const uint32_t ring_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)ring;
+  const uint32_t rings_lds = ring_lds - (uint32_t)(w * kRingWave);
+#define MEGAMOE_XTILE(q, c) \
+  (rings_lds + (uint32_t)((2 * (q) + ((c) >> 1)) * kRingWave + (kRingWave - 2 * kTileBytes) + ((c) & 1) * kTileBytes))
+#pragma unroll
+  for (int r = 0; r < RT; ++r)
+#pragma unroll
+    for (int c = 0; c < NCT; ++c) acc[r][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+  StageShared st[2];
+  // Issue order W0, A0, W1, then per stage kb: A(kb+1), W(kb+2). When stage kb is waited
+  // for, only W(kb+1) was issued after A(kb), and W(kb) before it: vmcnt <= 2*RT. Every
+  // stage, live or not, issues the same loads and passes the same barrier (a branch around
+  // loads would make the compiler drain every load); only the MFMAs of stages past the
+  // end are skipped.
+  issue_a(ring, op, lt, phys(0), true);
+  wait_ready(ready);
+  issue_shared(MEGAMOE_XTILE(0, w), xrow, phys(0), st[0], op);
+  issue_a(ring + kSlot, op, lt, phys(min(1, nkb - 1)), 1 < nkb);
+  for (int kb0 = 0; kb0 < nkb; kb0 += 2 * D) {
+#pragma unroll
+    for (int s = 0; s < 2 * D; ++s) {  // 2*D: slot indices of both rings are compile-time
+      const int kb = kb0 + s;
+      wait_vmem<2 * RT>();
+      __builtin_amdgcn_s_barrier();
+      issue_shared(MEGAMOE_XTILE((s + 1) & 1, w), xrow, phys(min(kb + 1, nkb - 1)), st[(s + 1) & 1], op);
+      i32x8 at[RT];
+      read_slot<RT>(at, ring_lds + (s % D) * kSlot + lt.rd0, ring_lds + (s % D) * kSlot + lt.rd1);
+      i32x8 bt[NCT];
+#pragma unroll
+      for (int c = 0; c < NCT; ++c) {
+        i32x4 lo, hi;
+        asm volatile("ds_read_b128 %0, %2\n\tds_read_b128 %1, %3"
+                     : "=&v"(lo), "=&v"(hi)
+                     : "v"(MEGAMOE_XTILE(s & 1, c) + lt.rd0), "v"(MEGAMOE_XTILE(s & 1, c) + lt.rd1)
+                     : "memory");
+        bt[c] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(bt[0]), "+v"(bt[1]), "+v"(bt[2]), "+v"(bt[3]));
+      issue_a(ring + ((s + 2) % D) * kSlot, op, lt, phys(min(kb + 2, nkb - 1)), kb + 2 < nkb);
+      float sw = st[s & 1].sw, sx[NCT];
+      asm volatile("" : "+v"(sw));
+#pragma unroll
+      for (int c = 0; c < NCT; ++c) {
+        sx[c] = st[s & 1].sx[c];
+        asm volatile("" : "+v"(sx[c]));
+      }
+      if (kb < nkb) {
+        const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < NCT; ++c) {
+          const float k = sw * sx[c];
+#pragma unroll
+          for (int r = 0; r < RT; ++r) {
+            const f32x4 pr = mfma_e4m3(at[r], bt[c], zero);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) acc[r][c][v] = __builtin_fmaf(pr[v], k, acc[r][c][v]);
+          }
+        }
+      }
+    }
+  }
+  // The last stage requested one more activation tile into another wave's ring: every wave
+  // waits for its loads and the workgroup passes a barrier before any ring is reused.
+  wait_vmem<0>();
+  __builtin_amdgcn_s_barrier();
+#undef MEGAMOE_XTILE
+}
+
 // Rows of one chunk: rows r = 0 .. n-1 map to grouped buffer row row0 + r and to token
 // perm[row0 + r] / K (routed) or row0 + r (shared expert, perm == NULL).
 struct ChunkRows {
@@ -1573,7 +1684,19 @@ __device__ void down_unit(const DownArgs& a, const uint8_t* wd, const float* sd,
     op.sx[c] = hs + (size_t)(cr.row0 + r) * scale_ld(nkb) + kb0;
   }
   f32x4 acc[2][NCT];
-  stream_gemm<2, NCT, 1, NCT == 4 ? 3 : 4>(op, nkbp, rot, ring, acc, ready);
+  if constexpr (NCT == 4) {
+    // DMA sources of this wave's column tile: lane l moves chunk (l % 8) ^ (l / 8) of row
+    // 8i + l / 8 (clamped to the chunk's rows), as the weight tiles.
+    const int lr = lane >> 3;
+    const uint8_t* xrow[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      xrow[i] = hq + (size_t)(cr.row0 + min(16 * w + 8 * i + lr, cr.n - 1)) * ldk + (size_t)kb0 * kBlock +
+                (((lane & 7) ^ lr) << 4);
+    stream_gemm_shared(op, xrow, nkbp, rot, ring, acc, ready);
+  } else {
+    stream_gemm<2, NCT, 1, 4>(op, nkbp, rot, ring, acc, ready);
+  }
 #pragma unroll
   for (int c = 0; c < NCT; ++c) {
     const int r = 16 * c + (lane & 15);
