@@ -1,6 +1,6 @@
 """Benchmark of the FP8 MoE decode layer on one MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--case ID | --all] [--no-cpu-baseline]
+    python bench.py [--steps K] [--warmup W] [--case ID | --all] [--no-cpu-baseline] [--cpu-budget S]
 
 A step is one call of the layer (router, routing, permute, gate/up + SwiGLU,
 down, combine) on one batch of synthetic inputs already resident in HBM. W
@@ -12,10 +12,11 @@ Infinity Cache cannot hold a step's weights.
 Printed: one JSON line (rank 0) with the headline metric of the DeepSeek-V3
 shape (or --case), the roofline of the dominant kernel (k_experts<false|true>:
 gate/up + SwiGLU + down; k_experts_mx for the MXFP4 forms) and the CPU oracle timed on a
-bounded sample. --all measures every other config and form (the block forms, the
-MXFP4 layer, rank 0's EP share, the epilogue variants), each in a child process,
-prints each child's line to stderr and summarizes them under "configs". For an EP
-case a step is rank 0's dispatch, local experts and combine (bench_ep_share).
+bounded sample. Without --case, the line's "configs" also holds the other four
+BASELINE.json configs, each measured the same way (time, p50/p95, TB/s, roofline, its
+own CPU baseline) in a child process; --all adds the other forms (the block forms, the
+MXFP4 layer, rank 0's EP share, the epilogue variants). For an EP case a step is rank 0's
+dispatch, local experts and combine (bench_ep_share).
 
 The kernel's duration comes from a second loop of K steps in which the library
 records HIP events at its stage boundaries on the stream its kernels run on
@@ -116,6 +117,17 @@ def copy_probe(mib: int) -> None:
     _log(f"[bench] copy probe: 3 x {mib} MiB read + {mib} MiB written")
 
 
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo), or the machine type where it is not listed."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
 def cpu_threads() -> int:
     n = len(os.sched_getaffinity(0))
     env = os.environ.get("OMP_NUM_THREADS", "")
@@ -151,10 +163,11 @@ def cpu_baseline(case, values_gpu, hit: int, budget_s: float) -> dict:
     s = case.shared_experts
     scale = (hit + s) / max(sampled + s, 1)
     return {"value": dt * scale * 1e6, "unit": "us/step", "cores": threads, "kind": "port",
+            "cpu_model": cpu_model(),
             "sample": (f"oracle.{reference.__module__.split('.')[-1]}.{reference.__name__} on tokens 0..{sample - 1} of the timed inputs "
                        f"({sampled} distinct experts{' + shared' if s else ''}, {dt:.2f} s), scaled by "
                        f"{hit + s}/{sampled + s} experts; torch {torch.__version__} CPU, {threads} threads, "
-                       f"{platform.processor() or platform.machine()}")}
+                       f"{cpu_model()}")}
 
 
 def bench_case(case, steps: int, warmup: int, want_cpu: bool, cpu_budget: float) -> dict:
@@ -170,7 +183,8 @@ def bench_case(case, steps: int, warmup: int, want_cpu: bool, cpu_budget: float)
     per_set = C.algorithmic_bytes(case, round(C.expected_hit_experts(case)))
     n_sets = max(1, min(8, math.ceil(ROTATE_BYTES / per_set)))
     _log(f"[bench] {case.id}: generating {n_sets} input set(s) on the GPU")
-    sets = [workloads.make_inputs(case, 7301 + i, dev) for i in range(n_sets)]
+    sets = [workloads.make_inputs(case, 7301 + i, dev, log=lambda m, i=i: _log(f"[bench] {case.id} set {i}: {m}"))
+            for i in range(n_sets)]
     torch.cuda.synchronize()
     _log(f"[bench] {case.id}: inputs ready; warmup")
 
@@ -275,10 +289,10 @@ def cpu_baseline_ep(case, experts_cpu: dict, received: dict, hit: int, budget_s:
             break
         n *= 2
     return {"value": dt * hit / max(sampled, 1) * 1e6, "unit": "us/step", "cores": threads, "kind": "port",
+            "cpu_model": cpu_model(),
             "sample": (f"oracle.ep.experts on the received rows of local experts 0..{n - 1} ({sampled} hit, "
                        f"{sel.numel()} rows, {dt:.2f} s), scaled by {hit}/{sampled} experts; dispatch and combine "
-                       f"not included; torch {torch.__version__} CPU, {threads} threads, "
-                       f"{platform.processor() or platform.machine()}")}
+                       f"not included; torch {torch.__version__} CPU, {threads} threads, {cpu_model()}")}
 
 
 def bench_ep_share(case, steps: int, warmup: int, want_cpu: bool, cpu_budget: float) -> dict:
@@ -399,18 +413,26 @@ def bench_ep_share(case, steps: int, warmup: int, want_cpu: bool, cpu_budget: fl
     return result
 
 
+def _config_entry(r: dict) -> dict:
+    """One config's record under "configs": time, bandwidth, roofline and CPU baseline."""
+    keep = ("us_per_step", "p50_us", "p95_us", "tb_per_s", "hbm_frac", "mfma_frac", "hit_experts", "bytes_per_step",
+            "stage_us", "rotation_sets", "roofline", "cpu_baseline", "dtype", "received_rows", "sent_rows")
+    return {k: r[k] for k in keep if k in r}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--case", default=None)
+    ap.add_argument("--case", default=None, help="measure this case only (its line alone)")
     ap.add_argument("--all", action="store_true",
-                    help="also measure the other configs and forms (block, MXFP4, EP share, epilogue variants)")
+                    help="also measure the other forms (block, MXFP4, EP share, epilogue variants)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU oracle work")
+    ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU oracle work per config")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="run a plain copy of this many MiB first (counter calibration)")
+    ap.add_argument("--child", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported by this build "
@@ -428,23 +450,35 @@ def main() -> int:
     if args.copy_probe_mib > 0:
         copy_probe(args.copy_probe_mib)
     head = C.case(args.case or C.HEADLINE)
-    every = C.CASES + C.BLOCK_CASES + C.MX_CASES + C.EP_CASES + C.VARIANT_CASES
-    others = [c for c in every if c.id != head.id] if args.all else []
+    if args.case:
+        others = []
+    else:
+        # The five BASELINE.json configs always; the other forms with --all.
+        others = [c for c in C.CASES if c.id != head.id]
+        if args.all:
+            others += C.BLOCK_CASES + C.MX_CASES + C.EP_CASES + C.VARIANT_CASES
     run = bench_ep_share if head.ep > 1 else bench_case
     r = run(head, args.steps, args.warmup, not args.no_cpu_baseline, args.cpu_budget)
     # Each other config runs in a child process of its own, on a fresh device heap: after a
     # config's inputs (up to 17 GB) are allocated and freed in this process, the next
     # config's weights land in fragmented memory and its expert kernel measures a few
     # percent slower.
-    results = {}
+    results = {head.id: r}
     for c in others:
-        child = subprocess.run([sys.executable, __file__, "--case", c.id, "--steps", str(args.steps), "--warmup",
-                                str(args.warmup), "--no-cpu-baseline"], stdout=subprocess.PIPE, text=True)
+        cmd = [sys.executable, __file__, "--case", c.id, "--steps", str(args.steps), "--warmup", str(args.warmup),
+               "--cpu-budget", str(args.cpu_budget), "--child"]
+        if args.no_cpu_baseline:
+            cmd.append("--no-cpu-baseline")
+        child = subprocess.run(cmd, stdout=subprocess.PIPE, text=True)
         if child.returncode != 0:
             print(f"bench.py: the {c.id} run failed (exit {child.returncode})", file=sys.stderr)
             return child.returncode
-        results[c.id] = json.loads(child.stdout.strip().splitlines()[-1])
-        _log(json.dumps(results[c.id]))
+        results[c.id] = json.loads(child.stdout.strip().splitlines()[-1])["result"]
+        _log(f"[bench] {c.id}: {results[c.id]['us_per_step']:.1f} us/step, "
+             f"{100 * results[c.id]['hbm_frac']:.1f}% of HBM peak")
+    if args.child:
+        print(json.dumps({"result": r}), flush=True)
+        return 0
     line = {
         "metric": (METRIC if head.id == C.HEADLINE else
                    f"MoE decode layer \u00b5s/step + achieved HBM TB/s (% of peak), {head.id}, 1 GPU"),
@@ -461,11 +495,7 @@ def main() -> int:
         "mfma_frac": r["mfma_frac"],
         "roofline": r["roofline"],
         "cpu_baseline": r.get("cpu_baseline"),
-        "configs": {cid: {"us_per_step": v["value"], "p50_us": v["p50_us"], "tb_per_s": v["achieved_tb_per_s"],
-                          "hbm_frac": v["hbm_frac"], "hit_experts": v["hit_experts"],
-                          "kernel": v["roofline"]["kernel"], "kernel_frac": v["roofline"]["frac"],
-                          "stage_us": v["stage_us"]}
-                    for cid, v in results.items()},
+        "configs": {cid: _config_entry(v) for cid, v in results.items()},
     }
     print(json.dumps(line), flush=True)
     return 0

@@ -72,50 +72,72 @@ def _expert(values, name: str, index=None):
 
 
 @torch.no_grad()
-def moe_layer(case, values: dict, *, widen: bool = False, tokens=None) -> dict:
-    """Outputs {'y', 'expert_ids', 'expert_weights'} for ``tokens`` (default: all)."""
-    bf = torch.float32 if widen else torch.bfloat16
-    pw = case.power_of_two
+def _layers(case, values: dict, widens, tokens=None) -> list[dict]:
+    """The layer under each schedule of ``widens`` (False: BF16, True: FP32), sharing the
+    routing (both schedules route the same fp32 scores of the bf16 input) and each hit
+    expert's dequantized weights."""
     x = values["x"].cpu()
     rows = list(range(x.shape[0])) if tokens is None else list(tokens)
     router = values["router"].cpu().float()
     bias = values.get("router_bias")
     bias = None if bias is None else bias.cpu()
-    act = x.to(bf)
+    pw = case.power_of_two
 
     ids, weights = [], []
     for t in rows:
-        i, w = route(case, router @ act[t].float(), bias)
+        i, w = route(case, router @ x[t].float(), bias)
         ids.append(i)
         weights.append(w)
     ids_t = torch.stack(ids) if rows else torch.empty((0, case.topk), dtype=torch.int64)
     w_t = torch.stack(weights) if rows else torch.empty((0, case.topk), dtype=torch.float32)
 
     H = x.shape[1]
-    down = {}  # (row index, slot) -> bf16 [H]
+    modes = [(torch.float32 if widen else torch.bfloat16) for widen in widens]
+    acts = [x.to(bf) for bf in modes]
+    down = [{} for _ in modes]  # per mode: (row index, slot) -> [H]
     cpu = {k: v.cpu() for k, v in values.items() if k != "x"}
+
+    def mlp(wg, wu, wd, m, t):
+        bf, act = modes[m], acts[m]
+        h = _swiglu(case, _linear(wg, act[t], pw, bf), _linear(wu, act[t], pw, bf), bf)
+        return _linear(wd, h, pw, bf)
+
     for e in sorted(set(ids_t.flatten().tolist())):
         wg, wu, wd = _expert(cpu, "gate", e), _expert(cpu, "up", e), _expert(cpu, "down", e)
         for r, t in enumerate(rows):
             for slot in (ids_t[r] == e).nonzero().flatten().tolist():
-                h = _swiglu(case, _linear(wg, act[t], pw, bf), _linear(wu, act[t], pw, bf), bf)
-                down[(r, slot)] = _linear(wd, h, pw, bf)
-    shared = {}
+                for m in range(len(modes)):
+                    down[m][(r, slot)] = mlp(wg, wu, wd, m, t)
+    shared = [{} for _ in modes]
     if case.shared_experts:
         wg, wu, wd = _expert(cpu, "shared_gate"), _expert(cpu, "shared_up"), _expert(cpu, "shared_down")
         for r, t in enumerate(rows):
-            h = _swiglu(case, _linear(wg, act[t], pw, bf), _linear(wu, act[t], pw, bf), bf)
-            shared[r] = _linear(wd, h, pw, bf)
+            for m in range(len(modes)):
+                shared[m][r] = mlp(wg, wu, wd, m, t)
 
-    y = torch.empty((len(rows), H), dtype=bf)
-    for r in range(len(rows)):
-        acc = torch.zeros(H, dtype=torch.float32)
-        for slot in range(case.topk):
-            acc = acc + down[(r, slot)].float() * w_t[r, slot]
-        if case.shared_experts:
-            acc = acc + shared[r].float()
-        y[r] = acc.to(bf)
-    return {"y": y, "expert_ids": ids_t, "expert_weights": w_t}
+    out = []
+    for m, bf in enumerate(modes):
+        y = torch.empty((len(rows), H), dtype=bf)
+        for r in range(len(rows)):
+            acc = torch.zeros(H, dtype=torch.float32)
+            for slot in range(case.topk):
+                acc = acc + down[m][(r, slot)].float() * w_t[r, slot]
+            if case.shared_experts:
+                acc = acc + shared[m][r].float()
+            y[r] = acc.to(bf)
+        out.append({"y": y, "expert_ids": ids_t.clone(), "expert_weights": w_t.clone()})
+    return out
+
+
+def moe_layer(case, values: dict, *, widen: bool = False, tokens=None) -> dict:
+    """Outputs {'y', 'expert_ids', 'expert_weights'} for ``tokens`` (default: all)."""
+    return _layers(case, values, (widen,), tokens)[0]
+
+
+def reference_and_oracle(case, values: dict, tokens=None) -> tuple[dict, dict]:
+    """``reference`` and ``oracle`` in one pass (each hit expert dequantized once)."""
+    want, exact = _layers(case, values, (False, True), tokens)
+    return want, exact
 
 
 def reference(case, values: dict, **kw) -> dict:

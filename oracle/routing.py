@@ -23,6 +23,8 @@ routers (megabench/tests/test_frontier.py:283-296 pattern).
 
 from __future__ import annotations
 
+import math
+
 import torch
 
 
@@ -57,3 +59,46 @@ def route(case, scores: torch.Tensor, bias: torch.Tensor | None):
         return route_sigmoid(scores, bias, case.topk, case.groups, case.top_groups, case.routed_scaling,
                              case.renormalize)
     return route_softmax(scores, case.topk, case.renormalize, case.routed_scaling)
+
+
+def selection_margins(case, scores: torch.Tensor, bias: torch.Tensor | None) -> dict:
+    """How far one token's selection is from a tie, on fp64 arithmetic of its fp32 scores.
+
+    The ids (in selection order) are fixed by the order of the top K + 1 candidates, and for
+    group-limited routing also by which TG groups are kept. ``expert`` is the smallest gap
+    between consecutive candidates among the top K + 1 choice values of the kept groups;
+    ``group`` the gap between the TG-th and the (TG+1)-th group score (inf without group
+    limiting); ``relative`` the smaller of the two, each divided by the larger magnitude of
+    its pair. A gap of 0 is a tie, decided by the lower index (the stable order). A token
+    whose relative margin is below the logits' rounding error (~1e-6 for an fp32 GEMV of
+    H ~ 7e3) may route differently under fp32 and exact logits; the reference's integer rule
+    (correctness.py:503-521) accepts either there."""
+    s = scores.double()
+    if case.router == "sigmoid":
+        prob = torch.sigmoid(s)
+        choice = prob if bias is None else prob + bias.double()
+    else:
+        choice = s
+    group_gap, group_rel = math.inf, math.inf
+    if case.router == "sigmoid" and case.groups > 1:
+        per_group = choice.view(case.groups, -1)
+        top2 = per_group.sort(dim=-1, descending=True, stable=True).values[:, :2]
+        gscore = top2.sum(-1) if per_group.shape[1] >= 2 else top2[:, 0]
+        gs = gscore.sort(descending=True, stable=True)
+        if case.top_groups < case.groups:
+            a, b = float(gs.values[case.top_groups - 1]), float(gs.values[case.top_groups])
+            group_gap = a - b
+            group_rel = group_gap / max(abs(a), abs(b), 1e-300)
+        mask = torch.ones(case.groups, dtype=torch.bool)
+        mask[gs.indices[:case.top_groups]] = False
+        choice = per_group.masked_fill(mask[:, None], -math.inf).flatten()
+    top = choice.sort(descending=True, stable=True).values[:case.topk + 1]
+    finite = top[torch.isfinite(top)]
+    expert_gap, expert_rel = math.inf, math.inf
+    for i in range(len(finite) - 1):
+        a, b = float(finite[i]), float(finite[i + 1])
+        gap = a - b
+        rel = gap / max(abs(a), abs(b), 1e-300)
+        if rel < expert_rel:
+            expert_gap, expert_rel = gap, rel
+    return {"expert": expert_gap, "group": group_gap, "relative": min(expert_rel, group_rel)}

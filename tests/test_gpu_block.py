@@ -97,10 +97,10 @@ def test_block_does_not_mutate_inputs_and_is_deterministic():
 
 
 @pytest.mark.parametrize("cid", [c.id for c in C.BLOCK_CASES])
-def test_full_size_block_on_sampled_tokens(cid):
+def test_full_size_block_on_every_token(cid):
     """Full geometry, inputs generated on the GPU: ids of every token (routing of the
     normalized rows, fp32 GEMV as frontier.py:343, and the correctly rounded logits), y of
-    three sampled tokens against the block oracle."""
+    every token against the block oracle."""
     case = C.case(cid)
     _log(f"full size block {cid}")
     values = workloads.make_inputs(case, 104729, DEV)
@@ -118,7 +118,6 @@ def test_full_size_block_on_sampled_tokens(cid):
         ei, ew = routing.route(case, exact_logits[t], cpu.get("router_bias"))
         assert torch.equal(ei, wi), f"token {t}: a top-k margin below the logits' rounding error"
         torch.testing.assert_close(got["expert_weights"][t].cpu(), ew, rtol=W_RTOL, atol=0)
-    rows = [0, case.tokens // 2, case.tokens - 1]
-    want, exact = layer.block_reference(case, cpu, tokens=rows), layer.block_oracle(case, cpu, tokens=rows)
-    check, band = _compare(case, got, want, exact, rows=rows)
+    want, exact = layer.block_reference(case, cpu), layer.block_oracle(case, cpu)
+    check, band = _compare(case, got, want, exact)
     _log(f"  {cid}: {check} band_rel={band['relative_error']:.3e}")

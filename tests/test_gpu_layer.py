@@ -47,13 +47,20 @@ def _to(values, device):
     return {k: v.to(device) for k, v in values.items()}
 
 
-def _compare(case, got, want, exact, rows=None):
+def _compare(case, got, want, exact, rows=None, strict_ids=True):
+    """ids (equal to the reference's, or with strict_ids=False under the reference's integer
+    rule only, the caller having checked them token by token), weights, and y under the
+    layer's bars and the band rule."""
     ids = got["expert_ids"].cpu()
     w = got["expert_weights"].cpu()
     y = got["y"].cpu()
     if rows is not None:
         ids, w, y = ids[rows], w[rows], y[rows]
-    assert torch.equal(ids, want["expert_ids"]), f"{case.id}: expert ids differ"
+    if strict_ids:
+        assert torch.equal(ids, want["expert_ids"]), f"{case.id}: expert ids differ"
+    # The reference's integer rule (correctness.py:503-521) is weaker than equality with the
+    # reference; it holds whenever the equality does, and is checked as the harness would.
+    assert metrics.integers_match(ids, want["expert_ids"], exact["expert_ids"])["pass"]
     torch.testing.assert_close(w, want["expert_weights"], rtol=LOGIT_RTOL, atol=0)
     check = metrics.layer_checks(y, want["y"])
     assert check["pass"], f"{case.id}: {check}"
@@ -137,10 +144,10 @@ def test_route_from_logits_matches_oracle_including_ties(cid):
 
 
 @pytest.mark.parametrize("cid", [c.id for c in C.CASES if c.id != "moe-fp8-tiny-t4"])
-def test_full_size_layer_on_sampled_tokens(cid):
-    """BASELINE.json geometry, inputs generated on the GPU; ids of every token and y of
-    three sampled tokens (each token's output depends only on its own row) against the
-    oracle."""
+def test_full_size_layer_on_every_token(cid):
+    """BASELINE.json geometry, inputs generated on the GPU; ids, weights and y of every token
+    against the oracle (every output element, as correctness.py:469-536 checks them), and
+    each token's top-k margin reported."""
     case = C.case(cid)
     _log(f"full size {cid}")
     values = workloads.make_inputs(case, 104729, DEV)
@@ -149,22 +156,36 @@ def test_full_size_layer_on_sampled_tokens(cid):
     cpu = {k: v.cpu() for k, v in values.items()}
     del values
     torch.cuda.empty_cache()
-    # Routing of every token. The ids must equal the reference's (logits from an fp32
-    # GEMV, as frontier.py:343 computes them). The weights are checked two ways: at
-    # W_RTOL against the oracle's routing of the correctly rounded logits the kernel
-    # uses (fp64 accumulation), and at LOGIT_RTOL against the fp32-GEMV reference, whose
-    # logits carry up to ~1e-5 absolute rounding error at H = 7168 that a sigmoid or
-    # softmax passes on to the weights.
+    # Routing of every token. The kernel's logits are correctly rounded (fp64 accumulation),
+    # so its ids must equal the routing of the exact logits, and its weights that routing's
+    # within W_RTOL. The reference's logits come from an fp32 GEMV (frontier.py:343), whose
+    # rounding (up to ~1e-5 absolute at H = 7168) moves the weights within LOGIT_RTOL and can
+    # reorder ids only where the token's selection margin is below it: there the reference's
+    # integer rule (each id equal to the reference's or the oracle's) applies, elsewhere the
+    # ids must equal the reference's too.
     x = cpu["x"].float()
+    bias = cpu.get("router_bias")
     exact_logits = (cpu["router"].double() @ x.double().T).T.float()
+    margins = []
+    near_ties = 0
     for t in range(case.tokens):
-        wi, ww = routing.route(case, cpu["router"] @ x[t], cpu.get("router_bias"))
-        assert torch.equal(got["expert_ids"][t].cpu(), wi), f"token {t}"
-        torch.testing.assert_close(got["expert_weights"][t].cpu(), ww, rtol=LOGIT_RTOL, atol=0)
-        ei, ew = routing.route(case, exact_logits[t], cpu.get("router_bias"))
-        assert torch.equal(ei, wi), f"token {t}: a top-k margin below the logits' rounding error"
+        mine = got["expert_ids"][t].cpu()
+        wi, ww = routing.route(case, cpu["router"] @ x[t], bias)
+        ei, ew = routing.route(case, exact_logits[t], bias)
+        m = routing.selection_margins(case, exact_logits[t], bias)
+        margins.append(m["relative"])
+        assert torch.equal(mine, ei), f"token {t}: ids differ from the exact-logit routing"
         torch.testing.assert_close(got["expert_weights"][t].cpu(), ew, rtol=W_RTOL, atol=0)
-    rows = [0, case.tokens // 2, case.tokens - 1]
-    want, exact = layer.reference(case, cpu, tokens=rows), layer.oracle(case, cpu, tokens=rows)
-    check, band = _compare(case, got, want, exact, rows=rows)
-    _log(f"  {cid}: {check} band_rel={band['relative_error']:.3e} ref_rel={band['reference_relative_error']:.3e}")
+        torch.testing.assert_close(got["expert_weights"][t].cpu(), ww, rtol=LOGIT_RTOL, atol=0)
+        if m["relative"] < 1e-6:
+            near_ties += 1
+            assert metrics.integers_match(mine, wi, ei)["pass"], f"token {t}"
+        else:
+            assert torch.equal(mine, wi), f"token {t}: ids differ from the fp32-GEMV routing"
+    srt = sorted(margins)
+    _log(f"  {cid}: top-k margin (relative) min {srt[0]:.3e} p10 {srt[len(srt) // 10]:.3e} "
+         f"median {srt[len(srt) // 2]:.3e}; tokens below 1e-6: {near_ties}")
+    want, exact = layer.reference_and_oracle(case, cpu)
+    check, band = _compare(case, got, want, exact, strict_ids=False)
+    _log(f"  {cid}: all {case.tokens} tokens {check} band_rel={band['relative_error']:.3e} "
+         f"ref_rel={band['reference_relative_error']:.3e}")

@@ -90,7 +90,7 @@ def test_mx_invalid_ids_give_nan(bad):
     assert torch.isfinite(y2.float()).all()
 
 
-def test_mx_full_size_on_sampled_tokens():
+def test_mx_full_size_on_every_token():
     case = C.case(MXCASE)
     _log(f"mx full size {case.id}")
     values = workloads.make_inputs(case, 104729, DEV)
@@ -99,10 +99,9 @@ def test_mx_full_size_on_sampled_tokens():
     cpu = {k: v.cpu() for k, v in values.items()}
     del values
     torch.cuda.empty_cache()
-    rows = [0, case.tokens // 2, case.tokens - 1]
-    want = mx.reference(case, cpu, tokens=rows)["y"]
-    exact = mx.oracle(case, cpu, tokens=rows)["y"]
-    check, band = _check(case, got.cpu()[rows], want, exact)
+    want = mx.reference(case, cpu)["y"]
+    exact = mx.oracle(case, cpu)["y"]
+    check, band = _check(case, got.cpu(), want, exact)
     _log(f"  {case.id}: {check} band_rel={band['relative_error']:.3e}")
 
 

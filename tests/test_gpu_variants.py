@@ -66,7 +66,7 @@ def test_glm_layer_matches_oracle_on_development_geometry(case):
         _compare(case, got, want, exact)
 
 
-def test_glm_full_size_on_sampled_tokens():
+def test_glm_full_size_on_every_token():
     case = GLM
     _log(f"glm full size {case.id}")
     values = workloads.make_inputs(case, 104729, DEV)
@@ -75,9 +75,8 @@ def test_glm_full_size_on_sampled_tokens():
     cpu = {k: v.cpu() for k, v in values.items()}
     del values
     torch.cuda.empty_cache()
-    rows = [0, case.tokens // 2, case.tokens - 1]
-    want, exact = layer.reference(case, cpu, tokens=rows), layer.oracle(case, cpu, tokens=rows)
-    _log(f"  {_compare(case, got, want, exact, rows)}")
+    want, exact = layer.reference_and_oracle(case, cpu)
+    _log(f"  {_compare(case, got, want, exact)}")
 
 
 def test_default_epilogue_equals_plain_forward():

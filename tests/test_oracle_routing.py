@@ -180,3 +180,57 @@ def test_routing_invariants():
         ids, w = routing.route_softmax(s, 8, renormalize=True)
         assert bool((w[:-1] >= w[1:]).all())
         torch.testing.assert_close(w.sum(), torch.tensor(1.0), rtol=1e-6, atol=0)
+
+
+class _Rule:
+    """The routing fields of a case, for selection_margins."""
+
+    def __init__(self, router, topk, groups=1, top_groups=1):
+        self.router, self.topk, self.groups, self.top_groups = router, topk, groups, top_groups
+
+
+def test_selection_margins_closed_forms():
+    # softmax: top K+1 = 3, 2, 1; gaps 1 and 1, relative 1/3 and 1/2.
+    m = routing.selection_margins(_Rule("softmax", 2), torch.tensor([3.0, 1.0, 2.0, 0.0]), None)
+    assert m["expert"] == 1.0 and m["group"] == float("inf") and m["relative"] == pytest.approx(1 / 3)
+    # an exact tie inside the top K + 1 has margin 0
+    m = routing.selection_margins(_Rule("softmax", 2), torch.tensor([0.5, 2.0, 0.5, -1.0]), None)
+    assert m["expert"] == 0.0 and m["relative"] == 0.0
+    # a tie below the (K+1)-th candidate does not matter
+    m = routing.selection_margins(_Rule("softmax", 1), torch.tensor([4.0, 2.0, 1.0, 1.0]), None)
+    assert m["expert"] == 2.0
+    # sigmoid, 2 groups of 2, keep 1: group scores p0+p1 vs p2+p3
+    s = torch.tensor([0.0, 0.0, 1.0, -1.0])
+    p = torch.sigmoid(s.double())
+    m = routing.selection_margins(_Rule("sigmoid", 1, 2, 1), s, None)
+    assert m["group"] == pytest.approx(float(p[0] + p[1] - p[2] - p[3]))
+    assert m["expert"] == 0.0  # the kept group holds a tie (experts 0 and 1)
+
+
+@pytest.mark.parametrize("rule", [_Rule("softmax", 8), _Rule("sigmoid", 8, 8, 4), _Rule("sigmoid", 8)])
+def test_selection_margins_bound_the_perturbations_that_keep_the_ids(rule):
+    # Any change of the scores smaller than a quarter of the smallest absolute gap keeps the
+    # ids and their order (sigmoid moves a choice by at most a quarter of the score change,
+    # a group score by at most half); moving the (K+1)-th candidate past the K-th changes them.
+    g = torch.Generator().manual_seed(17)
+    E = 64
+    for _ in range(20):
+        s = torch.randn(E, generator=g)
+        bias = torch.randn(E, generator=g) * 0.1 if rule.router == "sigmoid" else None
+        m = routing.selection_margins(rule, s, bias)
+        gap = min(m["expert"], m["group"])
+        case = type("C", (), {"router": rule.router, "topk": rule.topk, "groups": rule.groups,
+                              "top_groups": rule.top_groups, "routed_scaling": 1.0, "renormalize": True})
+        ids, _ = routing.route(case, s, bias)
+        for _ in range(5):
+            noise = (torch.rand(E, generator=g, dtype=torch.float64) * 2 - 1) * gap / 4 * 0.999
+            ids2, _ = routing.route(case, (s.double() + noise).float(), bias)
+            if gap > 1e-5:  # well above fp32 rounding of the perturbed scores
+                assert torch.equal(ids2, ids)
+    if rule.router == "softmax":
+        s = torch.arange(E, dtype=torch.float32)
+        ids, _ = routing.route(case, s, None)
+        t = s.clone()
+        t[E - rule.topk - 1] += 1.5  # the (K+1)-th passes the K-th: gap 1
+        assert routing.selection_margins(rule, s, None)["expert"] == 1.0
+        assert not torch.equal(routing.route(case, t, None)[0], ids)

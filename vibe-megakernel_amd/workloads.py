@@ -41,26 +41,48 @@ def _normal(seed: int, name: str, shape, std: float, device) -> torch.Tensor:
 
 
 def quantize_weight(w: torch.Tensor, power_of_two: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
-    """E4M3 payload [R, C] and fp32 scales [ceil(R/128), ceil(C/128)] of an fp32 matrix."""
-    rows, cols = w.shape
+    """E4M3 payload [..., R, C] and fp32 scales [..., ceil(R/128), ceil(C/128)] of fp32
+    matrices [..., R, C] (any leading batch dimensions, e.g. a batch of experts)."""
+    rows, cols = w.shape[-2:]
+    lead = w.shape[:-2]
     pr, pc = (-rows) % BLOCK, (-cols) % BLOCK
-    padded = torch.nn.functional.pad(w.float(), (0, pc, 0, pr))
-    blocks = padded.view(padded.shape[0] // BLOCK, BLOCK, padded.shape[1] // BLOCK, BLOCK)
-    amax = blocks.abs().amax(dim=(1, 3))
+    padded = torch.nn.functional.pad(w.float(), (0, pc, 0, pr)) if pr or pc else w.float()
+    br, bc = padded.shape[-2] // BLOCK, padded.shape[-1] // BLOCK
+    blocks = padded.view(*lead, br, BLOCK, bc, BLOCK)
+    amax = blocks.abs().amax(dim=(-3, -1))
     scale = amax.clamp_min(1e-4) / 448.0
     if power_of_two:
         scale = torch.exp2(torch.ceil(torch.log2(scale)))
-    q = (blocks / scale[:, None, :, None]).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
-    return q.view(padded.shape)[:rows, :cols].contiguous(), scale
+    q = (blocks / scale[..., :, None, :, None]).clamp_(-448.0, 448.0).to(torch.float8_e4m3fn)
+    q = q.view(padded.shape)
+    if pr or pc:
+        q = q[..., :rows, :cols].contiguous()
+    return q, scale
 
 
-def _expert_stack(seed, name, experts, rows, cols, std, device, power_of_two):
+# Expert stacks are generated in batches of at most this many fp32 bytes (one randn and one
+# batched quantization per batch, a few dozen kernels per stack instead of ~20 per expert).
+STACK_BATCH_BYTES = 2 << 30
+
+
+def _expert_stack(seed, name, experts, rows, cols, std, device, power_of_two, log=None):
+    """E4M3 stack [experts, rows, cols] and its scales. One generator per stack, seeded from
+    (seed, name), draws the experts in order, in batches whose size depends on the matrix
+    shape only, so a (seed, case) pair always yields the same stack."""
     payload = torch.empty((experts, rows, cols), dtype=torch.float8_e4m3fn, device=device)
     scales = torch.empty((experts, -(-rows // BLOCK), -(-cols // BLOCK)), dtype=torch.float32, device=device)
-    for e in range(experts):
-        q, s = quantize_weight(_normal(seed, f"{name}:{e}", (rows, cols), std, device), power_of_two)
-        payload[e].copy_(q)
-        scales[e].copy_(s)
+    gen = torch.Generator(device=device).manual_seed(seed_for(seed, name))
+    per = max(1, min(experts, STACK_BATCH_BYTES // (4 * rows * cols)))
+    for e0 in range(0, experts, per):
+        n = min(per, experts - e0)
+        w = torch.randn((n, rows, cols), generator=gen, device=device, dtype=torch.float32).mul_(std)
+        q, s = quantize_weight(w, power_of_two)
+        del w
+        payload[e0:e0 + n].copy_(q)
+        scales[e0:e0 + n].copy_(s)
+        del q, s
+    if log:
+        log(f"{name}: {experts} x [{rows}, {cols}] E4M3 in {-(-experts // per)} batch(es)")
     return payload, scales
 
 
@@ -170,7 +192,9 @@ def make_ep_inputs(case: Case, seed: int, device="cpu", rank: int = 0) -> dict[s
     return values
 
 
-def make_inputs(case: Case, seed: int, device="cpu") -> dict[str, torch.Tensor]:
+def make_inputs(case: Case, seed: int, device="cpu", log=None) -> dict[str, torch.Tensor]:
+    """Inputs of ``case``; ``log`` (a callable taking a line of text, or None) hears one line
+    per weight stack as it is made."""
     if case.format == "mxfp4":
         return make_mx_inputs(case, seed, device)
     T, H, E, I, S = case.tokens, case.hidden, case.experts, case.intermediate, case.shared_experts
@@ -184,11 +208,13 @@ def make_inputs(case: Case, seed: int, device="cpu") -> dict[str, torch.Tensor]:
     if bias is not None:
         values["router_bias"] = bias
     for name, rows, cols in (("gate", I, H), ("up", I, H), ("down", H, I)):
-        values[name], values[name + "_scale"] = _expert_stack(seed, name, E, rows, cols, std, device, pw)
+        values[name], values[name + "_scale"] = _expert_stack(seed, name, E, rows, cols, std, device, pw, log)
     if S:
         for name, rows, cols in (("shared_gate", S * I, H), ("shared_up", S * I, H), ("shared_down", H, S * I)):
             values[name], values[name + "_scale"] = quantize_weight(
                 _normal(seed, name, (rows, cols), std, device), pw)
+            if log:
+                log(f"{name}: [{rows}, {cols}] E4M3")
     return values
 
 
