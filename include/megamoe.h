@@ -42,8 +42,14 @@ enum megamoe_status {
   MEGAMOE_ERR_SHAPE = 2,            /* geometry the layer does not define (H or I not a multiple of 128, K > E, ...) */
   MEGAMOE_ERR_WORKSPACE = 3,        /* workspace smaller than megamoe_workspace_bytes() */
   MEGAMOE_ERR_HIP = 4,              /* a HIP runtime call or kernel launch failed */
-  MEGAMOE_ERR_UNSUPPORTED = 5       /* within the layer's definition but beyond this build's limits */
+  MEGAMOE_ERR_UNSUPPORTED = 5,      /* within the layer's definition but beyond this build's limits */
+  MEGAMOE_ERR_SCRATCH = 6           /* megamoe_forward_noalloc: the call needs more workspace than
+                                       MEGAMOE_SCRATCH_BYTES */
 };
+
+/* Size of the fixed device scratch of megamoe_forward_noalloc (32 MiB per GPU, held from the
+ * library's first use on that GPU until the process ends). */
+#define MEGAMOE_SCRATCH_BYTES (32u << 20)
 
 enum megamoe_gate {
   MEGAMOE_GATE_SOFTMAX = 0, /* ids = top-k logits (stable); w = softmax over the selected logits (renormalize=1)
@@ -115,6 +121,17 @@ int megamoe_workspace_bytes(const megamoe_desc* desc, size_t* bytes);
  * Replaces the MoE block of megabench/tasks/frontier.py:335-354 (sigmoid
  * configs) and megabench/tasks/references/moe.py:66-78 (softmax configs). */
 int megamoe_forward(const megamoe_desc* desc, const megamoe_tensors* t, void* stream);
+
+/* megamoe_forward with no workspace argument and no allocation: the workspace is the
+ * library's fixed device scratch (MEGAMOE_SCRATCH_BYTES per GPU, a file-scope device array),
+ * so the call allocates nothing, in the library or in any routine it calls. For callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc). No reference counterpart. t->workspace and t->workspace_bytes are
+ * ignored. Returns MEGAMOE_ERR_SCRATCH, launching nothing, when megamoe_workspace_bytes(desc)
+ * exceeds MEGAMOE_SCRATCH_BYTES (each of the five benchmark configs fits: Kimi-K2 at 128 tokens needs
+ * 27 MiB). All calls on one GPU share its scratch: calls that overlap on that GPU (on two
+ * streams, or from two threads) race and must be ordered by the caller. */
+int megamoe_forward_noalloc(const megamoe_desc* desc, const megamoe_tensors* t, void* stream);
 
 /* megamoe_forward with a device event between its stages; blocks until the
  * call has finished and writes the elapsed ms of each stage to stage_ms[0..4]
@@ -299,10 +316,10 @@ int megamoe_quantize_rows(int32_t rows, int32_t cols, const void* x, uint8_t* q,
 /* Text for a status code (static storage). */
 const char* megamoe_status_string(int status);
 
-/* ABI version of this library: 5 (1, plus megamoe_block_forward and megamoe_rms_norm in 2,
+/* ABI version of this library: 6 (1, plus megamoe_block_forward and megamoe_rms_norm in 2,
  * plus megamoe_mx_workspace_bytes and megamoe_mx_forward in 3, plus megamoe_ep_dispatch,
  * megamoe_ep_experts and megamoe_ep_combine in 4, plus megamoe_forward_ex and
- * megamoe_combine_by_expert_id in 5). */
+ * megamoe_combine_by_expert_id in 5, plus megamoe_forward_noalloc in 6). */
 int megamoe_abi_version(void);
 
 #ifdef __cplusplus

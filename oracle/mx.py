@@ -122,35 +122,51 @@ def swiglu_clamped(l1: torch.Tensor, weights: torch.Tensor, limit: float) -> tor
 
 
 @torch.no_grad()
-def layer(case, values: dict, *, widen: bool = False, tokens=None) -> dict:
-    """Outputs {'y'} of the serial layer for ``tokens`` (default all)."""
-    bf = torch.float32 if widen else torch.bfloat16
+def _layers(case, values: dict, widens, tokens=None) -> list[dict]:
+    """The serial layer under each schedule of ``widens``, each expert's weights unpacked once."""
     limit = case.swiglu_limit
     ids = values["topk_idx"].cpu()
     wts = values["topk_weights"].cpu()
     rows = list(range(ids.shape[0])) if tokens is None else list(tokens)
-    x = unpack_activation_e8m0(values["x"].cpu(), values["x_scales"].cpu()).to(bf)
-    H = x.shape[1]
-    d = {}
+    modes = [(torch.float32 if widen else torch.bfloat16) for widen in widens]
+    x32 = unpack_activation_e8m0(values["x"].cpu(), values["x_scales"].cpu())
+    H = x32.shape[1]
+    d = [{} for _ in modes]
     for e in sorted(set(ids[rows].flatten().tolist())):
-        w1 = unpack_mxfp4(values["l1_blocks"][e].cpu(), values["l1_scales"][e].cpu()).to(bf)
-        w2 = unpack_mxfp4(values["l2_blocks"][e].cpu(), values["l2_scales"][e].cpu()).to(bf)
+        w1_32 = unpack_mxfp4(values["l1_blocks"][e].cpu(), values["l1_scales"][e].cpu())
+        w2_32 = unpack_mxfp4(values["l2_blocks"][e].cpu(), values["l2_scales"][e].cpu())
         pairs = [(r, s) for r, t in enumerate(rows) for s in range(ids.shape[1]) if int(ids[t, s]) == e]
-        xt = torch.stack([x[rows[r]] for r, _ in pairs])
         w = torch.stack([wts[rows[r], s] for r, s in pairs])
-        l1 = (xt.float() @ w1.float().T).to(bf)
-        a = swiglu_clamped(l1, w, limit)
-        h = a if widen else unpack_activation_e8m0(*pack_activation_e8m0(a)).to(bf)
-        out = (h.float() @ w2.float().T).to(bf)
-        for i, key in enumerate(pairs):
-            d[key] = out[i]
-    y = torch.empty((len(rows), H), dtype=bf)
-    for r in range(len(rows)):
-        acc = torch.zeros(H, dtype=torch.float32)
-        for s in range(ids.shape[1]):
-            acc = acc + d[(r, s)].float()
-        y[r] = acc.to(bf)
-    return {"y": y}
+        for m, bf in enumerate(modes):
+            w1, w2 = w1_32.to(bf), w2_32.to(bf)
+            xt = torch.stack([x32[rows[r]].to(bf) for r, _ in pairs])
+            l1 = (xt.float() @ w1.float().T).to(bf)
+            a = swiglu_clamped(l1, w, limit)
+            h = a if bf == torch.float32 else unpack_activation_e8m0(*pack_activation_e8m0(a)).to(bf)
+            out = (h.float() @ w2.float().T).to(bf)
+            for i, key in enumerate(pairs):
+                d[m][key] = out[i]
+    outs = []
+    for m, bf in enumerate(modes):
+        y = torch.empty((len(rows), H), dtype=bf)
+        for r in range(len(rows)):
+            acc = torch.zeros(H, dtype=torch.float32)
+            for s in range(ids.shape[1]):
+                acc = acc + d[m][(r, s)].float()
+            y[r] = acc.to(bf)
+        outs.append({"y": y})
+    return outs
+
+
+def layer(case, values: dict, *, widen: bool = False, tokens=None) -> dict:
+    """Outputs {'y'} of the serial layer for ``tokens`` (default all)."""
+    return _layers(case, values, (widen,), tokens)[0]
+
+
+def reference_and_oracle(case, values: dict, tokens=None) -> tuple[dict, dict]:
+    """``reference`` and ``oracle`` in one pass (each expert's weights unpacked once)."""
+    want, exact = _layers(case, values, (False, True), tokens)
+    return want, exact
 
 
 def reference(case, values: dict, **kw) -> dict:

@@ -37,9 +37,9 @@ def test_library_exports_every_declared_function():
 
 def test_version_and_status_strings():
     lib = _lib.load()
-    assert lib.megamoe_abi_version() == _lib.ABI_VERSION == 5
-    texts = {code: _lib.status_string(code) for code in range(6)}
-    assert texts[_lib.OK] == "ok" and len(set(texts.values())) == 6
+    assert lib.megamoe_abi_version() == _lib.ABI_VERSION == 6
+    texts = {code: _lib.status_string(code) for code in range(7)}
+    assert texts[_lib.OK] == "ok" and len(set(texts.values())) == 7
     assert _lib.status_string(99) == "unknown status"
 
 
@@ -188,3 +188,25 @@ def test_case_table_of_the_forms():
         C.Case.from_dict({**C.case("moe-mxfp4-deepseek-v4-pro-t64").to_dict(), "swiglu": "bf16"})
     with pytest.raises(ValueError):  # expert parallelism is defined for the MXFP4 form
         C.Case.from_dict({**C.case(C.HEADLINE).to_dict(), "gpus": 8, "ep": 8})
+
+
+def test_noalloc_refuses_a_workspace_beyond_the_scratch():
+    """megamoe_forward_noalloc checks the geometry's workspace against MEGAMOE_SCRATCH_BYTES on
+    the host and refuses, reading no pointer and launching nothing (so this runs on the CPU);
+    every benchmark config fits."""
+    lib = _lib.load()
+    for case in C.CASES:
+        assert submission.MoELayer(case).workspace_bytes <= _lib.SCRATCH_BYTES, case.id
+    kimi = C.case("moe-fp8-kimi-k2-t128")
+    big = C.Case.from_dict({**kimi.to_dict(), "id": "kimi-k2-t256", "params": {**kimi.params, "tokens": 256}})
+    desc = submission.make_desc(big)
+    size = ctypes.c_size_t(0)
+    assert lib.megamoe_workspace_bytes(ctypes.byref(desc), ctypes.byref(size)) == _lib.OK
+    assert size.value > _lib.SCRATCH_BYTES
+    assert lib.megamoe_forward_noalloc(ctypes.byref(desc), ctypes.byref(_lib.Tensors()), None) == _lib.ERR_SCRATCH
+    assert "scratch" in _lib.status_string(_lib.ERR_SCRATCH)
+
+
+def test_scratch_size_matches_the_header():
+    m = re.search(r"#define MEGAMOE_SCRATCH_BYTES \((\d+)u << (\d+)\)", HEADER.read_text())
+    assert m and int(m.group(1)) << int(m.group(2)) == _lib.SCRATCH_BYTES

@@ -99,9 +99,8 @@ def test_mx_full_size_on_every_token():
     cpu = {k: v.cpu() for k, v in values.items()}
     del values
     torch.cuda.empty_cache()
-    want = mx.reference(case, cpu)["y"]
-    exact = mx.oracle(case, cpu)["y"]
-    check, band = _check(case, got.cpu(), want, exact)
+    want, exact = mx.reference_and_oracle(case, cpu)
+    check, band = _check(case, got.cpu(), want["y"], exact["y"])
     _log(f"  {case.id}: {check} band_rel={band['relative_error']:.3e}")
 
 

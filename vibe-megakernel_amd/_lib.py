@@ -13,7 +13,8 @@ from pathlib import Path
 PACKAGE_DIR = Path(__file__).resolve().parent
 LIBRARY = PACKAGE_DIR / "libmegamoe.so"
 
-OK, ERR_INVALID_ARGUMENT, ERR_SHAPE, ERR_WORKSPACE, ERR_HIP, ERR_UNSUPPORTED = range(6)
+OK, ERR_INVALID_ARGUMENT, ERR_SHAPE, ERR_WORKSPACE, ERR_HIP, ERR_UNSUPPORTED, ERR_SCRATCH = range(7)
+SCRATCH_BYTES = 32 << 20  # MEGAMOE_SCRATCH_BYTES
 GATE_SOFTMAX, GATE_SIGMOID = 0, 1
 STAGES = ("router", "select_quant", "permute", "experts", "combine")
 STAGES_MX = ("permute", "experts", "combine")  # the MXFP4 form (routing and x are inputs)
@@ -23,8 +24,8 @@ SYMBOLS = ("megamoe_workspace_bytes", "megamoe_forward", "megamoe_forward_events
            "megamoe_router_logits", "megamoe_route", "megamoe_quantize_rows", "megamoe_status_string",
            "megamoe_abi_version", "megamoe_block_forward", "megamoe_rms_norm", "megamoe_mx_workspace_bytes",
            "megamoe_mx_forward", "megamoe_ep_dispatch", "megamoe_ep_experts", "megamoe_ep_combine",
-           "megamoe_forward_ex", "megamoe_combine_by_expert_id")
-ABI_VERSION = 5
+           "megamoe_forward_ex", "megamoe_combine_by_expert_id", "megamoe_forward_noalloc")
+ABI_VERSION = 6
 
 
 class Desc(ctypes.Structure):
@@ -88,6 +89,7 @@ def load() -> ctypes.CDLL:
     P = ctypes.POINTER
     lib.megamoe_workspace_bytes.argtypes = [P(Desc), P(c_size_t)]
     lib.megamoe_forward.argtypes = [P(Desc), P(Tensors), c_void_p]
+    lib.megamoe_forward_noalloc.argtypes = [P(Desc), P(Tensors), c_void_p]
     lib.megamoe_forward_events.argtypes = [P(Desc), P(Tensors), c_void_p, P(c_void_p)]
     lib.megamoe_forward_timed.argtypes = [P(Desc), P(Tensors), c_void_p, P(ctypes.c_float)]
     lib.megamoe_router_logits.argtypes = [P(Desc), c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]

@@ -31,6 +31,7 @@
 
 #include <hip/hip_runtime.h>
 #include <math.h>
+#include <mutex>
 #include <type_traits>
 #include <stdint.h>
 #include <string.h>
@@ -113,6 +114,30 @@ __device__ __forceinline__ float wave_max(float v) {
 }
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
+
+// Device-coherent stores: relaxed agent-scope atomic stores, which write through the XCD's
+// L2 to memory, so a workgroup on another XCD that has not read the line before reads the
+// new value (the hand-over rule of the expert and layer kernels below).
+__device__ __forceinline__ void store_coherent(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_coherent(uint64_t* p, uint64_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_coherent(int64_t* p, int64_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_coherent(int* p, int v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_coherent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_coherent(double* p, double v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// All of this wavefront's memory operations complete (vmcnt, expcnt and lgkmcnt zero).
+__device__ __forceinline__ void publish_fence() { __builtin_amdgcn_s_waitcnt(0); }
 
 // ---------------------------------------------------------------------------------------
 // Dynamic E4M3 quantization of one full 128-wide block by one wavefront (two values per
@@ -326,13 +351,11 @@ __device__ __forceinline__ void quant_x_group(int group, const uint16_t* __restr
 // workgroups of their own, so every workgroup does the same work and the grid spreads
 // evenly over the CUs.
 template <int NTT>
-__global__ __launch_bounds__(kRouterWaves * 64) void k_router(const uint16_t* __restrict__ x,
-                                                              const float* __restrict__ w,
-                                                              double* __restrict__ partial, int T, int H, int E,
-                                                              int n_et, int nsplit) {
-  __shared__ f64x4 red[kRouterWaves - 1][NTT][64];
+__device__ __forceinline__ void router_tile(const uint16_t* __restrict__ x, const float* __restrict__ w,
+                                            double* __restrict__ partial, int T, int H, int E, int n_et, int nsplit,
+                                            int unit, f64x4* red) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const int et = blockIdx.x % n_et, split = (blockIdx.x / n_et) % nsplit, pass = blockIdx.x / (n_et * nsplit);
+  const int et = unit % n_et, split = (unit / n_et) % nsplit, pass = unit / (n_et * nsplit);
   const int span = H / nsplit / kRouterWaves;  // channels per wavefront, a multiple of 16
   const int k0 = split * (H / nsplit) + wv * span;
   const int g = lane >> 4;
@@ -386,7 +409,7 @@ __global__ __launch_bounds__(kRouterWaves * 64) void k_router(const uint16_t* __
     // Slices of the split, added in wavefront order.
     if (wv > 0) {
 #pragma unroll
-      for (int i = 0; i < NTT; ++i) red[wv - 1][i][lane] = acc[i];
+      for (int i = 0; i < NTT; ++i) red[((wv - 1) * NTT + i) * 64 + lane] = acc[i];
     }
     __syncthreads();
     if (wv == 0) {
@@ -394,7 +417,7 @@ __global__ __launch_bounds__(kRouterWaves * 64) void k_router(const uint16_t* __
       for (int q = 0; q < kRouterWaves - 1; ++q)
 #pragma unroll
         for (int i = 0; i < NTT; ++i) {
-          const f64x4 o = red[q][i][lane];
+          const f64x4 o = red[(q * NTT + i) * 64 + lane];
 #pragma unroll
           for (int v = 0; v < 4; ++v) acc[i][v] += o[v];
         }
@@ -405,12 +428,21 @@ __global__ __launch_bounds__(kRouterWaves * 64) void k_router(const uint16_t* __
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
             const int eo = et * kRouterTile + g + 4 * v;
-            if (eo < E) partial[((size_t)split * T + t) * E + eo] = acc[i][v];
+            if (eo < E) store_coherent(&partial[((size_t)split * T + t) * E + eo], acc[i][v]);
           }
         }
       }
     }
   }
+}
+
+template <int NTT>
+__global__ __launch_bounds__(kRouterWaves * 64) void k_router(const uint16_t* __restrict__ x,
+                                                              const float* __restrict__ w,
+                                                              double* __restrict__ partial, int T, int H, int E,
+                                                              int n_et, int nsplit) {
+  __shared__ f64x4 red[(kRouterWaves - 1) * NTT * 64];
+  router_tile<NTT>(x, w, partial, T, H, E, n_et, nsplit, blockIdx.x, red);
 }
 
 // logits[t][e] = fp32(sum of the splits in split order); used by megamoe_router_logits.
@@ -531,79 +563,25 @@ __device__ __forceinline__ unsigned long long select_key(float score, int e) {
 constexpr int kSelectTokens = 1;
 
 
+// LDS of one token's routing.
+struct SelectLds {
+  float logit[kSelectTokens][kMaxExperts];
+  float gscore[kSelectTokens][kMaxGroups];
+  int pick_id[kSelectTokens][kMaxTopK];
+  float pick_val[kSelectTokens][kMaxTopK];
+};
+
+// Wavefront `wv` routes token t from the logits in LDS (one wavefront per token, no barrier).
 template <int VPL>
-__global__ __launch_bounds__(256) void k_select(const double* __restrict__ partial, int nsplit,
-                                                const float* __restrict__ logits_in, const float* __restrict__ bias,
-                                                int T, int E, int K, int G, int TG, int gate, int renorm,
-                                                float scaling, int64_t* __restrict__ ids_out,
-                                                float* __restrict__ w_out, int n_sel, const uint16_t* __restrict__ x,
-                                                uint8_t* __restrict__ xq, float* __restrict__ xs, int H, int pow2) {
-  if ((int)blockIdx.x >= n_sel) {
-    quant_x_group((int)blockIdx.x - n_sel, x, xq, xs, T, H, pow2);
-    return;
-  }
-  __shared__ float lds_logit[kSelectTokens][kMaxExperts];
-  __shared__ float gscore[kSelectTokens][kMaxGroups];
-  __shared__ int pick_id_s[kSelectTokens][kMaxTopK];
-  __shared__ float pick_val_s[kSelectTokens][kMaxTopK];
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const int t0 = blockIdx.x * kSelectTokens, t = t0 + wv;
-  const bool token_ok = t < T;
-  const int ws = wv < kSelectTokens ? wv : 0;  // the wavefronts past kSelectTokens only load
-  float* choice_lds = lds_logit[ws];
-  int* pick_id = pick_id_s[ws];
-  float* pick_val = pick_val_s[ws];
-
-  float bias_v[VPL];
-#pragma unroll
-  for (int j = 0; j < VPL; ++j) {
-    const float v = bias ? bias[min(lane + 64 * j, E - 1)] : 0.0f;
-    bias_v[j] = lane + 64 * j < E ? v : 0.0f;
-  }
-
-  // Logits of the workgroup's tokens into LDS: thread i sums the splits (in split order)
-  // of entries i, i+256, ... (kSelectTokens * E <= 64 * VPL of them, up to kMaxSplits
-  // splits each), every load issued before the first add.
-  const int n_here = min(kSelectTokens, T - t0) * E;
-  if (logits_in) {
-#pragma unroll
-    for (int r = 0; r < (kSelectTokens * 64 * VPL + 255) / 256; ++r) {
-      const int i = threadIdx.x + 256 * r;
-      const float v = logits_in[(size_t)t0 * E + min(i, n_here - 1)];
-      if (i < n_here) lds_logit[i / E][i % E] = v;
-    }
-  } else {
-    const size_t stride = (size_t)T * E;
-    const double* p = partial + (size_t)t0 * E;
-    constexpr int NE = (kSelectTokens * 64 * VPL + 255) / 256;  // entries per thread
-    constexpr int R = NE < 2 ? NE : 2;                           // entries per round of loads
-#pragma unroll
-    for (int r0 = 0; r0 < NE; r0 += R) {
-      double part[R][kMaxSplits];
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        const int i = threadIdx.x + 256 * (r0 + r);
-#pragma unroll
-        for (int q = 0; q < kMaxSplits; ++q) {
-          // Clamped, unconditional loads (entries past the end are dropped below).
-          const double v = p[(size_t)min(q, nsplit - 1) * stride + min(i, n_here - 1)];
-          part[r][q] = q < nsplit ? v : 0.0;
-        }
-      }
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        const int i = threadIdx.x + 256 * (r0 + r);
-        double s = 0.0;
-#pragma unroll
-        for (int q = 0; q < kMaxSplits; ++q)
-          if (q < nsplit) s += part[r][q];
-        if (i < n_here) lds_logit[i / E][i % E] = (float)s;
-      }
-    }
-  }
-  __syncthreads();
-  if (wv >= kSelectTokens) return;  // no barrier follows
-
+__device__ __forceinline__ void route_token(SelectLds& L, int lane, int wv, int t, bool token_ok,
+                                            const float (&bias_v)[VPL], int E, int K, int G, int TG, int gate,
+                                            int renorm, float scaling, int64_t* __restrict__ ids_out,
+                                            float* __restrict__ w_out) {
+  auto& lds_logit = L.logit;
+  auto& gscore = L.gscore;
+  float* choice_lds = lds_logit[wv];
+  int* pick_id = L.pick_id[wv];
+  float* pick_val = L.pick_val[wv];
   float logit[VPL], prob[VPL], choice[VPL];
   bool valid[VPL];
 #pragma unroll
@@ -728,10 +706,93 @@ __global__ __launch_bounds__(256) void k_select(const double* __restrict__ parti
     w = expf(my_val - m) / s * scaling;
   }
   if (lane < K) {
-    ids_out[(size_t)t * K + lane] = my_id;
-    w_out[(size_t)t * K + lane] = w;
+    store_coherent(&ids_out[(size_t)t * K + lane], (int64_t)my_id);
+    store_coherent(&w_out[(size_t)t * K + lane], w);
   }
 }
+
+// Routing of token `token` (kSelectTokens = 1) by the workgroup's 256 threads: all load and
+// sum the split partials, wavefront 0 routes. ids and weights go out as device-coherent
+// stores (a later workgroup of the single-launch kernel reads them).
+template <int VPL>
+__device__ __forceinline__ void select_token(const double* __restrict__ partial, int nsplit,
+                                             const float* __restrict__ logits_in, const float* __restrict__ bias,
+                                             int T, int E, int K, int G, int TG, int gate, int renorm, float scaling,
+                                             int64_t* __restrict__ ids_out, float* __restrict__ w_out, int token,
+                                             SelectLds& L) {
+  auto& lds_logit = L.logit;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int t0 = token * kSelectTokens, t = t0 + wv;
+  const bool token_ok = t < T;
+
+  float bias_v[VPL];
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    const float v = bias ? bias[min(lane + 64 * j, E - 1)] : 0.0f;
+    bias_v[j] = lane + 64 * j < E ? v : 0.0f;
+  }
+
+  // Logits of the workgroup's tokens into LDS: thread i sums the splits (in split order)
+  // of entries i, i+256, ... (kSelectTokens * E <= 64 * VPL of them, up to kMaxSplits
+  // splits each), every load issued before the first add.
+  const int n_here = min(kSelectTokens, T - t0) * E;
+  if (logits_in) {
+#pragma unroll
+    for (int r = 0; r < (kSelectTokens * 64 * VPL + 255) / 256; ++r) {
+      const int i = threadIdx.x + 256 * r;
+      const float v = logits_in[(size_t)t0 * E + min(i, n_here - 1)];
+      if (i < n_here) lds_logit[i / E][i % E] = v;
+    }
+  } else {
+    const size_t stride = (size_t)T * E;
+    const double* p = partial + (size_t)t0 * E;
+    constexpr int NE = (kSelectTokens * 64 * VPL + 255) / 256;  // entries per thread
+    constexpr int R = NE < 2 ? NE : 2;                           // entries per round of loads
+#pragma unroll
+    for (int r0 = 0; r0 < NE; r0 += R) {
+      double part[R][kMaxSplits];
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int i = threadIdx.x + 256 * (r0 + r);
+#pragma unroll
+        for (int q = 0; q < kMaxSplits; ++q) {
+          // Clamped, unconditional loads (entries past the end are dropped below).
+          const double v = p[(size_t)min(q, nsplit - 1) * stride + min(i, n_here - 1)];
+          part[r][q] = q < nsplit ? v : 0.0;
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int i = threadIdx.x + 256 * (r0 + r);
+        double s = 0.0;
+#pragma unroll
+        for (int q = 0; q < kMaxSplits; ++q)
+          if (q < nsplit) s += part[r][q];
+        if (i < n_here) lds_logit[i / E][i % E] = (float)s;
+      }
+    }
+  }
+  __syncthreads();
+  if (wv < kSelectTokens) route_token<VPL>(L, lane, wv, t, token_ok, bias_v, E, K, G, TG, gate, renorm, scaling,
+                                           ids_out, w_out);
+}
+
+template <int VPL>
+__global__ __launch_bounds__(256) void k_select(const double* __restrict__ partial, int nsplit,
+                                                const float* __restrict__ logits_in, const float* __restrict__ bias,
+                                                int T, int E, int K, int G, int TG, int gate, int renorm,
+                                                float scaling, int64_t* __restrict__ ids_out,
+                                                float* __restrict__ w_out, int n_sel, const uint16_t* __restrict__ x,
+                                                uint8_t* __restrict__ xq, float* __restrict__ xs, int H, int pow2) {
+  if ((int)blockIdx.x >= n_sel) {
+    quant_x_group((int)blockIdx.x - n_sel, x, xq, xs, T, H, pow2);
+    return;
+  }
+  __shared__ SelectLds lds;
+  select_token<VPL>(partial, nsplit, logits_in, bias, T, E, K, G, TG, gate, renorm, scaling, ids_out, w_out,
+                    blockIdx.x, lds);
+}
+
 
 // ---------------------------------------------------------------------------------------
 // Histogram, scan, stable permutation and the expert work lists, in one workgroup.
@@ -939,17 +1000,6 @@ __global__ __launch_bounds__(1024) void k_permute(const int64_t* __restrict__ id
 // writers have landed, so no cache holds a copy of a line from before its last write.
 // ---------------------------------------------------------------------------------------
 
-__device__ __forceinline__ void store_coherent(uint32_t* p, uint32_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void store_coherent(uint64_t* p, uint64_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void store_coherent(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-// All of this wavefront's memory operations complete (vmcnt, expcnt and lgkmcnt zero).
-__device__ __forceinline__ void publish_fence() { __builtin_amdgcn_s_waitcnt(0); }
 
 // ---------------------------------------------------------------------------------------
 // Expert GEMM core. One wavefront multiplies RT row tiles (16 weight rows each) by NCT
@@ -3617,9 +3667,45 @@ bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 }  // namespace
 
+// ---------------------------------------------------------------------------------------
+// Fixed device scratch of megamoe_forward_noalloc: the workspace of one layer call in a
+// file-scope device array, which each GPU the library runs on holds (its own copy, at its
+// own address) until the process ends. In host code `scratch` names a host-side stand-in,
+// not device memory, so host code never passes it to a kernel or a copy: the device
+// address comes from hipGetSymbolAddress, taken once per device with that device current,
+// and is kept per device. The forward path initialises what it needs in the workspace
+// itself (the permute kernel clears the queue, readiness and pair counters each call), so
+// the array's contents from an earlier call do not matter; calls that overlap on one GPU
+// share the array and race.
+// ---------------------------------------------------------------------------------------
+
+static __device__ __align__(256) uint8_t scratch[MEGAMOE_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_address[kMaxDevices] = {};
+
+// The current device's copy of `scratch`.
+int scratch_address(void** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return MEGAMOE_ERR_HIP;
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_address[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return MEGAMOE_ERR_HIP;
+    g_scratch_address[dev] = p;
+  }
+  *out = g_scratch_address[dev];
+  return MEGAMOE_OK;
+}
+
+}  // namespace
+
 extern "C" {
 
-int megamoe_abi_version(void) { return 5; }
+int megamoe_abi_version(void) { return 6; }
 
 const char* megamoe_status_string(int status) {
   switch (status) {
@@ -3629,6 +3715,7 @@ const char* megamoe_status_string(int status) {
     case MEGAMOE_ERR_WORKSPACE: return "workspace smaller than megamoe_workspace_bytes()";
     case MEGAMOE_ERR_HIP: return "HIP runtime error";
     case MEGAMOE_ERR_UNSUPPORTED: return "geometry beyond this build's limits";
+    case MEGAMOE_ERR_SCRATCH: return "the layer needs more workspace than the fixed device scratch (MEGAMOE_SCRATCH_BYTES)";
     default: return "unknown status";
   }
 }
@@ -3643,6 +3730,19 @@ int megamoe_workspace_bytes(const megamoe_desc* desc, size_t* bytes) {
 
 int megamoe_forward(const megamoe_desc* desc, const megamoe_tensors* t, void* stream) {
   return forward_impl(desc, t, (hipStream_t)stream, nullptr);
+}
+
+int megamoe_forward_noalloc(const megamoe_desc* desc, const megamoe_tensors* t, void* stream) {
+  int rc = validate(desc);
+  if (rc) return rc;
+  if (!t) return MEGAMOE_ERR_INVALID_ARGUMENT;
+  if (make_layout(*desc).total > (size_t)MEGAMOE_SCRATCH_BYTES) return MEGAMOE_ERR_SCRATCH;
+  void* ws = nullptr;
+  if ((rc = scratch_address(&ws))) return rc;
+  megamoe_tensors with_scratch = *t;
+  with_scratch.workspace = ws;
+  with_scratch.workspace_bytes = MEGAMOE_SCRATCH_BYTES;
+  return forward_impl(desc, &with_scratch, (hipStream_t)stream, nullptr);
 }
 
 int megamoe_forward_events(const megamoe_desc* desc, const megamoe_tensors* t, void* stream, void* const* events) {

@@ -103,7 +103,7 @@ class MoELayer:
         device = self.check_mx_inputs(inputs)
         c = self.case
         y = torch.empty((c.tokens, c.hidden), dtype=torch.bfloat16, device=device)
-        ws = self.workspace(device)
+        ws = None if noalloc else self.workspace(device)
         ptr = {name: inputs[name].data_ptr() for name in _lib.MX_TENSOR_FIELDS if name not in ("y", "workspace")}
         tensors = _lib.MxTensors(**ptr, y=y.data_ptr(), workspace=ws.data_ptr(), workspace_bytes=self.workspace_bytes)
         stream = ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
@@ -146,7 +146,7 @@ class MoELayer:
             _expect(inputs["shared_down_scale"], "shared_down_scale", f32, (bh, bs), device)
         return device
 
-    def _call(self, inputs: dict, timed: bool, events=None):
+    def _call(self, inputs: dict, timed: bool, events=None, noalloc=False):
         if self.mx:
             if timed:
                 raise ValueError("timed() covers the fp8 layer form; use record() for the MXFP4 form")
@@ -156,7 +156,7 @@ class MoELayer:
         y = torch.empty((c.tokens, c.hidden), dtype=torch.bfloat16, device=device)
         ids = torch.empty((c.tokens, c.topk), dtype=torch.int64, device=device)
         weights = torch.empty((c.tokens, c.topk), dtype=torch.float32, device=device)
-        ws = self.workspace(device)
+        ws = None if noalloc else self.workspace(device)
         ptr = {name: (inputs[name].data_ptr() if name in inputs and (name != "router_bias" or c.bias != "none")
                       else None) for name in _INPUTS}
         if not c.shared_experts:
@@ -164,10 +164,16 @@ class MoELayer:
                 if name.startswith("shared_"):
                     ptr[name] = None
         tensors = _lib.Tensors(**ptr, y=y.data_ptr(), expert_ids=ids.data_ptr(),
-                               expert_weights=weights.data_ptr(), workspace=ws.data_ptr(),
-                               workspace_bytes=self.workspace_bytes)
+                               expert_weights=weights.data_ptr(), workspace=None if ws is None else ws.data_ptr(),
+                               workspace_bytes=0 if ws is None else self.workspace_bytes)
         stream = ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
         with torch.cuda.device(device):
+            if noalloc:
+                if self.block is not None or self.epilogue is not None or timed or events is not None:
+                    raise ValueError("the no-allocation entry point covers the plain layer form")
+                _lib.check(self.lib.megamoe_forward_noalloc(ctypes.byref(self.desc), ctypes.byref(tensors), stream),
+                           f"{c.id}: forward (no allocation)")
+                return {"y": y, "expert_ids": ids, "expert_weights": weights}
             if self.block is not None or self.epilogue is not None:
                 if timed:
                     raise ValueError("timed() covers the plain layer form; use record() for the block form and "
@@ -199,6 +205,11 @@ class MoELayer:
 
     def __call__(self, inputs: dict) -> dict:
         return self._call(inputs, timed=False)
+
+    def noalloc(self, inputs: dict) -> dict:
+        """One call of megamoe_forward_noalloc: the library's fixed device scratch stands in
+        for the workspace (the outputs are still allocated here, as the caller's)."""
+        return self._call(inputs, timed=False, noalloc=True)
 
     def timed(self, inputs: dict) -> tuple[dict, list[float]]:
         """One call with a device event between stages; returns (outputs, per-stage ms)."""
