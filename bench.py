@@ -92,10 +92,15 @@ def fp8_kernel(case) -> str:
     return "k_experts<true>" if split else "k_experts<false>"
 
 
-def measured_traffic(case) -> float | None:
-    """HBM bytes per k_experts launch from profiles/k_experts_<case>_counters.md: the line
+def layer_kernel(case) -> str:
+    """The single-launch kernel of the fp8 forms (k_layer; split gate/up as fp8_kernel)."""
+    return fp8_kernel(case).replace("k_experts", "k_layer")
+
+
+def measured_traffic(case, kernel: str = "k_experts") -> float | None:
+    """HBM bytes per launch of ``kernel`` from profiles/<kernel>_<case>_counters.md: the line
     ``traffic_bytes_per_launch: <number>`` (FETCH_SIZE + WRITE_SIZE, calibrated on a copy)."""
-    path = PROFILES / f"k_experts_{case.id}_counters.md"
+    path = PROFILES / f"{kernel}_{case.id}_counters.md"
     if not path.exists():
         return None
     for line in path.read_text().splitlines():
@@ -170,36 +175,21 @@ def cpu_baseline(case, values_gpu, hit: int, budget_s: float) -> dict:
                        f"{cpu_model()}")}
 
 
-def bench_case(case, steps: int, warmup: int, want_cpu: bool, cpu_budget: float) -> dict:
+def _time_layer(layer, sets, steps: int, warmup: int, outs: list | None = None) -> dict:
+    """K calls back to back between two device events (the value), K calls each between
+    its own pair (p50, p95), and K calls in which the library records events at its stage
+    boundaries on the stream its kernels run on (per-stage means)."""
     import torch
 
-    pkg = __graft_entry__.load_package()  # noqa: F841
-    from vibe_megakernel_amd import _lib
-    from vibe_megakernel_amd import cases as C
-    from vibe_megakernel_amd import submission, workloads
-
     dev = torch.device("cuda:0")
-    layer = submission.MoELayer(case)
-    per_set = C.algorithmic_bytes(case, round(C.expected_hit_experts(case)))
-    n_sets = max(1, min(8, math.ceil(ROTATE_BYTES / per_set)))
-    _log(f"[bench] {case.id}: generating {n_sets} input set(s) on the GPU")
-    sets = [workloads.make_inputs(case, 7301 + i, dev, log=lambda m, i=i: _log(f"[bench] {case.id} set {i}: {m}"))
-            for i in range(n_sets)]
-    torch.cuda.synchronize()
-    _log(f"[bench] {case.id}: inputs ready; warmup")
-
-    # Warmup runs straight into the timed region: the distinct-expert count, which needs a
-    # host round trip, is taken from the warmup outputs after the timed loops (a few ms of
-    # idle device before timing measurably slows the first timed calls).
-    outs = []
+    n_sets = len(sets)
+    # Warmup runs straight into the timed region: a host round trip between them leaves the
+    # device idle for a few ms, which measurably slows the first timed calls.
     for i in range(max(warmup, n_sets)):
-        outs.append(layer(sets[i % n_sets]))
-
-    _log(f"[bench] {case.id}: timing {steps} steps")
+        o = layer(sets[i % n_sets])
+        if outs is not None and i < n_sets:
+            outs.append(o)
     stream = torch.cuda.current_stream(dev)
-    # The timed region: K calls back to back between two events. An event recorded between
-    # calls costs a few us of device time per step, so the per-step distribution (p50, p95)
-    # comes from a second loop of K calls, each bracketed by its own pair of events.
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     start.record(stream)
@@ -207,8 +197,7 @@ def bench_case(case, steps: int, warmup: int, want_cpu: bool, cpu_budget: float)
         layer(sets[i % n_sets])
     end.record(stream)
     torch.cuda.synchronize()
-    total_ms = start.elapsed_time(end)
-    ms = total_ms / steps
+    ms = start.elapsed_time(end) / steps
     per_step = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
     for i, (e0, e1) in enumerate(per_step):
         e0.record(stream)
@@ -216,11 +205,7 @@ def bench_case(case, steps: int, warmup: int, want_cpu: bool, cpu_budget: float)
         e1.record(stream)
     torch.cuda.synchronize()
     step_ms = [a.elapsed_time(b) for a, b in per_step]
-
-    # Per-stage device time over a second loop of the same K steps: the library records
-    # events at its stage boundaries on the stream its kernels run on.
-    stages = layer.stages
-    nev = len(stages) + 1
+    nev = len(layer.stages) + 1
     events = [[torch.cuda.Event(enable_timing=True) for _ in range(nev)] for _ in range(steps)]
     for row in events:
         for e in row:
@@ -230,35 +215,80 @@ def bench_case(case, steps: int, warmup: int, want_cpu: bool, cpu_budget: float)
         layer.record(sets[i % n_sets], events[i])
     torch.cuda.synchronize()
     stage = [[row[j].elapsed_time(row[j + 1]) for j in range(nev - 1)] for row in events]
-    stage_ms = [statistics.mean(s[j] for s in stage) for j in range(nev - 1)]
+    stage_ms = [statistics.mean(s_[j] for s_ in stage) for j in range(nev - 1)]
+    return {"ms": ms, "p50_us": statistics.median(step_ms) * 1e3,
+            "p95_us": sorted(step_ms)[min(len(step_ms) - 1, int(0.95 * (len(step_ms) - 1) + 0.5))] * 1e3,
+            "stage_us": {name: v * 1e3 for name, v in zip(layer.stages, stage_ms)}}
+
+
+def bench_case(case, steps: int, warmup: int, want_cpu: bool, cpu_budget: float) -> dict:
+    import torch
+
+    __graft_entry__.load_package()
+    from vibe_megakernel_amd import cases as C
+    from vibe_megakernel_amd import submission, workloads
+
+    dev = torch.device("cuda:0")
+    layer = submission.MoELayer(case)  # the submission's path: one launch for the fp8 forms
+    per_set = C.algorithmic_bytes(case, round(C.expected_hit_experts(case)))
+    n_sets = max(1, min(8, math.ceil(ROTATE_BYTES / per_set)))
+    _log(f"[bench] {case.id}: generating {n_sets} input set(s) on the GPU")
+    sets = [workloads.make_inputs(case, 7301 + i, dev, log=lambda m, i=i: _log(f"[bench] {case.id} set {i}: {m}"))
+            for i in range(n_sets)]
+    torch.cuda.synchronize()
+    _log(f"[bench] {case.id}: inputs ready; warmup and timing {steps} steps")
+    outs: list = []
+    r = _time_layer(layer, sets, steps, warmup, outs)
     if case.format == "mxfp4":
         hit = statistics.mean(len(torch.unique(v["topk_idx"])) for v in sets)
     else:
         hit = statistics.mean(len(torch.unique(o["expert_ids"])) for o in outs[:n_sets])
+    del outs
 
     bytes_step = C.algorithmic_bytes(case, 0) + (C.algorithmic_bytes(case, 1) - C.algorithmic_bytes(case, 0)) * hit
-    kb = kernel_bytes(case, hit)
-    ex_ms = stage_ms[stages.index("experts")]
-    ex_bytes = kb["gate_up"] + kb["down"]
+    ms = r["ms"]
     result = {
-        "case": case.id, "ms_per_step": ms, "us_per_step": ms * 1e3,
-        "p50_us": statistics.median(step_ms) * 1e3,
-        "p95_us": sorted(step_ms)[min(len(step_ms) - 1, int(0.95 * (len(step_ms) - 1) + 0.5))] * 1e3,
+        "case": case.id, "ms_per_step": ms, "us_per_step": ms * 1e3, "p50_us": r["p50_us"], "p95_us": r["p95_us"],
         "hit_experts": hit, "bytes_per_step": bytes_step,
         "tb_per_s": bytes_step / (ms * 1e-3) / 1e12,
         "hbm_frac": bytes_step / (ms * 1e-3) / PEAK_HBM,
         "mfma_frac": C.algorithmic_flops(case) / (ms * 1e-3) / PEAK_FP8,
-        "stage_us": {name: v * 1e3 for name, v in zip(stages, stage_ms)},
+        "launches_per_step": case.max_gpu_launches,
+        "stage_us": r["stage_us"],
         "rotation_sets": n_sets,
-        "roofline": {"bound": "hbm", "achieved": ex_bytes / (ex_ms * 1e-3) / 1e9, "peak": PEAK_HBM / 1e9,
-                     "unit": "GB/s", "frac": ex_bytes / (ex_ms * 1e-3) / PEAK_HBM,
-                     "traffic": measured_traffic(case),
-                     "kernel": (mx_kernel(case.tokens * case.topk, case.experts) if case.format == "mxfp4"
-                                else fp8_kernel(case)),
-                     "kernel_us": ex_ms * 1e3, "bytes_per_launch": ex_bytes},
         "dtype": ("e2m1xe4m3->fp32 (E8M0 scales per 32; bf16 out)" if case.format == "mxfp4"
                   else "e4m3xe4m3->fp32 (bf16 in/out)"),
     }
+    if layer.single_launch:
+        # One kernel per step: its roofline is the whole layer's algorithmic bytes over the
+        # mean duration of the launch (events the library records around it, on its stream).
+        k_ms = r["stage_us"]["layer"] * 1e-3
+        result["roofline"] = {"bound": "hbm", "achieved": bytes_step / (k_ms * 1e-3) / 1e9, "peak": PEAK_HBM / 1e9,
+                              "unit": "GB/s", "frac": bytes_step / (k_ms * 1e-3) / PEAK_HBM,
+                              "traffic": measured_traffic(case, "k_layer"), "kernel": layer_kernel(case),
+                              "kernel_us": k_ms * 1e3, "bytes_per_launch": bytes_step}
+        # The stream-ordered kernels of the same layer, for their per-stage times and the
+        # expert kernel's own roofline.
+        five = submission.MoELayer(case, single_launch=False)
+        r5 = _time_layer(five, sets, steps, warmup)
+        kb = kernel_bytes(case, hit)
+        ex_ms = r5["stage_us"]["experts"] * 1e-3
+        ex_bytes = kb["gate_up"] + kb["down"]
+        result["stream_ordered"] = {
+            "us_per_step": r5["ms"] * 1e3, "p50_us": r5["p50_us"], "stage_us": r5["stage_us"],
+            "launches_per_step": 5 + (case.norm != "none"),
+            "expert_kernel": {"kernel": fp8_kernel(case), "kernel_us": ex_ms * 1e3, "bytes_per_launch": ex_bytes,
+                              "frac": ex_bytes / (ex_ms * 1e-3) / PEAK_HBM,
+                              "traffic": measured_traffic(case)}}
+    else:
+        kb = kernel_bytes(case, hit)
+        ex_ms = r["stage_us"]["experts"] * 1e-3
+        ex_bytes = kb["gate_up"] + kb["down"]
+        result["roofline"] = {"bound": "hbm", "achieved": ex_bytes / (ex_ms * 1e-3) / 1e9, "peak": PEAK_HBM / 1e9,
+                              "unit": "GB/s", "frac": ex_bytes / (ex_ms * 1e-3) / PEAK_HBM,
+                              "traffic": measured_traffic(case),
+                              "kernel": mx_kernel(case.tokens * case.topk, case.experts),
+                              "kernel_us": ex_ms * 1e3, "bytes_per_launch": ex_bytes}
     if want_cpu:
         _log(f"[bench] {case.id}: CPU oracle baseline")
         result["cpu_baseline"] = cpu_baseline(case, sets[0], round(hit), cpu_budget)
@@ -416,7 +446,8 @@ def bench_ep_share(case, steps: int, warmup: int, want_cpu: bool, cpu_budget: fl
 def _config_entry(r: dict) -> dict:
     """One config's record under "configs": time, bandwidth, roofline and CPU baseline."""
     keep = ("us_per_step", "p50_us", "p95_us", "tb_per_s", "hbm_frac", "mfma_frac", "hit_experts", "bytes_per_step",
-            "stage_us", "rotation_sets", "roofline", "cpu_baseline", "dtype", "received_rows", "sent_rows")
+            "launches_per_step", "stage_us", "rotation_sets", "roofline", "stream_ordered", "cpu_baseline", "dtype",
+            "received_rows", "sent_rows")
     return {k: r[k] for k in keep if k in r}
 
 

@@ -113,8 +113,8 @@ typedef struct megamoe_tensors {
   size_t workspace_bytes;
 } megamoe_tensors;
 
-/* Bytes of device workspace megamoe_forward needs for `desc` (host call).
- * No reference counterpart: the reference allocates through PyTorch. */
+/* Bytes of device workspace megamoe_forward (and megamoe_layer_forward) needs for `desc`
+ * (host call). No reference counterpart: the reference allocates through PyTorch. */
 int megamoe_workspace_bytes(const megamoe_desc* desc, size_t* bytes);
 
 /* The whole layer: router, routing, permute, gate/up + SwiGLU, down, combine.
@@ -210,6 +210,23 @@ typedef struct megamoe_epilogue {
  * glm53.py:263-274 for GLM-5.3-Flash. */
 int megamoe_forward_ex(const megamoe_desc* desc, const megamoe_tensors* t, const megamoe_block* block,
                        const megamoe_epilogue* epilogue, void* stream, void* const* events);
+
+/* The layer (block == NULL) or the block, with an optional epilogue variant, as ONE kernel
+ * launch: the arguments and results are megamoe_forward_ex's, bit for bit. The reference
+ * harness audits each call's kernel launches against the case's budget, one by default
+ * (megabench/cases.py:32, megabench/harness/benchmark.py:73-100); the stream-ordered form
+ * above takes five (six with the block's normalization). One persistent kernel drains a
+ * queue of units in dependency order: RMSNorm rows (block form), router tiles, per-token
+ * routing (with the token's activation quantization), the permute (run by the routing unit
+ * that finishes last), gate/up and down units, combine units.
+ * Workspace: megamoe_workspace_bytes(desc) bytes, ZEROED before its first use with this
+ * entry point (e.g. hipMemset once after allocation); each call leaves its control words
+ * zero again, so later calls need nothing. Calls sharing a workspace must be ordered (one
+ * stream). `events` is NULL or events[0..1] (hipEvent_t, created by the caller), recorded
+ * before and after the launch. Replaces frontier.py:335-354 (and glm53.py:263-274 for the
+ * clamped-SwiGLU form) as megamoe_forward_ex does. */
+int megamoe_layer_forward(const megamoe_desc* desc, const megamoe_tensors* t, const megamoe_block* block,
+                          const megamoe_epilogue* epilogue, void* stream, void* const* events);
 
 /* GPT-OSS's combine (gptoss.py:112-124): per token t, its K expert outputs (bf16
  * expert_out [T*K, H], row t*K + k for slot k) accumulate in ascending expert id order
@@ -316,10 +333,11 @@ int megamoe_quantize_rows(int32_t rows, int32_t cols, const void* x, uint8_t* q,
 /* Text for a status code (static storage). */
 const char* megamoe_status_string(int status);
 
-/* ABI version of this library: 6 (1, plus megamoe_block_forward and megamoe_rms_norm in 2,
+/* ABI version of this library: 7 (1, plus megamoe_block_forward and megamoe_rms_norm in 2,
  * plus megamoe_mx_workspace_bytes and megamoe_mx_forward in 3, plus megamoe_ep_dispatch,
  * megamoe_ep_experts and megamoe_ep_combine in 4, plus megamoe_forward_ex and
- * megamoe_combine_by_expert_id in 5, plus megamoe_forward_noalloc in 6). */
+ * megamoe_combine_by_expert_id in 5, plus megamoe_forward_noalloc in 6, plus
+ * megamoe_layer_forward in 7). */
 int megamoe_abi_version(void);
 
 #ifdef __cplusplus

@@ -1,0 +1,92 @@
+"""The layer as one kernel launch (megamoe_layer_forward) on the GPU, through the C ABI.
+
+Its results equal the stream-ordered kernels' (megamoe_forward / megamoe_forward_ex) bit for
+bit, on every form (layer, block, clamped bf16 SwiGLU) and on development and full
+geometries, over consecutive calls with different inputs on one workspace (the kernel
+leaves its control words zero for the next call); and a call launches exactly one kernel,
+counted as the reference harness audits it (torch.profiler's device events of one call,
+megabench/harness/benchmark.py:73-100). Parity with the CPU oracle is covered by the other
+GPU tests, which call the same default path (submission.build)."""
+
+from __future__ import annotations
+
+import sys
+
+import pytest
+import torch
+
+from vibe_megakernel_amd import cases as C
+from vibe_megakernel_amd import submission, workloads
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def _log(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def _to(values):
+    return {k: v.to(DEV) for k, v in values.items()}
+
+
+def _same(a, b, what):
+    for k in ("y", "expert_ids", "expert_weights"):
+        assert torch.equal(a[k], b[k]), f"{what}: {k} differs"
+
+
+def _dev_cases():
+    out = [C.case("moe-fp8-tiny-t4")]
+    out += [C.development(c) for c in C.CASES[1:]]
+    out.append(C.development(C.case(C.HEADLINE), tokens=37))
+    out.append(C.development(C.case("moe-fp8-kimi-k2-t128"), tokens=70, experts=8, topk=4))
+    out.append(C.development(C.case("moe-fp8-mixtral-t16"), hidden=4096, intermediate=512))  # split gate/up
+    out += [C.development(c) for c in C.BLOCK_CASES]
+    out += [C.development(c) for c in C.VARIANT_CASES]
+    return out
+
+
+@pytest.mark.parametrize("case", _dev_cases(), ids=lambda c: c.id)
+def test_single_launch_equals_stream_ordered_on_development_geometry(case):
+    _log(f"single launch {case.id} T={case.tokens} E={case.experts}")
+    one = submission.MoELayer(case)
+    five = submission.MoELayer(case, single_launch=False)
+    assert one.single_launch and not five.single_launch
+    for seed in (5, 6, 7):  # consecutive calls on one workspace
+        values = _to(workloads.make_inputs(case, seed, "cpu"))
+        a, b = one(values), five(values)
+        torch.cuda.synchronize()
+        _same(a, b, f"{case.id} seed {seed}")
+        assert torch.isfinite(a["y"].float()).all()
+
+
+@pytest.mark.parametrize("cid", [c.id for c in C.CASES])
+def test_single_launch_equals_stream_ordered_at_full_size(cid):
+    case = C.case(cid)
+    _log(f"single launch full size {cid}")
+    values = workloads.make_inputs(case, 104729, DEV)
+    one = submission.MoELayer(case)
+    five = submission.MoELayer(case, single_launch=False)
+    for _ in range(2):
+        a, b = one(values), five(values)
+        torch.cuda.synchronize()
+        _same(a, b, cid)
+
+
+def test_one_call_is_one_kernel_launch():
+    from torch.profiler import ProfilerActivity, profile
+
+    case = C.case(C.HEADLINE)
+    dev = C.development(case)
+    values = _to(workloads.make_inputs(dev, 3, "cpu"))
+    run = submission.build(dev.to_dict())
+    run(values)  # the workspace is made (and zeroed) on the first call
+    torch.cuda.synchronize()
+    with profile(activities=[ProfilerActivity.CPU, ProfilerActivity.CUDA]) as prof:
+        run(values)
+        torch.cuda.synchronize()
+    kernels = [e.name for e in prof.events() if e.device_type == torch.autograd.DeviceType.CUDA]
+    _log(f"device events of one call: {kernels}")
+    assert len(kernels) == 1 and "k_layer" in kernels[0], kernels
+    assert dev.max_gpu_launches == 1

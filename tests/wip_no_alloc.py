@@ -40,7 +40,7 @@ def test_noalloc_equals_forward_on_two_calls_the_second_smaller():
     small = C.development(C.case(C.HEADLINE), tokens=20)
     sizes = []
     for case, seed in ((big, 41), (small, 42)):
-        layer = submission.MoELayer(case)
+        layer = submission.MoELayer(case, single_launch=False)  # megamoe_forward, the existing entry
         sizes.append(layer.workspace_bytes)
         assert layer.workspace_bytes <= _lib.SCRATCH_BYTES
         _log(f"noalloc {case.id} T={case.tokens} E={case.experts} workspace={layer.workspace_bytes}")

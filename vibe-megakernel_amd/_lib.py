@@ -24,8 +24,9 @@ SYMBOLS = ("megamoe_workspace_bytes", "megamoe_forward", "megamoe_forward_events
            "megamoe_router_logits", "megamoe_route", "megamoe_quantize_rows", "megamoe_status_string",
            "megamoe_abi_version", "megamoe_block_forward", "megamoe_rms_norm", "megamoe_mx_workspace_bytes",
            "megamoe_mx_forward", "megamoe_ep_dispatch", "megamoe_ep_experts", "megamoe_ep_combine",
-           "megamoe_forward_ex", "megamoe_combine_by_expert_id", "megamoe_forward_noalloc")
-ABI_VERSION = 6
+           "megamoe_forward_ex", "megamoe_combine_by_expert_id", "megamoe_forward_noalloc",
+           "megamoe_layer_forward")
+ABI_VERSION = 7
 
 
 class Desc(ctypes.Structure):
@@ -106,6 +107,7 @@ def load() -> ctypes.CDLL:
     lib.megamoe_ep_combine.argtypes = [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, c_void_p, c_void_p, c_void_p,
                                        c_void_p]
     lib.megamoe_forward_ex.argtypes = [P(Desc), P(Tensors), P(Block), P(Epilogue), c_void_p, P(c_void_p)]
+    lib.megamoe_layer_forward.argtypes = [P(Desc), P(Tensors), P(Block), P(Epilogue), c_void_p, P(c_void_p)]
     lib.megamoe_combine_by_expert_id.argtypes = [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, c_void_p, c_void_p,
                                                  c_void_p, c_void_p, c_void_p, c_void_p]
     lib.megamoe_status_string.argtypes = [c_int]

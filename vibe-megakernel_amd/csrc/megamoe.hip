@@ -153,6 +153,23 @@ __device__ __forceinline__ void quant_block(const uint16_t* src, uint8_t* dst, f
   if (lane == 0) *scale = s;
 }
 
+// The same quantization of one full 128-wide block with four values per lane on lanes
+// 0..31, so each lane writes its codes as one 4-byte device-coherent store (the
+// single-launch kernel's expert units read them from other workgroups).
+__device__ __forceinline__ void quant_block4(const uint16_t* src, uint8_t* dst, float* scale, int pow2, int lane) {
+  const int l = lane & 31;
+  const uint2 four = *reinterpret_cast<const uint2*>(src + 4 * l);
+  const float v[4] = {bf16_bits_to_f32(four.x & 0xffffu), bf16_bits_to_f32(four.x >> 16),
+                      bf16_bits_to_f32(four.y & 0xffffu), bf16_bits_to_f32(four.y >> 16)};
+  const float m = lane < 32 ? fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))) : 0.0f;
+  const float s = act_scale(wave_max(m), pow2);
+  uint32_t q = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) q |= f32_to_e4m3(clamp448(v[i] / s)) << (8 * i);
+  if (lane < 32) store_coherent(reinterpret_cast<uint32_t*>(dst + 4 * l), q);
+  if (lane == 0) store_coherent(scale, s);
+}
+
 // Ragged rows (any column count): one wavefront per (row, 128-column block).
 __global__ __launch_bounds__(256) void k_quant_rows(const uint16_t* __restrict__ x, uint8_t* __restrict__ q,
                                                     float* __restrict__ scales, int rows, int cols, int pow2) {
@@ -236,18 +253,17 @@ __device__ __forceinline__ void norm_store(const NormChunks& c, uint16_t* orow, 
       const float w0 = bf16_bits_to_f32(gw[i] & 0xffffu), w1 = bf16_bits_to_f32(gw[i] >> 16);
       o[i] = f32_to_bf16_bits(__fmul_rn(n0, w0)) | (f32_to_bf16_bits(__fmul_rn(n1, w1)) << 16);
     }
-    if (e < H) *reinterpret_cast<uint2*>(orow + e) = make_uint2(o[0], o[1]);
+    if (e < H) store_coherent(reinterpret_cast<uint64_t*>(orow + e), (uint64_t)o[0] | ((uint64_t)o[1] << 32));
   }
 }
 
 // Every thread issues the loads of its chunks of x and gamma at once; a row of up to
 // kNormPass elements stays in registers from the sum of squares to the output (longer rows
 // reload their later passes).
-__global__ __launch_bounds__(256) void k_norm(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
-                                              int rows, int H, float eps, int weight_in_fp32,
-                                              uint16_t* __restrict__ out) {
-  __shared__ double part[4];
-  const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+__device__ __forceinline__ void norm_row(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, int row,
+                                         int H, float eps, int weight_in_fp32, uint16_t* __restrict__ out,
+                                         double* part) {
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const uint16_t* xr = x + (size_t)row * H;
   uint16_t* orow = out + (size_t)row * H;
   NormChunks first;
@@ -273,6 +289,13 @@ __global__ __launch_bounds__(256) void k_norm(const uint16_t* __restrict__ x, co
     norm_load(more, xr, w, base, H, tid);
     norm_store(more, orow, base, H, tid, r, weight_in_fp32);
   }
+}
+
+__global__ __launch_bounds__(256) void k_norm(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+                                              int rows, int H, float eps, int weight_in_fp32,
+                                              uint16_t* __restrict__ out) {
+  __shared__ double part[4];
+  norm_row(x, w, blockIdx.x, H, eps, weight_in_fp32, out, part);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -867,22 +890,33 @@ __device__ __forceinline__ int chunk_class(int rows) { return rows > 32 ? 0 : (r
 // With `wide` (the MXFP4 form, no shared expert), a chunk of more than 32 rows is worked by
 // wide units, 4 per 128-channel block of gate/up and 2 per 128-row block of down (times
 // the K parts); those chunks lead the lists, and meta[kMetaWide] counts them.
-__global__ __launch_bounds__(1024) void k_permute(const int64_t* __restrict__ ids, int64_t base, int T, int K, int E,
-                                                  int S, int nbI, int nbH, int ks, int chunk, int wide,
-                                                  PermuteOut out) {
-  extern __shared__ int smem[];
-  __shared__ int bad_ids;
-  int* bad = &bad_ids;
+__device__ __forceinline__ void store_coherent(int4* p, int4 v) {
+  store_coherent(reinterpret_cast<uint64_t*>(p), (uint64_t)(uint32_t)v.x | ((uint64_t)(uint32_t)v.y << 32));
+  store_coherent(reinterpret_cast<uint64_t*>(p) + 1, (uint64_t)(uint32_t)v.z | ((uint64_t)(uint32_t)v.w << 32));
+}
+
+// The permute by one workgroup of any size (a multiple of 64, at least 256): thread i owns
+// the contiguous experts [i*ept, i*ept + ept) (ept = ceil(E / threads)), so the scan over
+// threads runs in expert order. LDS: `smem` holds 32 + E + E*ceil(T/32) ints; flags[0..1]
+// are two more. Every output goes out as a device-coherent store: the single-launch
+// kernel's expert units read them from other workgroups.
+__device__ __forceinline__ void permute_block(const int64_t* __restrict__ ids, int64_t base, int T, int K, int E, int S, int nbI,
+                              int nbH, int ks, int chunk, int wide, const PermuteOut& out, int* smem, int* flags) {
+  int* bad = flags;
+  int* hits = flags + 1;
   unsigned long long* tmp = (unsigned long long*)smem;  // 16
   int* cnt = smem + 32;                                  // E
   unsigned* bm = (unsigned*)(cnt + E);                   // E * words
   const int words = (T + 31) / 32;
-  const int tid = threadIdx.x, n = T * K;
-  for (int i = tid; i < E; i += blockDim.x) cnt[i] = 0;
-  for (int i = tid; i < E * words; i += blockDim.x) bm[i] = 0u;
-  if (tid == 0) *bad = 0;
+  const int tid = threadIdx.x, nt = blockDim.x, n = T * K;
+  for (int i = tid; i < E; i += nt) cnt[i] = 0;
+  for (int i = tid; i < E * words; i += nt) bm[i] = 0u;
+  if (tid == 0) {
+    *bad = 0;
+    *hits = 0;
+  }
   __syncthreads();
-  for (int i = tid; i < n; i += blockDim.x) {
+  for (int i = tid; i < n; i += nt) {
     const int64_t e64 = ids[i] - base;
     const int t = i / K;
     if (e64 < 0 || e64 >= E) {
@@ -896,24 +930,35 @@ __global__ __launch_bounds__(1024) void k_permute(const int64_t* __restrict__ id
   __syncthreads();
   if (*bad) {
     if (tid == 0) {
-      out.meta[kMetaUnitsGU] = 0;
-      out.meta[kMetaUnitsDN] = 0;
-      out.meta[kMetaQueueGU] = 0;
-      out.meta[kMetaError] = 1;
+      store_coherent(&out.meta[kMetaUnitsGU], 0);
+      store_coherent(&out.meta[kMetaUnitsDN], 0);
+      store_coherent(&out.meta[kMetaQueueGU], 0);
+      store_coherent(&out.meta[kMetaError], 1);
     }
     return;
   }
-  // E <= 1024 = blockDim: one expert per thread.
-  const int c = tid < E ? cnt[tid] : 0;
-  const int full = c / chunk, rem = c % chunk;
-  const int a4 = full + (rem > 32 ? 1 : 0), a2 = (rem > 16 && rem <= 32) ? 1 : 0, a1 = (rem > 0 && rem <= 16) ? 1 : 0;
-  const int nhit = __syncthreads_count(c > 0);
+  const int ept = (E + nt - 1) / nt, e_lo = min(E, tid * ept), e_hi = min(E, e_lo + ept);
+  auto classes = [chunk](int c, int& a4, int& a2, int& a1) {
+    const int full = c / chunk, rem = c % chunk;
+    a4 = full + (rem > 32 ? 1 : 0);
+    a2 = (rem > 16 && rem <= 32) ? 1 : 0;
+    a1 = (rem > 0 && rem <= 16) ? 1 : 0;
+  };
+  unsigned long long mine = 0ull;
+  int my_hits = 0;
+  for (int e = e_lo; e < e_hi; ++e) {
+    const int c = cnt[e];
+    int a4, a2, a1;
+    classes(c, a4, a2, a1);
+    mine += (unsigned long long)c | ((unsigned long long)a4 << 21) | ((unsigned long long)a2 << 36) |
+            ((unsigned long long)a1 << 47);
+    my_hits += c > 0;
+  }
+  if (my_hits) atomicAdd(hits, my_hits);
   unsigned long long tot = 0;
-  const unsigned long long packed =
-      block_exclusive_scan((unsigned long long)c | ((unsigned long long)a4 << 21) |
-                               ((unsigned long long)a2 << 36) | ((unsigned long long)a1 << 47), tmp, &tot);
-  const int off = (int)(packed & 0x1fffffu), p4 = (int)((packed >> 21) & 0x7fffu),
-            p2 = (int)((packed >> 36) & 0x7ffu), p1 = (int)((packed >> 47) & 0x7ffu);
+  const unsigned long long packed = block_exclusive_scan(mine, tmp, &tot);
+  int off = (int)(packed & 0x1fffffu), p4 = (int)((packed >> 21) & 0x7fffu), p2 = (int)((packed >> 36) & 0x7ffu),
+      p1 = (int)((packed >> 47) & 0x7ffu);
   const int total = (int)(tot & 0x1fffffu), t4 = (int)((tot >> 21) & 0x7fffu), t2 = (int)((tot >> 36) & 0x7ffu),
             t1 = (int)((tot >> 47) & 0x7ffu);
   // Shared expert chunks of T rows.
@@ -925,27 +970,36 @@ __global__ __launch_bounds__(1024) void k_permute(const int64_t* __restrict__ id
   const int dbase[3] = {0, s4 + t4, s4 + t4 + s2 + t2};
   const int gshared[3] = {S * s4, S * s2, S * s1};
   const int dshared[3] = {s4, s2, s1};
-  if (tid < E) {
-    out.counts[tid] = c;
-    out.offsets[tid] = off;
+  for (int e = e_lo; e < e_hi; ++e) {
+    const int c = cnt[e];
+    int a4, a2, a1;
+    classes(c, a4, a2, a1);
+    const int full = c / chunk, rem = c % chunk;
+    store_coherent(&out.counts[e], c);
+    store_coherent(&out.offsets[e], off);
     for (int i = 0; i < a4; ++i) {
-      const int4 ch = make_int4(tid, chunk * i, min(chunk, c - chunk * i), 0);
-      out.gu[gbase[0] + gshared[0] + p4 + i] = ch;
-      out.dn[dbase[0] + dshared[0] + p4 + i] = ch;
-      out.dn_of_gu[gbase[0] + gshared[0] + p4 + i] = dbase[0] + dshared[0] + p4 + i;
+      const int4 ch = make_int4(e, chunk * i, min(chunk, c - chunk * i), 0);
+      store_coherent(&out.gu[gbase[0] + gshared[0] + p4 + i], ch);
+      store_coherent(&out.dn[dbase[0] + dshared[0] + p4 + i], ch);
+      store_coherent(&out.dn_of_gu[gbase[0] + gshared[0] + p4 + i], dbase[0] + dshared[0] + p4 + i);
     }
     if (a2) {
-      const int4 ch = make_int4(tid, chunk * full, rem, 0);
-      out.gu[gbase[1] + gshared[1] + p2] = ch;
-      out.dn[dbase[1] + dshared[1] + p2] = ch;
-      out.dn_of_gu[gbase[1] + gshared[1] + p2] = dbase[1] + dshared[1] + p2;
+      const int4 ch = make_int4(e, chunk * full, rem, 0);
+      store_coherent(&out.gu[gbase[1] + gshared[1] + p2], ch);
+      store_coherent(&out.dn[dbase[1] + dshared[1] + p2], ch);
+      store_coherent(&out.dn_of_gu[gbase[1] + gshared[1] + p2], dbase[1] + dshared[1] + p2);
     }
     if (a1) {
-      const int4 ch = make_int4(tid, chunk * full, rem, 0);
-      out.gu[gbase[2] + gshared[2] + p1] = ch;
-      out.dn[dbase[2] + dshared[2] + p1] = ch;
-      out.dn_of_gu[gbase[2] + gshared[2] + p1] = dbase[2] + dshared[2] + p1;
+      const int4 ch = make_int4(e, chunk * full, rem, 0);
+      store_coherent(&out.gu[gbase[2] + gshared[2] + p1], ch);
+      store_coherent(&out.dn[dbase[2] + dshared[2] + p1], ch);
+      store_coherent(&out.dn_of_gu[gbase[2] + gshared[2] + p1], dbase[2] + dshared[2] + p1);
     }
+    cnt[e] = off;  // the expert's first row, for the ranks below (only this thread reads cnt[e] above)
+    off += c;
+    p4 += a4;
+    p2 += a2;
+    p1 += a1;
   }
   if (tid == 0) {
     if (S > 0) {
@@ -955,37 +1009,44 @@ __global__ __launch_bounds__(1024) void k_permute(const int64_t* __restrict__ id
         const int idx = cls == 0 ? i : 0;        // index within the shared part of the class
         const int per_copy = cls == 0 ? s4 : 1;  // shared chunks of this class per copy
         for (int s = 0; s < S; ++s) {
-          out.gu[gbase[cls] + s * per_copy + idx] = make_int4(E, chunk * i, rows, s * nbI);
-          out.dn_of_gu[gbase[cls] + s * per_copy + idx] = dbase[cls] + idx;
+          store_coherent(&out.gu[gbase[cls] + s * per_copy + idx], make_int4(E, chunk * i, rows, s * nbI));
+          store_coherent(&out.dn_of_gu[gbase[cls] + s * per_copy + idx], dbase[cls] + idx);
         }
-        out.dn[dbase[cls] + idx] = make_int4(E, chunk * i, rows, 0);
+        store_coherent(&out.dn[dbase[cls] + idx], make_int4(E, chunk * i, rows, 0));
       }
     }
-    out.offsets[E] = total;
-    out.meta[kMetaHit] = nhit;
+    store_coherent(&out.offsets[E], total);
+    store_coherent(&out.meta[kMetaHit], *hits);
     const int wf = wide ? 4 : 1, wfd = wide ? 2 : 1;  // units per block of a chunk of over 32 rows
-    out.meta[kMetaUnitsGU] = (S * (s4 + s2 + s1) + wf * t4 + t2 + t1) * nbI;
-    out.meta[kMetaUnitsDN] = (s4 + s2 + s1 + wfd * t4 + t2 + t1) * nbH * ks;
-    out.meta[kMetaWide] = wide ? t4 : 0;
-    out.meta[kMetaQueueGU] = 0;
-    out.meta[kMetaQueueDN] = 0;
-    out.meta[kMetaError] = 0;
+    store_coherent(&out.meta[kMetaUnitsGU], (S * (s4 + s2 + s1) + wf * t4 + t2 + t1) * nbI);
+    store_coherent(&out.meta[kMetaUnitsDN], (s4 + s2 + s1 + wfd * t4 + t2 + t1) * nbH * ks);
+    store_coherent(&out.meta[kMetaWide], wide ? t4 : 0);
+    store_coherent(&out.meta[kMetaQueueGU], 0);
+    store_coherent(&out.meta[kMetaQueueDN], 0);
+    store_coherent(&out.meta[kMetaError], 0);
   }
   const int dtot = s4 + s2 + s1 + t4 + t2 + t1;
-  for (int i = tid; i < dtot; i += blockDim.x) out.ready[i] = 0;
+  for (int i = tid; i < dtot; i += nt) store_coherent(&out.ready[i], 0);
   if (out.pairs)
-    for (int i = tid; i < (S * (s4 + s2 + s1) + t4 + t2 + t1) * nbI; i += blockDim.x) out.pairs[i] = 0;
-  if (tid < E) cnt[tid] = off;  // reuse as offsets (every thread read its count above)
+    for (int i = tid; i < (S * (s4 + s2 + s1) + t4 + t2 + t1) * nbI; i += nt) store_coherent(&out.pairs[i], 0);
   __syncthreads();
-  for (int i = tid; i < n; i += blockDim.x) {
+  for (int i = tid; i < n; i += nt) {
     const int e = (int)(ids[i] - base), t = i / K;
     const unsigned* row = bm + e * words;
     int rank = __popc(row[t >> 5] & ((1u << (t & 31)) - 1u));
     for (int q = 0; q < (t >> 5); ++q) rank += __popc(row[q]);
     const int pos = cnt[e] + rank;
-    out.perm[pos] = i;
-    out.inv[i] = pos;
+    store_coherent(&out.perm[pos], i);
+    store_coherent(&out.inv[i], pos);
   }
+}
+
+__global__ __launch_bounds__(1024) void k_permute(const int64_t* __restrict__ ids, int64_t base, int T, int K, int E,
+                                                  int S, int nbI, int nbH, int ks, int chunk, int wide,
+                                                  PermuteOut out) {
+  extern __shared__ int smem[];
+  __shared__ int flags[2];
+  permute_block(ids, base, T, K, E, S, nbI, nbH, ks, chunk, wide, out, smem, flags);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -1419,7 +1480,7 @@ struct GateUpArgs {
 // block, so SwiGLU pairs matching registers; the per-row amax over the 128-block for the
 // requantization of h is reduced across the four wavefronts through LDS.
 template <int NCT>
-__device__ void gateup_unit(const GateUpArgs& a, const uint8_t* wg, const uint8_t* wu, const float* sg,
+__device__ __forceinline__ void gateup_unit(const GateUpArgs& a, const uint8_t* wg, const uint8_t* wu, const float* sg,
                             const float* su, const ChunkRows& cr, int jb, uint8_t* hq, float* hs, int ldh,
                             int rot, float (*red)[64], uint8_t* ring) {
   const int lane = opaque_lane(), w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1491,7 +1552,7 @@ __device__ void gateup_unit(const GateUpArgs& a, const uint8_t* wg, const uint8_
 
 // Gate/up unit u of the work list: chunk u / nbI, 128-row block u % nbI of the chunk's
 // expert (plus the slice offset of a shared-expert copy).
-__device__ void gateup_work(const GateUpArgs& a, int u, float (*red)[64], uint8_t* ring) {
+__device__ __forceinline__ void gateup_work(const GateUpArgs& a, int u, float (*red)[64], uint8_t* ring) {
   const int nbI = a.I / kBlock, nkb = a.H / kBlock;
   const int4 ch = a.chunks[u / nbI];
   const int j = u % nbI, jb = ch.w + j;
@@ -1546,7 +1607,7 @@ __device__ void gateup_work(const GateUpArgs& a, int u, float (*red)[64], uint8_
 // stores complete before its increment), and never read earlier in the kernel, so no
 // cache can hold a stale copy of it.
 template <int NCT>
-__device__ bool gateup_half(const GateUpArgs& a, const uint8_t* wt, const float* sc, const ChunkRows& cr, int jb,
+__device__ __forceinline__ bool gateup_half(const GateUpArgs& a, const uint8_t* wt, const float* sc, const ChunkRows& cr, int jb,
                             int half, uint8_t* hq, float* hs, uint16_t* st_mine, const uint16_t* st_other, int ldh,
                             int* pair, int rot, float (*red)[64], int* flag, uint8_t* ring) {
   const int lane = opaque_lane(), w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1650,7 +1711,7 @@ __device__ bool gateup_half(const GateUpArgs& a, const uint8_t* wt, const float*
 // Gate/up unit u of the work list: block pair u / 2 (chunk (u/2) / nbI, 128-row block
 // (u/2) % nbI of the chunk's expert, plus the slice offset of a shared-expert copy), half
 // u % 2 (gate, then up). Returns true if this unit completed the block of h.
-__device__ bool gateup_work_split(const GateUpArgs& a, int u, float (*red)[64], int* flag, uint8_t* ring) {
+__device__ __forceinline__ bool gateup_work_split(const GateUpArgs& a, int u, float (*red)[64], int* flag, uint8_t* ring) {
   const int nbI = a.I / kBlock, nkb = a.H / kBlock;
   const int pair = u >> 1, half = u & 1;
   const int4 ch = a.chunks[pair / nbI];
@@ -1715,7 +1776,7 @@ struct DownArgs {
 // owns rows 32w .. 32w+31. With one part the result is d in bf16; with several, each part
 // stores its fp32 partial to pd and the combine adds the parts in order before rounding.
 template <int NCT>
-__device__ void down_unit(const DownArgs& a, const uint8_t* wd, const float* sd, int ldk, const uint8_t* hq,
+__device__ __forceinline__ void down_unit(const DownArgs& a, const uint8_t* wd, const float* sd, int ldk, const uint8_t* hq,
                           const float* hs, const ChunkRows& cr, int j, int kp, uint16_t* d, float* pd,
                           int rot, const ReadyWait& ready, uint8_t* ring) {
   const int lane = opaque_lane(), w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1754,12 +1815,16 @@ __device__ void down_unit(const DownArgs& a, const uint8_t* wd, const float* sd,
 #pragma unroll
       for (int p = 0; p < 2; ++p) {
         const size_t o = (size_t)(cr.row0 + r) * a.H + (size_t)j * kBlock + 32 * w + 16 * p + 4 * (lane >> 4);
+        // Device-coherent stores: the combine (a later kernel, or a later unit of the
+        // single-launch kernel on another XCD) reads them.
         if (a.ks == 1) {
           const uint32_t lo = f32_to_bf16_bits(acc[p][c][0]) | (f32_to_bf16_bits(acc[p][c][1]) << 16);
           const uint32_t hi = f32_to_bf16_bits(acc[p][c][2]) | (f32_to_bf16_bits(acc[p][c][3]) << 16);
-          *reinterpret_cast<uint2*>(d + o) = make_uint2(lo, hi);
+          store_coherent(reinterpret_cast<uint64_t*>(d + o), (uint64_t)lo | ((uint64_t)hi << 32));
         } else {
-          *reinterpret_cast<f32x4*>(pd + o) = acc[p][c];
+          uint64_t* q = reinterpret_cast<uint64_t*>(pd + o);
+          store_coherent(q, (uint64_t)__float_as_uint(acc[p][c][0]) | ((uint64_t)__float_as_uint(acc[p][c][1]) << 32));
+          store_coherent(q + 1, (uint64_t)__float_as_uint(acc[p][c][2]) | ((uint64_t)__float_as_uint(acc[p][c][3]) << 32));
         }
       }
     }
@@ -1768,7 +1833,7 @@ __device__ void down_unit(const DownArgs& a, const uint8_t* wd, const float* sd,
 
 // Down unit v of the work list: chunk v / (nbH*ks), then 128-row block j of the down
 // matrix and K part kp (v % (nbH*ks) = j*ks + kp).
-__device__ void down_work(const DownArgs& a, int v, const ReadyWait& ready, uint8_t* ring) {
+__device__ __forceinline__ void down_work(const DownArgs& a, int v, const ReadyWait& ready, uint8_t* ring) {
   const int nbH = a.H / kBlock, nbI = a.I / kBlock;
   const int4 ch = a.chunks[v / (nbH * a.ks)];
   const int rem = v % (nbH * a.ks), j = rem / a.ks, kp = rem % a.ks;
@@ -1999,6 +2064,244 @@ __global__ __launch_bounds__(256, 2) void k_experts(ExpertArgs args) {
     if (threadIdx.x == 0) slot = next;
     __syncthreads();
     u = slot;
+  }
+}
+
+// =======================================================================================
+// The whole layer as one launch (megamoe_layer_forward). One persistent kernel drains one
+// queue whose order is the layer's dependency order:
+//
+//   norm units     one per token row (block form only): RMSNorm of x into the workspace
+//   router units   the router tiles of k_router (expert tile, split of H, token pass)
+//   select units   one per token: quantize the token's row of x (it needs nothing), wait
+//                  for every router unit, then sum the partials and route the token as
+//                  k_select does; the select unit that finishes last runs the permute
+//                  (histogram, scan, permutation, work lists) in its own workgroup
+//   expert units   the gate/up and down units of k_experts, from the permute's lists
+//   combine units  2048 outputs each, once every down unit is done
+//
+// A unit waits only for units earlier in the queue, each of which was claimed by a
+// workgroup that is running it, so every wait ends whatever number of workgroups the
+// device keeps resident (waits are also bounded in time, as in k_experts; a wait that
+// gives up sets the error word and the combine writes NaN). The hand-overs between units
+// follow k_experts' rule: data crosses workgroups as device-coherent stores, is published
+// by a counter raised after the stores completed, and no workgroup reads a line before
+// its last write.
+//
+// The control words (queue, counters, error) must be zero when a call starts: the
+// workspace is zeroed once when it is allocated, and the last workgroup to leave a call
+// zeroes them again, so a call is exactly one launch.
+// =======================================================================================
+
+constexpr int kCtlQueue = 0, kCtlNormed = 32, kCtlRouted = 64, kCtlSelected = 96, kCtlPermuted = 128,
+              kCtlDown = 160, kCtlExited = 192, kCtlError = 224, kCtlInts = 256;  // one 128-byte line each
+constexpr int kCombineUnit = 256 * 8;  // outputs per combine unit
+
+struct LayerArgs {
+  ExpertArgs ex;
+  const uint16_t* x_in;     // the layer's (or block's) input x [T, H]
+  const uint16_t* x;        // the rows the router and the experts read: x_in, or the normalized rows
+  const uint16_t* norm_w;   // bf16 gamma [H]; NULL: no normalization
+  uint16_t* xn;             // normalized rows [T, H] (workspace)
+  const float* router;
+  const float* bias;
+  double* partial;
+  int64_t* ids;
+  float* wts;
+  uint8_t* xq;
+  float* xs;
+  PermuteOut po;
+  uint16_t* y;
+  const uint16_t* residual;  // NULL: no residual add
+  int* ctl;
+  float eps, scaling;
+  int weight_in_fp32;
+  int T, H, E, K, S, G, TG, gate, renorm, pow2;
+  int nsplit, n_et, ntt, vpl, ks;
+  int n_norm, n_router;
+};
+
+// Thread 0 waits (bounded in time) until *count >= need, then the workgroup passes a barrier;
+// the acquire keeps the loads that follow below it.
+__device__ __forceinline__ void wait_count(const int* count, int need, int* error) {
+  wait_ready(ReadyWait{count, need, error});
+}
+
+__device__ __forceinline__ int load_count(const int* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// After a unit's stores: they complete, then thread 0 raises `count`.
+__device__ __forceinline__ int publish_count(int* count) {
+  publish_fence();
+  __syncthreads();
+  return threadIdx.x == 0 ? atomicAdd(count, 1) : 0;
+}
+
+template <int NTT>
+__device__ __forceinline__ void layer_router(const LayerArgs& a, int unit, uint8_t* lds) {
+  router_tile<NTT>(a.x, a.router, a.partial, a.T, a.H, a.E, a.n_et, a.nsplit, unit, reinterpret_cast<f64x4*>(lds));
+}
+
+template <int VPL>
+__device__ __forceinline__ void layer_select(const LayerArgs& a, int token, uint8_t* lds) {
+  select_token<VPL>(a.partial, a.nsplit, nullptr, a.bias, a.T, a.E, a.K, a.G, a.TG, a.gate, a.renorm, a.scaling,
+                    a.ids, a.wts, token, *reinterpret_cast<SelectLds*>(lds));
+}
+
+// Combine unit c: outputs [c * kCombineUnit, +kCombineUnit) of y, as k_combine.
+__device__ __forceinline__ void layer_combine(const LayerArgs& a, int c) {
+  const DownArgs& dn = a.ex.dn;
+  const int i = c * (kCombineUnit / 8) + threadIdx.x, per_row = a.H / 8;
+  if (i >= a.T * per_row) return;
+  if (load_count(&a.ctl[kCtlError])) {
+    *reinterpret_cast<uint4*>(a.y + (size_t)i * 8) = make_uint4(0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u);
+    return;
+  }
+  const int t = i / per_row, h0 = (i % per_row) * 8;
+  float acc[8];
+  if (a.ks > 1)
+    combine8_parts(dn.p_r, dn.p_s, a.ks, a.po.inv, a.wts, a.T, a.H, a.K, a.S, t, h0, acc);
+  else
+    combine8(dn.d_r, dn.d_s, a.po.inv, a.wts, a.H, a.K, a.S, t, h0, acc);
+  uint32_t o[4];
+  if (a.residual) {
+    const uint4 v = *reinterpret_cast<const uint4*>(a.residual + (size_t)t * a.H + h0);
+    const uint32_t q[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float lo = __fadd_rn(bf16_bits_to_f32(q[j] & 0xffffu), round_bf16(acc[2 * j]));
+      const float hi = __fadd_rn(bf16_bits_to_f32(q[j] >> 16), round_bf16(acc[2 * j + 1]));
+      o[j] = f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o[j] = f32_to_bf16_bits(acc[2 * j]) | (f32_to_bf16_bits(acc[2 * j + 1]) << 16);
+  }
+  *reinterpret_cast<uint4*>(a.y + (size_t)t * a.H + h0) = make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+template <bool SPLIT>
+__global__ __launch_bounds__(256, 2) void k_layer(LayerArgs args) {
+  typedef const __attribute__((address_space(4))) LayerArgs* ArgsPtr;
+  __shared__ float red[4][64];
+  __shared__ __attribute__((aligned(16))) uint8_t rings[4 * kRingWave];  // weight rings; front-end scratch
+  __shared__ int slot, flag, flags[2], units[2];
+  __shared__ double part[4];
+  static_assert(sizeof(LayerArgs) % 8 == 0, "argument segment layout");
+  static_assert(sizeof(SelectLds) <= sizeof(rings) && (kRouterWaves - 1) * 4 * 64 * sizeof(f64x4) <= sizeof(rings),
+                "front-end scratch in the rings");
+  int* ctl = args.ctl;
+  const int fixed = args.n_norm + args.n_router + args.T;  // units listed before the routing is known
+  int total = INT_MAX;                                      // every unit, once the permute has run
+  int n_gu = 0, n_dn = 0;
+  if (threadIdx.x == 0) slot = atomicAdd(&ctl[kCtlQueue], 1);
+  __syncthreads();
+  int u = slot, next = 0;
+  while (true) {
+    if (u >= fixed && total == INT_MAX) {
+      // The first unit past the select units: the work lists are known once the permute
+      // has run (its meta words were never read before in this call).
+      wait_count(&ctl[kCtlPermuted], 1, &ctl[kCtlError]);
+      if (threadIdx.x == 0) {
+        // If the wait gave up (error word set), the lists are not to be read: no expert
+        // units, only the combine units, which then write NaN.
+        const bool lists = load_count(&ctl[kCtlPermuted]) != 0;
+        units[0] = lists ? (SPLIT ? 2 : 1) * load_count(&args.po.meta[kMetaUnitsGU]) : 0;
+        units[1] = lists ? load_count(&args.po.meta[kMetaUnitsDN]) : 0;
+      }
+      __syncthreads();
+      n_gu = units[0];
+      n_dn = units[1];
+      total = fixed + n_gu + n_dn + (args.T * args.H + kCombineUnit - 1) / kCombineUnit;
+    }
+    if (u >= total) break;
+    // The arguments are re-read per unit (as in k_experts) so each unit derives its
+    // addresses afresh instead of every path's values being held across the loop.
+    ArgsPtr ap = (ArgsPtr)__builtin_amdgcn_kernarg_segment_ptr();
+    asm volatile("" : "+s"(ap));
+    LayerArgs a;
+    __builtin_memcpy(&a, (const LayerArgs*)ap, sizeof(a));
+    __syncthreads();
+    if (threadIdx.x == 0) next = atomicAdd(&ctl[kCtlQueue], 1);
+    if (u < a.n_norm) {
+      norm_row(a.x_in, a.norm_w, u, a.H, a.eps, a.weight_in_fp32, a.xn, part);
+      publish_count(&ctl[kCtlNormed]);
+    } else if (u < a.n_norm + a.n_router) {
+      if (a.n_norm) wait_count(&ctl[kCtlNormed], a.n_norm, &ctl[kCtlError]);
+      const int r = u - a.n_norm;
+      if (a.ntt == 1)
+        layer_router<1>(a, r, rings);
+      else if (a.ntt == 2)
+        layer_router<2>(a, r, rings);
+      else
+        layer_router<4>(a, r, rings);
+      publish_count(&ctl[kCtlRouted]);
+    } else if (u < fixed) {
+      const int t = u - a.n_norm - a.n_router;
+      if (a.n_norm) wait_count(&ctl[kCtlNormed], a.n_norm, &ctl[kCtlError]);
+      // This token's row of x in E4M3 per 128 (needs nothing else; runs while the router does).
+      const int nbh = a.H / kBlock, lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+      for (int b = wv; b < nbh; b += 4) {
+        const size_t o = (size_t)t * a.H + (size_t)b * kBlock;
+        quant_block4(a.x + o, a.xq + o, a.xs + (size_t)t * nbh + b, a.pow2, lane);
+      }
+      wait_count(&ctl[kCtlRouted], a.n_router, &ctl[kCtlError]);
+      if (a.vpl == 1)
+        layer_select<1>(a, t, rings);
+      else if (a.vpl == 2)
+        layer_select<2>(a, t, rings);
+      else if (a.vpl == 4)
+        layer_select<4>(a, t, rings);
+      else if (a.vpl == 8)
+        layer_select<8>(a, t, rings);
+      else
+        layer_select<16>(a, t, rings);
+      const int done = publish_count(&ctl[kCtlSelected]);
+      if (threadIdx.x == 0) flag = done == a.T - 1;
+      __syncthreads();
+      if (flag) {
+        // Every token is routed: this workgroup runs the permute, then publishes the lists.
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        permute_block(a.ids, 0, a.T, a.K, a.E, a.S, a.ex.gu.I / kBlock, a.H / kBlock, a.ks, kChunkRows, 0, a.po,
+                      reinterpret_cast<int*>(rings), flags);
+        publish_fence();
+        __syncthreads();
+        if (threadIdx.x == 0) __hip_atomic_store(&ctl[kCtlPermuted], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    } else if (u < fixed + n_gu) {
+      const int g = u - fixed, nbI = a.ex.gu.I / kBlock;
+      uint8_t* ring = rings + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) * kRingWave;
+      bool done = true;
+      if constexpr (SPLIT)
+        done = gateup_work_split(a.ex.gu, g, red, &flag, ring);
+      else
+        gateup_work(a.ex.gu, g, red, ring);
+      if (done) {
+        publish_fence();
+        __syncthreads();
+        if (threadIdx.x == 0) atomicAdd(&a.ex.ready[a.ex.dn_of_gu[(SPLIT ? g >> 1 : g) / nbI]], 1);
+      }
+    } else if (u < fixed + n_gu + n_dn) {
+      const int v = u - fixed - n_gu, nbI = a.ex.gu.I / kBlock, nbH = a.H / kBlock, c = v / (nbH * a.ks);
+      uint8_t* ring = rings + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) * kRingWave;
+      const ReadyWait ready{&a.ex.ready[c], a.ex.dn.chunks[c].x == a.E ? a.S * nbI : nbI, &ctl[kCtlError]};
+      down_work(a.ex.dn, v, ready, ring);
+      publish_count(&ctl[kCtlDown]);
+    } else {
+      wait_count(&ctl[kCtlDown], n_dn, &ctl[kCtlError]);
+      layer_combine(a, u - fixed - n_gu - n_dn);
+    }
+    if (threadIdx.x == 0) slot = next;
+    __syncthreads();
+    u = slot;
+  }
+  // Leaving: the last workgroup out (every other one has made its last claim) zeroes the
+  // control words for the next call.
+  if (threadIdx.x == 0 && atomicAdd(&ctl[kCtlExited], 1) == (int)gridDim.x - 1) {
+    const int words[] = {kCtlQueue, kCtlNormed, kCtlRouted, kCtlSelected, kCtlPermuted, kCtlDown, kCtlError,
+                         kCtlExited};
+    for (int w : words) __hip_atomic_store(&ctl[w], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -2989,7 +3292,7 @@ inline size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
 struct Layout {
   size_t xn, partial, xq, xs, counts, offsets, meta, perm, inv, gu, dn, dn_of_gu, ready, pairs, hq_r, hs_r, hq_s, hs_s,
-      st_r, st_s, d_r, d_s, p_r, p_s, spare, total;
+      st_r, st_s, d_r, d_s, p_r, p_s, spare, ctl, total;
   int nsplit;
   int ks;  // K parts of each down unit
 };
@@ -3068,6 +3371,7 @@ Layout make_layout(const megamoe_desc& d) {
   L.p_r = take(L.ks > 1 ? L.ks * T * K * H * sizeof(float) : 0);
   L.p_s = take(L.ks > 1 && S ? L.ks * T * H * sizeof(float) : 0);
   L.spare = take(16 * (H > I * (S > 1 ? S : 1) ? H : I * (S > 1 ? S : 1)));
+  L.ctl = take(kCtlInts * sizeof(int));  // the single-launch kernel's control words
   L.total = at;
   return L;
 }
@@ -3095,6 +3399,7 @@ struct DeviceInfo {
   int experts_per_cu = 0;     // resident k_experts workgroups per CU
   int experts_mx_per_cu = 0;  // resident k_experts_mx workgroups per CU
   int batch_mx_per_cu = 0;    // resident k_experts_mx_batch workgroups per CU
+  int layer_per_cu = 0;       // resident k_layer workgroups per CU
 };
 
 int device_info(DeviceInfo* out) {
@@ -3117,6 +3422,12 @@ int device_info(DeviceInfo* out) {
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_experts_mx_batch, 256, 0) != hipSuccess)
       return MEGAMOE_ERR_HIP;
     di.batch_mx_per_cu = per_cu > 0 ? per_cu : 1;
+    int per_cu_split2 = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_layer<false>, 256, 0) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu_split2, k_layer<true>, 256, 0) != hipSuccess)
+      return MEGAMOE_ERR_HIP;
+    per_cu = per_cu_split2 < per_cu ? per_cu_split2 : per_cu;
+    di.layer_per_cu = per_cu > 0 ? per_cu : 1;
     di.cus = cus > 0 ? cus : 1;
   }
   *out = di;
@@ -3200,6 +3511,47 @@ int launch_norm(int rows, int cols, const void* x, const void* w, float eps, int
   return MEGAMOE_OK;
 }
 
+PermuteOut make_permute_out(const Layout& L, char* ws) {
+  return PermuteOut{(int*)(ws + L.counts), (int*)(ws + L.offsets), (int*)(ws + L.meta), (int*)(ws + L.perm),
+                    (int*)(ws + L.inv),    (int4*)(ws + L.gu),     (int4*)(ws + L.dn),  (int*)(ws + L.dn_of_gu),
+                    (int*)(ws + L.ready),  (int*)(ws + L.pairs)};
+}
+
+// The expert kernels' arguments for a forward call over workspace `ws`.
+void fill_expert_args(const megamoe_desc& d, const Layout& L, const megamoe_tensors* t, char* ws,
+                      const PermuteOut& po, const megamoe_epilogue* epi, ExpertArgs& ea) {
+  const int T = d.tokens, H = d.hidden, E = d.experts, K = d.topk, I = d.intermediate, S = d.shared_experts;
+  GateUpArgs& ga = ea.gu;
+  ga.xq = (const uint8_t*)(ws + L.xq);
+  ga.xs = (const float*)(ws + L.xs);
+  ga.gate = t->gate; ga.gate_scale = t->gate_scale;
+  ga.up = t->up; ga.up_scale = t->up_scale;
+  ga.sgate = t->shared_gate; ga.sgate_scale = t->shared_gate_scale;
+  ga.sup = t->shared_up; ga.sup_scale = t->shared_up_scale;
+  ga.offsets = po.offsets; ga.perm = po.perm; ga.chunks = po.gu; ga.meta = po.meta;
+  ga.hq_r = (uint8_t*)(ws + L.hq_r); ga.hs_r = (float*)(ws + L.hs_r);
+  ga.hq_s = (uint8_t*)(ws + L.hq_s); ga.hs_s = (float*)(ws + L.hs_s);
+  ga.st_r = (uint16_t*)(ws + L.st_r); ga.st_s = (uint16_t*)(ws + L.st_s);
+  ga.pairs = po.pairs;
+  ga.spare = (const uint8_t*)(ws + L.spare);
+  ga.T = T; ga.H = H; ga.I = I; ga.K = K; ga.S = S; ga.E = E; ga.pow2 = d.pow2_scales;
+  ga.swiglu = epi ? epi->swiglu : 0;
+  ga.limit = epi ? epi->swiglu_limit : 0.0f;
+  DownArgs& da = ea.dn;
+  da.down = t->down; da.down_scale = t->down_scale;
+  da.sdown = t->shared_down; da.sdown_scale = t->shared_down_scale;
+  da.offsets = po.offsets; da.perm = po.perm; da.chunks = po.dn; da.meta = po.meta;
+  da.hq_r = ga.hq_r; da.hs_r = ga.hs_r; da.hq_s = ga.hq_s; da.hs_s = ga.hs_s;
+  da.d_r = (uint16_t*)(ws + L.d_r); da.d_s = (uint16_t*)(ws + L.d_s);
+  da.spare = ga.spare;
+  da.p_r = (float*)(ws + L.p_r);
+  da.p_s = (float*)(ws + L.p_s);
+  da.ks = L.ks;
+  da.T = T; da.H = H; da.I = I; da.K = K; da.S = S; da.E = E;
+  ea.dn_of_gu = po.dn_of_gu;
+  ea.ready = po.ready;
+}
+
 // The layer; with `blk`, the block form: RMSNorm of x before the router (the layer then
 // reads the normalized rows) and the residual add in the combine.
 int forward_impl(const megamoe_desc* desc, const megamoe_tensors* t, hipStream_t st, hipEvent_t* ev,
@@ -3242,9 +3594,7 @@ int forward_impl(const megamoe_desc* desc, const megamoe_tensors* t, hipStream_t
     return rc;
   if (mark(2) != hipSuccess) return MEGAMOE_ERR_HIP;
 
-  PermuteOut po{(int*)(ws + L.counts), (int*)(ws + L.offsets), (int*)(ws + L.meta), (int*)(ws + L.perm),
-                (int*)(ws + L.inv),    (int4*)(ws + L.gu),     (int4*)(ws + L.dn),  (int*)(ws + L.dn_of_gu),
-                (int*)(ws + L.ready),  (int*)(ws + L.pairs)};
+  const PermuteOut po = make_permute_out(L, ws);
   const int nbI = I / kBlock, nbH = H / kBlock;
   const size_t lds = ((size_t)E * (1 + (T + 31) / 32) + 32) * 4;
   hipLaunchKernelGGL(k_permute, dim3(1), dim3(1024), lds, st, t->expert_ids, (int64_t)0, T, K, E, S, nbI, nbH, L.ks,
@@ -3253,35 +3603,9 @@ int forward_impl(const megamoe_desc* desc, const megamoe_tensors* t, hipStream_t
   if (mark(3) != hipSuccess) return MEGAMOE_ERR_HIP;
 
   ExpertArgs ea;
-  GateUpArgs& ga = ea.gu;
-  ga.xq = (const uint8_t*)(ws + L.xq);
-  ga.xs = (const float*)(ws + L.xs);
-  ga.gate = t->gate; ga.gate_scale = t->gate_scale;
-  ga.up = t->up; ga.up_scale = t->up_scale;
-  ga.sgate = t->shared_gate; ga.sgate_scale = t->shared_gate_scale;
-  ga.sup = t->shared_up; ga.sup_scale = t->shared_up_scale;
-  ga.offsets = po.offsets; ga.perm = po.perm; ga.chunks = po.gu; ga.meta = po.meta;
-  ga.hq_r = (uint8_t*)(ws + L.hq_r); ga.hs_r = (float*)(ws + L.hs_r);
-  ga.hq_s = (uint8_t*)(ws + L.hq_s); ga.hs_s = (float*)(ws + L.hs_s);
-  ga.st_r = (uint16_t*)(ws + L.st_r); ga.st_s = (uint16_t*)(ws + L.st_s);
-  ga.pairs = po.pairs;
-  ga.spare = (const uint8_t*)(ws + L.spare);
-  ga.T = T; ga.H = H; ga.I = I; ga.K = K; ga.S = S; ga.E = E; ga.pow2 = d.pow2_scales;
-  ga.swiglu = epi ? epi->swiglu : 0;
-  ga.limit = epi ? epi->swiglu_limit : 0.0f;
-  DownArgs& da = ea.dn;
-  da.down = t->down; da.down_scale = t->down_scale;
-  da.sdown = t->shared_down; da.sdown_scale = t->shared_down_scale;
-  da.offsets = po.offsets; da.perm = po.perm; da.chunks = po.dn; da.meta = po.meta;
-  da.hq_r = ga.hq_r; da.hs_r = ga.hs_r; da.hq_s = ga.hq_s; da.hs_s = ga.hs_s;
-  da.d_r = (uint16_t*)(ws + L.d_r); da.d_s = (uint16_t*)(ws + L.d_s);
-  da.spare = ga.spare;
-  da.p_r = (float*)(ws + L.p_r);
-  da.p_s = (float*)(ws + L.p_s);
-  da.ks = L.ks;
-  da.T = T; da.H = H; da.I = I; da.K = K; da.S = S; da.E = E;
-  ea.dn_of_gu = po.dn_of_gu;
-  ea.ready = po.ready;
+  fill_expert_args(d, L, t, ws, po, epi, ea);
+  const GateUpArgs& ga = ea.gu;
+  const DownArgs& da = ea.dn;
   // As many workgroups as fit on the device at once, and no more than the most units the
   // routing can produce.
   const bool split = split_gate_up(d);
@@ -3303,6 +3627,82 @@ int forward_impl(const megamoe_desc* desc, const megamoe_tensors* t, hipStream_t
                      (const uint16_t*)(blk && blk->residual ? t->x : nullptr), (uint16_t*)t->y);
   MEGAMOE_LAUNCH_CHECK();
   if (mark(5) != hipSuccess) return MEGAMOE_ERR_HIP;
+  return MEGAMOE_OK;
+}
+
+// The layer (with `blk`, the block form) as one launch of k_layer; see the kernel for the
+// unit queue. `ev` is NULL or two events, recorded before and after the launch.
+int forward_layer_impl(const megamoe_desc* desc, const megamoe_tensors* t, const megamoe_block* blk,
+                       const megamoe_epilogue* epi, hipStream_t st, hipEvent_t* ev) {
+  int rc = validate(desc);
+  if (rc) return rc;
+  if (!t) return MEGAMOE_ERR_INVALID_ARGUMENT;
+  if (blk && !(blk->eps >= 0.0f)) return MEGAMOE_ERR_INVALID_ARGUMENT;
+  const megamoe_desc& d = *desc;
+  auto mark = [&](int i) { return ev ? hipEventRecord(ev[i], st) : hipSuccess; };
+  if (d.tokens == 0) return (mark(0) == hipSuccess && mark(1) == hipSuccess) ? MEGAMOE_OK : MEGAMOE_ERR_HIP;
+  if (!t->x || !t->router || !t->gate || !t->gate_scale || !t->up || !t->up_scale || !t->down ||
+      !t->down_scale || !t->y || !t->expert_ids || !t->expert_weights || !t->workspace)
+    return MEGAMOE_ERR_INVALID_ARGUMENT;
+  if (d.shared_experts > 0 && (!t->shared_gate || !t->shared_gate_scale || !t->shared_up ||
+                               !t->shared_up_scale || !t->shared_down || !t->shared_down_scale))
+    return MEGAMOE_ERR_INVALID_ARGUMENT;
+  const Layout L = make_layout(d);
+  if (t->workspace_bytes < L.total) return MEGAMOE_ERR_WORKSPACE;
+  DeviceInfo di;
+  if ((rc = device_info(&di))) return rc;
+  char* ws = (char*)t->workspace;
+  const int T = d.tokens, H = d.hidden, E = d.experts, I = d.intermediate, S = d.shared_experts;
+  const int nbI = I / kBlock, nbH = H / kBlock;
+
+  LayerArgs la{};
+  la.po = make_permute_out(L, ws);
+  fill_expert_args(d, L, t, ws, la.po, epi, la.ex);
+  const bool norm = blk && blk->norm_weight;
+  la.x_in = (const uint16_t*)t->x;
+  la.xn = (uint16_t*)(ws + L.xn);
+  la.x = norm ? la.xn : la.x_in;
+  la.norm_w = norm ? (const uint16_t*)blk->norm_weight : nullptr;
+  la.eps = blk ? blk->eps : 0.0f;
+  la.weight_in_fp32 = blk ? blk->weight_in_fp32 : 0;
+  la.router = t->router;
+  la.bias = t->router_bias;
+  la.partial = (double*)(ws + L.partial);
+  la.ids = t->expert_ids;
+  la.wts = t->expert_weights;
+  la.xq = (uint8_t*)(ws + L.xq);
+  la.xs = (float*)(ws + L.xs);
+  la.y = (uint16_t*)t->y;
+  la.residual = blk && blk->residual ? (const uint16_t*)t->x : nullptr;
+  la.ctl = (int*)(ws + L.ctl);
+  la.scaling = d.routed_scaling;
+  la.T = T; la.H = H; la.E = E; la.K = d.topk; la.S = S; la.G = d.groups; la.TG = d.top_groups;
+  la.gate = d.gate; la.renorm = d.renormalize; la.pow2 = d.pow2_scales;
+  la.nsplit = L.nsplit;
+  la.n_et = (E + kRouterTile - 1) / kRouterTile;
+  const int tiles = (T + kRouterTile - 1) / kRouterTile;
+  la.ntt = tiles <= 1 ? 1 : (tiles <= 2 ? 2 : 4);
+  const int passes = (tiles + la.ntt - 1) / la.ntt;
+  la.vpl = E <= 64 ? 1 : (E <= 128 ? 2 : (E <= 256 ? 4 : (E <= 512 ? 8 : 16)));
+  la.ks = L.ks;
+  la.n_norm = norm ? T : 0;
+  la.n_router = la.n_et * la.nsplit * passes;
+
+  // As many workgroups as fit on the device at once, and no more than the most units the
+  // queue can hold.
+  const bool split = split_gate_up(d);
+  const size_t units_max = (size_t)la.n_norm + la.n_router + T + (split ? 2 : 1) * max_chunks(d, S) * (size_t)nbI +
+                           max_chunks(d, S > 0 ? 1 : 0) * (size_t)nbH * L.ks +
+                           ((size_t)T * H + kCombineUnit - 1) / kCombineUnit;
+  const size_t resident = (size_t)di.cus * di.layer_per_cu;
+  const unsigned grid = (unsigned)(units_max < resident ? units_max : resident);
+  if (mark(0) != hipSuccess) return MEGAMOE_ERR_HIP;
+  if (split)
+    hipLaunchKernelGGL(k_layer<true>, dim3(grid), dim3(256), 0, st, la);
+  else
+    hipLaunchKernelGGL(k_layer<false>, dim3(grid), dim3(256), 0, st, la);
+  MEGAMOE_LAUNCH_CHECK();
+  if (mark(1) != hipSuccess) return MEGAMOE_ERR_HIP;
   return MEGAMOE_OK;
 }
 
@@ -3705,7 +4105,7 @@ int scratch_address(void** out) {
 
 extern "C" {
 
-int megamoe_abi_version(void) { return 6; }
+int megamoe_abi_version(void) { return 7; }
 
 const char* megamoe_status_string(int status) {
   switch (status) {
@@ -3730,6 +4130,17 @@ int megamoe_workspace_bytes(const megamoe_desc* desc, size_t* bytes) {
 
 int megamoe_forward(const megamoe_desc* desc, const megamoe_tensors* t, void* stream) {
   return forward_impl(desc, t, (hipStream_t)stream, nullptr);
+}
+
+int megamoe_layer_forward(const megamoe_desc* desc, const megamoe_tensors* t, const megamoe_block* block,
+                          const megamoe_epilogue* epilogue, void* stream, void* const* events) {
+  hipEvent_t ev[2];
+  if (events) {
+    if (!events[0] || !events[1]) return MEGAMOE_ERR_INVALID_ARGUMENT;
+    ev[0] = (hipEvent_t)events[0];
+    ev[1] = (hipEvent_t)events[1];
+  }
+  return forward_layer_impl(desc, t, block, epilogue, (hipStream_t)stream, events ? ev : nullptr);
 }
 
 int megamoe_forward_noalloc(const megamoe_desc* desc, const megamoe_tensors* t, void* stream) {
