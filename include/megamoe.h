@@ -228,6 +228,16 @@ int megamoe_forward_ex(const megamoe_desc* desc, const megamoe_tensors* t, const
 int megamoe_layer_forward(const megamoe_desc* desc, const megamoe_tensors* t, const megamoe_block* block,
                           const megamoe_epilogue* epilogue, void* stream, void* const* events);
 
+/* Outcome of the last megamoe_layer_forward (or megamoe_forward / megamoe_forward_ex) call on
+ * `workspace`: *gave_up = 1 if one of its bounded waits between workgroups gave up (after
+ * 0.2 s; every kernel still ends, and y is NaN), else 0. Synchronizes `stream` (a host call
+ * that copies one word). No reference counterpart: the reference's eager layer has no
+ * waits. Test hook: with the environment variable MEGAMOE_FORCE_WAIT_TIMEOUT=1,
+ * megamoe_layer_forward's combine units wait for one more down unit than there is, for
+ * 20 us, so the call reports a wait that gave up. */
+int megamoe_layer_status(const megamoe_desc* desc, const void* workspace, size_t workspace_bytes, int32_t* gave_up,
+                         void* stream);
+
 /* GPT-OSS's combine (gptoss.py:112-124): per token t, its K expert outputs (bf16
  * expert_out [T*K, H], row t*K + k for slot k) accumulate in ascending expert id order
  * (expert_ids int64 [T*K], distinct within a token; a repeated id counts once), in bf16:
@@ -333,11 +343,11 @@ int megamoe_quantize_rows(int32_t rows, int32_t cols, const void* x, uint8_t* q,
 /* Text for a status code (static storage). */
 const char* megamoe_status_string(int status);
 
-/* ABI version of this library: 7 (1, plus megamoe_block_forward and megamoe_rms_norm in 2,
+/* ABI version of this library: 8 (1, plus megamoe_block_forward and megamoe_rms_norm in 2,
  * plus megamoe_mx_workspace_bytes and megamoe_mx_forward in 3, plus megamoe_ep_dispatch,
  * megamoe_ep_experts and megamoe_ep_combine in 4, plus megamoe_forward_ex and
  * megamoe_combine_by_expert_id in 5, plus megamoe_forward_noalloc in 6, plus
- * megamoe_layer_forward in 7). */
+ * megamoe_layer_forward in 7, plus megamoe_layer_status in 8). */
 int megamoe_abi_version(void);
 
 #ifdef __cplusplus

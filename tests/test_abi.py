@@ -37,7 +37,7 @@ def test_library_exports_every_declared_function():
 
 def test_version_and_status_strings():
     lib = _lib.load()
-    assert lib.megamoe_abi_version() == _lib.ABI_VERSION == 7
+    assert lib.megamoe_abi_version() == _lib.ABI_VERSION == 8
     texts = {code: _lib.status_string(code) for code in range(7)}
     assert texts[_lib.OK] == "ok" and len(set(texts.values())) == 7
     assert _lib.status_string(99) == "unknown status"
@@ -167,10 +167,31 @@ def test_ep_and_variant_entry_points_check_arguments_before_any_gpu_call():
     for bad in (_lib.Epilogue(swiglu=2, swiglu_limit=0.0), _lib.Epilogue(swiglu=1, swiglu_limit=-1.0),
                 _lib.Epilogue(swiglu=0, swiglu_limit=float("nan"))):
         assert lib.megamoe_forward_ex(P(d8), P(ft), None, P(bad), None, None) == _lib.ERR_INVALID_ARGUMENT
+        assert lib.megamoe_layer_forward(P(d8), P(ft), None, P(bad), None, None) == _lib.ERR_INVALID_ARGUMENT
     ok = _lib.Epilogue(swiglu=1, swiglu_limit=10.0)
     assert lib.megamoe_forward_ex(P(d8), P(ft), None, P(ok), None, None) == _lib.ERR_INVALID_ARGUMENT  # no tensors
+    assert lib.megamoe_layer_forward(P(d8), P(ft), None, P(ok), None, None) == _lib.ERR_INVALID_ARGUMENT
+    blk = _lib.Block(norm_weight=None, eps=-1.0, weight_in_fp32=1, residual=1)
+    assert lib.megamoe_layer_forward(P(d8), P(ft), P(blk), None, None, None) == _lib.ERR_INVALID_ARGUMENT  # eps < 0
     d8.tokens = 0
     assert lib.megamoe_forward_ex(P(d8), P(ft), None, P(ok), None, None) == _lib.OK
+    assert lib.megamoe_layer_forward(P(d8), P(ft), None, P(ok), None, None) == _lib.OK
+
+
+def test_permute_limits_allow_a_full_ep_share():
+    """The permute ranks rows without its token bitmap when the bitmap would not fit in LDS,
+    so the local experts accept every received-row count a rank can get: ep 8 x 512 tokens x
+    6 slots = 24576 rows over 48 local experts (and the fp8 layer any token count whose
+    packed counters fit)."""
+    lib = _lib.load()
+    size = ctypes.c_size_t(0)
+    for rows in (1, 10000, 24576, 49152):
+        d = _lib.Desc(tokens=rows, hidden=7168, experts=48, topk=1, intermediate=3072)
+        assert lib.megamoe_mx_workspace_bytes(ctypes.byref(d), ctypes.byref(size)) == _lib.OK, rows
+    for tokens in (64, 4096, 16384):
+        d = submission.make_desc(C.Case.from_dict({**C.case(C.HEADLINE).to_dict(), "id": "t",
+                                                   "params": {**C.case(C.HEADLINE).params, "tokens": tokens}}))
+        assert lib.megamoe_workspace_bytes(ctypes.byref(d), ctypes.byref(size)) == _lib.OK, tokens
 
 
 def test_case_table_of_the_forms():

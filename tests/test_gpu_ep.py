@@ -181,3 +181,41 @@ def test_empty_share():
     out = EP.Experts(*(values[k][:local] for k in WEIGHTS), 0, case.swiglu_limit)(
         z8, zs, torch.empty(0, dtype=torch.int64, device=DEV), torch.empty(0, dtype=torch.float32, device=DEV))
     assert out.shape == (0, H)
+
+
+def test_worst_case_received_rows():
+    """A rank that receives every row its 8 senders can send it (ep 8 x 512 tokens x 6 slots =
+    24576 rows over its 48 local experts, heavily skewed): beyond the permute's token bitmap,
+    so the ranking runs in tiles. Each row's result depends only on the row and its expert,
+    so the call equals the same rows worked in eight calls of 3072 (bitmap form), bit for bit,
+    and sampled experts are within the layer's bars of the oracle."""
+    local, R, H, I = 48, 24576, 256, 256
+    case = replace(EPCASE, id="ep-worst", params=dict(tokens=R, experts=local, topk=1, hidden=H, intermediate=I))
+    _log(f"ep worst case: {R} received rows over {local} local experts")
+    serial = replace(case, gpus=1, ep=1)
+    values = workloads.make_mx_inputs(serial, 77)
+    g = torch.Generator().manual_seed(5)
+    # Zipf-like skew: expert e with weight (e+1)^-1.1, a few hot experts
+    p = torch.arange(1, local + 1, dtype=torch.float64).pow(-1.1)
+    ids = torch.multinomial(p / p.sum(), R, replacement=True, generator=g).to(torch.int64)
+    gpu = {k: v.to(DEV) for k, v in values.items()}
+    rows, scales = gpu["x"], gpu["x_scales"]
+    wts = gpu["topk_weights"][:, 0].contiguous()
+    experts = EP.Experts(*(gpu[k] for k in WEIGHTS), 0, case.swiglu_limit)
+    ids_d = ids.to(DEV)
+    whole = experts(rows, scales, ids_d, wts)
+    parts = torch.cat([experts(rows[i:i + 3072], scales[i:i + 3072], ids_d[i:i + 3072], wts[i:i + 3072])
+                       for i in range(0, R, 3072)])
+    torch.cuda.synchronize()
+    assert torch.isfinite(whole.float()).all()
+    assert torch.equal(whole, parts)
+    hot = torch.bincount(ids, minlength=local)
+    for e in (int(hot.argmax()), int(hot.argmin())):
+        sel = (ids == e).nonzero().flatten()[:64]
+        weights = {k: values[k][e:e + 1] for k in WEIGHTS}
+        args = (values["x"][sel].view(torch.uint8), values["x_scales"][sel], ids[sel], values["topk_weights"][sel, 0])
+        want = OE.experts(case, weights, *args, base=e)
+        exact = OE.experts(case, weights, *args, base=e, widen=True)
+        got = whole.cpu()[sel]
+        assert metrics.layer_checks(got, want)["pass"], e
+        assert metrics.band(want, got, exact, bf16_rtol=case.bf16_rtol, noise_factor=case.noise_factor)["pass"], e

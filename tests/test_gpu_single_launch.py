@@ -90,3 +90,26 @@ def test_one_call_is_one_kernel_launch():
     _log(f"device events of one call: {kernels}")
     assert len(kernels) == 1 and "k_layer" in kernels[0], kernels
     assert dev.max_gpu_launches == 1
+
+
+def test_a_wait_that_gives_up_is_reported(monkeypatch):
+    """The test hook makes the combine units wait for one down unit more than there is, for
+    20 us: every kernel ends, y is NaN, and the status word reports it; the next call on the
+    same workspace is whole again and reports nothing."""
+    case = C.development(C.case(C.HEADLINE))
+    layer = submission.MoELayer(case)
+    values = _to(workloads.make_inputs(case, 8, "cpu"))
+    good = layer(values)
+    torch.cuda.synchronize()
+    assert not layer.gave_up(torch.device(DEV))
+    monkeypatch.setenv("MEGAMOE_FORCE_WAIT_TIMEOUT", "1")
+    bad = layer(values)
+    torch.cuda.synchronize()
+    assert torch.isnan(bad["y"].float()).all()
+    assert torch.equal(bad["expert_ids"], good["expert_ids"])
+    assert layer.gave_up(torch.device(DEV))
+    monkeypatch.delenv("MEGAMOE_FORCE_WAIT_TIMEOUT")
+    again = layer(values)
+    torch.cuda.synchronize()
+    _same(again, good, "after a forced give-up")
+    assert not layer.gave_up(torch.device(DEV))

@@ -25,8 +25,8 @@ SYMBOLS = ("megamoe_workspace_bytes", "megamoe_forward", "megamoe_forward_events
            "megamoe_abi_version", "megamoe_block_forward", "megamoe_rms_norm", "megamoe_mx_workspace_bytes",
            "megamoe_mx_forward", "megamoe_ep_dispatch", "megamoe_ep_experts", "megamoe_ep_combine",
            "megamoe_forward_ex", "megamoe_combine_by_expert_id", "megamoe_forward_noalloc",
-           "megamoe_layer_forward")
-ABI_VERSION = 7
+           "megamoe_layer_forward", "megamoe_layer_status")
+ABI_VERSION = 8
 
 
 class Desc(ctypes.Structure):
@@ -108,6 +108,7 @@ def load() -> ctypes.CDLL:
                                        c_void_p]
     lib.megamoe_forward_ex.argtypes = [P(Desc), P(Tensors), P(Block), P(Epilogue), c_void_p, P(c_void_p)]
     lib.megamoe_layer_forward.argtypes = [P(Desc), P(Tensors), P(Block), P(Epilogue), c_void_p, P(c_void_p)]
+    lib.megamoe_layer_status.argtypes = [P(Desc), c_void_p, c_size_t, P(ctypes.c_int32), c_void_p]
     lib.megamoe_combine_by_expert_id.argtypes = [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, c_void_p, c_void_p,
                                                  c_void_p, c_void_p, c_void_p, c_void_p]
     lib.megamoe_status_string.argtypes = [c_int]

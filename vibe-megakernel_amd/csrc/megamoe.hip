@@ -32,6 +32,7 @@
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <mutex>
+#include <stdlib.h>
 #include <type_traits>
 #include <stdint.h>
 #include <string.h>
@@ -897,20 +898,33 @@ __device__ __forceinline__ void store_coherent(int4* p, int4 v) {
 
 // The permute by one workgroup of any size (a multiple of 64, at least 256): thread i owns
 // the contiguous experts [i*ept, i*ept + ept) (ept = ceil(E / threads)), so the scan over
-// threads runs in expert order. LDS: `smem` holds 32 + E + E*ceil(T/32) ints; flags[0..1]
-// are two more. Every output goes out as a device-coherent store: the single-launch
-// kernel's expert units read them from other workgroups.
-__device__ __forceinline__ void permute_block(const int64_t* __restrict__ ids, int64_t base, int T, int K, int E, int S, int nbI,
-                              int nbH, int ks, int chunk, int wide, const PermuteOut& out, int* smem, int* flags) {
+// threads runs in expert order. Every output goes out as a device-coherent store: the
+// single-launch kernel's expert units read them from other workgroups.
+//
+// An entry's row within its expert is its rank among the entries of that expert in (token,
+// slot) order, i.e. the number of earlier entries of the flat [T*K] id array with the same
+// expert (a token picks an expert at most once). Two ways to count it:
+//   tile_waves == 0: a per-expert token bitmap in LDS and a popcount (32 + E + E*ceil(T/32)
+//     ints of `smem`);
+//   tile_waves > 0: without the bitmap, for any T: the entries in tiles of 64*tile_waves,
+//     each wavefront of a tile ranking its 64 entries with a ballot per distinct expert,
+//     the tile's waves added per expert in wave order through LDS, and a running count per
+//     expert across tiles (32 + E + E*tile_waves ints). Repeated ids within a token are
+//     found by comparing each entry with its token's other slots.
+// flags[0..1] are two more LDS ints.
+__device__ __forceinline__ void permute_block(const int64_t* __restrict__ ids, int64_t base, int T, int K, int E,
+                                              int S, int nbI, int nbH, int ks, int chunk, int wide,
+                                              const PermuteOut& out, int* smem, int* flags, int tile_waves = 0) {
   int* bad = flags;
   int* hits = flags + 1;
   unsigned long long* tmp = (unsigned long long*)smem;  // 16
   int* cnt = smem + 32;                                  // E
-  unsigned* bm = (unsigned*)(cnt + E);                   // E * words
+  unsigned* bm = (unsigned*)(cnt + E);                   // E * words (bitmap), or tile_waves * E (tiles)
   const int words = (T + 31) / 32;
   const int tid = threadIdx.x, nt = blockDim.x, n = T * K;
   for (int i = tid; i < E; i += nt) cnt[i] = 0;
-  for (int i = tid; i < E * words; i += nt) bm[i] = 0u;
+  if (!tile_waves)
+    for (int i = tid; i < E * words; i += nt) bm[i] = 0u;
   if (tid == 0) {
     *bad = 0;
     *hits = 0;
@@ -925,7 +939,12 @@ __device__ __forceinline__ void permute_block(const int64_t* __restrict__ ids, i
     }
     const int e = (int)e64;
     atomicAdd(&cnt[e], 1);
-    if (atomicOr(&bm[e * words + (t >> 5)], 1u << (t & 31)) & (1u << (t & 31))) *bad = 1;
+    if (!tile_waves) {
+      if (atomicOr(&bm[e * words + (t >> 5)], 1u << (t & 31)) & (1u << (t & 31))) *bad = 1;
+    } else {
+      for (int k2 = 0; k2 < K; ++k2)
+        if (t * K + k2 != i && ids[t * K + k2] == ids[i]) *bad = 1;
+    }
   }
   __syncthreads();
   if (*bad) {
@@ -1030,23 +1049,84 @@ __device__ __forceinline__ void permute_block(const int64_t* __restrict__ ids, i
   if (out.pairs)
     for (int i = tid; i < (S * (s4 + s2 + s1) + t4 + t2 + t1) * nbI; i += nt) store_coherent(&out.pairs[i], 0);
   __syncthreads();
-  for (int i = tid; i < n; i += nt) {
-    const int e = (int)(ids[i] - base), t = i / K;
-    const unsigned* row = bm + e * words;
-    int rank = __popc(row[t >> 5] & ((1u << (t & 31)) - 1u));
-    for (int q = 0; q < (t >> 5); ++q) rank += __popc(row[q]);
-    const int pos = cnt[e] + rank;
-    store_coherent(&out.perm[pos], i);
-    store_coherent(&out.inv[i], pos);
+  if (!tile_waves) {
+    for (int i = tid; i < n; i += nt) {
+      const int e = (int)(ids[i] - base), t = i / K;
+      const unsigned* row = bm + e * words;
+      int rank = __popc(row[t >> 5] & ((1u << (t & 31)) - 1u));
+      for (int q = 0; q < (t >> 5); ++q) rank += __popc(row[q]);
+      const int pos = cnt[e] + rank;
+      store_coherent(&out.perm[pos], i);
+      store_coherent(&out.inv[i], pos);
+    }
+    return;
+  }
+  // Tiles of 64 * tile_waves entries (cnt[e] holds the running first free row of expert e).
+  int* wcount = reinterpret_cast<int*>(bm);  // [tile_waves][E]
+  const int lane = tid & 63, w = tid >> 6, tile = 64 * tile_waves;
+  for (int b0 = 0; b0 < n; b0 += tile) {
+    for (int q = tid; q < tile_waves * E; q += nt) wcount[q] = 0;
+    __syncthreads();
+    const int i = b0 + tid;
+    const bool live = w < tile_waves && i < n;
+    const int e = live ? (int)(ids[i] - base) : -1;
+    int my_rank = 0;
+    if (w < tile_waves) {
+      unsigned long long rest = __ballot(live);
+      while (rest) {
+        const int leader = __ffsll((long long)rest) - 1;
+        const int le = __shfl(e, leader);
+        const unsigned long long m = __ballot(live && e == le);
+        if (live && e == le) my_rank = __popcll(m & lanes_below());
+        if (lane == 0) wcount[w * E + le] = __popcll(m);
+        rest &= ~m;
+      }
+    }
+    __syncthreads();
+    if (live) {
+      int pos = cnt[e] + my_rank;
+      for (int q = 0; q < w; ++q) pos += wcount[q * E + e];
+      store_coherent(&out.perm[pos], i);
+      store_coherent(&out.inv[i], pos);
+    }
+    __syncthreads();
+    for (int q = tid; q < E; q += nt) {
+      int add = 0;
+      for (int v = 0; v < tile_waves; ++v) add += wcount[v * E + q];
+      cnt[q] += add;
+    }
+    __syncthreads();
   }
 }
 
+// LDS ints of permute_block: the bitmap form when it fits in `capacity` ints, else the tiled
+// form with as many waves per tile as fit (up to the workgroup's). Returns the tile waves
+// (0: bitmap) or -1 if neither fits.
+__host__ __device__ inline int permute_tile_waves(int T, int E, int threads, int capacity) {
+  const size_t words = ((size_t)T + 31) / 32;
+  if ((size_t)E * (1 + words) + 32 <= (size_t)capacity) return 0;
+  const int fit = (capacity - 32 - E) / E, waves = threads / 64;
+  return fit >= 1 ? (fit < waves ? fit : waves) : -1;
+}
+constexpr int kPermuteLdsInts = 16384;  // 64 KB
+
 __global__ __launch_bounds__(1024) void k_permute(const int64_t* __restrict__ ids, int64_t base, int T, int K, int E,
                                                   int S, int nbI, int nbH, int ks, int chunk, int wide,
-                                                  PermuteOut out) {
+                                                  PermuteOut out, int tile_waves) {
   extern __shared__ int smem[];
   __shared__ int flags[2];
-  permute_block(ids, base, T, K, E, S, nbI, nbH, ks, chunk, wide, out, smem, flags);
+  permute_block(ids, base, T, K, E, S, nbI, nbH, ks, chunk, wide, out, smem, flags, tile_waves);
+}
+
+// Launches k_permute with the LDS its form needs.
+int launch_permute(const int64_t* ids, int64_t base, int T, int K, int E, int S, int nbI, int nbH, int ks, int chunk,
+                   int wide, const PermuteOut& po, hipStream_t st) {
+  const int tw = permute_tile_waves(T, E, 1024, kPermuteLdsInts);
+  if (tw < 0) return MEGAMOE_ERR_UNSUPPORTED;
+  const size_t ints = tw ? 32 + (size_t)E * (1 + tw) : 32 + (size_t)E * (1 + (T + 31) / 32);
+  hipLaunchKernelGGL(k_permute, dim3(1), dim3(1024), ints * 4, st, ids, base, T, K, E, S, nbI, nbH, ks, chunk, wide,
+                     po, tw);
+  return hipGetLastError() == hipSuccess ? MEGAMOE_OK : MEGAMOE_ERR_HIP;
 }
 
 // ---------------------------------------------------------------------------------------
@@ -1185,6 +1265,8 @@ struct ReadyWait {
   const int* count;  // NULL: nothing to wait for
   int need;
   int* error;        // set to 1 if the bounded wait gives up
+  uint64_t ticks = kWaitTicks;  // the bound, in 100 MHz ticks
+  bool patient = false;         // many workgroups wait on this count: poll less often
 };
 
 // Thread 0 polls the count (bounded in time), then the workgroup passes a barrier. The barrier
@@ -1197,11 +1279,14 @@ __device__ __forceinline__ void wait_ready(const ReadyWait& w) {
     const uint64_t t0 = wall_clock64();
     for (int polls = 0; __hip_atomic_load(w.count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < w.need; ++polls) {
       if ((polls & 15) == 15 && (__hip_atomic_load(w.error, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ||
-                                 wall_clock64() - t0 > kWaitTicks)) {
+                                 wall_clock64() - t0 > w.ticks)) {
         atomicExch(w.error, 1);
         break;
       }
-      __builtin_amdgcn_s_sleep(2);
+      if (w.patient)
+        __builtin_amdgcn_s_sleep(16);  // ~1000 cycles: hundreds of pollers of one word stay light
+      else
+        __builtin_amdgcn_s_sleep(2);
     }
   }
   __builtin_amdgcn_s_barrier();
@@ -1955,8 +2040,10 @@ __global__ __launch_bounds__(256) void k_combine(const uint16_t* __restrict__ d_
                                                  const float* __restrict__ p_r, const float* __restrict__ p_s, int ks,
                                                  const int* __restrict__ inv, const float* __restrict__ wts, int T,
                                                  int H, int K, int S, const int* __restrict__ meta,
-                                                 const uint16_t* __restrict__ residual, uint16_t* __restrict__ y) {
+                                                 const uint16_t* __restrict__ residual, uint16_t* __restrict__ y,
+                                                 int* __restrict__ status) {
   const int i = blockIdx.x * 256 + threadIdx.x, per_row = H / 8;
+  if (status && i == 0) *status = meta[kMetaError];  // the call's outcome, kept after it
   if (i >= T * per_row) return;
   if (meta[kMetaError]) {
     *reinterpret_cast<uint4*>(y + (size_t)i * 8) = make_uint4(0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u);
@@ -2093,8 +2180,11 @@ __global__ __launch_bounds__(256, 2) void k_experts(ExpertArgs args) {
 // zeroes them again, so a call is exactly one launch.
 // =======================================================================================
 
+// kCtlStatus is not zeroed: it keeps the last call's outcome (1: a bounded wait gave up and y
+// is NaN) for megamoe_layer_status; the stream-ordered form's combine writes it too.
 constexpr int kCtlQueue = 0, kCtlNormed = 32, kCtlRouted = 64, kCtlSelected = 96, kCtlPermuted = 128,
-              kCtlDown = 160, kCtlExited = 192, kCtlError = 224, kCtlInts = 256;  // one 128-byte line each
+              kCtlDown = 160, kCtlExited = 192, kCtlError = 224, kCtlStatus = 256,
+              kCtlInts = 288;  // one 128-byte line each
 constexpr int kCombineUnit = 256 * 8;  // outputs per combine unit
 
 struct LayerArgs {
@@ -2119,12 +2209,15 @@ struct LayerArgs {
   int T, H, E, K, S, G, TG, gate, renorm, pow2;
   int nsplit, n_et, ntt, vpl, ks;
   int n_norm, n_router;
+  int force_timeout;  // test hook: the combine units wait for one down unit too many, 20 us at most
+  int pad_;
 };
 
 // Thread 0 waits (bounded in time) until *count >= need, then the workgroup passes a barrier;
-// the acquire keeps the loads that follow below it.
+// the acquire keeps the loads that follow below it. Many workgroups wait on these counts at
+// once (the router's, the permute's, the down units'), so they poll patiently.
 __device__ __forceinline__ void wait_count(const int* count, int need, int* error) {
-  wait_ready(ReadyWait{count, need, error});
+  wait_ready(ReadyWait{count, need, error, kWaitTicks, true});
 }
 
 __device__ __forceinline__ int load_count(const int* p) {
@@ -2195,6 +2288,7 @@ __global__ __launch_bounds__(256, 2) void k_layer(LayerArgs args) {
   const int fixed = args.n_norm + args.n_router + args.T;  // units listed before the routing is known
   int total = INT_MAX;                                      // every unit, once the permute has run
   int n_gu = 0, n_dn = 0;
+  int my_down = 0;  // down units this workgroup finished and has not yet counted
   if (threadIdx.x == 0) slot = atomicAdd(&ctl[kCtlQueue], 1);
   __syncthreads();
   int u = slot, next = 0;
@@ -2214,6 +2308,15 @@ __global__ __launch_bounds__(256, 2) void k_layer(LayerArgs args) {
       n_gu = units[0];
       n_dn = units[1];
       total = fixed + n_gu + n_dn + (args.T * args.H + kCombineUnit - 1) / kCombineUnit;
+    }
+    // Down units are counted once per workgroup, when it moves past them (to a combine unit
+    // or out): their stores complete first. The combine units wait for the full count, which
+    // every workgroup with down units adds to before it combines or leaves.
+    if (my_down && u >= fixed + n_gu + n_dn) {
+      publish_fence();
+      __syncthreads();
+      if (threadIdx.x == 0) atomicAdd(&ctl[kCtlDown], my_down);
+      my_down = 0;
     }
     if (u >= total) break;
     // The arguments are re-read per unit (as in k_experts) so each unit derives its
@@ -2264,7 +2367,7 @@ __global__ __launch_bounds__(256, 2) void k_layer(LayerArgs args) {
         // Every token is routed: this workgroup runs the permute, then publishes the lists.
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
         permute_block(a.ids, 0, a.T, a.K, a.E, a.S, a.ex.gu.I / kBlock, a.H / kBlock, a.ks, kChunkRows, 0, a.po,
-                      reinterpret_cast<int*>(rings), flags);
+                      reinterpret_cast<int*>(rings), flags, permute_tile_waves(a.T, a.E, 256, kPermuteLdsInts));
         publish_fence();
         __syncthreads();
         if (threadIdx.x == 0) __hip_atomic_store(&ctl[kCtlPermuted], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -2287,9 +2390,10 @@ __global__ __launch_bounds__(256, 2) void k_layer(LayerArgs args) {
       uint8_t* ring = rings + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) * kRingWave;
       const ReadyWait ready{&a.ex.ready[c], a.ex.dn.chunks[c].x == a.E ? a.S * nbI : nbI, &ctl[kCtlError]};
       down_work(a.ex.dn, v, ready, ring);
-      publish_count(&ctl[kCtlDown]);
+      ++my_down;
     } else {
-      wait_count(&ctl[kCtlDown], n_dn, &ctl[kCtlError]);
+      wait_ready(ReadyWait{&ctl[kCtlDown], n_dn + a.force_timeout, &ctl[kCtlError],
+                           a.force_timeout ? (uint64_t)2000 : kWaitTicks, true});
       layer_combine(a, u - fixed - n_gu - n_dn);
     }
     if (threadIdx.x == 0) slot = next;
@@ -2299,6 +2403,7 @@ __global__ __launch_bounds__(256, 2) void k_layer(LayerArgs args) {
   // Leaving: the last workgroup out (every other one has made its last claim) zeroes the
   // control words for the next call.
   if (threadIdx.x == 0 && atomicAdd(&ctl[kCtlExited], 1) == (int)gridDim.x - 1) {
+    __hip_atomic_store(&ctl[kCtlStatus], load_count(&ctl[kCtlError]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const int words[] = {kCtlQueue, kCtlNormed, kCtlRouted, kCtlSelected, kCtlPermuted, kCtlDown, kCtlError,
                          kCtlExited};
     for (int w : words) __hip_atomic_store(&ctl[w], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -3386,9 +3491,8 @@ int validate(const megamoe_desc* d) {
   if (d->gate != MEGAMOE_GATE_SOFTMAX && d->gate != MEGAMOE_GATE_SIGMOID) return MEGAMOE_ERR_SHAPE;
   if (d->groups > 1 && (size_t)d->top_groups * (d->experts / d->groups) < (size_t)d->topk) return MEGAMOE_ERR_SHAPE;
   if (d->experts > kMaxExperts || d->topk > kMaxTopK || d->groups > 64) return MEGAMOE_ERR_UNSUPPORTED;
-  // Permute bitmap in LDS: (32 scan words + E counts + E*ceil(T/32) bitmap words) * 4 bytes.
-  const size_t words = ((size_t)d->tokens + 31) / 32;
-  if (((size_t)d->experts * (1 + words) + 32) * 4 > 64 * 1024) return MEGAMOE_ERR_UNSUPPORTED;
+  // The permute's LDS (bitmap form, or the tiled form for long token counts).
+  if (permute_tile_waves(d->tokens, d->experts, 256, kPermuteLdsInts) < 0) return MEGAMOE_ERR_UNSUPPORTED;
   // The permute kernel's packed scan holds up to 2^21-1 rows and 2^15-1 chunks.
   if ((size_t)d->tokens * d->topk >= ((size_t)1 << 21) - kMaxExperts * 64) return MEGAMOE_ERR_UNSUPPORTED;
   return MEGAMOE_OK;
@@ -3596,10 +3700,7 @@ int forward_impl(const megamoe_desc* desc, const megamoe_tensors* t, hipStream_t
 
   const PermuteOut po = make_permute_out(L, ws);
   const int nbI = I / kBlock, nbH = H / kBlock;
-  const size_t lds = ((size_t)E * (1 + (T + 31) / 32) + 32) * 4;
-  hipLaunchKernelGGL(k_permute, dim3(1), dim3(1024), lds, st, t->expert_ids, (int64_t)0, T, K, E, S, nbI, nbH, L.ks,
-                     kChunkRows, 0, po);
-  MEGAMOE_LAUNCH_CHECK();
+  if ((rc = launch_permute(t->expert_ids, 0, T, K, E, S, nbI, nbH, L.ks, kChunkRows, 0, po, st))) return rc;
   if (mark(3) != hipSuccess) return MEGAMOE_ERR_HIP;
 
   ExpertArgs ea;
@@ -3624,7 +3725,8 @@ int forward_impl(const megamoe_desc* desc, const megamoe_tensors* t, hipStream_t
   hipLaunchKernelGGL(k_combine, dim3((rows8 + 255) / 256), dim3(256), 0, st, (const uint16_t*)da.d_r,
                      (const uint16_t*)da.d_s, (const float*)da.p_r, (const float*)da.p_s, L.ks, (const int*)po.inv,
                      (const float*)t->expert_weights, T, H, K, S, (const int*)po.meta,
-                     (const uint16_t*)(blk && blk->residual ? t->x : nullptr), (uint16_t*)t->y);
+                     (const uint16_t*)(blk && blk->residual ? t->x : nullptr), (uint16_t*)t->y,
+                     (int*)(ws + L.ctl) + kCtlStatus);
   MEGAMOE_LAUNCH_CHECK();
   if (mark(5) != hipSuccess) return MEGAMOE_ERR_HIP;
   return MEGAMOE_OK;
@@ -3687,6 +3789,8 @@ int forward_layer_impl(const megamoe_desc* desc, const megamoe_tensors* t, const
   la.ks = L.ks;
   la.n_norm = norm ? T : 0;
   la.n_router = la.n_et * la.nsplit * passes;
+  const char* force = getenv("MEGAMOE_FORCE_WAIT_TIMEOUT");
+  la.force_timeout = force && force[0] == '1' ? 1 : 0;
 
   // As many workgroups as fit on the device at once, and no more than the most units the
   // queue can hold.
@@ -3725,8 +3829,7 @@ int validate_mx(const megamoe_desc* d) {
     return MEGAMOE_ERR_SHAPE;
   if (d->hidden % kMxStageK || d->intermediate % kMxStageK || d->topk > d->experts) return MEGAMOE_ERR_SHAPE;
   if (d->experts > kMaxExperts || d->topk > kMaxTopK) return MEGAMOE_ERR_UNSUPPORTED;
-  const size_t words = ((size_t)d->tokens + 31) / 32;
-  if (((size_t)d->experts * (1 + words) + 32) * 4 > 64 * 1024) return MEGAMOE_ERR_UNSUPPORTED;
+  if (permute_tile_waves(d->tokens, d->experts, 1024, kPermuteLdsInts) < 0) return MEGAMOE_ERR_UNSUPPORTED;
   if ((size_t)d->tokens * d->topk >= ((size_t)1 << 21) - kMaxExperts * 64) return MEGAMOE_ERR_UNSUPPORTED;
   return MEGAMOE_OK;
 }
@@ -3807,10 +3910,9 @@ int forward_mx_impl(const megamoe_desc* desc, float limit, const megamoe_mx_tens
   // chunks of up to 64 rows, down units of 256 rows, no wide units.
   const bool batch = (int64_t)T * K >= (int64_t)kBatchMinRows * E && (H / kMxStageK) % 2 == 0 &&
                      (I / kMxStageK / L.ks) % 2 == 0;
-  const size_t lds = ((size_t)E * (1 + (T + 31) / 32) + 32) * 4;
-  hipLaunchKernelGGL(k_permute, dim3(1), dim3(1024), lds, st, t->topk_idx, base, T, K, E, 0, nbI,
-                     batch ? nbH / 2 : nbH, L.ks, batch ? kBatchRows : kChunkRowsMx, batch ? 0 : 1, po);
-  MEGAMOE_LAUNCH_CHECK();
+  if ((rc = launch_permute(t->topk_idx, base, T, K, E, 0, nbI, batch ? nbH / 2 : nbH, L.ks,
+                           batch ? kBatchRows : kChunkRowsMx, batch ? 0 : 1, po, st)))
+    return rc;
   if (mark(1) != hipSuccess) return MEGAMOE_ERR_HIP;
 
   ExpertMxArgs ea;
@@ -3858,7 +3960,7 @@ int forward_mx_impl(const megamoe_desc* desc, float limit, const megamoe_mx_tens
     hipLaunchKernelGGL(k_combine, dim3((rows8 + 255) / 256), dim3(256), 0, st, (const uint16_t*)da.d,
                        (const uint16_t*)nullptr, (const float*)da.pd, (const float*)nullptr, L.ks,
                        (const int*)po.inv, (const float*)nullptr, T, H, K, 0, (const int*)po.meta,
-                       (const uint16_t*)nullptr, (uint16_t*)t->y);
+                       (const uint16_t*)nullptr, (uint16_t*)t->y, (int*)nullptr);
   MEGAMOE_LAUNCH_CHECK();
   if (mark(3) != hipSuccess) return MEGAMOE_ERR_HIP;
   return MEGAMOE_OK;
@@ -4105,7 +4207,7 @@ int scratch_address(void** out) {
 
 extern "C" {
 
-int megamoe_abi_version(void) { return 7; }
+int megamoe_abi_version(void) { return 8; }
 
 const char* megamoe_status_string(int status) {
   switch (status) {
@@ -4134,6 +4236,8 @@ int megamoe_forward(const megamoe_desc* desc, const megamoe_tensors* t, void* st
 
 int megamoe_layer_forward(const megamoe_desc* desc, const megamoe_tensors* t, const megamoe_block* block,
                           const megamoe_epilogue* epilogue, void* stream, void* const* events) {
+  if (epilogue && ((epilogue->swiglu != 0 && epilogue->swiglu != 1) || !(epilogue->swiglu_limit >= 0.0f)))
+    return MEGAMOE_ERR_INVALID_ARGUMENT;
   hipEvent_t ev[2];
   if (events) {
     if (!events[0] || !events[1]) return MEGAMOE_ERR_INVALID_ARGUMENT;
@@ -4141,6 +4245,22 @@ int megamoe_layer_forward(const megamoe_desc* desc, const megamoe_tensors* t, co
     ev[1] = (hipEvent_t)events[1];
   }
   return forward_layer_impl(desc, t, block, epilogue, (hipStream_t)stream, events ? ev : nullptr);
+}
+
+int megamoe_layer_status(const megamoe_desc* desc, const void* workspace, size_t workspace_bytes, int32_t* gave_up,
+                         void* stream) {
+  const int rc = validate(desc);
+  if (rc) return rc;
+  if (!workspace || !gave_up) return MEGAMOE_ERR_INVALID_ARGUMENT;
+  const Layout L = make_layout(*desc);
+  if (workspace_bytes < L.total) return MEGAMOE_ERR_WORKSPACE;
+  int32_t v = 0;
+  if (hipMemcpyAsync(&v, (const char*)workspace + L.ctl + kCtlStatus * sizeof(int), sizeof(v), hipMemcpyDeviceToHost,
+                     (hipStream_t)stream) != hipSuccess ||
+      hipStreamSynchronize((hipStream_t)stream) != hipSuccess)
+    return MEGAMOE_ERR_HIP;
+  *gave_up = v;
+  return MEGAMOE_OK;
 }
 
 int megamoe_forward_noalloc(const megamoe_desc* desc, const megamoe_tensors* t, void* stream) {

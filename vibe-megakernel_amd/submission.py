@@ -233,6 +233,19 @@ class MoELayer:
     def __call__(self, inputs: dict) -> dict:
         return self._call(inputs, timed=False)
 
+    def gave_up(self, device: torch.device) -> bool:
+        """Whether the last call on this (device, current stream)'s workspace had a bounded
+        wait give up (its y is NaN); synchronizes the stream (megamoe_layer_status)."""
+        if self.mx:
+            raise ValueError("the status word covers the fp8 layer forms")
+        ws = self.workspace(device)
+        flag = ctypes.c_int32(0)
+        stream = ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+        with torch.cuda.device(device):
+            _lib.check(self.lib.megamoe_layer_status(ctypes.byref(self.desc), ws.data_ptr(), self.workspace_bytes,
+                                                     ctypes.byref(flag), stream), f"{self.case.id}: status")
+        return bool(flag.value)
+
     def noalloc(self, inputs: dict) -> dict:
         """One call of megamoe_forward_noalloc: the library's fixed device scratch stands in
         for the workspace (the outputs are still allocated here, as the caller's)."""
