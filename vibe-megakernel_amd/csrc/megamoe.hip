@@ -33,6 +33,7 @@
 #include <math.h>
 #include <mutex>
 #include <stdlib.h>
+#include <stddef.h>
 #include <type_traits>
 #include <stdint.h>
 #include <string.h>
@@ -137,8 +138,22 @@ __device__ __forceinline__ void store_coherent(float* p, float v) {
 __device__ __forceinline__ void store_coherent(double* p, double v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+__device__ __forceinline__ void store_coherent(int4* p, int4 v) {
+  store_coherent(reinterpret_cast<uint64_t*>(p), (uint64_t)(uint32_t)v.x | ((uint64_t)(uint32_t)v.y << 32));
+  store_coherent(reinterpret_cast<uint64_t*>(p) + 1, (uint64_t)(uint32_t)v.z | ((uint64_t)(uint32_t)v.w << 32));
+}
 // All of this wavefront's memory operations complete (vmcnt, expcnt and lgkmcnt zero).
 __device__ __forceinline__ void publish_fence() { __builtin_amdgcn_s_waitcnt(0); }
+
+// A store that another workgroup of the same kernel reads (CO: device-coherent, as above)
+// or that only later kernels read (a plain store; kernel boundaries order it).
+template <bool CO, class T>
+__device__ __forceinline__ void store_out(T* p, T v) {
+  if constexpr (CO)
+    store_coherent(p, v);
+  else
+    *p = v;
+}
 
 // ---------------------------------------------------------------------------------------
 // Dynamic E4M3 quantization of one full 128-wide block by one wavefront (two values per
@@ -237,6 +252,7 @@ __device__ __forceinline__ double norm_squares(const NormChunks& c) {
   return s;
 }
 
+template <bool CO>
 __device__ __forceinline__ void norm_store(const NormChunks& c, uint16_t* orow, int base, int H, int tid, float r,
                                            int weight_in_fp32) {
 #pragma unroll
@@ -254,13 +270,14 @@ __device__ __forceinline__ void norm_store(const NormChunks& c, uint16_t* orow, 
       const float w0 = bf16_bits_to_f32(gw[i] & 0xffffu), w1 = bf16_bits_to_f32(gw[i] >> 16);
       o[i] = f32_to_bf16_bits(__fmul_rn(n0, w0)) | (f32_to_bf16_bits(__fmul_rn(n1, w1)) << 16);
     }
-    if (e < H) store_coherent(reinterpret_cast<uint64_t*>(orow + e), (uint64_t)o[0] | ((uint64_t)o[1] << 32));
+    if (e < H) store_out<CO>(reinterpret_cast<uint64_t*>(orow + e), (uint64_t)o[0] | ((uint64_t)o[1] << 32));
   }
 }
 
 // Every thread issues the loads of its chunks of x and gamma at once; a row of up to
 // kNormPass elements stays in registers from the sum of squares to the output (longer rows
 // reload their later passes).
+template <bool CO>
 __device__ __forceinline__ void norm_row(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, int row,
                                          int H, float eps, int weight_in_fp32, uint16_t* __restrict__ out,
                                          double* part) {
@@ -284,11 +301,11 @@ __device__ __forceinline__ void norm_row(const uint16_t* __restrict__ x, const u
   // sqrtf and / are correctly rounded in HIP device code by default
   // (-fhip-fp32-correctly-rounded-divide-sqrt); __fsqrt_rn is the ~1 ulp hardware sqrt.
   const float r = 1.0f / __builtin_sqrtf(__fadd_rn(m, eps));
-  norm_store(first, orow, 0, H, tid, r, weight_in_fp32);
+  norm_store<CO>(first, orow, 0, H, tid, r, weight_in_fp32);
   for (int base = kNormPass; base < H; base += kNormPass) {
     NormChunks more;
     norm_load(more, xr, w, base, H, tid);
-    norm_store(more, orow, base, H, tid, r, weight_in_fp32);
+    norm_store<CO>(more, orow, base, H, tid, r, weight_in_fp32);
   }
 }
 
@@ -296,7 +313,7 @@ __global__ __launch_bounds__(256) void k_norm(const uint16_t* __restrict__ x, co
                                               int rows, int H, float eps, int weight_in_fp32,
                                               uint16_t* __restrict__ out) {
   __shared__ double part[4];
-  norm_row(x, w, blockIdx.x, H, eps, weight_in_fp32, out, part);
+  norm_row<false>(x, w, blockIdx.x, H, eps, weight_in_fp32, out, part);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -374,7 +391,7 @@ __device__ __forceinline__ void quant_x_group(int group, const uint16_t* __restr
 // wavefront order through LDS and the split's partial is stored in fp64. Passes are
 // workgroups of their own, so every workgroup does the same work and the grid spreads
 // evenly over the CUs.
-template <int NTT>
+template <int NTT, bool CO>
 __device__ __forceinline__ void router_tile(const uint16_t* __restrict__ x, const float* __restrict__ w,
                                             double* __restrict__ partial, int T, int H, int E, int n_et, int nsplit,
                                             int unit, f64x4* red) {
@@ -452,7 +469,7 @@ __device__ __forceinline__ void router_tile(const uint16_t* __restrict__ x, cons
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
             const int eo = et * kRouterTile + g + 4 * v;
-            if (eo < E) store_coherent(&partial[((size_t)split * T + t) * E + eo], acc[i][v]);
+            if (eo < E) store_out<CO>(&partial[((size_t)split * T + t) * E + eo], acc[i][v]);
           }
         }
       }
@@ -466,7 +483,7 @@ __global__ __launch_bounds__(kRouterWaves * 64) void k_router(const uint16_t* __
                                                               double* __restrict__ partial, int T, int H, int E,
                                                               int n_et, int nsplit) {
   __shared__ f64x4 red[(kRouterWaves - 1) * NTT * 64];
-  router_tile<NTT>(x, w, partial, T, H, E, n_et, nsplit, blockIdx.x, red);
+  router_tile<NTT, false>(x, w, partial, T, H, E, n_et, nsplit, blockIdx.x, red);
 }
 
 // logits[t][e] = fp32(sum of the splits in split order); used by megamoe_router_logits.
@@ -596,7 +613,7 @@ struct SelectLds {
 };
 
 // Wavefront `wv` routes token t from the logits in LDS (one wavefront per token, no barrier).
-template <int VPL>
+template <int VPL, bool CO>
 __device__ __forceinline__ void route_token(SelectLds& L, int lane, int wv, int t, bool token_ok,
                                             const float (&bias_v)[VPL], int E, int K, int G, int TG, int gate,
                                             int renorm, float scaling, int64_t* __restrict__ ids_out,
@@ -730,15 +747,15 @@ __device__ __forceinline__ void route_token(SelectLds& L, int lane, int wv, int 
     w = expf(my_val - m) / s * scaling;
   }
   if (lane < K) {
-    store_coherent(&ids_out[(size_t)t * K + lane], (int64_t)my_id);
-    store_coherent(&w_out[(size_t)t * K + lane], w);
+    store_out<CO>(&ids_out[(size_t)t * K + lane], (int64_t)my_id);
+    store_out<CO>(&w_out[(size_t)t * K + lane], w);
   }
 }
 
 // Routing of token `token` (kSelectTokens = 1) by the workgroup's 256 threads: all load and
 // sum the split partials, wavefront 0 routes. ids and weights go out as device-coherent
 // stores (a later workgroup of the single-launch kernel reads them).
-template <int VPL>
+template <int VPL, bool CO>
 __device__ __forceinline__ void select_token(const double* __restrict__ partial, int nsplit,
                                              const float* __restrict__ logits_in, const float* __restrict__ bias,
                                              int T, int E, int K, int G, int TG, int gate, int renorm, float scaling,
@@ -797,7 +814,7 @@ __device__ __forceinline__ void select_token(const double* __restrict__ partial,
     }
   }
   __syncthreads();
-  if (wv < kSelectTokens) route_token<VPL>(L, lane, wv, t, token_ok, bias_v, E, K, G, TG, gate, renorm, scaling,
+  if (wv < kSelectTokens) route_token<VPL, CO>(L, lane, wv, t, token_ok, bias_v, E, K, G, TG, gate, renorm, scaling,
                                            ids_out, w_out);
 }
 
@@ -813,8 +830,8 @@ __global__ __launch_bounds__(256) void k_select(const double* __restrict__ parti
     return;
   }
   __shared__ SelectLds lds;
-  select_token<VPL>(partial, nsplit, logits_in, bias, T, E, K, G, TG, gate, renorm, scaling, ids_out, w_out,
-                    blockIdx.x, lds);
+  select_token<VPL, false>(partial, nsplit, logits_in, bias, T, E, K, G, TG, gate, renorm, scaling, ids_out, w_out,
+                           blockIdx.x, lds);
 }
 
 
@@ -891,10 +908,6 @@ __device__ __forceinline__ int chunk_class(int rows) { return rows > 32 ? 0 : (r
 // With `wide` (the MXFP4 form, no shared expert), a chunk of more than 32 rows is worked by
 // wide units, 4 per 128-channel block of gate/up and 2 per 128-row block of down (times
 // the K parts); those chunks lead the lists, and meta[kMetaWide] counts them.
-__device__ __forceinline__ void store_coherent(int4* p, int4 v) {
-  store_coherent(reinterpret_cast<uint64_t*>(p), (uint64_t)(uint32_t)v.x | ((uint64_t)(uint32_t)v.y << 32));
-  store_coherent(reinterpret_cast<uint64_t*>(p) + 1, (uint64_t)(uint32_t)v.z | ((uint64_t)(uint32_t)v.w << 32));
-}
 
 // The permute by one workgroup of any size (a multiple of 64, at least 256): thread i owns
 // the contiguous experts [i*ept, i*ept + ept) (ept = ceil(E / threads)), so the scan over
@@ -912,6 +925,7 @@ __device__ __forceinline__ void store_coherent(int4* p, int4 v) {
 //     expert across tiles (32 + E + E*tile_waves ints). Repeated ids within a token are
 //     found by comparing each entry with its token's other slots.
 // flags[0..1] are two more LDS ints.
+template <bool CO>
 __device__ __forceinline__ void permute_block(const int64_t* __restrict__ ids, int64_t base, int T, int K, int E,
                                               int S, int nbI, int nbH, int ks, int chunk, int wide,
                                               const PermuteOut& out, int* smem, int* flags, int tile_waves = 0) {
@@ -949,10 +963,10 @@ __device__ __forceinline__ void permute_block(const int64_t* __restrict__ ids, i
   __syncthreads();
   if (*bad) {
     if (tid == 0) {
-      store_coherent(&out.meta[kMetaUnitsGU], 0);
-      store_coherent(&out.meta[kMetaUnitsDN], 0);
-      store_coherent(&out.meta[kMetaQueueGU], 0);
-      store_coherent(&out.meta[kMetaError], 1);
+      store_out<CO>(&out.meta[kMetaUnitsGU], 0);
+      store_out<CO>(&out.meta[kMetaUnitsDN], 0);
+      store_out<CO>(&out.meta[kMetaQueueGU], 0);
+      store_out<CO>(&out.meta[kMetaError], 1);
     }
     return;
   }
@@ -994,25 +1008,25 @@ __device__ __forceinline__ void permute_block(const int64_t* __restrict__ ids, i
     int a4, a2, a1;
     classes(c, a4, a2, a1);
     const int full = c / chunk, rem = c % chunk;
-    store_coherent(&out.counts[e], c);
-    store_coherent(&out.offsets[e], off);
+    store_out<CO>(&out.counts[e], c);
+    store_out<CO>(&out.offsets[e], off);
     for (int i = 0; i < a4; ++i) {
       const int4 ch = make_int4(e, chunk * i, min(chunk, c - chunk * i), 0);
-      store_coherent(&out.gu[gbase[0] + gshared[0] + p4 + i], ch);
-      store_coherent(&out.dn[dbase[0] + dshared[0] + p4 + i], ch);
-      store_coherent(&out.dn_of_gu[gbase[0] + gshared[0] + p4 + i], dbase[0] + dshared[0] + p4 + i);
+      store_out<CO>(&out.gu[gbase[0] + gshared[0] + p4 + i], ch);
+      store_out<CO>(&out.dn[dbase[0] + dshared[0] + p4 + i], ch);
+      store_out<CO>(&out.dn_of_gu[gbase[0] + gshared[0] + p4 + i], dbase[0] + dshared[0] + p4 + i);
     }
     if (a2) {
       const int4 ch = make_int4(e, chunk * full, rem, 0);
-      store_coherent(&out.gu[gbase[1] + gshared[1] + p2], ch);
-      store_coherent(&out.dn[dbase[1] + dshared[1] + p2], ch);
-      store_coherent(&out.dn_of_gu[gbase[1] + gshared[1] + p2], dbase[1] + dshared[1] + p2);
+      store_out<CO>(&out.gu[gbase[1] + gshared[1] + p2], ch);
+      store_out<CO>(&out.dn[dbase[1] + dshared[1] + p2], ch);
+      store_out<CO>(&out.dn_of_gu[gbase[1] + gshared[1] + p2], dbase[1] + dshared[1] + p2);
     }
     if (a1) {
       const int4 ch = make_int4(e, chunk * full, rem, 0);
-      store_coherent(&out.gu[gbase[2] + gshared[2] + p1], ch);
-      store_coherent(&out.dn[dbase[2] + dshared[2] + p1], ch);
-      store_coherent(&out.dn_of_gu[gbase[2] + gshared[2] + p1], dbase[2] + dshared[2] + p1);
+      store_out<CO>(&out.gu[gbase[2] + gshared[2] + p1], ch);
+      store_out<CO>(&out.dn[dbase[2] + dshared[2] + p1], ch);
+      store_out<CO>(&out.dn_of_gu[gbase[2] + gshared[2] + p1], dbase[2] + dshared[2] + p1);
     }
     cnt[e] = off;  // the expert's first row, for the ranks below (only this thread reads cnt[e] above)
     off += c;
@@ -1028,26 +1042,26 @@ __device__ __forceinline__ void permute_block(const int64_t* __restrict__ ids, i
         const int idx = cls == 0 ? i : 0;        // index within the shared part of the class
         const int per_copy = cls == 0 ? s4 : 1;  // shared chunks of this class per copy
         for (int s = 0; s < S; ++s) {
-          store_coherent(&out.gu[gbase[cls] + s * per_copy + idx], make_int4(E, chunk * i, rows, s * nbI));
-          store_coherent(&out.dn_of_gu[gbase[cls] + s * per_copy + idx], dbase[cls] + idx);
+          store_out<CO>(&out.gu[gbase[cls] + s * per_copy + idx], make_int4(E, chunk * i, rows, s * nbI));
+          store_out<CO>(&out.dn_of_gu[gbase[cls] + s * per_copy + idx], dbase[cls] + idx);
         }
-        store_coherent(&out.dn[dbase[cls] + idx], make_int4(E, chunk * i, rows, 0));
+        store_out<CO>(&out.dn[dbase[cls] + idx], make_int4(E, chunk * i, rows, 0));
       }
     }
-    store_coherent(&out.offsets[E], total);
-    store_coherent(&out.meta[kMetaHit], *hits);
+    store_out<CO>(&out.offsets[E], total);
+    store_out<CO>(&out.meta[kMetaHit], *hits);
     const int wf = wide ? 4 : 1, wfd = wide ? 2 : 1;  // units per block of a chunk of over 32 rows
-    store_coherent(&out.meta[kMetaUnitsGU], (S * (s4 + s2 + s1) + wf * t4 + t2 + t1) * nbI);
-    store_coherent(&out.meta[kMetaUnitsDN], (s4 + s2 + s1 + wfd * t4 + t2 + t1) * nbH * ks);
-    store_coherent(&out.meta[kMetaWide], wide ? t4 : 0);
-    store_coherent(&out.meta[kMetaQueueGU], 0);
-    store_coherent(&out.meta[kMetaQueueDN], 0);
-    store_coherent(&out.meta[kMetaError], 0);
+    store_out<CO>(&out.meta[kMetaUnitsGU], (S * (s4 + s2 + s1) + wf * t4 + t2 + t1) * nbI);
+    store_out<CO>(&out.meta[kMetaUnitsDN], (s4 + s2 + s1 + wfd * t4 + t2 + t1) * nbH * ks);
+    store_out<CO>(&out.meta[kMetaWide], wide ? t4 : 0);
+    store_out<CO>(&out.meta[kMetaQueueGU], 0);
+    store_out<CO>(&out.meta[kMetaQueueDN], 0);
+    store_out<CO>(&out.meta[kMetaError], 0);
   }
   const int dtot = s4 + s2 + s1 + t4 + t2 + t1;
-  for (int i = tid; i < dtot; i += nt) store_coherent(&out.ready[i], 0);
+  for (int i = tid; i < dtot; i += nt) store_out<CO>(&out.ready[i], 0);
   if (out.pairs)
-    for (int i = tid; i < (S * (s4 + s2 + s1) + t4 + t2 + t1) * nbI; i += nt) store_coherent(&out.pairs[i], 0);
+    for (int i = tid; i < (S * (s4 + s2 + s1) + t4 + t2 + t1) * nbI; i += nt) store_out<CO>(&out.pairs[i], 0);
   __syncthreads();
   if (!tile_waves) {
     for (int i = tid; i < n; i += nt) {
@@ -1056,8 +1070,8 @@ __device__ __forceinline__ void permute_block(const int64_t* __restrict__ ids, i
       int rank = __popc(row[t >> 5] & ((1u << (t & 31)) - 1u));
       for (int q = 0; q < (t >> 5); ++q) rank += __popc(row[q]);
       const int pos = cnt[e] + rank;
-      store_coherent(&out.perm[pos], i);
-      store_coherent(&out.inv[i], pos);
+      store_out<CO>(&out.perm[pos], i);
+      store_out<CO>(&out.inv[i], pos);
     }
     return;
   }
@@ -1086,8 +1100,8 @@ __device__ __forceinline__ void permute_block(const int64_t* __restrict__ ids, i
     if (live) {
       int pos = cnt[e] + my_rank;
       for (int q = 0; q < w; ++q) pos += wcount[q * E + e];
-      store_coherent(&out.perm[pos], i);
-      store_coherent(&out.inv[i], pos);
+      store_out<CO>(&out.perm[pos], i);
+      store_out<CO>(&out.inv[i], pos);
     }
     __syncthreads();
     for (int q = tid; q < E; q += nt) {
@@ -1115,7 +1129,7 @@ __global__ __launch_bounds__(1024) void k_permute(const int64_t* __restrict__ id
                                                   PermuteOut out, int tile_waves) {
   extern __shared__ int smem[];
   __shared__ int flags[2];
-  permute_block(ids, base, T, K, E, S, nbI, nbH, ks, chunk, wide, out, smem, flags, tile_waves);
+  permute_block<false>(ids, base, T, K, E, S, nbI, nbH, ks, chunk, wide, out, smem, flags, tile_waves);
 }
 
 // Launches k_permute with the LDS its form needs.
@@ -1267,6 +1281,7 @@ struct ReadyWait {
   int* error;        // set to 1 if the bounded wait gives up
   uint64_t ticks = kWaitTicks;  // the bound, in 100 MHz ticks
   bool patient = false;         // many workgroups wait on this count: poll less often
+  int max_naps = 2;             // patient waits: naps of ~1000 cycles between polls, doubling up to this
 };
 
 // Thread 0 polls the count (bounded in time), then the workgroup passes a barrier. The barrier
@@ -1277,16 +1292,22 @@ __device__ __forceinline__ void wait_ready(const ReadyWait& w) {
   if (!w.count) return;
   if (threadIdx.x == 0) {
     const uint64_t t0 = wall_clock64();
+    int naps = 1;  // patient waits: 1, 2, ... max_naps naps of ~1000 cycles between polls
     for (int polls = 0; __hip_atomic_load(w.count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < w.need; ++polls) {
       if ((polls & 15) == 15 && (__hip_atomic_load(w.error, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ||
                                  wall_clock64() - t0 > w.ticks)) {
         atomicExch(w.error, 1);
         break;
       }
-      if (w.patient)
-        __builtin_amdgcn_s_sleep(16);  // ~1000 cycles: hundreds of pollers of one word stay light
-      else
+      if (w.patient) {
+        // Hundreds of workgroups wait on one word at once (the router's, the permute's and
+        // the down units' counts): each poll is a load at the memory channel that holds the
+        // word, which every weight stream also crosses, so the polls back off.
+        for (int k = 0; k < naps; ++k) __builtin_amdgcn_s_sleep(16);
+        naps = 2 * naps < w.max_naps ? 2 * naps : w.max_naps;
+      } else {
         __builtin_amdgcn_s_sleep(2);
+      }
     }
   }
   __builtin_amdgcn_s_barrier();
@@ -1860,7 +1881,7 @@ struct DownArgs {
 // requantized h rows, over K part kp of a.ks (K blocks [kp*nkb/ks, (kp+1)*nkb/ks)). Wave w
 // owns rows 32w .. 32w+31. With one part the result is d in bf16; with several, each part
 // stores its fp32 partial to pd and the combine adds the parts in order before rounding.
-template <int NCT>
+template <int NCT, bool CO>
 __device__ __forceinline__ void down_unit(const DownArgs& a, const uint8_t* wd, const float* sd, int ldk, const uint8_t* hq,
                           const float* hs, const ChunkRows& cr, int j, int kp, uint16_t* d, float* pd,
                           int rot, const ReadyWait& ready, uint8_t* ring) {
@@ -1905,11 +1926,11 @@ __device__ __forceinline__ void down_unit(const DownArgs& a, const uint8_t* wd, 
         if (a.ks == 1) {
           const uint32_t lo = f32_to_bf16_bits(acc[p][c][0]) | (f32_to_bf16_bits(acc[p][c][1]) << 16);
           const uint32_t hi = f32_to_bf16_bits(acc[p][c][2]) | (f32_to_bf16_bits(acc[p][c][3]) << 16);
-          store_coherent(reinterpret_cast<uint64_t*>(d + o), (uint64_t)lo | ((uint64_t)hi << 32));
+          store_out<CO>(reinterpret_cast<uint64_t*>(d + o), (uint64_t)lo | ((uint64_t)hi << 32));
         } else {
           uint64_t* q = reinterpret_cast<uint64_t*>(pd + o);
-          store_coherent(q, (uint64_t)__float_as_uint(acc[p][c][0]) | ((uint64_t)__float_as_uint(acc[p][c][1]) << 32));
-          store_coherent(q + 1, (uint64_t)__float_as_uint(acc[p][c][2]) | ((uint64_t)__float_as_uint(acc[p][c][3]) << 32));
+          store_out<CO>(q, (uint64_t)__float_as_uint(acc[p][c][0]) | ((uint64_t)__float_as_uint(acc[p][c][1]) << 32));
+          store_out<CO>(q + 1, (uint64_t)__float_as_uint(acc[p][c][2]) | ((uint64_t)__float_as_uint(acc[p][c][3]) << 32));
         }
       }
     }
@@ -1918,6 +1939,7 @@ __device__ __forceinline__ void down_unit(const DownArgs& a, const uint8_t* wd, 
 
 // Down unit v of the work list: chunk v / (nbH*ks), then 128-row block j of the down
 // matrix and K part kp (v % (nbH*ks) = j*ks + kp).
+template <bool CO>
 __device__ __forceinline__ void down_work(const DownArgs& a, int v, const ReadyWait& ready, uint8_t* ring) {
   const int nbH = a.H / kBlock, nbI = a.I / kBlock;
   const int4 ch = a.chunks[v / (nbH * a.ks)];
@@ -1932,22 +1954,22 @@ __device__ __forceinline__ void down_work(const DownArgs& a, int v, const ReadyW
     const uint8_t* wd = a.sdown + (size_t)j * kBlock * ldk;
     const float* sd = a.sdown_scale + (size_t)j * (ldk / kBlock);
     if (cr.n <= 16)
-      down_unit<1>(a, wd, sd, ldk, a.hq_s, a.hs_s, cr, j, kp, a.d_s, pd_s, rot, ready, ring);
+      down_unit<1, CO>(a, wd, sd, ldk, a.hq_s, a.hs_s, cr, j, kp, a.d_s, pd_s, rot, ready, ring);
     else if (cr.n <= 32)
-      down_unit<2>(a, wd, sd, ldk, a.hq_s, a.hs_s, cr, j, kp, a.d_s, pd_s, rot, ready, ring);
+      down_unit<2, CO>(a, wd, sd, ldk, a.hq_s, a.hs_s, cr, j, kp, a.d_s, pd_s, rot, ready, ring);
     else
-      down_unit<4>(a, wd, sd, ldk, a.hq_s, a.hs_s, cr, j, kp, a.d_s, pd_s, rot, ready, ring);
+      down_unit<4, CO>(a, wd, sd, ldk, a.hq_s, a.hs_s, cr, j, kp, a.d_s, pd_s, rot, ready, ring);
   } else {
     const ChunkRows cr{ch.z, a.offsets[ch.x] + ch.y, a.perm, a.K};
     const size_t rowblk = (size_t)ch.x * nbH + j;
     const uint8_t* wd = a.down + rowblk * kBlock * a.I;
     const float* sd = a.down_scale + rowblk * nbI;
     if (cr.n <= 16)
-      down_unit<1>(a, wd, sd, a.I, a.hq_r, a.hs_r, cr, j, kp, a.d_r, pd_r, rot, ready, ring);
+      down_unit<1, CO>(a, wd, sd, a.I, a.hq_r, a.hs_r, cr, j, kp, a.d_r, pd_r, rot, ready, ring);
     else if (cr.n <= 32)
-      down_unit<2>(a, wd, sd, a.I, a.hq_r, a.hs_r, cr, j, kp, a.d_r, pd_r, rot, ready, ring);
+      down_unit<2, CO>(a, wd, sd, a.I, a.hq_r, a.hs_r, cr, j, kp, a.d_r, pd_r, rot, ready, ring);
     else
-      down_unit<4>(a, wd, sd, a.I, a.hq_r, a.hs_r, cr, j, kp, a.d_r, pd_r, rot, ready, ring);
+      down_unit<4, CO>(a, wd, sd, a.I, a.hq_r, a.hs_r, cr, j, kp, a.d_r, pd_r, rot, ready, ring);
   }
 }
 
@@ -2146,7 +2168,7 @@ __global__ __launch_bounds__(256, 2) void k_experts(ExpertArgs args) {
     } else {
       const int v = u - total_gu, c = v / (nbH * a.dn.ks);
       const ReadyWait ready{&a.ready[c], a.dn.chunks[c].x == a.dn.E ? a.dn.S * nbI : nbI, &meta[kMetaError]};
-      down_work(a.dn, v, ready, ring);
+      down_work<false>(a.dn, v, ready, ring);
     }
     if (threadIdx.x == 0) slot = next;
     __syncthreads();
@@ -2233,12 +2255,13 @@ __device__ __forceinline__ int publish_count(int* count) {
 
 template <int NTT>
 __device__ __forceinline__ void layer_router(const LayerArgs& a, int unit, uint8_t* lds) {
-  router_tile<NTT>(a.x, a.router, a.partial, a.T, a.H, a.E, a.n_et, a.nsplit, unit, reinterpret_cast<f64x4*>(lds));
+  router_tile<NTT, true>(a.x, a.router, a.partial, a.T, a.H, a.E, a.n_et, a.nsplit, unit,
+                         reinterpret_cast<f64x4*>(lds));
 }
 
 template <int VPL>
 __device__ __forceinline__ void layer_select(const LayerArgs& a, int token, uint8_t* lds) {
-  select_token<VPL>(a.partial, a.nsplit, nullptr, a.bias, a.T, a.E, a.K, a.G, a.TG, a.gate, a.renorm, a.scaling,
+  select_token<VPL, true>(a.partial, a.nsplit, nullptr, a.bias, a.T, a.E, a.K, a.G, a.TG, a.gate, a.renorm, a.scaling,
                     a.ids, a.wts, token, *reinterpret_cast<SelectLds*>(lds));
 }
 
@@ -2277,58 +2300,33 @@ __device__ __forceinline__ void layer_combine(const LayerArgs& a, int c) {
 template <bool SPLIT>
 __global__ __launch_bounds__(256, 2) void k_layer(LayerArgs args) {
   typedef const __attribute__((address_space(4))) LayerArgs* ArgsPtr;
+  typedef const __attribute__((address_space(4))) ExpertArgs* ExArgsPtr;
   __shared__ float red[4][64];
   __shared__ __attribute__((aligned(16))) uint8_t rings[4 * kRingWave];  // weight rings; front-end scratch
   __shared__ int slot, flag, flags[2], units[2];
   __shared__ double part[4];
-  static_assert(sizeof(LayerArgs) % 8 == 0, "argument segment layout");
+  static_assert(sizeof(LayerArgs) % 8 == 0 && offsetof(LayerArgs, ex) == 0, "argument segment layout");
   static_assert(sizeof(SelectLds) <= sizeof(rings) && (kRouterWaves - 1) * 4 * 64 * sizeof(f64x4) <= sizeof(rings),
                 "front-end scratch in the rings");
   int* ctl = args.ctl;
   const int fixed = args.n_norm + args.n_router + args.T;  // units listed before the routing is known
-  int total = INT_MAX;                                      // every unit, once the permute has run
-  int n_gu = 0, n_dn = 0;
-  int my_down = 0;  // down units this workgroup finished and has not yet counted
   if (threadIdx.x == 0) slot = atomicAdd(&ctl[kCtlQueue], 1);
   __syncthreads();
   int u = slot, next = 0;
-  while (true) {
-    if (u >= fixed && total == INT_MAX) {
-      // The first unit past the select units: the work lists are known once the permute
-      // has run (its meta words were never read before in this call).
-      wait_count(&ctl[kCtlPermuted], 1, &ctl[kCtlError]);
-      if (threadIdx.x == 0) {
-        // If the wait gave up (error word set), the lists are not to be read: no expert
-        // units, only the combine units, which then write NaN.
-        const bool lists = load_count(&ctl[kCtlPermuted]) != 0;
-        units[0] = lists ? (SPLIT ? 2 : 1) * load_count(&args.po.meta[kMetaUnitsGU]) : 0;
-        units[1] = lists ? load_count(&args.po.meta[kMetaUnitsDN]) : 0;
-      }
-      __syncthreads();
-      n_gu = units[0];
-      n_dn = units[1];
-      total = fixed + n_gu + n_dn + (args.T * args.H + kCombineUnit - 1) / kCombineUnit;
-    }
-    // Down units are counted once per workgroup, when it moves past them (to a combine unit
-    // or out): their stores complete first. The combine units wait for the full count, which
-    // every workgroup with down units adds to before it combines or leaves.
-    if (my_down && u >= fixed + n_gu + n_dn) {
-      publish_fence();
-      __syncthreads();
-      if (threadIdx.x == 0) atomicAdd(&ctl[kCtlDown], my_down);
-      my_down = 0;
-    }
-    if (u >= total) break;
+
+  // Phase 1: the front-end units (claims only grow, so a workgroup never comes back here).
+  // A workgroup claims its next unit only when it has finished this one: the front-end units
+  // are short and every routing unit waits for the slowest router unit, so a unit must not be
+  // reserved by a busy workgroup while an idle one could start it.
+  while (u < fixed) {
     // The arguments are re-read per unit (as in k_experts) so each unit derives its
     // addresses afresh instead of every path's values being held across the loop.
     ArgsPtr ap = (ArgsPtr)__builtin_amdgcn_kernarg_segment_ptr();
     asm volatile("" : "+s"(ap));
     LayerArgs a;
     __builtin_memcpy(&a, (const LayerArgs*)ap, sizeof(a));
-    __syncthreads();
-    if (threadIdx.x == 0) next = atomicAdd(&ctl[kCtlQueue], 1);
     if (u < a.n_norm) {
-      norm_row(a.x_in, a.norm_w, u, a.H, a.eps, a.weight_in_fp32, a.xn, part);
+      norm_row<true>(a.x_in, a.norm_w, u, a.H, a.eps, a.weight_in_fp32, a.xn, part);
       publish_count(&ctl[kCtlNormed]);
     } else if (u < a.n_norm + a.n_router) {
       if (a.n_norm) wait_count(&ctl[kCtlNormed], a.n_norm, &ctl[kCtlError]);
@@ -2340,7 +2338,7 @@ __global__ __launch_bounds__(256, 2) void k_layer(LayerArgs args) {
       else
         layer_router<4>(a, r, rings);
       publish_count(&ctl[kCtlRouted]);
-    } else if (u < fixed) {
+    } else {
       const int t = u - a.n_norm - a.n_router;
       if (a.n_norm) wait_count(&ctl[kCtlNormed], a.n_norm, &ctl[kCtlError]);
       // This token's row of x in E4M3 per 128 (needs nothing else; runs while the router does).
@@ -2366,42 +2364,97 @@ __global__ __launch_bounds__(256, 2) void k_layer(LayerArgs args) {
       if (flag) {
         // Every token is routed: this workgroup runs the permute, then publishes the lists.
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-        permute_block(a.ids, 0, a.T, a.K, a.E, a.S, a.ex.gu.I / kBlock, a.H / kBlock, a.ks, kChunkRows, 0, a.po,
-                      reinterpret_cast<int*>(rings), flags, permute_tile_waves(a.T, a.E, 256, kPermuteLdsInts));
+        permute_block<true>(a.ids, 0, a.T, a.K, a.E, a.S, a.ex.gu.I / kBlock, a.H / kBlock, a.ks, kChunkRows, 0,
+                            a.po, reinterpret_cast<int*>(rings), flags,
+                            permute_tile_waves(a.T, a.E, 256, kPermuteLdsInts));
         publish_fence();
         __syncthreads();
         if (threadIdx.x == 0) __hip_atomic_store(&ctl[kCtlPermuted], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
-    } else if (u < fixed + n_gu) {
-      const int g = u - fixed, nbI = a.ex.gu.I / kBlock;
-      uint8_t* ring = rings + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) * kRingWave;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) slot = atomicAdd(&ctl[kCtlQueue], 1);
+    __syncthreads();
+    u = slot;
+  }
+
+  // Phase 2: the work lists, once the permute has run (its meta words were never read before
+  // in this call). If the wait gave up (error word set), the lists are not read: no expert
+  // units, only the combine units, which then write NaN.
+  wait_count(&ctl[kCtlPermuted], 1, &ctl[kCtlError]);
+  if (threadIdx.x == 0) {
+    const bool lists = load_count(&ctl[kCtlPermuted]) != 0;
+    units[0] = lists ? (SPLIT ? 2 : 1) * load_count(&args.po.meta[kMetaUnitsGU]) : 0;
+    units[1] = lists ? load_count(&args.po.meta[kMetaUnitsDN]) : 0;
+  }
+  __syncthreads();
+  const int n_gu = units[0], n_dn = units[1];
+  const int experts_end = fixed + n_gu + n_dn;
+  const int total = experts_end + (args.T * args.H + kCombineUnit - 1) / kCombineUnit;
+
+  // Phase 3: the expert units, as k_experts runs them (its loop, over the permute's lists).
+  int my_down = 0;  // down units this workgroup finished and has not yet counted
+  while (u < experts_end) {
+    ExArgsPtr ap = (ExArgsPtr)__builtin_amdgcn_kernarg_segment_ptr();  // LayerArgs::ex is at offset 0
+    asm volatile("" : "+s"(ap));
+    ExpertArgs a;
+    __builtin_memcpy(&a, (const ExpertArgs*)ap, sizeof(a));
+    const int nbI = a.gu.I / kBlock, nbH = a.dn.H / kBlock;
+    uint8_t* ring = rings + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) * kRingWave;
+    __syncthreads();
+    if (threadIdx.x == 0) next = atomicAdd(&ctl[kCtlQueue], 1);
+    if (u < fixed + n_gu) {
+      const int g = u - fixed;
       bool done = true;
       if constexpr (SPLIT)
-        done = gateup_work_split(a.ex.gu, g, red, &flag, ring);
+        done = gateup_work_split(a.gu, g, red, &flag, ring);
       else
-        gateup_work(a.ex.gu, g, red, ring);
+        gateup_work(a.gu, g, red, ring);
       if (done) {
         publish_fence();
         __syncthreads();
-        if (threadIdx.x == 0) atomicAdd(&a.ex.ready[a.ex.dn_of_gu[(SPLIT ? g >> 1 : g) / nbI]], 1);
+        if (threadIdx.x == 0) atomicAdd(&a.ready[a.dn_of_gu[(SPLIT ? g >> 1 : g) / nbI]], 1);
       }
-    } else if (u < fixed + n_gu + n_dn) {
-      const int v = u - fixed - n_gu, nbI = a.ex.gu.I / kBlock, nbH = a.H / kBlock, c = v / (nbH * a.ks);
-      uint8_t* ring = rings + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) * kRingWave;
-      const ReadyWait ready{&a.ex.ready[c], a.ex.dn.chunks[c].x == a.E ? a.S * nbI : nbI, &ctl[kCtlError]};
-      down_work(a.ex.dn, v, ready, ring);
-      ++my_down;
     } else {
-      wait_ready(ReadyWait{&ctl[kCtlDown], n_dn + a.force_timeout, &ctl[kCtlError],
-                           a.force_timeout ? (uint64_t)2000 : kWaitTicks, true});
-      layer_combine(a, u - fixed - n_gu - n_dn);
+      const int v = u - fixed - n_gu, c = v / (nbH * a.dn.ks);
+      const ReadyWait ready{&a.ready[c], a.dn.chunks[c].x == a.dn.E ? a.dn.S * nbI : nbI, &ctl[kCtlError]};
+      down_work<true>(a.dn, v, ready, ring);
+      ++my_down;
     }
     if (threadIdx.x == 0) slot = next;
     __syncthreads();
     u = slot;
   }
-  // Leaving: the last workgroup out (every other one has made its last claim) zeroes the
-  // control words for the next call.
+  // Down units are counted once per workgroup, when it moves past them: their d rows (device-
+  // coherent stores) complete first. (An agent-scope release after plain stores instead
+  // writes back the XCD's whole L2, once per workgroup: measured far slower.) The combine
+  // units wait for the full count, which every workgroup with down units adds to before it
+  // combines or leaves.
+  if (my_down) {
+    publish_fence();
+    __syncthreads();
+    if (threadIdx.x == 0) atomicAdd(&ctl[kCtlDown], my_down);
+  }
+
+  // Phase 4: the combine units, once every down unit is counted.
+  if (u < total) {
+    ArgsPtr ap = (ArgsPtr)__builtin_amdgcn_kernarg_segment_ptr();
+    asm volatile("" : "+s"(ap));
+    LayerArgs a;
+    __builtin_memcpy(&a, (const LayerArgs*)ap, sizeof(a));
+    wait_ready(ReadyWait{&ctl[kCtlDown], n_dn + a.force_timeout, &ctl[kCtlError],
+                         a.force_timeout ? (uint64_t)2000 : kWaitTicks, true, 8});
+    while (u < total) {
+      __syncthreads();
+      if (threadIdx.x == 0) next = atomicAdd(&ctl[kCtlQueue], 1);
+      layer_combine(a, u - experts_end);
+      if (threadIdx.x == 0) slot = next;
+      __syncthreads();
+      u = slot;
+    }
+  }
+  // Leaving: the last workgroup out (every other one has made its last claim) keeps the
+  // call's outcome in the status word and zeroes the control words for the next call.
   if (threadIdx.x == 0 && atomicAdd(&ctl[kCtlExited], 1) == (int)gridDim.x - 1) {
     __hip_atomic_store(&ctl[kCtlStatus], load_count(&ctl[kCtlError]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const int words[] = {kCtlQueue, kCtlNormed, kCtlRouted, kCtlSelected, kCtlPermuted, kCtlDown, kCtlError,
