@@ -233,7 +233,7 @@ int megamoe_layer_forward(const megamoe_desc* desc, const megamoe_tensors* t, co
  * 0.2 s; every kernel still ends, and y is NaN), else 0. Synchronizes `stream` (a host call
  * that copies one word). No reference counterpart: the reference's eager layer has no
  * waits. Test hook: with the environment variable MEGAMOE_FORCE_WAIT_TIMEOUT=1,
- * megamoe_layer_forward's combine units wait for one more down unit than there is, for
+ * megamoe_layer_forward's combine units wait for a count the down units never reach, for
  * 20 us, so the call reports a wait that gave up. */
 int megamoe_layer_status(const megamoe_desc* desc, const void* workspace, size_t workspace_bytes, int32_t* gave_up,
                          void* stream);

@@ -2195,19 +2195,33 @@ __global__ __launch_bounds__(256, 2) void k_experts(ExpertArgs args) {
 // gives up sets the error word and the combine writes NaN). The hand-overs between units
 // follow k_experts' rule: data crosses workgroups as device-coherent stores, is published
 // by a counter raised after the stores completed, and no workgroup reads a line before
-// its last write.
+// its last write. The waits on a whole phase (norm, router, permute, down units) poll the
+// spread flags of a signal instead of the counter itself (see kSigLines).
 //
-// The control words (queue, counters, error) must be zero when a call starts: the
+// The control words (queue, counters, flags, error) must be zero when a call starts: the
 // workspace is zeroed once when it is allocated, and the last workgroup to leave a call
 // zeroes them again, so a call is exactly one launch.
 // =======================================================================================
 
 // kCtlStatus is not zeroed: it keeps the last call's outcome (1: a bounded wait gave up and y
 // is NaN) for megamoe_layer_status; the stream-ordered form's combine writes it too.
-constexpr int kCtlQueue = 0, kCtlNormed = 32, kCtlRouted = 64, kCtlSelected = 96, kCtlPermuted = 128,
-              kCtlDown = 160, kCtlExited = 192, kCtlError = 224, kCtlStatus = 256,
-              kCtlInts = 288;  // one 128-byte line each
+constexpr int kCtlQueue = 0, kCtlNormed = 32, kCtlRouted = 64, kCtlSelected = 96, kCtlDown = 160,
+              kCtlExited = 192, kCtlError = 224, kCtlStatus = 256;  // one 128-byte line each
 constexpr int kCombineUnit = 256 * 8;  // outputs per combine unit
+
+// Signals: "every norm unit is done", "every router unit is done", "the work lists are
+// written", "every down unit is done". Hundreds of workgroups wait on each at once. Polled
+// through one word, the waits slowed the workgroups still working by up to 3x (the last
+// DeepSeek-V3 down units took 37-55 us instead of 12-16; measured per unit): every poll is a
+// device-coherent load at the one memory line that holds the word, which every weight stream
+// crosses too. So a signal is kSigLines flag words on lines of their own (4352 bytes apart,
+// which differ in the low and the high address bits that pick a cache and memory channel):
+// the workgroup whose increment completes a count raises all of them, and each waiting
+// workgroup polls the one its index picks.
+constexpr int kSigNormed = 0, kSigRouted = 1, kSigPermuted = 2, kSigDown = 3, kSignals = 4;
+constexpr int kSigLines = 16, kSigStride = (4096 + 256) / 4;  // flags per signal; ints between flags
+constexpr int kCtlSig = 512;                                  // the first flag
+constexpr int kCtlInts = kCtlSig + kSignals * kSigLines * kSigStride;
 
 struct LayerArgs {
   ExpertArgs ex;
@@ -2231,26 +2245,49 @@ struct LayerArgs {
   int T, H, E, K, S, G, TG, gate, renorm, pow2;
   int nsplit, n_et, ntt, vpl, ks;
   int n_norm, n_router;
-  int force_timeout;  // test hook: the combine units wait for one down unit too many, 20 us at most
+  int force_timeout;  // test hook: the combine units wait for a flag value never raised, 20 us at most
   int pad_;
 };
 
-// Thread 0 waits (bounded in time) until *count >= need, then the workgroup passes a barrier;
-// the acquire keeps the loads that follow below it. Many workgroups wait on these counts at
-// once (the router's, the permute's, the down units'), so they poll patiently.
-__device__ __forceinline__ void wait_count(const int* count, int need, int* error) {
-  wait_ready(ReadyWait{count, need, error, kWaitTicks, true});
+__device__ __forceinline__ int* signal_flag(int* ctl, int sig, int line) {
+  return ctl + kCtlSig + (sig * kSigLines + line) * kSigStride;
+}
+
+// The flag of signal `sig` this workgroup polls (workgroups are dealt to the 8 XCDs in turn,
+// so the bits above the lowest three spread each XCD's waiters over the lines).
+__device__ __forceinline__ int* my_signal_flag(int* ctl, int sig) {
+  return signal_flag(ctl, sig, (blockIdx.x >> 3) & (kSigLines - 1));
+}
+
+// Raises signal `sig`, by the workgroup whose count increment completed it (after the atomic
+// returned, so every unit's stores, completed before its own increment, are in memory).
+__device__ __forceinline__ void raise_signal(int* ctl, int sig) {
+  if (threadIdx.x < kSigLines)
+    __hip_atomic_store(signal_flag(ctl, sig, threadIdx.x), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Thread 0 waits (bounded in time) until this workgroup's flag of `sig` reaches `need` (1;
+// more only for the timeout test hook), then the workgroup passes a barrier; the acquire
+// keeps the loads that follow below it.
+__device__ __forceinline__ void wait_signal(int* ctl, int sig, int need = 1, uint64_t ticks = kWaitTicks) {
+  wait_ready(ReadyWait{my_signal_flag(ctl, sig), need, &ctl[kCtlError], ticks, true});
 }
 
 __device__ __forceinline__ int load_count(const int* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// After a unit's stores: they complete, then thread 0 raises `count`.
-__device__ __forceinline__ int publish_count(int* count) {
+// After a unit's stores: they complete, then thread 0 adds `add` to ctl[word]; the
+// workgroup whose addition brings it to `need` raises `sig` (if sig >= 0). Returns the
+// count before the addition (in every thread).
+__device__ __forceinline__ int publish_count(int* ctl, int word, int add, int need, int sig, int* old_lds) {
   publish_fence();
   __syncthreads();
-  return threadIdx.x == 0 ? atomicAdd(count, 1) : 0;
+  if (threadIdx.x == 0) *old_lds = atomicAdd(&ctl[word], add);
+  __syncthreads();
+  const int old = *old_lds;
+  if (sig >= 0 && old + add == need) raise_signal(ctl, sig);
+  return old;
 }
 
 template <int NTT>
@@ -2327,9 +2364,9 @@ __global__ __launch_bounds__(256, 2) void k_layer(LayerArgs args) {
     __builtin_memcpy(&a, (const LayerArgs*)ap, sizeof(a));
     if (u < a.n_norm) {
       norm_row<true>(a.x_in, a.norm_w, u, a.H, a.eps, a.weight_in_fp32, a.xn, part);
-      publish_count(&ctl[kCtlNormed]);
+      publish_count(ctl, kCtlNormed, 1, a.n_norm, kSigNormed, &units[0]);
     } else if (u < a.n_norm + a.n_router) {
-      if (a.n_norm) wait_count(&ctl[kCtlNormed], a.n_norm, &ctl[kCtlError]);
+      if (a.n_norm) wait_signal(ctl, kSigNormed);
       const int r = u - a.n_norm;
       if (a.ntt == 1)
         layer_router<1>(a, r, rings);
@@ -2337,17 +2374,17 @@ __global__ __launch_bounds__(256, 2) void k_layer(LayerArgs args) {
         layer_router<2>(a, r, rings);
       else
         layer_router<4>(a, r, rings);
-      publish_count(&ctl[kCtlRouted]);
+      publish_count(ctl, kCtlRouted, 1, a.n_router, kSigRouted, &units[0]);
     } else {
       const int t = u - a.n_norm - a.n_router;
-      if (a.n_norm) wait_count(&ctl[kCtlNormed], a.n_norm, &ctl[kCtlError]);
+      if (a.n_norm) wait_signal(ctl, kSigNormed);
       // This token's row of x in E4M3 per 128 (needs nothing else; runs while the router does).
       const int nbh = a.H / kBlock, lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
       for (int b = wv; b < nbh; b += 4) {
         const size_t o = (size_t)t * a.H + (size_t)b * kBlock;
         quant_block4(a.x + o, a.xq + o, a.xs + (size_t)t * nbh + b, a.pow2, lane);
       }
-      wait_count(&ctl[kCtlRouted], a.n_router, &ctl[kCtlError]);
+      wait_signal(ctl, kSigRouted);
       if (a.vpl == 1)
         layer_select<1>(a, t, rings);
       else if (a.vpl == 2)
@@ -2358,10 +2395,7 @@ __global__ __launch_bounds__(256, 2) void k_layer(LayerArgs args) {
         layer_select<8>(a, t, rings);
       else
         layer_select<16>(a, t, rings);
-      const int done = publish_count(&ctl[kCtlSelected]);
-      if (threadIdx.x == 0) flag = done == a.T - 1;
-      __syncthreads();
-      if (flag) {
+      if (publish_count(ctl, kCtlSelected, 1, a.T, -1, &units[0]) == a.T - 1) {
         // Every token is routed: this workgroup runs the permute, then publishes the lists.
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
         permute_block<true>(a.ids, 0, a.T, a.K, a.E, a.S, a.ex.gu.I / kBlock, a.H / kBlock, a.ks, kChunkRows, 0,
@@ -2369,7 +2403,7 @@ __global__ __launch_bounds__(256, 2) void k_layer(LayerArgs args) {
                             permute_tile_waves(a.T, a.E, 256, kPermuteLdsInts));
         publish_fence();
         __syncthreads();
-        if (threadIdx.x == 0) __hip_atomic_store(&ctl[kCtlPermuted], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        raise_signal(ctl, kSigPermuted);
       }
     }
     __syncthreads();
@@ -2381,9 +2415,9 @@ __global__ __launch_bounds__(256, 2) void k_layer(LayerArgs args) {
   // Phase 2: the work lists, once the permute has run (its meta words were never read before
   // in this call). If the wait gave up (error word set), the lists are not read: no expert
   // units, only the combine units, which then write NaN.
-  wait_count(&ctl[kCtlPermuted], 1, &ctl[kCtlError]);
+  wait_signal(ctl, kSigPermuted);
   if (threadIdx.x == 0) {
-    const bool lists = load_count(&ctl[kCtlPermuted]) != 0;
+    const bool lists = load_count(my_signal_flag(ctl, kSigPermuted)) != 0;
     units[0] = lists ? (SPLIT ? 2 : 1) * load_count(&args.po.meta[kMetaUnitsGU]) : 0;
     units[1] = lists ? load_count(&args.po.meta[kMetaUnitsDN]) : 0;
   }
@@ -2427,23 +2461,18 @@ __global__ __launch_bounds__(256, 2) void k_layer(LayerArgs args) {
   }
   // Down units are counted once per workgroup, when it moves past them: their d rows (device-
   // coherent stores) complete first. (An agent-scope release after plain stores instead
-  // writes back the XCD's whole L2, once per workgroup: measured far slower.) The combine
-  // units wait for the full count, which every workgroup with down units adds to before it
-  // combines or leaves.
-  if (my_down) {
-    publish_fence();
-    __syncthreads();
-    if (threadIdx.x == 0) atomicAdd(&ctl[kCtlDown], my_down);
-  }
+  // writes back the XCD's whole L2, once per workgroup: measured far slower.) The workgroup
+  // whose count completes the down units raises the signal the combine units wait for.
+  if (my_down) publish_count(ctl, kCtlDown, my_down, n_dn, kSigDown, &units[0]);
 
-  // Phase 4: the combine units, once every down unit is counted.
+  // Phase 4: the combine units, once every down unit is counted (no down units: the lists
+  // were not written, the error word is set and the combine writes NaN).
   if (u < total) {
     ArgsPtr ap = (ArgsPtr)__builtin_amdgcn_kernarg_segment_ptr();
     asm volatile("" : "+s"(ap));
     LayerArgs a;
     __builtin_memcpy(&a, (const LayerArgs*)ap, sizeof(a));
-    wait_ready(ReadyWait{&ctl[kCtlDown], n_dn + a.force_timeout, &ctl[kCtlError],
-                         a.force_timeout ? (uint64_t)2000 : kWaitTicks, true, 8});
+    if (n_dn) wait_signal(ctl, kSigDown, 1 + a.force_timeout, a.force_timeout ? (uint64_t)2000 : kWaitTicks);
     while (u < total) {
       __syncthreads();
       if (threadIdx.x == 0) next = atomicAdd(&ctl[kCtlQueue], 1);
@@ -2453,13 +2482,27 @@ __global__ __launch_bounds__(256, 2) void k_layer(LayerArgs args) {
       u = slot;
     }
   }
-  // Leaving: the last workgroup out (every other one has made its last claim) keeps the
-  // call's outcome in the status word and zeroes the control words for the next call.
-  if (threadIdx.x == 0 && atomicAdd(&ctl[kCtlExited], 1) == (int)gridDim.x - 1) {
-    __hip_atomic_store(&ctl[kCtlStatus], load_count(&ctl[kCtlError]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const int words[] = {kCtlQueue, kCtlNormed, kCtlRouted, kCtlSelected, kCtlPermuted, kCtlDown, kCtlError,
-                         kCtlExited};
-    for (int w : words) __hip_atomic_store(&ctl[w], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // Leaving: the last workgroup out (every other one has finished its last wait and unit)
+  // keeps the call's outcome in the status word and zeroes the counters and the signal flags
+  // for the next call.
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const bool last = atomicAdd(&ctl[kCtlExited], 1) == (int)gridDim.x - 1;
+    if (last)
+      __hip_atomic_store(&ctl[kCtlStatus], load_count(&ctl[kCtlError]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    slot = last;
+  }
+  __syncthreads();
+  if (slot) {
+    constexpr int words[] = {kCtlQueue, kCtlNormed, kCtlRouted, kCtlSelected, kCtlDown, kCtlError, kCtlExited};
+    constexpr int n_words = sizeof(words) / sizeof(words[0]);
+    static_assert(n_words + kSignals * kSigLines <= 256, "one store per thread");
+    const int i = threadIdx.x;
+    if (i < n_words)
+      __hip_atomic_store(&ctl[words[i]], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else if (i < n_words + kSignals * kSigLines)
+      __hip_atomic_store(signal_flag(ctl, (i - n_words) / kSigLines, (i - n_words) % kSigLines), 0,
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
