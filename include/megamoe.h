@@ -129,7 +129,7 @@ int megamoe_forward(const megamoe_desc* desc, const megamoe_tensors* t, void* st
  * that forbid hipMalloc). No reference counterpart. t->workspace and t->workspace_bytes are
  * ignored. Returns MEGAMOE_ERR_SCRATCH, launching nothing, when megamoe_workspace_bytes(desc)
  * exceeds MEGAMOE_SCRATCH_BYTES (each of the five benchmark configs fits: Kimi-K2 at 128 tokens needs
- * 27 MiB). All calls on one GPU share its scratch: calls that overlap on that GPU (on two
+ * 29 MiB). All calls on one GPU share its scratch: calls that overlap on that GPU (on two
  * streams, or from two threads) race and must be ordered by the caller. */
 int megamoe_forward_noalloc(const megamoe_desc* desc, const megamoe_tensors* t, void* stream);
 

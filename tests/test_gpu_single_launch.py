@@ -93,7 +93,7 @@ def test_one_call_is_one_kernel_launch():
 
 
 def test_a_wait_that_gives_up_is_reported(monkeypatch):
-    """The test hook makes the combine units wait for one down unit more than there is, for
+    """The test hook makes the combine units wait for a count the down units never reach, for
     20 us: every kernel ends, y is NaN, and the status word reports it; the next call on the
     same workspace is whole again and reports nothing."""
     case = C.development(C.case(C.HEADLINE))
