@@ -170,11 +170,11 @@ __device__ __forceinline__ void quant_block(const uint16_t* src, uint8_t* dst, f
 }
 
 // The same quantization of one full 128-wide block with four values per lane on lanes
-// 0..31, so each lane writes its codes as one 4-byte device-coherent store (the
-// single-launch kernel's expert units read them from other workgroups).
-__device__ __forceinline__ void quant_block4(const uint16_t* src, uint8_t* dst, float* scale, int pow2, int lane) {
+// 0..31 (`four`, loaded by the caller), so each lane writes its codes as one 4-byte
+// device-coherent store (the single-launch kernel's expert units read them from other
+// workgroups).
+__device__ __forceinline__ void quant_four(uint2 four, uint8_t* dst, float* scale, int pow2, int lane) {
   const int l = lane & 31;
-  const uint2 four = *reinterpret_cast<const uint2*>(src + 4 * l);
   const float v[4] = {bf16_bits_to_f32(four.x & 0xffffu), bf16_bits_to_f32(four.x >> 16),
                       bf16_bits_to_f32(four.y & 0xffffu), bf16_bits_to_f32(four.y >> 16)};
   const float m = lane < 32 ? fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))) : 0.0f;
@@ -184,6 +184,27 @@ __device__ __forceinline__ void quant_block4(const uint16_t* src, uint8_t* dst, 
   for (int i = 0; i < 4; ++i) q |= f32_to_e4m3(clamp448(v[i] / s)) << (8 * i);
   if (lane < 32) store_coherent(reinterpret_cast<uint32_t*>(dst + 4 * l), q);
   if (lane == 0) store_coherent(scale, s);
+}
+
+// One row of x (nbh blocks) by the workgroup's four wavefronts, wavefront wv taking blocks
+// wv, wv + 4, ...: each wavefront issues the loads of up to 8 of its blocks before it
+// reduces the first.
+__device__ __forceinline__ void quant_row(const uint16_t* x, uint8_t* xq, float* xs, int nbh, int pow2, int lane,
+                                          int wv) {
+  constexpr int kBatch = 8;
+  for (int b0 = wv; b0 < nbh; b0 += 4 * kBatch) {
+    uint2 four[kBatch];
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      const int b = min(b0 + 4 * j, nbh - 1);  // clamped into the row; blocks past the end are dropped
+      four[j] = *reinterpret_cast<const uint2*>(x + (size_t)b * kBlock + 4 * (lane & 31));
+    }
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      const int b = b0 + 4 * j;
+      if (b < nbh) quant_four(four[j], xq + (size_t)b * kBlock, xs + b, pow2, lane);
+    }
+  }
 }
 
 // Ragged rows (any column count): one wavefront per (row, 128-column block).
@@ -2393,10 +2414,7 @@ __global__ __launch_bounds__(256, 2) void k_layer(LayerArgs args) {
       if (a.n_norm) wait_signal(ctl, kSigNormed);
       // This token's row of x in E4M3 per 128 (needs nothing else; runs while the router does).
       const int nbh = a.H / kBlock, lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-      for (int b = wv; b < nbh; b += 4) {
-        const size_t o = (size_t)t * a.H + (size_t)b * kBlock;
-        quant_block4(a.x + o, a.xq + o, a.xs + (size_t)t * nbh + b, a.pow2, lane);
-      }
+      quant_row(a.x + (size_t)t * a.H, a.xq + (size_t)t * a.H, a.xs + (size_t)t * nbh, nbh, a.pow2, lane, wv);
       wait_signal(ctl, kSigRouted);
       if (a.vpl == 1)
         layer_select<1>(a, t, rings);
