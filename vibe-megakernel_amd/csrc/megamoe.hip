@@ -1345,6 +1345,7 @@ __device__ __forceinline__ void wait_ready(const ReadyWait& w) {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 }
 
+
 // The RT tiles of one ring slot in MFMA layout. The reads are inline asm: the compiler
 // takes any LDS read that follows a global_load_lds as depending on the most recent one
 // and would wait for every load in flight (vmcnt 0) before it, while the ring's own vmcnt
@@ -2006,28 +2007,47 @@ __device__ __forceinline__ void down_work(const DownArgs& a, int v, const ReadyW
 
 // y[t, h0 .. h0+7] = bf16( sum_slot fp32(d[t,slot]) * w[t,slot]  (slot order, each product
 //                          rounded) + fp32(shared[t]) )          frontier.py:349-354
+//
+// Slots are worked eight at a time: their rows (inv) and weights first (SlotRows; the
+// single-launch kernel loads them before it waits for the down units, since the permute and
+// the routing wrote them), then every d load of the eight at once.
+struct SlotRows {
+  int row[8];
+  float w[8];
+};
+
+__device__ __forceinline__ void load_slots(const int* __restrict__ inv, const float* __restrict__ wts, int K, int t,
+                                           int s0, SlotRows& r) {
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    const int s = min(s0 + u, K - 1);  // clamped, unconditional loads
+    r.row[u] = inv[t * K + s];
+    r.w[u] = wts ? wts[t * K + s] : 1.0f;  // no weights: already applied (the MXFP4 form)
+  }
+}
+
 __device__ __forceinline__ void combine8(const uint16_t* __restrict__ d_r, const uint16_t* __restrict__ d_s,
                                          const int* __restrict__ inv, const float* __restrict__ wts, int H, int K,
-                                         int S, int t, int h0, float (&acc)[8]) {
+                                         int S, int t, int h0, float (&acc)[8], const SlotRows* first = nullptr) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
-  for (int s0 = 0; s0 < K; s0 += 8) {  // eight slots' loads in flight at a time
+  for (int s0 = 0; s0 < K; s0 += 8) {
+    SlotRows r;
+    if (s0 == 0 && first)
+      r = *first;
+    else
+      load_slots(inv, wts, K, t, s0, r);
     uint4 v[8];
-    float wv[8];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int s = min(s0 + u, K - 1);  // clamped, unconditional loads
-      v[u] = *reinterpret_cast<const uint4*>(d_r + (size_t)inv[t * K + s] * H + h0);
-      wv[u] = wts ? wts[t * K + s] : 1.0f;  // no weights: already applied (the MXFP4 form)
-    }
+    for (int u = 0; u < 8; ++u) v[u] = *reinterpret_cast<const uint4*>(d_r + (size_t)r.row[u] * H + h0);
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       if (s0 + u < K) {
         const uint32_t q[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          acc[2 * i] = __fadd_rn(acc[2 * i], __fmul_rn(bf16_bits_to_f32(q[i] & 0xffffu), wv[u]));
-          acc[2 * i + 1] = __fadd_rn(acc[2 * i + 1], __fmul_rn(bf16_bits_to_f32(q[i] >> 16), wv[u]));
+          acc[2 * i] = __fadd_rn(acc[2 * i], __fmul_rn(bf16_bits_to_f32(q[i] & 0xffffu), r.w[u]));
+          acc[2 * i + 1] = __fadd_rn(acc[2 * i + 1], __fmul_rn(bf16_bits_to_f32(q[i] >> 16), r.w[u]));
         }
       }
     }
@@ -2043,47 +2063,66 @@ __device__ __forceinline__ void combine8(const uint16_t* __restrict__ d_r, const
   }
 }
 
+// d = bf16(the sum of the KS fp32 parts of a row, in part order) for the 8 outputs at `src`
+// (parts `part` floats apart): every part's load is issued before the first add.
+template <int KS>
+__device__ __forceinline__ void sum_parts8(const float* __restrict__ src, size_t part, float (&dv)[8]) {
+  f32x4 lo[KS], hi[KS];
+#pragma unroll
+  for (int kp = 0; kp < KS; ++kp) {
+    lo[kp] = *reinterpret_cast<const f32x4*>(src + kp * part);
+    hi[kp] = *reinterpret_cast<const f32x4*>(src + kp * part + 4);
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) dv[i] = 0.0f;
+#pragma unroll
+  for (int kp = 0; kp < KS; ++kp) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      dv[i] = __fadd_rn(dv[i], lo[kp][i]);
+      dv[4 + i] = __fadd_rn(dv[4 + i], hi[kp][i]);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) dv[i] = round_bf16(dv[i]);
+}
+
+__device__ __forceinline__ void sum_parts8(const float* __restrict__ src, size_t part, int ks, float (&dv)[8]) {
+  if (ks == 2)
+    sum_parts8<2>(src, part, dv);
+  else if (ks == 4)
+    sum_parts8<4>(src, part, dv);
+  else
+    sum_parts8<8>(src, part, dv);  // down_splits gives 2, 4 or 8 parts when it splits
+}
+
 // The same combine when the down GEMMs were split over ks K parts: d = bf16(sum of the
 // fp32 parts in part order) for every slot row and for the shared row, then as combine8.
 __device__ __forceinline__ void combine8_parts(const float* __restrict__ p_r, const float* __restrict__ p_s, int ks,
                                                const int* __restrict__ inv, const float* __restrict__ wts, int T,
-                                               int H, int K, int S, int t, int h0, float (&acc)[8]) {
+                                               int H, int K, int S, int t, int h0, float (&acc)[8],
+                                               const SlotRows* first = nullptr) {
   const size_t TK = (size_t)T * K;
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
-  for (int s = 0; s < K; ++s) {
-    const int row = inv[t * K + s];
-    const float wv = wts ? wts[t * K + s] : 1.0f;
-    float dv[8];
+  for (int s0 = 0; s0 < K; s0 += 8) {
+    SlotRows r;
+    if (s0 == 0 && first)
+      r = *first;
+    else
+      load_slots(inv, wts, K, t, s0, r);
+    for (int u = 0; u < 8 && s0 + u < K; ++u) {
+      float dv[8];
+      sum_parts8(p_r + (size_t)r.row[u] * H + h0, TK * H, ks, dv);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) dv[i] = 0.0f;
-    for (int kp = 0; kp < ks; ++kp) {
-      const float* src = p_r + ((size_t)kp * TK + row) * H + h0;
-      const f32x4 lo = *reinterpret_cast<const f32x4*>(src), hi = *reinterpret_cast<const f32x4*>(src + 4);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        dv[i] = __fadd_rn(dv[i], lo[i]);
-        dv[4 + i] = __fadd_rn(dv[4 + i], hi[i]);
-      }
+      for (int i = 0; i < 8; ++i) acc[i] = __fadd_rn(acc[i], __fmul_rn(dv[i], r.w[u]));
     }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) acc[i] = __fadd_rn(acc[i], __fmul_rn(round_bf16(dv[i]), wv));
   }
   if (S > 0) {
     float dv[8];
+    sum_parts8(p_s + (size_t)t * H + h0, (size_t)T * H, ks, dv);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) dv[i] = 0.0f;
-    for (int kp = 0; kp < ks; ++kp) {
-      const float* src = p_s + ((size_t)kp * T + t) * H + h0;
-      const f32x4 lo = *reinterpret_cast<const f32x4*>(src), hi = *reinterpret_cast<const f32x4*>(src + 4);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        dv[i] = __fadd_rn(dv[i], lo[i]);
-        dv[4 + i] = __fadd_rn(dv[4 + i], hi[i]);
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) acc[i] = __fadd_rn(acc[i], round_bf16(dv[i]));
+    for (int i = 0; i < 8; ++i) acc[i] = __fadd_rn(acc[i], dv[i]);
   }
 }
 
@@ -2336,8 +2375,9 @@ __device__ __forceinline__ void layer_select(const LayerArgs& a, int token, uint
                     a.ids, a.wts, token, *reinterpret_cast<SelectLds*>(lds));
 }
 
-// Combine unit c: outputs [c * kCombineUnit, +kCombineUnit) of y, as k_combine.
-__device__ __forceinline__ void layer_combine(const LayerArgs& a, int c) {
+// Combine unit c: outputs [c * kCombineUnit, +kCombineUnit) of y, as k_combine (`first`:
+// the thread's first eight slots, loaded already, or NULL).
+__device__ __forceinline__ void layer_combine(const LayerArgs& a, int c, const SlotRows* first = nullptr) {
   const DownArgs& dn = a.ex.dn;
   const int i = c * (kCombineUnit / 8) + threadIdx.x, per_row = a.H / 8;
   if (i >= a.T * per_row) return;
@@ -2348,9 +2388,9 @@ __device__ __forceinline__ void layer_combine(const LayerArgs& a, int c) {
   const int t = i / per_row, h0 = (i % per_row) * 8;
   float acc[8];
   if (a.ks > 1)
-    combine8_parts(dn.p_r, dn.p_s, a.ks, a.po.inv, a.wts, a.T, a.H, a.K, a.S, t, h0, acc);
+    combine8_parts(dn.p_r, dn.p_s, a.ks, a.po.inv, a.wts, a.T, a.H, a.K, a.S, t, h0, acc, first);
   else
-    combine8(dn.d_r, dn.d_s, a.po.inv, a.wts, a.H, a.K, a.S, t, h0, acc);
+    combine8(dn.d_r, dn.d_s, a.po.inv, a.wts, a.H, a.K, a.S, t, h0, acc, first);
   uint32_t o[4];
   if (a.residual) {
     const uint4 v = *reinterpret_cast<const uint4*>(a.residual + (size_t)t * a.H + h0);
@@ -2504,11 +2544,20 @@ __global__ __launch_bounds__(256, 2) void k_layer(LayerArgs args) {
     asm volatile("" : "+s"(ap));
     LayerArgs a;
     __builtin_memcpy(&a, (const LayerArgs*)ap, sizeof(a));
+    // The first unit's slot rows and weights (written before the lists were published) load
+    // while the down units finish.
+    SlotRows first;
+    {
+      const int i = (u - experts_end) * (kCombineUnit / 8) + threadIdx.x, per_row = a.H / 8;
+      load_slots(a.po.inv, a.wts, a.K, min(i, a.T * per_row - 1) / per_row, 0, first);
+    }
     if (n_dn) wait_signal(ctl, kSigDown, 1 + a.force_timeout, a.force_timeout ? (uint64_t)2000 : kWaitTicks);
+    bool use_first = true;
     while (u < total) {
       __syncthreads();
       if (threadIdx.x == 0) next = atomicAdd(&ctl[kCtlQueue], 1);
-      layer_combine(a, u - experts_end);
+      layer_combine(a, u - experts_end, use_first ? &first : nullptr);
+      use_first = false;
       if (threadIdx.x == 0) slot = next;
       __syncthreads();
       u = slot;
@@ -3555,17 +3604,18 @@ int down_splits(const megamoe_desc& d) {
 }
 
 // Whether the expert kernel works gate and up of each 128-row block as separate units
-// (k_experts<true>). Worth it when the whole-block units cannot fill two rounds of a
-// reference grid (2 per CU on 256 CUs) even if every expert is hit, so the last blocks of
-// each expert (which its down units wait for) land late, and the rows are long enough (32
-// or more K blocks) for the hand-over between the halves to be cheap next to the stream:
-// a Mixtral-shaped layer (8 experts of 112 blocks, H 4096) ran 6% faster split, and the
-// DeepSeek-V3, Kimi-K2 and Qwen3-30B-A3B shapes 3-7% slower. Depends on the geometry
-// only; both forms give the same bits.
+// (k_experts<true>). Worth it only when the whole-block units cannot fill one round of a
+// reference grid (2 per CU on 256 CUs) even if every expert is hit, and the rows are long
+// enough (32 or more K blocks) for the hand-over between the halves to be cheap next to the
+// stream. A Mixtral-shaped layer (8 experts of 112 blocks: 896 units, 1.75 rounds) streams
+// its gate/up phase at 6.3-6.6 TB/s split and at 6.9-7.0 whole (per-unit timelines;
+// 231 -> 224 us for the stream-ordered expert kernel, 286 -> 282 us for the single launch),
+// and DeepSeek-V3, Kimi-K2 and Qwen3-30B-A3B measured 3-7% slower split. Depends on the
+// geometry only; both forms give the same bits.
 bool split_gate_up(const megamoe_desc& d) {
   const size_t hit = (size_t)(d.experts < (int64_t)d.tokens * d.topk ? d.experts : (int64_t)d.tokens * d.topk);
   const size_t units = (hit + (size_t)d.shared_experts) * (size_t)(d.intermediate / kBlock);
-  return units < 2 * 512 && d.hidden / kBlock >= 32;
+  return units < 512 && d.hidden / kBlock >= 32;
 }
 
 Layout make_layout(const megamoe_desc& d) {
@@ -3915,7 +3965,12 @@ int forward_layer_impl(const megamoe_desc* desc, const megamoe_tensors* t, const
   la.nsplit = L.nsplit;
   la.n_et = (E + kRouterTile - 1) / kRouterTile;
   const int tiles = (T + kRouterTile - 1) / kRouterTile;
+  // Token tiles per router unit: k_router's choice, halved while the units still fit in one
+  // round of the grid (a shorter fp64 MFMA chain per unit: Qwen3-30B-A3B 139 -> 136 us).
   la.ntt = tiles <= 1 ? 1 : (tiles <= 2 ? 2 : 4);
+  while (la.ntt > 1 && (size_t)la.n_et * L.nsplit * ((tiles + la.ntt / 2 - 1) / (la.ntt / 2)) <=
+                           (size_t)di.cus * di.layer_per_cu)
+    la.ntt /= 2;
   const int passes = (tiles + la.ntt - 1) / la.ntt;
   la.vpl = E <= 64 ? 1 : (E <= 128 ? 2 : (E <= 256 ? 4 : (E <= 512 ? 8 : 16)));
   la.ks = L.ks;
