@@ -78,22 +78,32 @@ def kernel_bytes(case, hit: int) -> dict:
 
 
 def mx_kernel(rows: int, experts: int) -> str:
-    """The MXFP4 expert kernel the library runs: batch mode from 24 rows per expert on
-    average (kBatchMinRows in the library), the decode kernel below."""
+    """The MXFP4 expert kernel of the stream-ordered form: batch mode from 24 rows per expert
+    on average (kBatchMinRows in the library), the decode kernel below."""
     return "k_experts_mx_batch" if rows >= 24 * experts else "k_experts_mx"
 
 
 def fp8_kernel(case) -> str:
     """The FP8 expert kernel the library runs: the split gate/up form when the whole-block
-    gate/up units cannot fill two rounds of a 512-workgroup grid with every expert hit and
+    gate/up units cannot fill one round of a 512-workgroup grid with every expert hit and
     the rows have 32 or more K blocks (split_gate_up in csrc/megamoe.hip)."""
     hit = min(case.experts, case.tokens * case.topk) + case.shared_experts
-    split = hit * (case.intermediate // 128) < 2 * 512 and case.hidden // 128 >= 32
+    split = hit * (case.intermediate // 128) < 512 and case.hidden // 128 >= 32
     return "k_experts<true>" if split else "k_experts<false>"
 
 
+def expert_kernel(case) -> str:
+    """The expert kernel of the stream-ordered form."""
+    if case.format == "mxfp4":
+        return mx_kernel(case.tokens * case.topk, case.experts)
+    return fp8_kernel(case)
+
+
 def layer_kernel(case) -> str:
-    """The single-launch kernel of the fp8 forms (k_layer; split gate/up as fp8_kernel)."""
+    """The single-launch kernel: k_layer for the fp8 forms (split gate/up as fp8_kernel),
+    k_layer_mx for the MXFP4 form."""
+    if case.format == "mxfp4":
+        return "k_layer_mx"
     return fp8_kernel(case).replace("k_experts", "k_layer")
 
 
@@ -265,7 +275,8 @@ def bench_case(case, steps: int, warmup: int, want_cpu: bool, cpu_budget: float)
         k_ms = r["stage_us"]["layer"] * 1e-3
         result["roofline"] = {"bound": "hbm", "achieved": bytes_step / (k_ms * 1e-3) / 1e9, "peak": PEAK_HBM / 1e9,
                               "unit": "GB/s", "frac": bytes_step / (k_ms * 1e-3) / PEAK_HBM,
-                              "traffic": measured_traffic(case, "k_layer"), "kernel": layer_kernel(case),
+                              "traffic": measured_traffic(case, layer_kernel(case).split("<")[0]),
+                              "kernel": layer_kernel(case),
                               "kernel_us": k_ms * 1e3, "bytes_per_launch": bytes_step}
         # The stream-ordered kernels of the same layer, for their per-stage times and the
         # expert kernel's own roofline.
@@ -276,10 +287,10 @@ def bench_case(case, steps: int, warmup: int, want_cpu: bool, cpu_budget: float)
         ex_bytes = kb["gate_up"] + kb["down"]
         result["stream_ordered"] = {
             "us_per_step": r5["ms"] * 1e3, "p50_us": r5["p50_us"], "stage_us": r5["stage_us"],
-            "launches_per_step": 5 + (case.norm != "none"),
-            "expert_kernel": {"kernel": fp8_kernel(case), "kernel_us": ex_ms * 1e3, "bytes_per_launch": ex_bytes,
+            "launches_per_step": len(five.stages),
+            "expert_kernel": {"kernel": expert_kernel(case), "kernel_us": ex_ms * 1e3, "bytes_per_launch": ex_bytes,
                               "frac": ex_bytes / (ex_ms * 1e-3) / PEAK_HBM,
-                              "traffic": measured_traffic(case)}}
+                              "traffic": measured_traffic(case, expert_kernel(case).split("<")[0])}}
     else:
         kb = kernel_bytes(case, hit)
         ex_ms = r["stage_us"]["experts"] * 1e-3

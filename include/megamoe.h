@@ -270,7 +270,7 @@ typedef struct megamoe_mx_tensors {
   size_t workspace_bytes;
 } megamoe_mx_tensors;
 
-/* Workspace of megamoe_mx_forward (host call). desc: tokens, hidden and intermediate
+/* Workspace of megamoe_mx_forward and megamoe_mx_layer_forward (host call). desc: tokens, hidden and intermediate
  * (multiples of 256), experts, topk; shared_experts must be 0; the other fields are
  * unused. No reference counterpart. */
 int megamoe_mx_workspace_bytes(const megamoe_desc* desc, size_t* bytes);
@@ -284,6 +284,23 @@ int megamoe_mx_workspace_bytes(const megamoe_desc* desc, size_t* bytes);
  * combine). Replaces megamoe.reference(serial=True), megamoe.py:153-182. */
 int megamoe_mx_forward(const megamoe_desc* desc, float swiglu_limit, const megamoe_mx_tensors* t, void* stream,
                        void* const* events);
+
+/* megamoe_mx_forward in one kernel launch (the reference's budget of one launch per call,
+ * megabench/cases.py:32): one persistent kernel runs the permute, the expert units and the
+ * combine, with the results of megamoe_mx_forward bit for bit. Rows that average 24 or more
+ * per expert (the batch-shaped EP share) take megamoe_mx_forward's kernels instead. Workspace:
+ * megamoe_mx_workspace_bytes(desc) bytes, ZEROED before its first use with this entry point;
+ * each call leaves its control words zero again. Calls sharing a workspace must be ordered.
+ * `events` is NULL or events[0..1], recorded before and after the call. Replaces
+ * megamoe.reference(serial=True), megamoe.py:153-182. */
+int megamoe_mx_layer_forward(const megamoe_desc* desc, float swiglu_limit, const megamoe_mx_tensors* t,
+                             void* stream, void* const* events);
+
+/* Outcome of the last megamoe_mx_layer_forward on `workspace`: *failed = 1 if one of its
+ * bounded waits gave up or the expert ids were bad (y is NaN), else 0. Synchronizes `stream`.
+ * No reference counterpart (test hook as megamoe_layer_status). */
+int megamoe_mx_layer_status(const megamoe_desc* desc, const void* workspace, size_t workspace_bytes, int32_t* failed,
+                            void* stream);
 
 /* Expert parallelism, one rank's share (megamoe.py:153-182 with ep ranks): expert e belongs
  * to rank e / (E/ep). A rank sends each (token, slot) row to the owner of the slot's expert,
@@ -343,11 +360,12 @@ int megamoe_quantize_rows(int32_t rows, int32_t cols, const void* x, uint8_t* q,
 /* Text for a status code (static storage). */
 const char* megamoe_status_string(int status);
 
-/* ABI version of this library: 8 (1, plus megamoe_block_forward and megamoe_rms_norm in 2,
+/* ABI version of this library: 9 (1, plus megamoe_block_forward and megamoe_rms_norm in 2,
  * plus megamoe_mx_workspace_bytes and megamoe_mx_forward in 3, plus megamoe_ep_dispatch,
  * megamoe_ep_experts and megamoe_ep_combine in 4, plus megamoe_forward_ex and
  * megamoe_combine_by_expert_id in 5, plus megamoe_forward_noalloc in 6, plus
- * megamoe_layer_forward in 7, plus megamoe_layer_status in 8). */
+ * megamoe_layer_forward in 7, plus megamoe_layer_status in 8, plus megamoe_mx_layer_forward
+ * and megamoe_mx_layer_status in 9). */
 int megamoe_abi_version(void);
 
 #ifdef __cplusplus

@@ -120,3 +120,54 @@ def test_rows_do_not_depend_on_the_kernel_mode():
     assert torch.equal(y_small, y_large[:8])
     want, exact = mx.reference(large, values)["y"], mx.oracle(large, values)["y"]
     _check(large, y_large.cpu(), want, exact)
+
+
+@pytest.mark.parametrize("case", _dev_cases() + [C.case(MXCASE)], ids=lambda c: f"T{c.tokens}-E{c.experts}-H{c.hidden}")
+def test_mx_single_launch_equals_stream_ordered(case):
+    """megamoe_mx_layer_forward (one launch; the batch-shaped geometries take the stream-ordered
+    kernels) gives megamoe_mx_forward's bits, over consecutive calls on one workspace."""
+    _log(f"mx single launch {case.id} T={case.tokens} E={case.experts}")
+    one = submission.MoELayer(case)
+    three = submission.MoELayer(case, single_launch=False)
+    assert one.single_launch and not three.single_launch
+    for seed in (5, 6):
+        values = workloads.make_inputs(case, seed, DEV)
+        a, b = one(values)["y"], three(values)["y"]
+        torch.cuda.synchronize()
+        assert torch.equal(a, b), f"{case.id} seed {seed}"
+        assert torch.isfinite(a.float()).all()
+    assert not one.gave_up(torch.device(DEV))
+
+
+def test_mx_one_call_is_one_kernel_launch():
+    from torch.profiler import ProfilerActivity, profile
+
+    case = C.development(C.case(MXCASE))
+    values = _to(workloads.make_inputs(case, 3, "cpu"), DEV)
+    run = submission.build(case.to_dict())
+    run(values)  # the workspace is made (and zeroed) on the first call
+    torch.cuda.synchronize()
+    with profile(activities=[ProfilerActivity.CPU, ProfilerActivity.CUDA]) as prof:
+        run(values)
+        torch.cuda.synchronize()
+    kernels = [e.name for e in prof.events() if e.device_type == torch.autograd.DeviceType.CUDA]
+    _log(f"device events of one call: {kernels}")
+    assert len(kernels) == 1 and "k_layer_mx" in kernels[0], kernels
+    assert case.max_gpu_launches == 1
+
+
+def test_mx_single_launch_reports_bad_ids():
+    """Bad ids make y NaN and the status word say so; the next good call clears it."""
+    case = C.development(C.case(MXCASE), tokens=8)
+    layer = submission.MoELayer(case)
+    values = workloads.make_inputs(case, 6, "cpu")
+    ids = values["topk_idx"].clone()
+    ids[3, 1] = case.experts
+    y = layer(_to({**values, "topk_idx": ids}, DEV))["y"]
+    torch.cuda.synchronize()
+    assert torch.isnan(y.float()).all()
+    assert layer.gave_up(torch.device(DEV))
+    y2 = layer(_to(values, DEV))["y"]
+    torch.cuda.synchronize()
+    assert torch.isfinite(y2.float()).all()
+    assert not layer.gave_up(torch.device(DEV))

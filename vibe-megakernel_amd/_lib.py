@@ -25,8 +25,8 @@ SYMBOLS = ("megamoe_workspace_bytes", "megamoe_forward", "megamoe_forward_events
            "megamoe_abi_version", "megamoe_block_forward", "megamoe_rms_norm", "megamoe_mx_workspace_bytes",
            "megamoe_mx_forward", "megamoe_ep_dispatch", "megamoe_ep_experts", "megamoe_ep_combine",
            "megamoe_forward_ex", "megamoe_combine_by_expert_id", "megamoe_forward_noalloc",
-           "megamoe_layer_forward", "megamoe_layer_status")
-ABI_VERSION = 8
+           "megamoe_layer_forward", "megamoe_layer_status", "megamoe_mx_layer_forward", "megamoe_mx_layer_status")
+ABI_VERSION = 9
 
 
 class Desc(ctypes.Structure):
@@ -102,6 +102,8 @@ def load() -> ctypes.CDLL:
                                      ctypes.c_int32, c_void_p, c_void_p]
     lib.megamoe_mx_workspace_bytes.argtypes = [P(Desc), P(c_size_t)]
     lib.megamoe_mx_forward.argtypes = [P(Desc), ctypes.c_float, P(MxTensors), c_void_p, P(c_void_p)]
+    lib.megamoe_mx_layer_forward.argtypes = [P(Desc), ctypes.c_float, P(MxTensors), c_void_p, P(c_void_p)]
+    lib.megamoe_mx_layer_status.argtypes = [P(Desc), c_void_p, c_size_t, P(ctypes.c_int32), c_void_p]
     lib.megamoe_ep_dispatch.argtypes = [P(Desc), ctypes.c_int32, P(MxTensors), P(EpSend), c_void_p]
     lib.megamoe_ep_experts.argtypes = [P(Desc), ctypes.c_float, ctypes.c_int64, P(MxTensors), c_void_p, P(c_void_p)]
     lib.megamoe_ep_combine.argtypes = [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, c_void_p, c_void_p, c_void_p,

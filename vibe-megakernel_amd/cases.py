@@ -222,7 +222,7 @@ BLOCK_CASES: tuple[Case, ...] = (
 MX_CASES: tuple[Case, ...] = (
     _case("moe-mxfp4-deepseek-v4-pro-t64", "deepseek-ai/DeepSeek-V4-Pro (routed experts, MXFP4)",
           params=dict(tokens=64, hidden=7168, experts=384, topk=6, intermediate=3072),
-          router="given", format="mxfp4", swiglu_limit=10.0, routed_scaling=2.5, max_gpu_launches=3,
+          router="given", format="mxfp4", swiglu_limit=10.0, routed_scaling=2.5,
           note="megamoe numerics in serial mode: E2M1 x E4M3 scaled MFMA, clamped SwiGLU, E8M0 requant"),
 )
 

@@ -3065,7 +3065,27 @@ struct DownMxArgs {
   const uint8_t* spare;
   int T, H, I, K, E, hs_ld, ks;
   int ebase;
+  int coherent;  // d (or its parts) as device-coherent stores: a unit of the same launch reads them
+  int pad_;
 };
+
+// A down unit's output: bf16 d (four values) or the fp32 part (four values).
+__device__ __forceinline__ void store_d_mx(const DownMxArgs& a, uint16_t* p, uint32_t lo, uint32_t hi) {
+  if (a.coherent)
+    store_coherent(reinterpret_cast<uint64_t*>(p), (uint64_t)lo | ((uint64_t)hi << 32));
+  else
+    *reinterpret_cast<uint2*>(p) = make_uint2(lo, hi);
+}
+
+__device__ __forceinline__ void store_part_mx(const DownMxArgs& a, float* p, const f32x4& v) {
+  if (a.coherent) {
+    uint64_t* q = reinterpret_cast<uint64_t*>(p);
+    store_coherent(q, (uint64_t)__float_as_uint(v[0]) | ((uint64_t)__float_as_uint(v[1]) << 32));
+    store_coherent(q + 1, (uint64_t)__float_as_uint(v[2]) | ((uint64_t)__float_as_uint(v[3]) << 32));
+  } else {
+    *reinterpret_cast<f32x4*>(p) = v;
+  }
+}
 
 // Where a down unit's bf16 d row goes: grouped row r of the workspace, or with one slot per
 // token and no K split, the token's output row (y = bf16(fp32(d)) = d needs no combine).
@@ -3108,9 +3128,9 @@ __device__ void down_mx_unit(const DownMxArgs& a, int e, int j, int kp, const Ch
         if (a.ks == 1) {
           const uint32_t lo = f32_to_bf16_bits(acc[p][c][0]) | (f32_to_bf16_bits(acc[p][c][1]) << 16);
           const uint32_t hi = f32_to_bf16_bits(acc[p][c][2]) | (f32_to_bf16_bits(acc[p][c][3]) << 16);
-          *reinterpret_cast<uint2*>(down_row_mx(a, cr, r) + col) = make_uint2(lo, hi);
+          store_d_mx(a, down_row_mx(a, cr, r) + col, lo, hi);
         } else {
-          *reinterpret_cast<f32x4*>(pd + (size_t)(cr.row0 + r) * a.H + col) = acc[p][c];
+          store_part_mx(a, pd + (size_t)(cr.row0 + r) * a.H + col, acc[p][c]);
         }
       }
     }
@@ -3154,9 +3174,9 @@ __device__ void down_mx_wide(const DownMxArgs& a, int e, int j64, int kp, const 
         if (a.ks == 1) {
           const uint32_t lo = f32_to_bf16_bits(acc[p][c][0]) | (f32_to_bf16_bits(acc[p][c][1]) << 16);
           const uint32_t hi = f32_to_bf16_bits(acc[p][c][2]) | (f32_to_bf16_bits(acc[p][c][3]) << 16);
-          *reinterpret_cast<uint2*>(down_row_mx(a, cr, r) + col) = make_uint2(lo, hi);
+          store_d_mx(a, down_row_mx(a, cr, r) + col, lo, hi);
         } else {
-          *reinterpret_cast<f32x4*>(pd + (size_t)(cr.row0 + r) * a.H + col) = acc[p][c];
+          store_part_mx(a, pd + (size_t)(cr.row0 + r) * a.H + col, acc[p][c]);
         }
       }
     }
@@ -3564,6 +3584,158 @@ __global__ __launch_bounds__(256, 1) void k_experts_mx_batch(ExpertMxArgs args) 
   }
 }
 
+// =======================================================================================
+// The MXFP4 form as one launch (megamoe_mx_layer_forward): the routing is an input, so the
+// queue is the permute (unit 0), the units of k_experts_mx over its lists, and combine units
+// of 2048 outputs (with one slot per token and no K split the down units write y, and the
+// combine units only write NaN if something failed). The hand-overs and signals are the
+// single-launch fp8 kernel's: device-coherent stores, counters raised after the stores
+// completed, spread flags for the waits on a whole phase, the control words zeroed by the
+// last workgroup out. The batch-shaped form (k_experts_mx_batch, the EP share) stays
+// stream-ordered.
+// =======================================================================================
+
+struct LayerMxArgs {
+  ExpertMxArgs ex;        // offset 0
+  const int64_t* ids;     // topk_idx [T, K]
+  int64_t base;           // id of local expert 0
+  PermuteOut po;
+  uint16_t* y;
+  int* ctl;
+  int T, H, K, E, ks;
+  int direct;             // the down units write y
+  int tile_waves;         // the permute's ranking form
+  int force_timeout;      // test hook, as LayerArgs::force_timeout
+};
+
+// Combine unit c of the MXFP4 form: outputs [c * kCombineUnit, +kCombineUnit) of y, as
+// k_combine without weights (applied in the gate/up epilogue) and without a shared expert.
+__device__ __forceinline__ void layer_mx_combine(const LayerMxArgs& a, int c) {
+  const DownMxArgs& dn = a.ex.dn;
+  const int i = c * (kCombineUnit / 8) + threadIdx.x, per_row = a.H / 8;
+  if (i >= a.T * per_row) return;
+  if (load_count(&a.ctl[kCtlError]) || load_count(&a.po.meta[kMetaError])) {
+    *reinterpret_cast<uint4*>(a.y + (size_t)i * 8) = make_uint4(0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u);
+    return;
+  }
+  if (a.direct) return;
+  const int t = i / per_row, h0 = (i % per_row) * 8;
+  float acc[8];
+  if (a.ks > 1)
+    combine8_parts(dn.pd, nullptr, a.ks, a.po.inv, nullptr, a.T, a.H, a.K, 0, t, h0, acc);
+  else
+    combine8(dn.d, nullptr, a.po.inv, nullptr, a.H, a.K, 0, t, h0, acc);
+  uint32_t o[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) o[j] = f32_to_bf16_bits(acc[2 * j]) | (f32_to_bf16_bits(acc[2 * j + 1]) << 16);
+  *reinterpret_cast<uint4*>(a.y + (size_t)i * 8) = make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+__global__ __launch_bounds__(256, 2) void k_layer_mx(LayerMxArgs args) {
+  typedef const __attribute__((address_space(4))) LayerMxArgs* ArgsPtr;
+  typedef const __attribute__((address_space(4))) ExpertMxArgs* ExArgsPtr;
+  __shared__ uint8_t red8[4][64];
+  __shared__ __attribute__((aligned(16))) uint8_t rings[4 * kRingWave];  // weight rings; the permute's LDS
+  __shared__ int slot, next, flags[2], units[3];
+  static_assert(sizeof(LayerMxArgs) % 8 == 0 && offsetof(LayerMxArgs, ex) == 0, "argument segment layout");
+  static_assert(kPermuteLdsInts * sizeof(int) <= sizeof(rings), "the permute's LDS in the rings");
+  int* ctl = args.ctl;
+  if (threadIdx.x == 0) slot = atomicAdd(&ctl[kCtlQueue], 1);
+  __syncthreads();
+  int u = slot;
+
+  // Phase 1: unit 0, the permute of the given routing (ids less the base; bad ids set the
+  // error word and leave no units).
+  if (u == 0) {
+    ArgsPtr ap = (ArgsPtr)__builtin_amdgcn_kernarg_segment_ptr();
+    asm volatile("" : "+s"(ap));
+    LayerMxArgs a;
+    __builtin_memcpy(&a, (const LayerMxArgs*)ap, sizeof(a));
+    permute_block<true>(a.ids, a.base, a.T, a.K, a.E, 0, a.ex.gu.I / kBlock, a.H / kBlock, a.ks, kChunkRowsMx, 1,
+                        a.po, reinterpret_cast<int*>(rings), flags, a.tile_waves);
+    publish_fence();
+    __syncthreads();
+    raise_signal(ctl, kSigPermuted);
+    __syncthreads();
+    if (threadIdx.x == 0) slot = atomicAdd(&ctl[kCtlQueue], 1);
+    __syncthreads();
+    u = slot;
+  }
+
+  // Phase 2: the work lists (none if the wait gave up or the ids were bad).
+  wait_signal(ctl, kSigPermuted);
+  if (threadIdx.x == 0) {
+    const bool lists = load_count(my_signal_flag(ctl, kSigPermuted)) != 0;
+    units[0] = lists ? load_count(&args.po.meta[kMetaUnitsGU]) : 0;
+    units[1] = lists ? load_count(&args.po.meta[kMetaUnitsDN]) : 0;
+    units[2] = lists ? load_count(&args.po.meta[kMetaWide]) : 0;
+  }
+  __syncthreads();
+  const int n_gu = units[0], n_dn = units[1], nwide = units[2];
+  const int experts_end = 1 + n_gu + n_dn;
+  const int total = experts_end + (args.T * args.H + kCombineUnit - 1) / kCombineUnit;
+
+  // Phase 3: the expert units, as k_experts_mx runs them.
+  int my_down = 0;
+  while (u < experts_end) {
+    ExArgsPtr ap = (ExArgsPtr)__builtin_amdgcn_kernarg_segment_ptr();  // LayerMxArgs::ex is at offset 0
+    asm volatile("" : "+s"(ap));
+    ExpertMxArgs a;
+    __builtin_memcpy(&a, (const ExpertMxArgs*)ap, sizeof(a));
+    uint8_t* ring = rings + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) * kRingWave;
+    __syncthreads();
+    if (threadIdx.x == 0) next = atomicAdd(&ctl[kCtlQueue], 1);
+    if (u - 1 < n_gu) {
+      const int c = gateup_mx_work(a.gu, u - 1, nwide, red8, ring);
+      publish_fence();
+      __syncthreads();
+      if (threadIdx.x == 0) atomicAdd(&a.ready[a.dn_of_gu[c]], 1);
+    } else {
+      down_mx_work(a.dn, u - 1 - n_gu, nwide, a.ready, &ctl[kCtlError], ring);
+      ++my_down;
+    }
+    __syncthreads();
+    u = next;
+  }
+  if (my_down) publish_count(ctl, kCtlDown, my_down, n_dn, kSigDown, &units[0]);
+
+  // Phase 4: the combine units, once every down unit is counted.
+  if (u < total) {
+    ArgsPtr ap = (ArgsPtr)__builtin_amdgcn_kernarg_segment_ptr();
+    asm volatile("" : "+s"(ap));
+    LayerMxArgs a;
+    __builtin_memcpy(&a, (const LayerMxArgs*)ap, sizeof(a));
+    if (n_dn) wait_signal(ctl, kSigDown, 1 + a.force_timeout, a.force_timeout ? (uint64_t)2000 : kWaitTicks);
+    while (u < total) {
+      __syncthreads();
+      if (threadIdx.x == 0) next = atomicAdd(&ctl[kCtlQueue], 1);
+      layer_mx_combine(a, u - experts_end);
+      __syncthreads();
+      u = next;
+    }
+  }
+  // Leaving: as k_layer (the status word keeps whether a wait gave up or the ids were bad).
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const bool last = atomicAdd(&ctl[kCtlExited], 1) == (int)gridDim.x - 1;
+    if (last)
+      __hip_atomic_store(&ctl[kCtlStatus], load_count(&ctl[kCtlError]) | load_count(&args.po.meta[kMetaError]),
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    slot = last;
+  }
+  __syncthreads();
+  if (slot) {
+    constexpr int words[] = {kCtlQueue, kCtlDown, kCtlError, kCtlExited};
+    constexpr int n_words = sizeof(words) / sizeof(words[0]);
+    const int i = threadIdx.x;
+    if (i < n_words)
+      __hip_atomic_store(&ctl[words[i]], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else if (i < n_words + kSignals * kSigLines)
+      __hip_atomic_store(signal_flag(ctl, (i - n_words) / kSigLines, (i - n_words) % kSigLines), 0,
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
 // ---------------------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------------------
@@ -3685,6 +3857,7 @@ struct DeviceInfo {
   int experts_mx_per_cu = 0;  // resident k_experts_mx workgroups per CU
   int batch_mx_per_cu = 0;    // resident k_experts_mx_batch workgroups per CU
   int layer_per_cu = 0;       // resident k_layer workgroups per CU
+  int layer_mx_per_cu = 0;    // resident k_layer_mx workgroups per CU
 };
 
 int device_info(DeviceInfo* out) {
@@ -3713,6 +3886,9 @@ int device_info(DeviceInfo* out) {
       return MEGAMOE_ERR_HIP;
     per_cu = per_cu_split2 < per_cu ? per_cu_split2 : per_cu;
     di.layer_per_cu = per_cu > 0 ? per_cu : 1;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_layer_mx, 256, 0) != hipSuccess)
+      return MEGAMOE_ERR_HIP;
+    di.layer_mx_per_cu = per_cu > 0 ? per_cu : 1;
     di.cus = cus > 0 ? cus : 1;
   }
   *out = di;
@@ -4022,7 +4198,7 @@ int validate_mx(const megamoe_desc* d) {
 }
 
 struct LayoutMx {
-  size_t counts, offsets, meta, perm, inv, gu, dn, dn_of_gu, ready, hq, hs, d, p, spare, total;
+  size_t counts, offsets, meta, perm, inv, gu, dn, dn_of_gu, ready, hq, hs, d, p, spare, ctl, total;
   int ks, hs_ld;
 };
 
@@ -4062,8 +4238,38 @@ LayoutMx make_layout_mx(const megamoe_desc& d) {
   L.ks = down_splits_mx(d);
   L.p = take(L.ks > 1 ? L.ks * T * K * H * sizeof(float) : 0);
   L.spare = take(16 * (H > I ? H : I) / 2);
+  L.ctl = take(kCtlInts * sizeof(int));  // the single-launch kernel's control words
   L.total = at;
   return L;
+}
+
+// The MXFP4 expert kernels' arguments over workspace `ws` (`coherent`: d is read by a unit of
+// the same launch).
+void fill_expert_mx_args(const megamoe_desc& d, const LayoutMx& L, const megamoe_mx_tensors* t, char* ws,
+                         const PermuteOut& po, float limit, int64_t base, bool direct, bool coherent,
+                         ExpertMxArgs& ea) {
+  const int T = d.tokens, H = d.hidden, E = d.experts, K = d.topk, I = d.intermediate;
+  GateUpMxArgs& ga = ea.gu;
+  ga.x = t->x; ga.xs = t->x_scales; ga.wts = t->topk_weights;
+  ga.l1 = t->l1_blocks; ga.l1s = t->l1_scales;
+  ga.offsets = po.offsets; ga.perm = po.perm; ga.chunks = po.gu; ga.meta = po.meta;
+  ga.hq = (uint8_t*)(ws + L.hq); ga.hs = (uint8_t*)(ws + L.hs);
+  ga.spare = (const uint8_t*)(ws + L.spare);
+  ga.T = T; ga.H = H; ga.I = I; ga.K = K; ga.E = E; ga.hs_ld = L.hs_ld; ga.limit = limit;
+  ga.ebase = (int)base;
+  DownMxArgs& da = ea.dn;
+  da.l2 = t->l2_blocks; da.l2s = t->l2_scales;
+  da.offsets = po.offsets; da.perm = po.perm; da.chunks = po.dn; da.meta = po.meta;
+  da.hq = ga.hq; da.hs = ga.hs;
+  da.d = (uint16_t*)(ws + L.d); da.pd = (float*)(ws + L.p);
+  da.y = direct ? (uint16_t*)t->y : nullptr;
+  da.spare = ga.spare;
+  da.T = T; da.H = H; da.I = I; da.K = K; da.E = E; da.hs_ld = L.hs_ld; da.ks = L.ks;
+  da.ebase = (int)base;
+  da.coherent = coherent ? 1 : 0;
+  da.pad_ = 0;
+  ea.dn_of_gu = po.dn_of_gu;
+  ea.ready = po.ready;
 }
 
 int forward_mx_impl(const megamoe_desc* desc, float limit, const megamoe_mx_tensors* t, hipStream_t st,
@@ -4103,26 +4309,9 @@ int forward_mx_impl(const megamoe_desc* desc, float limit, const megamoe_mx_tens
   if (mark(1) != hipSuccess) return MEGAMOE_ERR_HIP;
 
   ExpertMxArgs ea;
-  GateUpMxArgs& ga = ea.gu;
-  ga.x = t->x; ga.xs = t->x_scales; ga.wts = t->topk_weights;
-  ga.l1 = t->l1_blocks; ga.l1s = t->l1_scales;
-  ga.offsets = po.offsets; ga.perm = po.perm; ga.chunks = po.gu; ga.meta = po.meta;
-  ga.hq = (uint8_t*)(ws + L.hq); ga.hs = (uint8_t*)(ws + L.hs);
-  ga.spare = (const uint8_t*)(ws + L.spare);
-  ga.T = T; ga.H = H; ga.I = I; ga.K = K; ga.E = E; ga.hs_ld = L.hs_ld; ga.limit = limit;
-  ga.ebase = (int)base;
-  DownMxArgs& da = ea.dn;
-  da.l2 = t->l2_blocks; da.l2s = t->l2_scales;
-  da.offsets = po.offsets; da.perm = po.perm; da.chunks = po.dn; da.meta = po.meta;
-  da.hq = ga.hq; da.hs = ga.hs;
-  da.d = (uint16_t*)(ws + L.d); da.pd = (float*)(ws + L.p);
   const bool direct = K == 1 && L.ks == 1;  // the down units write y; no combine
-  da.y = direct ? (uint16_t*)t->y : nullptr;
-  da.spare = ga.spare;
-  da.T = T; da.H = H; da.I = I; da.K = K; da.E = E; da.hs_ld = L.hs_ld; da.ks = L.ks;
-  da.ebase = (int)base;
-  ea.dn_of_gu = po.dn_of_gu;
-  ea.ready = po.ready;
+  fill_expert_mx_args(d, L, t, ws, po, limit, base, direct, false, ea);
+  const DownMxArgs& da = ea.dn;
   if (batch) {
     const size_t chunks = max_chunks(d, 0, kBatchRows);
     const size_t units_max = chunks * (size_t)nbI + chunks * (size_t)(nbH / 2) * L.ks;
@@ -4151,6 +4340,62 @@ int forward_mx_impl(const megamoe_desc* desc, float limit, const megamoe_mx_tens
   MEGAMOE_LAUNCH_CHECK();
   if (mark(3) != hipSuccess) return MEGAMOE_ERR_HIP;
   return MEGAMOE_OK;
+}
+
+// The MXFP4 form as one launch of k_layer_mx (see the kernel). Batch-shaped rows (the
+// batch kernel's geometry) and permutes beyond one workgroup's LDS take the stream-ordered
+// kernels instead (forward_mx_impl). `ev`: NULL or two events, recorded around the call.
+int forward_mx_layer_impl(const megamoe_desc* desc, float limit, const megamoe_mx_tensors* t, hipStream_t st,
+                          hipEvent_t* ev, int64_t base = 0) {
+  int rc = validate_mx(desc);
+  if (rc) return rc;
+  if (!t || !(limit > 0.0f)) return MEGAMOE_ERR_INVALID_ARGUMENT;
+  const megamoe_desc& d = *desc;
+  auto mark = [&](int i) { return ev ? hipEventRecord(ev[i], st) : hipSuccess; };
+  if (d.tokens == 0) return (mark(0) == hipSuccess && mark(1) == hipSuccess) ? MEGAMOE_OK : MEGAMOE_ERR_HIP;
+  if (!t->x || !t->x_scales || !t->topk_idx || !t->topk_weights || !t->l1_blocks || !t->l1_scales ||
+      !t->l2_blocks || !t->l2_scales || !t->y || !t->workspace)
+    return MEGAMOE_ERR_INVALID_ARGUMENT;
+  const LayoutMx L = make_layout_mx(d);
+  if (t->workspace_bytes < L.total) return MEGAMOE_ERR_WORKSPACE;
+  const int T = d.tokens, H = d.hidden, E = d.experts, K = d.topk, I = d.intermediate;
+  const int nbI = I / kBlock, nbH = H / kBlock;
+  const bool batch = (int64_t)T * K >= (int64_t)kBatchMinRows * E && (H / kMxStageK) % 2 == 0 &&
+                     (I / kMxStageK / L.ks) % 2 == 0;
+  const int tile_waves = permute_tile_waves(T, E, 256, kPermuteLdsInts);
+  if (batch || tile_waves < 0) {  // the stream-ordered kernels, between the caller's two events
+    if (mark(0) != hipSuccess) return MEGAMOE_ERR_HIP;
+    if ((rc = forward_mx_impl(desc, limit, t, st, nullptr, base))) return rc;
+    return mark(1) == hipSuccess ? MEGAMOE_OK : MEGAMOE_ERR_HIP;
+  }
+  DeviceInfo di;
+  if ((rc = device_info(&di))) return rc;
+  char* ws = (char*)t->workspace;
+
+  LayerMxArgs la{};
+  la.po = PermuteOut{(int*)(ws + L.counts), (int*)(ws + L.offsets), (int*)(ws + L.meta), (int*)(ws + L.perm),
+                     (int*)(ws + L.inv),    (int4*)(ws + L.gu),     (int4*)(ws + L.dn),  (int*)(ws + L.dn_of_gu),
+                     (int*)(ws + L.ready)};
+  const bool direct = K == 1 && L.ks == 1;
+  fill_expert_mx_args(d, L, t, ws, la.po, limit, base, direct, true, la.ex);
+  la.ids = t->topk_idx;
+  la.base = base;
+  la.y = (uint16_t*)t->y;
+  la.ctl = (int*)(ws + L.ctl);
+  la.T = T; la.H = H; la.K = K; la.E = E; la.ks = L.ks;
+  la.direct = direct ? 1 : 0;
+  la.tile_waves = tile_waves;
+  const char* force = getenv("MEGAMOE_FORCE_WAIT_TIMEOUT");
+  la.force_timeout = force && force[0] == '1' ? 1 : 0;
+  // As many workgroups as fit on the device at once, and no more than the most units.
+  const size_t chunks = max_chunks(d, 0, kChunkRowsMx);
+  const size_t units_max = 1 + chunks * 4 * (size_t)nbI + chunks * 2 * (size_t)nbH * L.ks +
+                           ((size_t)T * H + kCombineUnit - 1) / kCombineUnit;
+  const size_t resident = (size_t)di.cus * di.layer_mx_per_cu;
+  if (mark(0) != hipSuccess) return MEGAMOE_ERR_HIP;
+  hipLaunchKernelGGL(k_layer_mx, dim3((unsigned)(units_max < resident ? units_max : resident)), dim3(256), 0, st, la);
+  MEGAMOE_LAUNCH_CHECK();
+  return mark(1) == hipSuccess ? MEGAMOE_OK : MEGAMOE_ERR_HIP;
 }
 
 
@@ -4394,7 +4639,7 @@ int scratch_address(void** out) {
 
 extern "C" {
 
-int megamoe_abi_version(void) { return 8; }
+int megamoe_abi_version(void) { return 9; }
 
 const char* megamoe_status_string(int status) {
   switch (status) {
@@ -4574,6 +4819,31 @@ int megamoe_mx_forward(const megamoe_desc* desc, float swiglu_limit, const megam
     }
   }
   return forward_mx_impl(desc, swiglu_limit, t, (hipStream_t)stream, events ? ev : nullptr);
+}
+int megamoe_mx_layer_forward(const megamoe_desc* desc, float swiglu_limit, const megamoe_mx_tensors* t,
+                             void* stream, void* const* events) {
+  hipEvent_t ev[2];
+  if (events) {
+    if (!events[0] || !events[1]) return MEGAMOE_ERR_INVALID_ARGUMENT;
+    ev[0] = (hipEvent_t)events[0];
+    ev[1] = (hipEvent_t)events[1];
+  }
+  return forward_mx_layer_impl(desc, swiglu_limit, t, (hipStream_t)stream, events ? ev : nullptr);
+}
+int megamoe_mx_layer_status(const megamoe_desc* desc, const void* workspace, size_t workspace_bytes, int32_t* failed,
+                            void* stream) {
+  const int rc = validate_mx(desc);
+  if (rc) return rc;
+  if (!workspace || !failed) return MEGAMOE_ERR_INVALID_ARGUMENT;
+  const LayoutMx L = make_layout_mx(*desc);
+  if (workspace_bytes < L.total) return MEGAMOE_ERR_WORKSPACE;
+  int32_t v = 0;
+  if (hipMemcpyAsync(&v, (const char*)workspace + L.ctl + kCtlStatus * sizeof(int), sizeof(v), hipMemcpyDeviceToHost,
+                     (hipStream_t)stream) != hipSuccess ||
+      hipStreamSynchronize((hipStream_t)stream) != hipSuccess)
+    return MEGAMOE_ERR_HIP;
+  *failed = v;
+  return MEGAMOE_OK;
 }
 
 int megamoe_ep_dispatch(const megamoe_desc* desc, int32_t ep, const megamoe_mx_tensors* t,

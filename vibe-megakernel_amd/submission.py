@@ -62,18 +62,19 @@ class MoELayer:
     workspace and they are ordered by that stream).
 
     The fp8 layer (and its block and epilogue forms) runs as one launch,
-    megamoe_layer_forward, by default; ``single_launch=False`` selects the stream-ordered
-    kernels of megamoe_forward / megamoe_forward_ex, whose stage boundaries ``record`` can
-    mark (router, select + quantization, permute, experts, combine). The MXFP4 form runs as
-    megamoe_mx_forward."""
+    megamoe_layer_forward, by default, and the MXFP4 form as megamoe_mx_layer_forward;
+    ``single_launch=False`` selects the stream-ordered kernels (megamoe_forward /
+    megamoe_forward_ex: router, select + quantization, permute, experts, combine;
+    megamoe_mx_forward: permute, experts, combine), whose stage boundaries ``record`` can
+    mark."""
 
     def __init__(self, case: Case, single_launch: bool = True):
         self.case = case
         self.lib = _lib.load()
         self.desc = make_desc(case)
         self.mx = case.format == "mxfp4"
-        self.single_launch = single_launch and not self.mx
-        self.stages = _lib.STAGES_MX if self.mx else (("layer",) if self.single_launch else _lib.STAGES)
+        self.single_launch = single_launch
+        self.stages = ("layer",) if single_launch else (_lib.STAGES_MX if self.mx else _lib.STAGES)
         size = ctypes.c_size_t(0)
         sizer = self.lib.megamoe_mx_workspace_bytes if self.mx else self.lib.megamoe_workspace_bytes
         _lib.check(sizer(ctypes.byref(self.desc), ctypes.byref(size)), f"{case.id}: workspace size")
@@ -124,9 +125,10 @@ class MoELayer:
         tensors = _lib.MxTensors(**ptr, y=y.data_ptr(), workspace=ws.data_ptr(), workspace_bytes=self.workspace_bytes)
         stream = ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
         handles = None if events is None else (ctypes.c_void_p * len(events))(*[e.cuda_event for e in events])
+        forward = self.lib.megamoe_mx_layer_forward if self.single_launch else self.lib.megamoe_mx_forward
         with torch.cuda.device(device):
-            _lib.check(self.lib.megamoe_mx_forward(ctypes.byref(self.desc), float(c.swiglu_limit),
-                                                   ctypes.byref(tensors), stream, handles), f"{c.id}: forward")
+            _lib.check(forward(ctypes.byref(self.desc), float(c.swiglu_limit), ctypes.byref(tensors), stream, handles),
+                       f"{c.id}: forward")
         return {"y": y}
 
     def check_inputs(self, inputs: dict) -> torch.device:
@@ -234,16 +236,16 @@ class MoELayer:
         return self._call(inputs, timed=False)
 
     def gave_up(self, device: torch.device) -> bool:
-        """Whether the last call on this (device, current stream)'s workspace had a bounded
-        wait give up (its y is NaN); synchronizes the stream (megamoe_layer_status)."""
-        if self.mx:
-            raise ValueError("the status word covers the fp8 layer forms")
+        """Whether the last single-launch call on this (device, current stream)'s workspace had
+        a bounded wait give up, or (the MXFP4 form) bad expert ids; its y is NaN then.
+        Synchronizes the stream (megamoe_layer_status / megamoe_mx_layer_status)."""
         ws = self.workspace(device)
         flag = ctypes.c_int32(0)
         stream = ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+        status = self.lib.megamoe_mx_layer_status if self.mx else self.lib.megamoe_layer_status
         with torch.cuda.device(device):
-            _lib.check(self.lib.megamoe_layer_status(ctypes.byref(self.desc), ws.data_ptr(), self.workspace_bytes,
-                                                     ctypes.byref(flag), stream), f"{self.case.id}: status")
+            _lib.check(status(ctypes.byref(self.desc), ws.data_ptr(), self.workspace_bytes, ctypes.byref(flag), stream),
+                       f"{self.case.id}: status")
         return bool(flag.value)
 
     def noalloc(self, inputs: dict) -> dict:
