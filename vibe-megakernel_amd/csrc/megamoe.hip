@@ -3002,7 +3002,11 @@ __device__ void gateup_mx_wide(const GateUpMxArgs& a, int e, int blk, const Chun
 }
 
 // Gate/up units: `nwide` wide chunks first (4 nbI units each, one per 32-channel block),
-// then narrow chunks (nbI units each). Returns the unit's chunk.
+// then narrow chunks (nbI units each). Returns the unit's chunk. CALLER: each kernel
+// instantiates its own copy, so the inliner sees one call site per copy (one copy shared by
+// k_experts_mx and k_layer_mx compiled k_experts_mx to 256 VGPRs with spills and scratch,
+// against 237 and none, and slowed it by 40%).
+template <int CALLER>
 __device__ int gateup_mx_work(const GateUpMxArgs& a, int u, int nwide, uint8_t (*red8)[64], uint8_t* ring) {
   const int nbI = a.I / kBlock;
   const int nst = a.H / kMxStageK;
@@ -3065,20 +3069,22 @@ struct DownMxArgs {
   const uint8_t* spare;
   int T, H, I, K, E, hs_ld, ks;
   int ebase;
-  int coherent;  // d (or its parts) as device-coherent stores: a unit of the same launch reads them
-  int pad_;
 };
 
-// A down unit's output: bf16 d (four values) or the fp32 part (four values).
-__device__ __forceinline__ void store_d_mx(const DownMxArgs& a, uint16_t* p, uint32_t lo, uint32_t hi) {
-  if (a.coherent)
+// A down unit's output: bf16 d (four values) or the fp32 part (four values). CO: device-
+// coherent stores, for a combine unit of the same launch (as store_out); a compile-time
+// choice, so the expert kernel's epilogue carries no second store path.
+template <bool CO>
+__device__ __forceinline__ void store_d_mx(uint16_t* p, uint32_t lo, uint32_t hi) {
+  if constexpr (CO)
     store_coherent(reinterpret_cast<uint64_t*>(p), (uint64_t)lo | ((uint64_t)hi << 32));
   else
     *reinterpret_cast<uint2*>(p) = make_uint2(lo, hi);
 }
 
-__device__ __forceinline__ void store_part_mx(const DownMxArgs& a, float* p, const f32x4& v) {
-  if (a.coherent) {
+template <bool CO>
+__device__ __forceinline__ void store_part_mx(float* p, const f32x4& v) {
+  if constexpr (CO) {
     uint64_t* q = reinterpret_cast<uint64_t*>(p);
     store_coherent(q, (uint64_t)__float_as_uint(v[0]) | ((uint64_t)__float_as_uint(v[1]) << 32));
     store_coherent(q + 1, (uint64_t)__float_as_uint(v[2]) | ((uint64_t)__float_as_uint(v[3]) << 32));
@@ -3094,7 +3100,7 @@ __device__ __forceinline__ uint16_t* down_row_mx(const DownMxArgs& a, const Chun
 }
 
 // Down unit: rows [j*128, +128) of the expert's down matrix over K part kp of ks.
-template <int NCT, bool PAIR>
+template <int NCT, bool PAIR, bool CO>
 __device__ void down_mx_unit(const DownMxArgs& a, int e, int j, int kp, const ChunkRows& cr, int rot,
                              const ReadyWait& ready, uint8_t* ring) {
   const int lane = opaque_lane(), w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -3128,9 +3134,9 @@ __device__ void down_mx_unit(const DownMxArgs& a, int e, int j, int kp, const Ch
         if (a.ks == 1) {
           const uint32_t lo = f32_to_bf16_bits(acc[p][c][0]) | (f32_to_bf16_bits(acc[p][c][1]) << 16);
           const uint32_t hi = f32_to_bf16_bits(acc[p][c][2]) | (f32_to_bf16_bits(acc[p][c][3]) << 16);
-          store_d_mx(a, down_row_mx(a, cr, r) + col, lo, hi);
+          store_d_mx<CO>(down_row_mx(a, cr, r) + col, lo, hi);
         } else {
-          store_part_mx(a, pd + (size_t)(cr.row0 + r) * a.H + col, acc[p][c]);
+          store_part_mx<CO>(pd + (size_t)(cr.row0 + r) * a.H + col, acc[p][c]);
         }
       }
     }
@@ -3140,7 +3146,7 @@ __device__ void down_mx_unit(const DownMxArgs& a, int e, int j, int kp, const Ch
 // Wide down unit, for a chunk of 33-128 rows: down rows [64 j64, +64) over K part kp, for
 // every row of the chunk; wave w takes column tiles [w NCT, w NCT + NCT), every wave
 // streaming the same weight rows (as gateup_mx_wide).
-template <int NCT, bool PAIR>
+template <int NCT, bool PAIR, bool CO>
 __device__ void down_mx_wide(const DownMxArgs& a, int e, int j64, int kp, const ChunkRows& cr, int rot,
                              const ReadyWait& ready, uint8_t* ring) {
   const int lane = opaque_lane(), w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -3174,9 +3180,9 @@ __device__ void down_mx_wide(const DownMxArgs& a, int e, int j64, int kp, const 
         if (a.ks == 1) {
           const uint32_t lo = f32_to_bf16_bits(acc[p][c][0]) | (f32_to_bf16_bits(acc[p][c][1]) << 16);
           const uint32_t hi = f32_to_bf16_bits(acc[p][c][2]) | (f32_to_bf16_bits(acc[p][c][3]) << 16);
-          store_d_mx(a, down_row_mx(a, cr, r) + col, lo, hi);
+          store_d_mx<CO>(down_row_mx(a, cr, r) + col, lo, hi);
         } else {
-          store_part_mx(a, pd + (size_t)(cr.row0 + r) * a.H + col, acc[p][c]);
+          store_part_mx<CO>(pd + (size_t)(cr.row0 + r) * a.H + col, acc[p][c]);
         }
       }
     }
@@ -3185,7 +3191,8 @@ __device__ void down_mx_wide(const DownMxArgs& a, int e, int j64, int kp, const 
 
 // Down units: `nwide` wide chunks first (2 nbH ks units each), then narrow chunks (nbH ks
 // each). A unit waits for every gate/up unit of its chunk: 4 nbI for a wide chunk, nbI
-// for a narrow one.
+// for a narrow one. CO: d as device-coherent stores (a unit of the same launch reads it).
+template <bool CO>
 __device__ void down_mx_work(const DownMxArgs& a, int v, int nwide, int* ready_counts, int* error,
                              uint8_t* ring) {
   const int nbH = a.H / kBlock, nbI = a.I / kBlock;
@@ -3200,15 +3207,15 @@ __device__ void down_mx_work(const DownMxArgs& a, int v, int nwide, int* ready_c
     if (nstp % 2 == 0) {
       const int rot = 2 * (key % (nstp / 2));
       if (two)
-        down_mx_wide<2, true>(a, ch.x, j64, kp, cr, rot, ready, ring);
+        down_mx_wide<2, true, CO>(a, ch.x, j64, kp, cr, rot, ready, ring);
       else
-        down_mx_wide<1, true>(a, ch.x, j64, kp, cr, rot, ready, ring);
+        down_mx_wide<1, true, CO>(a, ch.x, j64, kp, cr, rot, ready, ring);
     } else {
       const int rot = key % nstp;
       if (two)
-        down_mx_wide<2, false>(a, ch.x, j64, kp, cr, rot, ready, ring);
+        down_mx_wide<2, false, CO>(a, ch.x, j64, kp, cr, rot, ready, ring);
       else
-        down_mx_wide<1, false>(a, ch.x, j64, kp, cr, rot, ready, ring);
+        down_mx_wide<1, false, CO>(a, ch.x, j64, kp, cr, rot, ready, ring);
     }
     return;
   }
@@ -3223,15 +3230,15 @@ __device__ void down_mx_work(const DownMxArgs& a, int v, int nwide, int* ready_c
   if (nstp % 2 == 0) {
     const int rot = 2 * (key % (nstp / 2));
     if (cr.n <= 16)
-      down_mx_unit<1, true>(a, ch.x, j, kp, cr, rot, ready, ring);
+      down_mx_unit<1, true, CO>(a, ch.x, j, kp, cr, rot, ready, ring);
     else
-      down_mx_unit<2, true>(a, ch.x, j, kp, cr, rot, ready, ring);
+      down_mx_unit<2, true, CO>(a, ch.x, j, kp, cr, rot, ready, ring);
   } else {
     const int rot = key % nstp;
     if (cr.n <= 16)
-      down_mx_unit<1, false>(a, ch.x, j, kp, cr, rot, ready, ring);
+      down_mx_unit<1, false, CO>(a, ch.x, j, kp, cr, rot, ready, ring);
     else
-      down_mx_unit<2, false>(a, ch.x, j, kp, cr, rot, ready, ring);
+      down_mx_unit<2, false, CO>(a, ch.x, j, kp, cr, rot, ready, ring);
   }
 }
 
@@ -3524,12 +3531,12 @@ __global__ __launch_bounds__(256, 2) void k_experts_mx(ExpertMxArgs args) {
     __syncthreads();
     if (threadIdx.x == 0) next = atomicAdd(&meta[kMetaQueueGU], 1);
     if (u < total_gu) {
-      const int c = gateup_mx_work(a.gu, u, nwide, red8, ring);
+      const int c = gateup_mx_work<0>(a.gu, u, nwide, red8, ring);
       publish_fence();
       __syncthreads();
       if (threadIdx.x == 0) atomicAdd(&a.ready[a.dn_of_gu[c]], 1);
     } else {
-      down_mx_work(a.dn, u - total_gu, nwide, a.ready, &meta[kMetaError], ring);
+      down_mx_work<false>(a.dn, u - total_gu, nwide, a.ready, &meta[kMetaError], ring);
     }
     if (threadIdx.x == 0) slot = next;
     __syncthreads();
@@ -3686,12 +3693,12 @@ __global__ __launch_bounds__(256, 2) void k_layer_mx(LayerMxArgs args) {
     __syncthreads();
     if (threadIdx.x == 0) next = atomicAdd(&ctl[kCtlQueue], 1);
     if (u - 1 < n_gu) {
-      const int c = gateup_mx_work(a.gu, u - 1, nwide, red8, ring);
+      const int c = gateup_mx_work<1>(a.gu, u - 1, nwide, red8, ring);
       publish_fence();
       __syncthreads();
       if (threadIdx.x == 0) atomicAdd(&a.ready[a.dn_of_gu[c]], 1);
     } else {
-      down_mx_work(a.dn, u - 1 - n_gu, nwide, a.ready, &ctl[kCtlError], ring);
+      down_mx_work<true>(a.dn, u - 1 - n_gu, nwide, a.ready, &ctl[kCtlError], ring);
       ++my_down;
     }
     __syncthreads();
@@ -4243,11 +4250,9 @@ LayoutMx make_layout_mx(const megamoe_desc& d) {
   return L;
 }
 
-// The MXFP4 expert kernels' arguments over workspace `ws` (`coherent`: d is read by a unit of
-// the same launch).
+// The MXFP4 expert kernels' arguments over workspace `ws`.
 void fill_expert_mx_args(const megamoe_desc& d, const LayoutMx& L, const megamoe_mx_tensors* t, char* ws,
-                         const PermuteOut& po, float limit, int64_t base, bool direct, bool coherent,
-                         ExpertMxArgs& ea) {
+                         const PermuteOut& po, float limit, int64_t base, bool direct, ExpertMxArgs& ea) {
   const int T = d.tokens, H = d.hidden, E = d.experts, K = d.topk, I = d.intermediate;
   GateUpMxArgs& ga = ea.gu;
   ga.x = t->x; ga.xs = t->x_scales; ga.wts = t->topk_weights;
@@ -4266,8 +4271,6 @@ void fill_expert_mx_args(const megamoe_desc& d, const LayoutMx& L, const megamoe
   da.spare = ga.spare;
   da.T = T; da.H = H; da.I = I; da.K = K; da.E = E; da.hs_ld = L.hs_ld; da.ks = L.ks;
   da.ebase = (int)base;
-  da.coherent = coherent ? 1 : 0;
-  da.pad_ = 0;
   ea.dn_of_gu = po.dn_of_gu;
   ea.ready = po.ready;
 }
@@ -4310,7 +4313,7 @@ int forward_mx_impl(const megamoe_desc* desc, float limit, const megamoe_mx_tens
 
   ExpertMxArgs ea;
   const bool direct = K == 1 && L.ks == 1;  // the down units write y; no combine
-  fill_expert_mx_args(d, L, t, ws, po, limit, base, direct, false, ea);
+  fill_expert_mx_args(d, L, t, ws, po, limit, base, direct, ea);
   const DownMxArgs& da = ea.dn;
   if (batch) {
     const size_t chunks = max_chunks(d, 0, kBatchRows);
@@ -4377,7 +4380,7 @@ int forward_mx_layer_impl(const megamoe_desc* desc, float limit, const megamoe_m
                      (int*)(ws + L.inv),    (int4*)(ws + L.gu),     (int4*)(ws + L.dn),  (int*)(ws + L.dn_of_gu),
                      (int*)(ws + L.ready)};
   const bool direct = K == 1 && L.ks == 1;
-  fill_expert_mx_args(d, L, t, ws, la.po, limit, base, direct, true, la.ex);
+  fill_expert_mx_args(d, L, t, ws, la.po, limit, base, direct, la.ex);
   la.ids = t->topk_idx;
   la.base = base;
   la.y = (uint16_t*)t->y;
