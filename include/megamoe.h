@@ -357,15 +357,25 @@ int megamoe_ep_combine(int32_t tokens, int32_t hidden, int32_t topk, const void*
 int megamoe_quantize_rows(int32_t rows, int32_t cols, const void* x, uint8_t* q, float* scales,
                           int32_t pow2, void* stream);
 
+/* Self-test of the E4M3 encoder the kernels use (gfx950's v_cvt_pk_fp8_f32, round to nearest
+ * even, positive NaN recoded to 0x7f) against the bitwise rule of quantization.py:106,125:
+ * for every fp32 bit pattern m in [first, first + count) with the sign bit clear (count may
+ * reach 2^31 - first), m and -m, adds the number of codes that differ to *mismatches (a
+ * device pointer to a uint64 the caller zeroes). Every clamped value lies in [0, 448.0f =
+ * 0x43e00000] in magnitude or is NaN (0x7f800001 and up); infinity is clamped to 448 before
+ * any encoding, and the rule is not defined for it. Asynchronous on `stream`. No reference
+ * counterpart (test hook). */
+int megamoe_e4m3_selftest(uint32_t first, uint32_t count, uint64_t* mismatches, void* stream);
+
 /* Text for a status code (static storage). */
 const char* megamoe_status_string(int status);
 
-/* ABI version of this library: 9 (1, plus megamoe_block_forward and megamoe_rms_norm in 2,
+/* ABI version of this library: 10 (1, plus megamoe_block_forward and megamoe_rms_norm in 2,
  * plus megamoe_mx_workspace_bytes and megamoe_mx_forward in 3, plus megamoe_ep_dispatch,
  * megamoe_ep_experts and megamoe_ep_combine in 4, plus megamoe_forward_ex and
  * megamoe_combine_by_expert_id in 5, plus megamoe_forward_noalloc in 6, plus
  * megamoe_layer_forward in 7, plus megamoe_layer_status in 8, plus megamoe_mx_layer_forward
- * and megamoe_mx_layer_status in 9). */
+ * and megamoe_mx_layer_status in 9, plus megamoe_e4m3_selftest in 10). */
 int megamoe_abi_version(void);
 
 #ifdef __cplusplus

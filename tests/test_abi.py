@@ -20,7 +20,7 @@ HEADER = Path(__file__).resolve().parent.parent / "include" / "megamoe.h"
 
 def _declared() -> set[str]:
     text = HEADER.read_text()
-    return set(re.findall(r"^\s*(?:const\s+)?[a-z_0-9]+\s*\*?\s*(megamoe_[a-z_]+)\s*\(", text, flags=re.M))
+    return set(re.findall(r"^\s*(?:const\s+)?[a-z_0-9]+\s*\*?\s*(megamoe_[a-z_0-9]+)\s*\(", text, flags=re.M))
 
 
 def test_library_exports_every_declared_function():
@@ -31,13 +31,13 @@ def test_library_exports_every_declared_function():
         assert getattr(lib, name) is not None
     out = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIBRARY)], capture_output=True, text=True,
                          check=True).stdout
-    exported = set(re.findall(r"\bT (megamoe_[a-z_]+)$", out, flags=re.M))
+    exported = set(re.findall(r"\bT (megamoe_[a-z_0-9]+)$", out, flags=re.M))
     assert declared <= exported
 
 
 def test_version_and_status_strings():
     lib = _lib.load()
-    assert lib.megamoe_abi_version() == _lib.ABI_VERSION == 9
+    assert lib.megamoe_abi_version() == _lib.ABI_VERSION == 10
     texts = {code: _lib.status_string(code) for code in range(7)}
     assert texts[_lib.OK] == "ok" and len(set(texts.values())) == 7
     assert _lib.status_string(99) == "unknown status"
@@ -107,6 +107,8 @@ def test_null_and_workspace_checks_answer_before_any_gpu_call():
     assert lib.megamoe_quantize_rows(-1, 128, None, None, None, 0, None) == _lib.ERR_INVALID_ARGUMENT
     assert lib.megamoe_quantize_rows(0, 128, None, None, None, 0, None) == _lib.OK
     assert lib.megamoe_quantize_rows(4, 128, None, None, None, 0, None) == _lib.ERR_INVALID_ARGUMENT
+    assert lib.megamoe_e4m3_selftest(0, 16, None, None) == _lib.ERR_INVALID_ARGUMENT
+    assert lib.megamoe_e4m3_selftest(0x7F800000, 0x800001, 8, None) == _lib.ERR_INVALID_ARGUMENT
 
 
 def test_python_errors_follow_the_reference_behaviour():

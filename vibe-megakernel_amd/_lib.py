@@ -25,8 +25,9 @@ SYMBOLS = ("megamoe_workspace_bytes", "megamoe_forward", "megamoe_forward_events
            "megamoe_abi_version", "megamoe_block_forward", "megamoe_rms_norm", "megamoe_mx_workspace_bytes",
            "megamoe_mx_forward", "megamoe_ep_dispatch", "megamoe_ep_experts", "megamoe_ep_combine",
            "megamoe_forward_ex", "megamoe_combine_by_expert_id", "megamoe_forward_noalloc",
-           "megamoe_layer_forward", "megamoe_layer_status", "megamoe_mx_layer_forward", "megamoe_mx_layer_status")
-ABI_VERSION = 9
+           "megamoe_layer_forward", "megamoe_layer_status", "megamoe_mx_layer_forward", "megamoe_mx_layer_status",
+           "megamoe_e4m3_selftest")
+ABI_VERSION = 10
 
 
 class Desc(ctypes.Structure):
@@ -97,6 +98,7 @@ def load() -> ctypes.CDLL:
     lib.megamoe_route.argtypes = [P(Desc), c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]
     lib.megamoe_quantize_rows.argtypes = [ctypes.c_int32, ctypes.c_int32, c_void_p, c_void_p, c_void_p,
                                           ctypes.c_int32, c_void_p]
+    lib.megamoe_e4m3_selftest.argtypes = [ctypes.c_uint32, ctypes.c_uint32, c_void_p, c_void_p]
     lib.megamoe_block_forward.argtypes = [P(Desc), P(Tensors), P(Block), c_void_p, P(c_void_p)]
     lib.megamoe_rms_norm.argtypes = [ctypes.c_int32, ctypes.c_int32, c_void_p, c_void_p, ctypes.c_float,
                                      ctypes.c_int32, c_void_p, c_void_p]

@@ -98,6 +98,21 @@ __device__ __forceinline__ uint32_t f32_to_e4m3(float f) {
 
 __device__ __forceinline__ float clamp448(float v) { return v > 448.0f ? 448.0f : (v < -448.0f ? -448.0f : v); }
 
+// Four floats in [-448, 448] (or NaN) -> four E4M3FN codes in bytes 0..3, by gfx950's
+// v_cvt_pk_fp8_f32 (OCP E4M3, round to nearest even), two per instruction. It gives
+// f32_to_e4m3's code for every fp32 value in [-448, 448] of either sign (the whole range a
+// clamped value can take; megamoe_e4m3_selftest compares the two on all of them); for a
+// positive NaN it gives 0xff, which is set to 0x7f here, as f32_to_e4m3 (and torch) code it.
+__device__ __forceinline__ uint32_t e4m3x4(float a, float b, float c, float d) {
+  uint32_t w = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  w = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, (int)w, true);
+  const float v[4] = {a, b, c, d};
+  uint32_t pos_nan = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) pos_nan |= (__float_as_uint(v[i]) - 0x7f800001u < 0x7fffffu ? 0x80u : 0u) << (8 * i);
+  return w & ~pos_nan;
+}
+
 // Activation scale of one 128-block: max(amax, 1e-4) / 448 (quantization.py:57-58), or
 // the smallest power of two not below it when pow2 is set (quantization.py:59).
 __device__ __forceinline__ float act_scale(float amax, int pow2) {
@@ -164,47 +179,9 @@ __device__ __forceinline__ void quant_block(const uint16_t* src, uint8_t* dst, f
   const uint32_t two = *reinterpret_cast<const uint32_t*>(src + 2 * lane);
   const float v0 = bf16_bits_to_f32(two & 0xffffu), v1 = bf16_bits_to_f32(two >> 16);
   const float s = act_scale(wave_max(fmaxf(fabsf(v0), fabsf(v1))), pow2);
-  const uint32_t q = f32_to_e4m3(clamp448(v0 / s)) | (f32_to_e4m3(clamp448(v1 / s)) << 8);
+  const uint32_t q = e4m3x4(clamp448(v0 / s), clamp448(v1 / s), 0.0f, 0.0f);
   *reinterpret_cast<uint16_t*>(dst + 2 * lane) = (uint16_t)q;
   if (lane == 0) *scale = s;
-}
-
-// The same quantization of one full 128-wide block with four values per lane on lanes
-// 0..31 (`four`, loaded by the caller), so each lane writes its codes as one 4-byte
-// device-coherent store (the single-launch kernel's expert units read them from other
-// workgroups).
-__device__ __forceinline__ void quant_four(uint2 four, uint8_t* dst, float* scale, int pow2, int lane) {
-  const int l = lane & 31;
-  const float v[4] = {bf16_bits_to_f32(four.x & 0xffffu), bf16_bits_to_f32(four.x >> 16),
-                      bf16_bits_to_f32(four.y & 0xffffu), bf16_bits_to_f32(four.y >> 16)};
-  const float m = lane < 32 ? fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))) : 0.0f;
-  const float s = act_scale(wave_max(m), pow2);
-  uint32_t q = 0;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) q |= f32_to_e4m3(clamp448(v[i] / s)) << (8 * i);
-  if (lane < 32) store_coherent(reinterpret_cast<uint32_t*>(dst + 4 * l), q);
-  if (lane == 0) store_coherent(scale, s);
-}
-
-// One row of x (nbh blocks) by the workgroup's four wavefronts, wavefront wv taking blocks
-// wv, wv + 4, ...: each wavefront issues the loads of up to 8 of its blocks before it
-// reduces the first.
-__device__ __forceinline__ void quant_row(const uint16_t* x, uint8_t* xq, float* xs, int nbh, int pow2, int lane,
-                                          int wv) {
-  constexpr int kBatch = 8;
-  for (int b0 = wv; b0 < nbh; b0 += 4 * kBatch) {
-    uint2 four[kBatch];
-#pragma unroll
-    for (int j = 0; j < kBatch; ++j) {
-      const int b = min(b0 + 4 * j, nbh - 1);  // clamped into the row; blocks past the end are dropped
-      four[j] = *reinterpret_cast<const uint2*>(x + (size_t)b * kBlock + 4 * (lane & 31));
-    }
-#pragma unroll
-    for (int j = 0; j < kBatch; ++j) {
-      const int b = b0 + 4 * j;
-      if (b < nbh) quant_four(four[j], xq + (size_t)b * kBlock, xs + b, pow2, lane);
-    }
-  }
 }
 
 // Ragged rows (any column count): one wavefront per (row, 128-column block).
@@ -222,10 +199,28 @@ __global__ __launch_bounds__(256) void k_quant_rows(const uint16_t* __restrict__
     const float amax = wave_max(fmaxf(fabsf(v0), fabsf(v1)));
     const float s = act_scale(amax, pow2);
     uint8_t* dst = q + (size_t)r * cols;
-    if (c < cols) dst[c] = (uint8_t)f32_to_e4m3(clamp448(v0 / s));
-    if (c + 1 < cols) dst[c + 1] = (uint8_t)f32_to_e4m3(clamp448(v1 / s));
+    const uint32_t code = e4m3x4(clamp448(v0 / s), clamp448(v1 / s), 0.0f, 0.0f);
+    if (c < cols) dst[c] = (uint8_t)code;
+    if (c + 1 < cols) dst[c + 1] = (uint8_t)(code >> 8);
     if (lane == 0) scales[(size_t)r * nb + cb] = s;
   }
+}
+
+// Self-test of e4m3x4 against f32_to_e4m3 on the magnitudes [first, first + count) as fp32
+// bit patterns, each with both signs and in each of the four code slots: the mismatches are
+// added to *bad.
+__global__ __launch_bounds__(256) void k_e4m3_selftest(uint32_t first, uint32_t count,
+                                                       unsigned long long* __restrict__ bad) {
+  unsigned long long n = 0;
+  for (uint32_t i = blockIdx.x * 256u + threadIdx.x; i < count; i += gridDim.x * 256u) {
+#pragma unroll
+    for (int sgn = 0; sgn < 2; ++sgn) {
+      const float f = __uint_as_float((first + i) | (sgn ? 0x80000000u : 0u));
+      const uint32_t want = f32_to_e4m3(f) * 0x01010101u;
+      n += e4m3x4(f, f, f, f) != want;
+    }
+  }
+  if (n) atomicAdd(bad, n);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -589,6 +584,74 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
   v = max_step_u32<3>(v);
   v = max_step_u32<4>(v);
   return max_step_u32<5>(v);
+}
+
+// Largest magnitude among the four bf16 values of `four`, as bf16 bits. Non-negative floats
+// order as their bits do, so the block maximum below is an integer maximum; NaN counts as 0
+// (as fmaxf drops it).
+__device__ __forceinline__ uint32_t bf16x4_absmax_bits(uint2 four) {
+  const uint32_t w[2] = {four.x, four.y};
+  uint32_t m = 0;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const uint32_t lo = w[i] & 0x7fffu, hi = (w[i] >> 16) & 0x7fffu;
+    m = max(m, lo <= 0x7f80u ? lo : 0u);
+    m = max(m, hi <= 0x7f80u ? hi : 0u);
+  }
+  return m;
+}
+
+// Largest 32-bit value over each half of the wavefront (lanes 0..31 and 32..63 separately).
+__device__ __forceinline__ uint32_t half_wave_max_u32(uint32_t v) {
+  v = max_step_u32<0>(v);
+  v = max_step_u32<1>(v);
+  v = max_step_u32<2>(v);
+  v = max_step_u32<3>(v);
+  return max_step_u32<4>(v);
+}
+
+// One row of x (nbh blocks) in E4M3 per 128 by the workgroup's four wavefronts, wavefront wv
+// taking blocks wv, wv + 4, ... in batches of up to 8, two blocks at a time: each half of the
+// wavefront holds one block, four values per lane, so every instruction works on two blocks.
+// A batch's block maxima are reduced together (independent DPP and permlane chains over each
+// half, no LDS), then scale = max(amax, 1e-4)/448 and code = RNE(clamp(v / scale, +-448)) per
+// value (e4m3x4), as quant_block; each lane writes its four codes as one 4-byte device-
+// coherent store (the single-launch kernel's expert units read them from other workgroups),
+// a whole line per block. The scales gather in LDS (`lds`, nbh floats) and leave as one
+// contiguous store per 64 blocks. Blocks past the row's end are loaded from its last block
+// and not stored. Called by the whole workgroup.
+__device__ __forceinline__ void quant_row(const uint16_t* x, uint8_t* xq, float* xs, int nbh, int pow2, int lane,
+                                          int wv, float* lds) {
+  constexpr int kPairs = 4;  // blocks per wavefront and batch: 2 * kPairs
+  const int l = lane & 31, half = lane >> 5;
+  for (int b0 = wv; b0 < nbh; b0 += 4 * 2 * kPairs) {
+    uint2 four[kPairs];
+#pragma unroll
+    for (int j = 0; j < kPairs; ++j) {
+      const int b = min(b0 + 4 * (2 * j + half), nbh - 1);
+      four[j] = *reinterpret_cast<const uint2*>(x + (size_t)b * kBlock + 4 * l);
+    }
+    uint32_t m[kPairs];
+#pragma unroll
+    for (int j = 0; j < kPairs; ++j) m[j] = half_wave_max_u32(bf16x4_absmax_bits(four[j]));
+#pragma unroll
+    for (int j = 0; j < kPairs; ++j) {
+      const int b = b0 + 4 * (2 * j + half);
+      const float s = act_scale(__uint_as_float(m[j] << 16), pow2);
+      const uint32_t q = e4m3x4(clamp448(bf16_bits_to_f32(four[j].x & 0xffffu) / s),
+                                clamp448(bf16_bits_to_f32(four[j].x >> 16) / s),
+                                clamp448(bf16_bits_to_f32(four[j].y & 0xffffu) / s),
+                                clamp448(bf16_bits_to_f32(four[j].y >> 16) / s));
+      if (b < nbh) {
+        store_coherent(reinterpret_cast<uint32_t*>(xq + (size_t)b * kBlock + 4 * l), q);
+        if (l == 0) lds[b] = s;
+      }
+    }
+  }
+  __syncthreads();
+  if (wv == 0)
+    for (int b = lane; b < nbh; b += 64) store_coherent(xs + b, lds[b]);
+  __syncthreads();
 }
 
 // Merges the (largest, second largest) pairs of lanes at butterfly step STEP.
@@ -1678,9 +1741,8 @@ __device__ __forceinline__ void gateup_unit(const GateUpArgs& a, const uint8_t* 
       uint8_t* dst = hq + (size_t)(cr.row0 + col) * ldh + (size_t)jb * kBlock + 32 * w + 4 * (lane >> 4);
 #pragma unroll
       for (int p = 0; p < 2; ++p) {
-        uint32_t packed = 0;
-#pragma unroll
-        for (int v = 0; v < 4; ++v) packed |= f32_to_e4m3(clamp448(hv[c][p][v] / s)) << (8 * v);
+        const uint32_t packed = e4m3x4(clamp448(hv[c][p][0] / s), clamp448(hv[c][p][1] / s),
+                                       clamp448(hv[c][p][2] / s), clamp448(hv[c][p][3] / s));
         store_coherent(reinterpret_cast<uint32_t*>(dst + 16 * p), packed);
       }
       if (w == 0 && lane < 16) store_coherent(hs + (size_t)(cr.row0 + col) * nbh + jb, s);
@@ -1835,9 +1897,8 @@ __device__ __forceinline__ bool gateup_half(const GateUpArgs& a, const uint8_t* 
       uint8_t* dst = hq + (size_t)(cr.row0 + col) * ldh + (size_t)jb * kBlock + 32 * w + 4 * (lane >> 4);
 #pragma unroll
       for (int p = 0; p < 2; ++p) {
-        uint32_t packed = 0;
-#pragma unroll
-        for (int v = 0; v < 4; ++v) packed |= f32_to_e4m3(clamp448(hv[c][p][v] / s)) << (8 * v);
+        const uint32_t packed = e4m3x4(clamp448(hv[c][p][0] / s), clamp448(hv[c][p][1] / s),
+                                       clamp448(hv[c][p][2] / s), clamp448(hv[c][p][3] / s));
         store_coherent(reinterpret_cast<uint32_t*>(dst + 16 * p), packed);
       }
       if (w == 0 && lane < 16) store_coherent(hs + (size_t)(cr.row0 + col) * nbh + jb, s);
@@ -2454,7 +2515,8 @@ __global__ __launch_bounds__(256, 2) void k_layer(LayerArgs args) {
       if (a.n_norm) wait_signal(ctl, kSigNormed);
       // This token's row of x in E4M3 per 128 (needs nothing else; runs while the router does).
       const int nbh = a.H / kBlock, lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-      quant_row(a.x + (size_t)t * a.H, a.xq + (size_t)t * a.H, a.xs + (size_t)t * nbh, nbh, a.pow2, lane, wv);
+      quant_row(a.x + (size_t)t * a.H, a.xq + (size_t)t * a.H, a.xs + (size_t)t * nbh, nbh, a.pow2, lane, wv,
+                reinterpret_cast<float*>(rings));
       wait_signal(ctl, kSigRouted);
       if (a.vpl == 1)
         layer_select<1>(a, t, rings);
@@ -2913,9 +2975,8 @@ __device__ void gateup_mx_epilogue(const GateUpMxArgs& a, int jb, const ChunkRow
       uint8_t* dst = a.hq + (size_t)(cr.row0 + col) * a.I + (size_t)jb * kBlock + 32 * w + 4 * (lane >> 4);
 #pragma unroll
       for (int p = 0; p < 2; ++p) {
-        uint32_t packed = 0;
-#pragma unroll
-        for (int v = 0; v < 4; ++v) packed |= f32_to_e4m3(clamp448(__fmul_rn(hv[p][v], inv))) << (8 * v);
+        const uint32_t packed = e4m3x4(clamp448(__fmul_rn(hv[p][0], inv)), clamp448(__fmul_rn(hv[p][1], inv)),
+                                       clamp448(__fmul_rn(hv[p][2], inv)), clamp448(__fmul_rn(hv[p][3], inv)));
         store_coherent(reinterpret_cast<uint32_t*>(dst + 16 * p), packed);
       }
       if (lane < 16) red8[w][col] = (uint8_t)ex;
@@ -2991,9 +3052,8 @@ __device__ void gateup_mx_wide(const GateUpMxArgs& a, int e, int blk, const Chun
       uint8_t* dst = a.hq + (size_t)(cr.row0 + col) * a.I + (size_t)blk * 32 + 4 * (lane >> 4);
 #pragma unroll
       for (int p = 0; p < 2; ++p) {
-        uint32_t packed = 0;
-#pragma unroll
-        for (int v = 0; v < 4; ++v) packed |= f32_to_e4m3(clamp448(__fmul_rn(hv[p][v], inv))) << (8 * v);
+        const uint32_t packed = e4m3x4(clamp448(__fmul_rn(hv[p][0], inv)), clamp448(__fmul_rn(hv[p][1], inv)),
+                                       clamp448(__fmul_rn(hv[p][2], inv)), clamp448(__fmul_rn(hv[p][3], inv)));
         store_coherent(reinterpret_cast<uint32_t*>(dst + 16 * p), packed);
       }
       if (lane < 16) store_coherent_byte(a.hs + (size_t)(cr.row0 + col) * a.hs_ld + blk, (uint8_t)ex);
@@ -4642,7 +4702,7 @@ int scratch_address(void** out) {
 
 extern "C" {
 
-int megamoe_abi_version(void) { return 9; }
+int megamoe_abi_version(void) { return 10; }
 
 const char* megamoe_status_string(int status) {
   switch (status) {
@@ -4926,6 +4986,16 @@ int megamoe_quantize_rows(int32_t rows, int32_t cols, const void* x, uint8_t* q,
   if (rows == 0 || cols == 0) return MEGAMOE_OK;
   if (!x || !q || !scales) return MEGAMOE_ERR_INVALID_ARGUMENT;
   return launch_quant(rows, cols, x, q, scales, pow2, (hipStream_t)stream);
+}
+
+int megamoe_e4m3_selftest(uint32_t first, uint32_t count, uint64_t* mismatches, void* stream) {
+  if (!mismatches || (uint64_t)first + count > 0x80000000ull) return MEGAMOE_ERR_INVALID_ARGUMENT;
+  if (count == 0) return MEGAMOE_OK;
+  const uint32_t blocks = (count + 255u) / 256u;
+  hipLaunchKernelGGL(k_e4m3_selftest, dim3(blocks < 8192u ? blocks : 8192u), dim3(256), 0, (hipStream_t)stream,
+                     first, count, reinterpret_cast<unsigned long long*>(mismatches));
+  MEGAMOE_LAUNCH_CHECK();
+  return MEGAMOE_OK;
 }
 
 }  // extern "C"
