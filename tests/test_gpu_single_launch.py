@@ -113,3 +113,22 @@ def test_a_wait_that_gives_up_is_reported(monkeypatch):
     torch.cuda.synchronize()
     _same(again, good, "after a forced give-up")
     assert not layer.gave_up(torch.device(DEV))
+
+
+@pytest.mark.parametrize("cid", [C.HEADLINE, "moe-fp8-kimi-k2-t128", "moe-fp8-qwen3-30b-a3b-t32"])
+def test_router_units_left_by_their_workgroups_are_rescued(monkeypatch, cid):
+    """Router units go to the workgroup of the same index; a routing unit runs (and counts) any
+    whose workgroup has not started it, so the layer completes whatever number of workgroups
+    the device keeps resident. The test hook makes every odd workgroup leave its unit to them:
+    the results equal the stream-ordered form's bit for bit, and no wait gives up."""
+    monkeypatch.setenv("MEGAMOE_FORCE_RESCUE", "1")
+    for case in (C.development(C.case(cid)), C.case(cid)):
+        _log(f"forced rescue {case.id} T={case.tokens} E={case.experts}")
+        values = workloads.make_inputs(case, 11, DEV)
+        one = submission.MoELayer(case)
+        five = submission.MoELayer(case, single_launch=False)
+        for _ in range(2):
+            a, b = one(values), five(values)
+            torch.cuda.synchronize()
+            _same(a, b, f"{case.id} with forced rescue")
+        assert not one.gave_up(torch.device(DEV))

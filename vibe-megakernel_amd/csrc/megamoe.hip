@@ -2355,7 +2355,11 @@ constexpr int kCombineUnit = 256 * 8;  // outputs per combine unit
 constexpr int kSigNormed = 0, kSigRouted = 1, kSigPermuted = 2, kSigDown = 3, kSignals = 4;
 constexpr int kSigLines = 16, kSigStride = (4096 + 256) / 4;  // flags per signal; ints between flags
 constexpr int kCtlSig = 512;                                  // the first flag
-constexpr int kCtlInts = kCtlSig + kSignals * kSigLines * kSigStride;
+// Start flags of the router units that workgroups take by index (LayerArgs::n_first), one
+// per 128-byte line: 0 not started, 1 taken by its workgroup, 2 taken by a rescuing one.
+constexpr int kStartStride = 32, kMaxStartUnits = 1024;
+constexpr int kCtlStart = kCtlSig + kSignals * kSigLines * kSigStride;
+constexpr int kCtlInts = kCtlStart + kMaxStartUnits * kStartStride;
 
 struct LayerArgs {
   ExpertArgs ex;
@@ -2380,6 +2384,8 @@ struct LayerArgs {
   int nsplit, n_et, ntt, vpl, ks;
   int n_norm, n_router;
   int force_timeout;  // test hook: the combine units wait for a flag value never raised, 20 us at most
+  int n_first;        // router units [0, n_first) go to the workgroup of the same index (0: none)
+  int force_rescue;   // test hook: odd workgroups leave their router unit to the routing units
   int pad_;
 };
 
@@ -2428,6 +2434,58 @@ template <int NTT>
 __device__ __forceinline__ void layer_router(const LayerArgs& a, int unit, uint8_t* lds) {
   router_tile<NTT, true>(a.x, a.router, a.partial, a.T, a.H, a.E, a.n_et, a.nsplit, unit,
                          reinterpret_cast<f64x4*>(lds));
+}
+
+__device__ __forceinline__ void layer_router_unit(const LayerArgs& a, int r, uint8_t* lds) {
+  if (a.ntt == 1)
+    layer_router<1>(a, r, lds);
+  else if (a.ntt == 2)
+    layer_router<2>(a, r, lds);
+  else
+    layer_router<4>(a, r, lds);
+}
+
+// A routing unit waits this long for the router signal before it looks for router units
+// that were never started (see rescue_router_unit): 100 us, several times the router phase
+// of any config, so with every workgroup resident it never looks.
+constexpr uint64_t kRescueTicks = 10000;
+
+// Thread 0 polls signal `sig` for at most `ticks` (as wait_ready, without giving up for the
+// call); returns, in every thread, whether it came. When it did, the acquire after the
+// barrier keeps the loads that follow below it.
+__device__ __forceinline__ bool wait_signal_for(int* ctl, int sig, uint64_t ticks, int* lds) {
+  if (threadIdx.x == 0) {
+    const int* f = my_signal_flag(ctl, sig);
+    const uint64_t t0 = wall_clock64();
+    int came = 0, naps = 1;
+    while (!(came = load_count(f) != 0) && wall_clock64() - t0 < ticks) {
+      for (int k = 0; k < naps; ++k) __builtin_amdgcn_s_sleep(16);
+      naps = naps < 2 ? 2 * naps : 2;
+    }
+    *lds = came;
+  }
+  __syncthreads();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  const bool came = *lds != 0;
+  __syncthreads();
+  return came;
+}
+
+// Takes (start flag 0 -> 2) the lowest router unit in [0, n_first) whose workgroup has not
+// started it, for this workgroup to run; -1 if every one has started. In every thread.
+__device__ __forceinline__ int rescue_router_unit(int n_first, int* ctl, int* lds) {
+  for (;;) {
+    if (threadIdx.x == 0) lds[0] = n_first;
+    __syncthreads();
+    for (int b = threadIdx.x; b < n_first; b += 256)
+      if (load_count(&ctl[kCtlStart + b * kStartStride]) == 0) atomicMin(&lds[0], b);
+    __syncthreads();
+    const int b = lds[0];
+    if (b == n_first) return -1;
+    if (threadIdx.x == 0) lds[1] = atomicCAS(&ctl[kCtlStart + b * kStartStride], 0, 2) == 0;
+    __syncthreads();
+    if (lds[1]) return b;
+  }
 }
 
 template <int VPL>
@@ -2482,9 +2540,25 @@ __global__ __launch_bounds__(256, 2) void k_layer(LayerArgs args) {
                 "front-end scratch in the rings");
   int* ctl = args.ctl;
   const int fixed = args.n_norm + args.n_router + args.T;  // units listed before the routing is known
-  if (threadIdx.x == 0) slot = atomicAdd(&ctl[kCtlQueue], 1);
+  // Router units [0, n_first) go to the workgroup of the same index, the rest through the
+  // queue, whose first entry is unit n_first: 512 workgroups claiming their first unit from
+  // one counter at once took ~10 us to be served, and the router phase waited for the last.
+  // A workgroup taking unit b by index marks its start flag; if a routing unit took the unit
+  // meanwhile (rescue_router_unit: its workgroup had not started in 100 us), this one runs it
+  // anyway (same values) but does not count it.
+  const int n_first = args.n_first;
+  int counts = 1;  // thread 0: whether this workgroup counts its router unit
+  if (threadIdx.x == 0) {
+    if ((int)blockIdx.x < n_first && !(args.force_rescue && (blockIdx.x & 1))) {
+      counts = atomicCAS(&ctl[kCtlStart + blockIdx.x * kStartStride], 0, 1) == 0;
+      slot = blockIdx.x;
+    } else {
+      slot = n_first + atomicAdd(&ctl[kCtlQueue], 1);
+    }
+  }
   __syncthreads();
   int u = slot, next = 0;
+  int resume = -1;  // a routing unit to return to after running a rescued router unit
 
   // Phase 1: the front-end units (claims only grow, so a workgroup never comes back here).
   // A workgroup claims its next unit only when it has finished this one: the front-end units
@@ -2503,20 +2577,33 @@ __global__ __launch_bounds__(256, 2) void k_layer(LayerArgs args) {
     } else if (u < a.n_norm + a.n_router) {
       if (a.n_norm) wait_signal(ctl, kSigNormed);
       const int r = u - a.n_norm;
-      if (a.ntt == 1)
-        layer_router<1>(a, r, rings);
-      else if (a.ntt == 2)
-        layer_router<2>(a, r, rings);
-      else
-        layer_router<4>(a, r, rings);
-      publish_count(ctl, kCtlRouted, 1, a.n_router, kSigRouted, &units[0]);
+      layer_router_unit(a, r, rings);
+      // Counted unless a rescuing workgroup took it first (then that one counts it).
+      publish_fence();
+      __syncthreads();
+      if (threadIdx.x == 0) units[0] = counts ? atomicAdd(&ctl[kCtlRouted], 1) : -2;
+      if (threadIdx.x == 0) counts = 1;
+      __syncthreads();
+      if (units[0] == a.n_router - 1) raise_signal(ctl, kSigRouted);
     } else {
       const int t = u - a.n_norm - a.n_router;
       if (a.n_norm) wait_signal(ctl, kSigNormed);
       // This token's row of x in E4M3 per 128 (needs nothing else; runs while the router does).
       const int nbh = a.H / kBlock, lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-      quant_row(a.x + (size_t)t * a.H, a.xq + (size_t)t * a.H, a.xs + (size_t)t * nbh, nbh, a.pow2, lane, wv,
-                reinterpret_cast<float*>(rings));
+      const bool back = resume >= 0;  // after a rescued router unit: look again at once
+      if (!back)
+        quant_row(a.x + (size_t)t * a.H, a.xq + (size_t)t * a.H, a.xs + (size_t)t * nbh, nbh, a.pow2, lane, wv,
+                  reinterpret_cast<float*>(rings));
+      resume = -1;
+      if (n_first && (back || !wait_signal_for(ctl, kSigRouted, kRescueTicks, flags))) {
+        // A router unit whose workgroup never started: run it (and count it), then come back.
+        const int b = rescue_router_unit(n_first, ctl, flags);
+        if (b >= 0) {
+          resume = u;
+          u = a.n_norm + b;
+          continue;
+        }
+      }
       wait_signal(ctl, kSigRouted);
       if (a.vpl == 1)
         layer_select<1>(a, t, rings);
@@ -2539,8 +2626,13 @@ __global__ __launch_bounds__(256, 2) void k_layer(LayerArgs args) {
         raise_signal(ctl, kSigPermuted);
       }
     }
+    if (resume >= 0) {  // back to the routing unit that ran a rescued router unit
+      __syncthreads();
+      u = resume;
+      continue;
+    }
     __syncthreads();
-    if (threadIdx.x == 0) slot = atomicAdd(&ctl[kCtlQueue], 1);
+    if (threadIdx.x == 0) slot = n_first + atomicAdd(&ctl[kCtlQueue], 1);
     __syncthreads();
     u = slot;
   }
@@ -2569,7 +2661,7 @@ __global__ __launch_bounds__(256, 2) void k_layer(LayerArgs args) {
     const int nbI = a.gu.I / kBlock, nbH = a.dn.H / kBlock;
     uint8_t* ring = rings + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) * kRingWave;
     __syncthreads();
-    if (threadIdx.x == 0) next = atomicAdd(&ctl[kCtlQueue], 1);
+    if (threadIdx.x == 0) next = n_first + atomicAdd(&ctl[kCtlQueue], 1);
     if (u < fixed + n_gu) {
       const int g = u - fixed;
       bool done = true;
@@ -2617,7 +2709,7 @@ __global__ __launch_bounds__(256, 2) void k_layer(LayerArgs args) {
     bool use_first = true;
     while (u < total) {
       __syncthreads();
-      if (threadIdx.x == 0) next = atomicAdd(&ctl[kCtlQueue], 1);
+      if (threadIdx.x == 0) next = n_first + atomicAdd(&ctl[kCtlQueue], 1);
       layer_combine(a, u - experts_end, use_first ? &first : nullptr);
       use_first = false;
       if (threadIdx.x == 0) slot = next;
@@ -2646,6 +2738,8 @@ __global__ __launch_bounds__(256, 2) void k_layer(LayerArgs args) {
     else if (i < n_words + kSignals * kSigLines)
       __hip_atomic_store(signal_flag(ctl, (i - n_words) / kSigLines, (i - n_words) % kSigLines), 0,
                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int b = i; b < n_first; b += 256)
+      __hip_atomic_store(&ctl[kCtlStart + b * kStartStride], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -4230,6 +4324,13 @@ int forward_layer_impl(const megamoe_desc* desc, const megamoe_tensors* t, const
                            ((size_t)T * H + kCombineUnit - 1) / kCombineUnit;
   const size_t resident = (size_t)di.cus * di.layer_per_cu;
   const unsigned grid = (unsigned)(units_max < resident ? units_max : resident);
+  // Router units taken by workgroup index: the first round of them, when there are 64 or more
+  // (fewer are claimed from the queue in ~1 us: Mixtral's 8 measured 2 us slower by index);
+  // none in the block form, whose first units are the norm rows.
+  la.n_first = norm || la.n_router < 64 ? 0 : (int)grid < la.n_router ? (int)grid : la.n_router;
+  if (la.n_first > kMaxStartUnits) la.n_first = kMaxStartUnits;
+  const char* rescue = getenv("MEGAMOE_FORCE_RESCUE");
+  la.force_rescue = rescue && rescue[0] == '1' ? 1 : 0;
   if (mark(0) != hipSuccess) return MEGAMOE_ERR_HIP;
   if (split)
     hipLaunchKernelGGL(k_layer<true>, dim3(grid), dim3(256), 0, st, la);
