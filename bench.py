@@ -441,7 +441,8 @@ def bench_ep_share(case, steps: int, warmup: int, want_cpu: bool, cpu_budget: fl
         "stage_us": {name: x * 1e3 for name, x in zip(names, stage_ms)},
         "rotation_sets": 1, "received_rows": R, "sent_rows": T * K,
         "roofline": {"bound": "hbm", "achieved": ex_bytes / (ex_ms * 1e-3) / 1e9, "peak": PEAK_HBM / 1e9,
-                     "unit": "GB/s", "frac": ex_bytes / (ex_ms * 1e-3) / PEAK_HBM, "traffic": None,
+                     "unit": "GB/s", "frac": ex_bytes / (ex_ms * 1e-3) / PEAK_HBM,
+                     "traffic": measured_traffic(case, mx_kernel(R, local)),
                      "kernel": mx_kernel(R, local), "kernel_us": ex_ms * 1e3, "bytes_per_launch": ex_bytes},
         "dtype": "e2m1xe4m3->fp32 (E8M0 scales per 32; bf16 out)",
     }
