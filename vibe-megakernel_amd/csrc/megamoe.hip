@@ -934,31 +934,48 @@ __global__ __launch_bounds__(256) void k_select(const double* __restrict__ parti
 // in the gate/up list it appears once per I-sized slice of its S*I rows.
 // ---------------------------------------------------------------------------------------
 
-// Exclusive scan over the workgroup of a value packing four counters:
-// bits 0-20 rows, 21-35 chunks of 33-64 rows, 36-46 chunks of 17-32, 47-57 chunks of 1-16.
+// The 64-bit value of the lane N below in the same row of 16 lanes (DPP row_shr:N), 0 for the
+// lanes below N of each row. Needs every lane of the wavefront active.
+template <int N>
+__device__ __forceinline__ unsigned long long row_shr_u64(unsigned long long x) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)x, 0x110 + N, 0xF, 0xF, true);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)(x >> 32), 0x110 + N, 0xF, 0xF, true);
+  return ((unsigned long long)hi << 32) | lo;
+}
+
+__device__ __forceinline__ unsigned long long readlane_u64(unsigned long long x, int lane) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)x, lane);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(x >> 32), lane);
+  return ((unsigned long long)hi << 32) | lo;
+}
+
+// Exclusive scan over the workgroup (at most 16 wavefronts, all lanes active) of a value
+// packing four counters: bits 0-20 rows, 21-35 chunks of 33-64 rows, 36-46 chunks of 17-32,
+// 47-57 chunks of 1-16. Within a wavefront: DPP shifts inside each row of 16 lanes, then the
+// rows' totals read from lanes 15, 31 and 47 (no LDS round trips: the LDS shuffles took ~2
+// us on the single launch's critical path); across wavefronts: every thread adds the totals
+// of the wavefronts below it from LDS. `tmp` (16 entries) is written before the barrier and
+// read after it.
 __device__ unsigned long long block_exclusive_scan(unsigned long long v, unsigned long long* tmp,
                                                    unsigned long long* total) {
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6, nw = blockDim.x >> 6;
   unsigned long long x = v;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const unsigned long long y = __shfl_up(x, o);
-    if (lane >= o) x += y;
-  }
+  x += row_shr_u64<1>(x);
+  x += row_shr_u64<2>(x);
+  x += row_shr_u64<4>(x);
+  x += row_shr_u64<8>(x);
+  const unsigned long long r0 = readlane_u64(x, 15), r1 = readlane_u64(x, 31), r2 = readlane_u64(x, 47);
+  const int row = lane >> 4;
+  x += (row >= 1 ? r0 : 0ull) + (row >= 2 ? r1 : 0ull) + (row >= 3 ? r2 : 0ull);
   if (lane == 63) tmp[wid] = x;
   __syncthreads();
-  if (wid == 0) {
-    unsigned long long s = lane < nw ? tmp[lane] : 0ull;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const unsigned long long y = __shfl_up(s, o);
-      if (lane >= o) s += y;
-    }
-    if (lane < nw) tmp[lane] = s;
+  unsigned long long base = 0ull, all = 0ull;
+  for (int q = 0; q < nw; ++q) {
+    const unsigned long long t = tmp[q];
+    base += q < wid ? t : 0ull;
+    all += t;
   }
-  __syncthreads();
-  const unsigned long long base = wid ? tmp[wid - 1] : 0ull;
-  *total = tmp[nw - 1];
+  *total = all;
   return base + x - v;
 }
 
@@ -1038,9 +1055,18 @@ __device__ __forceinline__ void permute_block(const int64_t* __restrict__ ids, i
     *hits = 0;
   }
   __syncthreads();
-  for (int i = tid; i < n; i += nt) {
+  // Each thread's first kKeep entries stay in registers for the rank loop below (one load of
+  // the ids on the critical path instead of two).
+  constexpr int kKeep = 4;
+  int keep[kKeep];
+#pragma unroll
+  for (int j = 0; j < kKeep; ++j) keep[j] = 0;
+  for (int i = tid, j = 0; i < n; i += nt, ++j) {
     const int64_t e64 = ids[i] - base;
     const int t = i / K;
+#pragma unroll
+    for (int q = 0; q < kKeep; ++q)
+      if (q == j) keep[q] = (int)e64;
     if (e64 < 0 || e64 >= E) {
       *bad = 1;
       continue;
@@ -1158,8 +1184,13 @@ __device__ __forceinline__ void permute_block(const int64_t* __restrict__ ids, i
     for (int i = tid; i < (S * (s4 + s2 + s1) + t4 + t2 + t1) * nbI; i += nt) store_out<CO>(&out.pairs[i], 0);
   __syncthreads();
   if (!tile_waves) {
-    for (int i = tid; i < n; i += nt) {
-      const int e = (int)(ids[i] - base), t = i / K;
+    for (int i = tid, j = 0; i < n; i += nt, ++j) {
+      int e = 0;
+#pragma unroll
+      for (int q = 0; q < kKeep; ++q)
+        if (q == j) e = keep[q];
+      if (j >= kKeep) e = (int)(ids[i] - base);
+      const int t = i / K;
       const unsigned* row = bm + e * words;
       int rank = __popc(row[t >> 5] & ((1u << (t & 31)) - 1u));
       for (int q = 0; q < (t >> 5); ++q) rank += __popc(row[q]);
