@@ -2670,8 +2670,11 @@ __global__ __launch_bounds__(256, 2) void k_layer(LayerArgs args) {
 
   // Phase 2: the work lists, once the permute has run (its meta words were never read before
   // in this call). If the wait gave up (error word set), the lists are not read: no expert
-  // units, only the combine units, which then write NaN.
-  wait_signal(ctl, kSigPermuted);
+  // units, only the combine units, which then write NaN. Most workgroups wait here while the
+  // routing units and the permute, the critical path, run: their polls back off to ~3.6 us
+  // apart (8 naps) instead of ~0.9 (DeepSeek-V3 -1.7 us, Mixtral -2.2, Qwen3-30B-A3B -0.6,
+  // Kimi-K2 0, over two A/B runs; 16 naps measured no better).
+  wait_ready(ReadyWait{my_signal_flag(ctl, kSigPermuted), 1, &ctl[kCtlError], kWaitTicks, true, 8});
   if (threadIdx.x == 0) {
     const bool lists = load_count(my_signal_flag(ctl, kSigPermuted)) != 0;
     units[0] = lists ? (SPLIT ? 2 : 1) * load_count(&args.po.meta[kMetaUnitsGU]) : 0;
