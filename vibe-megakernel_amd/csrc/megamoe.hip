@@ -2626,16 +2626,20 @@ __global__ __launch_bounds__(256, 2) void k_layer(LayerArgs args) {
         quant_row(a.x + (size_t)t * a.H, a.xq + (size_t)t * a.H, a.xs + (size_t)t * nbh, nbh, a.pow2, lane, wv,
                   reinterpret_cast<float*>(rings));
       resume = -1;
-      if (n_first && (back || !wait_signal_for(ctl, kSigRouted, kRescueTicks, flags))) {
-        // A router unit whose workgroup never started: run it (and count it), then come back.
-        const int b = rescue_router_unit(n_first, ctl, flags);
-        if (b >= 0) {
-          resume = u;
-          u = a.n_norm + b;
-          continue;
+      bool routed = false;  // the router signal came (and was acquired) in the wait below
+      if (n_first) {
+        if (!back) routed = wait_signal_for(ctl, kSigRouted, kRescueTicks, flags);
+        if (!routed) {
+          // A router unit whose workgroup never started: run it (and count it), then come back.
+          const int b = rescue_router_unit(n_first, ctl, flags);
+          if (b >= 0) {
+            resume = u;
+            u = a.n_norm + b;
+            continue;
+          }
         }
       }
-      wait_signal(ctl, kSigRouted);
+      if (!routed) wait_signal(ctl, kSigRouted);
       if (a.vpl == 1)
         layer_select<1>(a, t, rings);
       else if (a.vpl == 2)
