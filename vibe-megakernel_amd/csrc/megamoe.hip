@@ -998,7 +998,20 @@ struct PermuteOut {
   int* ready;    // [down chunks, stride ready_stride] zeroed here, counted by the expert kernel
   int* pairs;    // [gate/up chunks * nbI] zeroed here (NULL: none), counted by the expert kernel
   int ready_stride = 1;  // ints between two chunks' counters
+  int* xcd = nullptr;    // the batch form's per-XCD queues (kXcdInts; NULL: none)
 };
+
+// The batch form's work split over the XCDs (the lists in expert order, `wide` 2): XCD x
+// takes the chunks [bound x, bound x+1) first (8 ranges of about equal chunk counts, cut at
+// expert boundaries), so the units of an expert, which read the same weights, run on one
+// XCD and meet in its L2. One queue counter per XCD and phase (gate/up, down), each on a
+// 128-byte line of its own, then the 9 bounds.
+constexpr int kXcds = 8, kXcdStride = 32, kXcdBound = 2 * kXcds * kXcdStride, kXcdInts = kXcdBound + kXcds + 1;
+
+// The XCD this workgroup runs on (hardware register XCC_ID), as a queue index.
+__device__ __forceinline__ int my_xcd() {
+  return __builtin_amdgcn_s_getreg(20 | (0 << 6) | (3 << 11)) % kXcds;
+}
 
 // Readiness counters of the fp8 form (one per down chunk): the down units poll them while
 // the gate/up units run, hundreds at a time early in the down phase. Each counter gets a
@@ -1016,9 +1029,13 @@ __device__ __forceinline__ int chunk_class(int rows) { return rows > 32 ? 0 : (r
 // work lists and every later kernel's work are skipped (the combine writes NaN). Expert
 // e here is id e + base (a rank's local experts under expert parallelism).
 //
-// With `wide` (the MXFP4 form, no shared expert), a chunk of more than 32 rows is worked by
+// With `wide` 1 (the MXFP4 form, no shared expert), a chunk of more than 32 rows is worked by
 // wide units, 4 per 128-channel block of gate/up and 2 per 128-row block of down (times
-// the K parts); those chunks lead the lists, and meta[kMetaWide] counts them.
+// the K parts); those chunks lead the lists, and meta[kMetaWide] counts them. With `wide` 2
+// (the batch form, no shared expert) the lists are in expert order instead: each expert's
+// chunks in a row, each record's .w holding its index in that group and the group's size
+// (bits 16 up), so the batch kernel can hand out a weight block's units for every chunk of
+// the expert one after another.
 
 // The permute by one workgroup of any size (a multiple of 64, at least 256): thread i owns
 // the contiguous experts [i*ept, i*ept + ept) (ept = ceil(E / threads)), so the scan over
@@ -1130,23 +1147,45 @@ __device__ __forceinline__ void permute_block(const int64_t* __restrict__ ids, i
     const int full = c / chunk, rem = c % chunk;
     store_out<CO>(&out.counts[e], c);
     store_out<CO>(&out.offsets[e], off);
-    for (int i = 0; i < a4; ++i) {
-      const int4 ch = make_int4(e, chunk * i, min(chunk, c - chunk * i), 0);
-      store_out<CO>(&out.gu[gbase[0] + gshared[0] + p4 + i], ch);
-      store_out<CO>(&out.dn[dbase[0] + dshared[0] + p4 + i], ch);
-      store_out<CO>(&out.dn_of_gu[gbase[0] + gshared[0] + p4 + i], dbase[0] + dshared[0] + p4 + i);
-    }
-    if (a2) {
-      const int4 ch = make_int4(e, chunk * full, rem, 0);
-      store_out<CO>(&out.gu[gbase[1] + gshared[1] + p2], ch);
-      store_out<CO>(&out.dn[dbase[1] + dshared[1] + p2], ch);
-      store_out<CO>(&out.dn_of_gu[gbase[1] + gshared[1] + p2], dbase[1] + dshared[1] + p2);
-    }
-    if (a1) {
-      const int4 ch = make_int4(e, chunk * full, rem, 0);
-      store_out<CO>(&out.gu[gbase[2] + gshared[2] + p1], ch);
-      store_out<CO>(&out.dn[dbase[2] + dshared[2] + p1], ch);
-      store_out<CO>(&out.dn_of_gu[gbase[2] + gshared[2] + p1], dbase[2] + dshared[2] + p1);
+    if (wide == 2) {
+      // Lists in expert order: expert e's chunks at the prefix of every class's chunks over
+      // the experts before it, .w = the chunk's index in its expert's group | group size << 16.
+      const int nch = a4 + a2 + a1, first = p4 + p2 + p1;
+      for (int i = 0; i < nch; ++i) {
+        const int4 ch = make_int4(e, chunk * i, min(chunk, c - chunk * i), i | (nch << 16));
+        store_out<CO>(&out.gu[first + i], ch);
+        store_out<CO>(&out.dn[first + i], ch);
+        store_out<CO>(&out.dn_of_gu[first + i], first + i);
+      }
+      // The XCD bounds inside this expert's group: bound x is the first group start at or
+      // past x * total / 8 (rounded up), so this group owns the targets in [first, first + nch).
+      if (out.xcd) {
+        const int total_ch = t4 + t2 + t1;
+        for (int x = 1; x < kXcds; ++x) {
+          const int target = (x * total_ch + kXcds - 1) / kXcds;
+          if (first <= target && target < first + nch)
+            store_out<CO>(&out.xcd[kXcdBound + x], target == first ? first : first + nch);
+        }
+      }
+    } else {
+      for (int i = 0; i < a4; ++i) {
+        const int4 ch = make_int4(e, chunk * i, min(chunk, c - chunk * i), 0);
+        store_out<CO>(&out.gu[gbase[0] + gshared[0] + p4 + i], ch);
+        store_out<CO>(&out.dn[dbase[0] + dshared[0] + p4 + i], ch);
+        store_out<CO>(&out.dn_of_gu[gbase[0] + gshared[0] + p4 + i], dbase[0] + dshared[0] + p4 + i);
+      }
+      if (a2) {
+        const int4 ch = make_int4(e, chunk * full, rem, 0);
+        store_out<CO>(&out.gu[gbase[1] + gshared[1] + p2], ch);
+        store_out<CO>(&out.dn[dbase[1] + dshared[1] + p2], ch);
+        store_out<CO>(&out.dn_of_gu[gbase[1] + gshared[1] + p2], dbase[1] + dshared[1] + p2);
+      }
+      if (a1) {
+        const int4 ch = make_int4(e, chunk * full, rem, 0);
+        store_out<CO>(&out.gu[gbase[2] + gshared[2] + p1], ch);
+        store_out<CO>(&out.dn[dbase[2] + dshared[2] + p1], ch);
+        store_out<CO>(&out.dn_of_gu[gbase[2] + gshared[2] + p1], dbase[2] + dshared[2] + p1);
+      }
     }
     cnt[e] = off;  // the expert's first row, for the ranks below (only this thread reads cnt[e] above)
     off += c;
@@ -1170,10 +1209,17 @@ __device__ __forceinline__ void permute_block(const int64_t* __restrict__ ids, i
     }
     store_out<CO>(&out.offsets[E], total);
     store_out<CO>(&out.meta[kMetaHit], *hits);
-    const int wf = wide ? 4 : 1, wfd = wide ? 2 : 1;  // units per block of a chunk of over 32 rows
+    const int wf = wide == 1 ? 4 : 1, wfd = wide == 1 ? 2 : 1;  // units per block of a chunk of over 32 rows
     store_out<CO>(&out.meta[kMetaUnitsGU], (S * (s4 + s2 + s1) + wf * t4 + t2 + t1) * nbI);
     store_out<CO>(&out.meta[kMetaUnitsDN], (s4 + s2 + s1 + wfd * t4 + t2 + t1) * nbH * ks);
-    store_out<CO>(&out.meta[kMetaWide], wide ? t4 : 0);
+    store_out<CO>(&out.meta[kMetaWide], wide == 1 ? t4 : 0);
+    if (out.xcd) {
+      const int total_ch = t4 + t2 + t1;
+      for (int q = 0; q < 2 * kXcds; ++q) store_out<CO>(&out.xcd[q * kXcdStride], 0);
+      store_out<CO>(&out.xcd[kXcdBound], 0);
+      for (int x = 1; x <= kXcds; ++x)  // targets no group holds: past the last chunk
+        if ((x * total_ch + kXcds - 1) / kXcds >= total_ch) store_out<CO>(&out.xcd[kXcdBound + x], total_ch);
+    }
     store_out<CO>(&out.meta[kMetaQueueGU], 0);
     store_out<CO>(&out.meta[kMetaQueueDN], 0);
     store_out<CO>(&out.meta[kMetaError], 0);
@@ -3697,7 +3743,30 @@ struct ExpertMxArgs {
   DownMxArgs dn;
   const int* dn_of_gu;
   int* ready;
+  int* xcd;  // the batch kernel's per-XCD queues (PermuteOut::xcd)
 };
+
+// Thread 0 of a batch workgroup on XCD x: its next unit, from x's gate/up queue, else from
+// the other XCDs' in turn, then from the down queues likewise (a down unit only once every
+// gate/up unit is taken, so the units a down unit waits for are held by running workgroups).
+// Queue y of a phase hands out the units of chunks [bnd[y], bnd[y+1]) in list order (`per`
+// units a chunk); `done` marks the queues this workgroup found empty (a queue only empties).
+// `total` once every queue is empty.
+__device__ __forceinline__ int claim_xcd(int* q, const int* bnd, int x, int nbI, int per, int total_gu, int total,
+                                         unsigned& done) {
+  for (int phase = 0; phase < 2; ++phase)
+    for (int k = 0; k < kXcds; ++k) {
+      const int y = (x + k) % kXcds, id = phase * kXcds + y;
+      if ((done >> id) & 1u) continue;
+      const int first = bnd[y] * (phase ? per : nbI), size = bnd[y + 1] * (phase ? per : nbI) - first;
+      if (size > 0) {
+        const int i = atomicAdd(&q[id * kXcdStride], 1);
+        if (i < size) return phase ? total_gu + first + i : first + i;
+      }
+      done |= 1u << id;
+    }
+  return total;
+}
 
 // The persistent expert kernel of the MXFP4 form: the queue, claims and readiness waits
 // of k_experts, with the MXFP4 units.
@@ -3743,11 +3812,17 @@ __global__ __launch_bounds__(256, 1) void k_experts_mx_batch(ExpertMxArgs args) 
   typedef const __attribute__((address_space(4))) ExpertMxArgs* ArgsPtr;
   __shared__ uint8_t red8[4][64];
   __shared__ __attribute__((aligned(16))) BatchLds lds;
-  __shared__ int slot;
+  __shared__ int slot, bnd[kXcds + 1];
   int* meta = args.gu.meta;
   const int total_gu = meta[kMetaUnitsGU];
   const int total = total_gu + meta[kMetaUnitsDN];
-  if (threadIdx.x == 0) slot = atomicAdd(&meta[kMetaQueueGU], 1);
+  // Units are claimed from the queue of this workgroup's XCD first (claim_xcd).
+  const int xcd = my_xcd(), cnbI = args.gu.I / kBlock, cper = args.dn.H / 256 * args.dn.ks;
+  unsigned done = 0;
+  if (threadIdx.x == 0) {
+    for (int i = 0; i <= kXcds; ++i) bnd[i] = args.xcd[kXcdBound + i];
+    slot = claim_xcd(args.xcd, bnd, xcd, cnbI, cper, total_gu, total, done);
+  }
   __syncthreads();
   int u = slot, next = 0;
   while (u < total) {
@@ -3757,9 +3832,14 @@ __global__ __launch_bounds__(256, 1) void k_experts_mx_batch(ExpertMxArgs args) 
     __builtin_memcpy(&a, (const ExpertMxArgs*)ap, sizeof(a));
     const int nbI = a.gu.I / kBlock, nbH2 = a.dn.H / 256;
     __syncthreads();
-    if (threadIdx.x == 0) next = atomicAdd(&meta[kMetaQueueGU], 1);
+    if (threadIdx.x == 0) next = claim_xcd(a.xcd, bnd, xcd, cnbI, cper, total_gu, total, done);
     if (u < total_gu) {
-      const int c = u / nbI, jb = u % nbI;
+      // Units in expert order, block-major within the expert: the units of one weight block
+      // for each chunk of the expert (its group of chunks, .w) are handed out one after
+      // another and start at the same K stage, so the weights streamed for the first are
+      // still cached when the others read them.
+      const int w0 = a.gu.chunks[u / nbI].w, cg = u / nbI - (w0 & 0xffff), ng = w0 >> 16, r = u - cg * nbI;
+      const int c = cg + r % ng, jb = r / ng;
       const int4 ch = a.gu.chunks[c];
       const ChunkRows cr{ch.z, a.gu.offsets[ch.x] + ch.y, a.gu.perm, a.gu.K};
       const int nst = a.gu.H / kMxStageK;
@@ -3768,8 +3848,9 @@ __global__ __launch_bounds__(256, 1) void k_experts_mx_batch(ExpertMxArgs args) 
       __syncthreads();
       if (threadIdx.x == 0) atomicAdd(&a.ready[a.dn_of_gu[c]], 1);
     } else {
-      const int v = u - total_gu, ks = a.dn.ks;
-      const int c = v / (nbH2 * ks), rem = v % (nbH2 * ks), j2 = rem / ks, kp = rem % ks;
+      const int v = u - total_gu, ks = a.dn.ks, per = nbH2 * ks;
+      const int w0 = a.dn.chunks[v / per].w, cg = v / per - (w0 & 0xffff), ng = w0 >> 16, r = v - cg * per;
+      const int c = cg + r % ng, j2 = r / ng / ks, kp = r / ng % ks;
       const int4 ch = a.dn.chunks[c];
       const ChunkRows cr{ch.z, a.dn.offsets[ch.x] + ch.y, a.dn.perm, a.dn.K};
       const ReadyWait ready{&a.ready[c], nbI, &meta[kMetaError]};
@@ -4406,7 +4487,7 @@ int validate_mx(const megamoe_desc* d) {
 }
 
 struct LayoutMx {
-  size_t counts, offsets, meta, perm, inv, gu, dn, dn_of_gu, ready, hq, hs, d, p, spare, ctl, total;
+  size_t counts, offsets, meta, perm, inv, gu, dn, dn_of_gu, ready, hq, hs, d, p, spare, ctl, xcd, total;
   int ks, hs_ld;
 };
 
@@ -4447,6 +4528,7 @@ LayoutMx make_layout_mx(const megamoe_desc& d) {
   L.p = take(L.ks > 1 ? L.ks * T * K * H * sizeof(float) : 0);
   L.spare = take(16 * (H > I ? H : I) / 2);
   L.ctl = take(kCtlInts * sizeof(int));  // the single-launch kernel's control words
+  L.xcd = take(kXcdInts * sizeof(int));  // the batch kernel's per-XCD queues
   L.total = at;
   return L;
 }
@@ -4474,6 +4556,7 @@ void fill_expert_mx_args(const megamoe_desc& d, const LayoutMx& L, const megamoe
   da.ebase = (int)base;
   ea.dn_of_gu = po.dn_of_gu;
   ea.ready = po.ready;
+  ea.xcd = po.xcd;
 }
 
 int forward_mx_impl(const megamoe_desc* desc, float limit, const megamoe_mx_tensors* t, hipStream_t st,
@@ -4504,11 +4587,13 @@ int forward_mx_impl(const megamoe_desc* desc, float limit, const megamoe_mx_tens
                 (int*)(ws + L.inv),    (int4*)(ws + L.gu),     (int4*)(ws + L.dn),  (int*)(ws + L.dn_of_gu),
                 (int*)(ws + L.ready)};
   // Batch mode (k_experts_mx_batch) when the rows per expert average kBatchMinRows or more:
-  // chunks of up to 64 rows, down units of 256 rows, no wide units.
+  // chunks of up to 64 rows, down units of 256 rows, no wide units; the lists in expert
+  // order and the units claimed from per-XCD queues.
   const bool batch = (int64_t)T * K >= (int64_t)kBatchMinRows * E && (H / kMxStageK) % 2 == 0 &&
                      (I / kMxStageK / L.ks) % 2 == 0;
+  if (batch) po.xcd = (int*)(ws + L.xcd);
   if ((rc = launch_permute(t->topk_idx, base, T, K, E, 0, nbI, batch ? nbH / 2 : nbH, L.ks,
-                           batch ? kBatchRows : kChunkRowsMx, batch ? 0 : 1, po, st)))
+                           batch ? kBatchRows : kChunkRowsMx, batch ? 2 : 1, po, st)))
     return rc;
   if (mark(1) != hipSuccess) return MEGAMOE_ERR_HIP;
 
