@@ -219,3 +219,47 @@ def test_worst_case_received_rows():
         got = whole.cpu()[sel]
         assert metrics.layer_checks(got, want)["pass"], e
         assert metrics.band(want, got, exact, bf16_rtol=case.bf16_rtol, noise_factor=case.noise_factor)["pass"], e
+
+
+def test_batch_share_on_few_experts_equals_small_calls():
+    """Batch mode (k_experts_mx_batch: 3072 rows for 128 local experts, H 2048, I 512, no K
+    split) with the rows on 3 experts (1800, 900 and 372 rows: chunk groups of 29, 15 and 6),
+    so 4 of the 8 per-XCD ranges of its work list are empty and their workgroups take units
+    from other XCDs' queues. Each row's result depends only on the row and its expert, so the
+    call equals the same rows worked in calls of 32 (decode units), bit for bit, and sampled
+    experts are within the layer's bars of the oracle."""
+    local, H, I = 128, 2048, 512
+    per_expert = {3: 1800, 60: 900, 127: 372}
+    R = sum(per_expert.values())
+    case = replace(EPCASE, id="ep-few", params=dict(tokens=R, experts=local, topk=1, hidden=H, intermediate=I))
+    _log(f"ep batch on few experts: {R} rows over {len(per_expert)} of {local} experts")
+    serial = replace(case, gpus=1, ep=1)
+    gpu = workloads.make_mx_inputs(serial, 91, DEV)
+    ids = torch.cat([torch.full((n,), e, dtype=torch.int64) for e, n in per_expert.items()])
+    ids = ids[torch.randperm(R, generator=torch.Generator().manual_seed(3))]
+    rows, scales = gpu["x"], gpu["x_scales"]
+    wts = gpu["topk_weights"][:, 0].contiguous()
+    experts = EP.Experts(*(gpu[k] for k in WEIGHTS), 0, case.swiglu_limit)
+    ids_d = ids.to(DEV)
+    from torch.profiler import ProfilerActivity, profile
+
+    with profile(activities=[ProfilerActivity.CPU, ProfilerActivity.CUDA]) as prof:
+        whole = experts(rows, scales, ids_d, wts)
+        torch.cuda.synchronize()
+    kernels = [e.name for e in prof.events() if e.device_type == torch.autograd.DeviceType.CUDA]
+    assert any("k_experts_mx_batch" in k for k in kernels), kernels
+    parts = torch.cat([experts(rows[i:i + 32], scales[i:i + 32], ids_d[i:i + 32], wts[i:i + 32])
+                       for i in range(0, R, 32)])
+    torch.cuda.synchronize()
+    assert torch.isfinite(whole.float()).all()
+    assert torch.equal(whole, parts)
+    x, xs, w0 = gpu["x"].cpu(), gpu["x_scales"].cpu(), gpu["topk_weights"][:, 0].cpu()
+    for e in per_expert:
+        sel = (ids == e).nonzero().flatten()[:64]
+        weights = {k: gpu[k][e:e + 1].cpu() for k in WEIGHTS}
+        args = (x[sel].view(torch.uint8), xs[sel], ids[sel], w0[sel])
+        want = OE.experts(case, weights, *args, base=e)
+        exact = OE.experts(case, weights, *args, base=e, widen=True)
+        got = whole.cpu()[sel]
+        assert metrics.layer_checks(got, want)["pass"], e
+        assert metrics.band(want, got, exact, bf16_rtol=case.bf16_rtol, noise_factor=case.noise_factor)["pass"], e

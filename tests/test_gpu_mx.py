@@ -104,19 +104,32 @@ def test_mx_full_size_on_every_token():
     _log(f"  {case.id}: {check} band_rel={band['relative_error']:.3e}")
 
 
+def _kernels_of(call):
+    """call()'s result and the names of the device kernels it ran."""
+    from torch.profiler import ProfilerActivity, profile
+
+    with profile(activities=[ProfilerActivity.CPU, ProfilerActivity.CUDA]) as prof:
+        out = call()
+        torch.cuda.synchronize()
+    return out, [e.name for e in prof.events() if e.device_type == torch.autograd.DeviceType.CUDA]
+
+
 def test_rows_do_not_depend_on_the_kernel_mode():
     """A row's result depends only on the row and its expert: the same 8 tokens give the same
     bits in a call of 8 tokens (decode units, 16 rows per expert at most) and as the first 8
-    of 200 tokens (100 rows per expert on average: batch units, chunks of 64 rows)."""
+    of 200 tokens (100 rows per expert on average: batch units, chunks of 64 rows, the
+    per-XCD queues). I = 4096 so both calls split the down units into 8 K parts of 2 stages
+    (batch mode needs an even stage count per part)."""
     base = C.case(MXCASE)
-    small = C.development(base, tokens=8, experts=4, topk=2, hidden=512, intermediate=512)
-    large = C.development(base, tokens=200, experts=4, topk=2, hidden=512, intermediate=512)
+    small = C.development(base, tokens=8, experts=4, topk=2, hidden=512, intermediate=4096)
+    large = C.development(base, tokens=200, experts=4, topk=2, hidden=512, intermediate=4096)
     _log("mx mode independence")
     values = workloads.make_inputs(large, 31, "cpu")
     head = {k: (v[:8] if k in ("x", "x_scales", "topk_idx", "topk_weights") else v) for k, v in values.items()}
-    y_small = submission.build(small.to_dict())(_to(head, DEV))["y"]
-    y_large = submission.build(large.to_dict())(_to(values, DEV))["y"]
-    torch.cuda.synchronize()
+    y_small, small_kernels = _kernels_of(lambda: submission.build(small.to_dict())(_to(head, DEV))["y"])
+    y_large, large_kernels = _kernels_of(lambda: submission.build(large.to_dict())(_to(values, DEV))["y"])
+    assert any("k_experts_mx_batch" in k for k in large_kernels), large_kernels
+    assert not any("k_experts_mx_batch" in k for k in small_kernels), small_kernels
     assert torch.equal(y_small, y_large[:8])
     want, exact = mx.reference(large, values)["y"], mx.oracle(large, values)["y"]
     _check(large, y_large.cpu(), want, exact)
