@@ -1056,7 +1056,8 @@ __device__ __forceinline__ int chunk_class(int rows) { return rows > 32 ? 0 : (r
 template <bool CO>
 __device__ __forceinline__ void permute_block(const int64_t* __restrict__ ids, int64_t base, int T, int K, int E,
                                               int S, int nbI, int nbH, int ks, int chunk, int wide,
-                                              const PermuteOut& out, int* smem, int* flags, int tile_waves = 0) {
+                                              const PermuteOut& out, int* smem, int* flags, int tile_waves = 0,
+                                              bool prefix = false) {
   int* bad = flags;
   int* hits = flags + 1;
   unsigned long long* tmp = (unsigned long long*)smem;  // 16
@@ -1230,6 +1231,31 @@ __device__ __forceinline__ void permute_block(const int64_t* __restrict__ ids, i
     for (int i = tid; i < (S * (s4 + s2 + s1) + t4 + t2 + t1) * nbI; i += nt) store_out<CO>(&out.pairs[i], 0);
   __syncthreads();
   if (!tile_waves) {
+    // With `prefix` (long rows: the stream-ordered permute of many rows), each expert's row
+    // first gets the exclusive popcount prefix of its words (E * words more ints after the
+    // bitmap; one wavefront a row, a scan over its lanes), so a rank is one prefix and one
+    // masked popcount instead of a walk over up to T/32 words.
+    const unsigned* pre = bm + E * words;
+    if (!CO && prefix) {
+      unsigned* pw = bm + E * words;
+      const int lane = tid & 63, nw = nt >> 6;
+      for (int r = tid >> 6; r < E; r += nw) {
+        int carry = 0;
+        for (int q0 = 0; q0 < words; q0 += 64) {
+          const int q = q0 + lane;
+          const int v = q < words ? __popc(bm[r * words + q]) : 0;
+          int incl = v;
+#pragma unroll
+          for (int o = 1; o < 64; o <<= 1) {
+            const int y = __shfl_up(incl, o);
+            if (lane >= o) incl += y;
+          }
+          if (q < words) pw[r * words + q] = (unsigned)(carry + incl - v);
+          carry += __shfl(incl, 63);
+        }
+      }
+      __syncthreads();
+    }
     for (int i = tid, j = 0; i < n; i += nt, ++j) {
       int e = 0;
 #pragma unroll
@@ -1239,7 +1265,10 @@ __device__ __forceinline__ void permute_block(const int64_t* __restrict__ ids, i
       const int t = i / K;
       const unsigned* row = bm + e * words;
       int rank = __popc(row[t >> 5] & ((1u << (t & 31)) - 1u));
-      for (int q = 0; q < (t >> 5); ++q) rank += __popc(row[q]);
+      if (!CO && prefix)
+        rank += (int)pre[e * words + (t >> 5)];
+      else
+        for (int q = 0; q < (t >> 5); ++q) rank += __popc(row[q]);
       const int pos = cnt[e] + rank;
       store_out<CO>(&out.perm[pos], i);
       store_out<CO>(&out.inv[i], pos);
@@ -1297,10 +1326,10 @@ constexpr int kPermuteLdsInts = 16384;  // 64 KB
 
 __global__ __launch_bounds__(1024) void k_permute(const int64_t* __restrict__ ids, int64_t base, int T, int K, int E,
                                                   int S, int nbI, int nbH, int ks, int chunk, int wide,
-                                                  PermuteOut out, int tile_waves) {
+                                                  PermuteOut out, int tile_waves, int prefix) {
   extern __shared__ int smem[];
   __shared__ int flags[2];
-  permute_block<false>(ids, base, T, K, E, S, nbI, nbH, ks, chunk, wide, out, smem, flags, tile_waves);
+  permute_block<false>(ids, base, T, K, E, S, nbI, nbH, ks, chunk, wide, out, smem, flags, tile_waves, prefix != 0);
 }
 
 // Launches k_permute with the LDS its form needs.
@@ -1308,9 +1337,13 @@ int launch_permute(const int64_t* ids, int64_t base, int T, int K, int E, int S,
                    int wide, const PermuteOut& po, hipStream_t st) {
   const int tw = permute_tile_waves(T, E, 1024, kPermuteLdsInts);
   if (tw < 0) return MEGAMOE_ERR_UNSUPPORTED;
-  const size_t ints = tw ? 32 + (size_t)E * (1 + tw) : 32 + (size_t)E * (1 + (T + 31) / 32);
+  // The bitmap form ranks from popcount prefixes when its rows are long (8 words or more)
+  // and the prefixes fit beside the bitmap.
+  const size_t words = ((size_t)T + 31) / 32;
+  const bool prefix = !tw && words >= 8 && 32 + (size_t)E * (1 + 2 * words) <= (size_t)kPermuteLdsInts;
+  const size_t ints = tw ? 32 + (size_t)E * (1 + tw) : 32 + (size_t)E * (1 + (prefix ? 2 : 1) * words);
   hipLaunchKernelGGL(k_permute, dim3(1), dim3(1024), ints * 4, st, ids, base, T, K, E, S, nbI, nbH, ks, chunk, wide,
-                     po, tw);
+                     po, tw, prefix ? 1 : 0);
   return hipGetLastError() == hipSuccess ? MEGAMOE_OK : MEGAMOE_ERR_HIP;
 }
 
