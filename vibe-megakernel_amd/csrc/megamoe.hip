@@ -1037,6 +1037,24 @@ __device__ __forceinline__ int chunk_class(int rows) { return rows > 32 ? 0 : (r
 // (bits 16 up), so the batch kernel can hand out a weight block's units for every chunk of
 // the expert one after another.
 
+// Part `part` of `parts` of the 128-byte lines of three matrices of `bytes` each (a multiple
+// of 128), touched by a workgroup of NT threads: one 4-byte load per line, the values folded
+// and kept by an empty asm, so the lines land in the caches for a later reader.
+template <int NT>
+__device__ __forceinline__ void touch_lines(const uint8_t* m0, const uint8_t* m1, const uint8_t* m2, size_t bytes,
+                                            int part, int parts) {
+  const size_t per_mat = bytes / 128, lines = 3 * per_mat, per = (lines + parts - 1) / parts;
+  const size_t l0 = (size_t)part * per, l1 = l0 + per < lines ? l0 + per : lines;
+  int acc = 0;
+#pragma unroll 4
+  for (size_t l = l0 + threadIdx.x; l < l1; l += NT) {
+    const size_t m = l / per_mat, o = (l % per_mat) * 128;
+    const uint8_t* base = m == 0 ? m0 : (m == 1 ? m1 : m2);
+    acc ^= *reinterpret_cast<const int*>(base + o);
+  }
+  asm volatile("" ::"v"(acc));
+}
+
 // The permute by one workgroup of any size (a multiple of 64, at least 256): thread i owns
 // the contiguous experts [i*ept, i*ept + ept) (ept = ceil(E / threads)), so the scan over
 // threads runs in expert order. Every output goes out as a device-coherent store: the
@@ -1326,15 +1344,29 @@ constexpr int kPermuteLdsInts = 16384;  // 64 KB
 
 __global__ __launch_bounds__(1024) void k_permute(const int64_t* __restrict__ ids, int64_t base, int T, int K, int E,
                                                   int S, int nbI, int nbH, int ks, int chunk, int wide,
-                                                  PermuteOut out, int tile_waves, int prefix) {
+                                                  PermuteOut out, int tile_waves, int prefix,
+                                                  const uint8_t* t0, const uint8_t* t1, const uint8_t* t2,
+                                                  size_t tbytes) {
   extern __shared__ int smem[];
   __shared__ int flags[2];
+  if (blockIdx.x > 0) {
+    // The workgroups after the first touch the three matrices' lines (the shared expert's
+    // weights, which the expert kernel's first units read) while the permute runs.
+    touch_lines<1024>(t0, t1, t2, tbytes, (int)blockIdx.x - 1, (int)gridDim.x - 1);
+    return;
+  }
   permute_block<false>(ids, base, T, K, E, S, nbI, nbH, ks, chunk, wide, out, smem, flags, tile_waves, prefix != 0);
 }
 
-// Launches k_permute with the LDS its form needs.
+// Workgroups of k_permute that touch the lines of three matrices while the permute runs.
+constexpr int kTouchGroups = 128;
+
+// Launches k_permute with the LDS its form needs; with `touch` (three matrices of tbytes
+// each), kTouchGroups more workgroups pull their lines into the caches meanwhile (the fp8
+// form's shared expert: the stream-ordered expert kernel's first units read them).
 int launch_permute(const int64_t* ids, int64_t base, int T, int K, int E, int S, int nbI, int nbH, int ks, int chunk,
-                   int wide, const PermuteOut& po, hipStream_t st) {
+                   int wide, const PermuteOut& po, hipStream_t st, const uint8_t* const* touch = nullptr,
+                   size_t tbytes = 0) {
   const int tw = permute_tile_waves(T, E, 1024, kPermuteLdsInts);
   if (tw < 0) return MEGAMOE_ERR_UNSUPPORTED;
   // The bitmap form ranks from popcount prefixes when its rows are long (8 words or more)
@@ -1342,8 +1374,10 @@ int launch_permute(const int64_t* ids, int64_t base, int T, int K, int E, int S,
   const size_t words = ((size_t)T + 31) / 32;
   const bool prefix = !tw && words >= 8 && 32 + (size_t)E * (1 + 2 * words) <= (size_t)kPermuteLdsInts;
   const size_t ints = tw ? 32 + (size_t)E * (1 + tw) : 32 + (size_t)E * (1 + (prefix ? 2 : 1) * words);
-  hipLaunchKernelGGL(k_permute, dim3(1), dim3(1024), ints * 4, st, ids, base, T, K, E, S, nbI, nbH, ks, chunk, wide,
-                     po, tw, prefix ? 1 : 0);
+  const bool touching = touch && tbytes > 0;
+  hipLaunchKernelGGL(k_permute, dim3(touching ? 1 + kTouchGroups : 1), dim3(1024), ints * 4, st, ids, base, T, K, E,
+                     S, nbI, nbH, ks, chunk, wide, po, tw, prefix ? 1 : 0, touching ? touch[0] : nullptr,
+                     touching ? touch[1] : nullptr, touching ? touch[2] : nullptr, touching ? tbytes : (size_t)0);
   return hipGetLastError() == hipSuccess ? MEGAMOE_OK : MEGAMOE_ERR_HIP;
 }
 
@@ -2644,17 +2678,7 @@ __device__ __forceinline__ void layer_combine(const LayerArgs& a, int c, const S
 // caches (the memory-side cache above all: the lines come from every XCD) instead of HBM.
 // Measured (A/B, four runs each): DeepSeek-V3 -2.8 us, GLM-5.3-Flash -6.6, Kimi-K2 -4.3.
 __device__ __forceinline__ void touch_shared_weights(const ExpertArgs& ex, int part, int parts) {
-  const size_t mat = (size_t)ex.gu.S * ex.gu.I * ex.gu.H, per_mat = mat / 128;  // lines of each matrix
-  const size_t lines = 3 * per_mat, per = (lines + parts - 1) / parts;
-  const size_t l0 = (size_t)part * per, l1 = l0 + per < lines ? l0 + per : lines;
-  int acc = 0;
-#pragma unroll 4
-  for (size_t l = l0 + threadIdx.x; l < l1; l += 256) {
-    const size_t m = l / per_mat, o = (l % per_mat) * 128;
-    const uint8_t* base = m == 0 ? ex.gu.sgate : (m == 1 ? ex.gu.sup : ex.dn.sdown);
-    acc ^= *reinterpret_cast<const int*>(base + o);
-  }
-  asm volatile("" ::"v"(acc));
+  touch_lines<256>(ex.gu.sgate, ex.gu.sup, ex.dn.sdown, (size_t)ex.gu.S * ex.gu.I * ex.gu.H, part, parts);
 }
 
 template <bool SPLIT>
@@ -4394,7 +4418,10 @@ int forward_impl(const megamoe_desc* desc, const megamoe_tensors* t, hipStream_t
 
   const PermuteOut po = make_permute_out(L, ws);
   const int nbI = I / kBlock, nbH = H / kBlock;
-  if ((rc = launch_permute(t->expert_ids, 0, T, K, E, S, nbI, nbH, L.ks, kChunkRows, 0, po, st))) return rc;
+  const uint8_t* shared_w[3] = {t->shared_gate, t->shared_up, t->shared_down};
+  if ((rc = launch_permute(t->expert_ids, 0, T, K, E, S, nbI, nbH, L.ks, kChunkRows, 0, po, st, S > 0 ? shared_w : nullptr,
+                           (size_t)S * I * H)))
+    return rc;
   if (mark(3) != hipSuccess) return MEGAMOE_ERR_HIP;
 
   ExpertArgs ea;
