@@ -149,10 +149,29 @@ def cpu_threads() -> int:
     return min(n, int(env)) if env.isdigit() and int(env) > 0 else n
 
 
-def cpu_baseline(case, values_gpu, hit: int, budget_s: float) -> dict:
+def parity_of(case, got: dict, want: dict, rows: list[int]) -> dict:
+    """The timed call's outputs on ``rows`` against the CPU oracle's (BF16 schedule) on the
+    same inputs: expert ids equal, y within max|y - y_ref| / max|y_ref| <= 1e-2 and cosine
+    >= 0.9999 (the layer's bars)."""
+    from oracle import metrics
+
+    y = got["y"][rows].cpu()
+    check = metrics.layer_checks(y, want["y"])
+    out = {"tokens": len(rows), "max_rel": check["max_rel"], "cosine": check["cosine"]}
+    ok = check["pass"]
+    if "expert_ids" in want and "expert_ids" in got:
+        same = int((got["expert_ids"][rows].cpu() == want["expert_ids"]).all(dim=1).sum())
+        out["tokens_with_equal_ids"] = same
+        ok = ok and same == len(rows)
+    out["ok"] = bool(ok)
+    return out
+
+
+def cpu_baseline(case, values_gpu, hit: int, budget_s: float, got: dict | None = None) -> dict:
     """The CPU oracle (BF16 schedule) on the first tokens of the same inputs, scaled by
     distinct experts computed (the oracle's cost is dominated by dequantizing each hit
-    expert once)."""
+    expert once). With ``got`` (the GPU outputs of a timed call on these inputs), the oracle's
+    outputs on those tokens check them: the result's "parity" entry."""
     import torch
 
     from oracle import layer, mx
@@ -177,37 +196,81 @@ def cpu_baseline(case, values_gpu, hit: int, budget_s: float) -> dict:
         sample *= 2
     s = case.shared_experts
     scale = (hit + s) / max(sampled + s, 1)
+    parity = None if got is None else parity_of(case, got, out, rows)
     return {"value": dt * scale * 1e6, "unit": "us/step", "cores": threads, "kind": "port",
-            "cpu_model": cpu_model(),
+            "cpu_model": cpu_model(), "parity": parity,
             "sample": (f"oracle.{reference.__module__.split('.')[-1]}.{reference.__name__} on tokens 0..{sample - 1} of the timed inputs "
                        f"({sampled} distinct experts{' + shared' if s else ''}, {dt:.2f} s), scaled by "
                        f"{hit + s}/{sampled + s} experts; torch {torch.__version__} CPU, {threads} threads, "
                        f"{cpu_model()}")}
 
 
+def _p95(values: list[float]) -> float:
+    """The 95th percentile with linear interpolation, as megabench/harness/benchmark.py:41-45."""
+    ordered = sorted(values)
+    at = (len(ordered) - 1) * 0.95
+    lo = int(at)
+    return ordered[lo] + (ordered[min(lo + 1, len(ordered) - 1)] - ordered[lo]) * (at - lo)
+
+
+def measure_like_harness(fn, inputs: dict, warmup: int, reps: int) -> dict:
+    """The reference harness's timing method (megabench/harness/benchmark.py:13-52): the same
+    inputs every call; a device synchronization before each rep; the host clock and a pair
+    of device events around each call, the end event waited on. So the host's cost of issuing
+    the call (the Python of run(), the C ABI, the launch) counts in both figures, as it does
+    when the harness grades a submission. Microseconds."""
+    import torch
+
+    for _ in range(warmup):
+        fn(inputs)
+    torch.cuda.synchronize()
+    host, event = [], []
+    for _ in range(reps):
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        t0 = time.perf_counter()
+        fn(inputs)
+        e1.record()
+        e1.synchronize()
+        event.append(e0.elapsed_time(e1) * 1e3)
+        host.append((time.perf_counter() - t0) * 1e6)
+    return {"method": "megabench/harness/benchmark.py:_measure (sync before each rep, same inputs)",
+            "reps": reps, "host_p50_us": statistics.median(host), "host_p95_us": _p95(host),
+            "event_p50_us": statistics.median(event), "event_p95_us": _p95(event)}
+
+
 def _time_layer(layer, sets, steps: int, warmup: int, outs: list | None = None) -> dict:
-    """K calls back to back between two device events (the value), K calls each between
-    its own pair (p50, p95), and K calls in which the library records events at its stage
-    boundaries on the stream its kernels run on (per-stage means)."""
+    """K calls back to back between two device events (the value; also the host's issue time
+    per call of that loop), K calls each between its own pair (p50, p95), and K calls in
+    which the library records events at its stage boundaries on the stream its kernels run
+    on (per-stage means). ``outs`` receives the outputs of the last timed call on each set."""
     import torch
 
     dev = torch.device("cuda:0")
     n_sets = len(sets)
     # Warmup runs straight into the timed region: a host round trip between them leaves the
     # device idle for a few ms, which measurably slows the first timed calls.
-    for i in range(max(warmup, n_sets)):
-        o = layer(sets[i % n_sets])
-        if outs is not None and i < n_sets:
-            outs.append(o)
+    for i in range(warmup):
+        layer(sets[i % n_sets])
     stream = torch.cuda.current_stream(dev)
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    last = [None] * n_sets
     torch.cuda.synchronize()
     start.record(stream)
+    t0 = time.perf_counter()
     for i in range(steps):
-        layer(sets[i % n_sets])
+        last[i % n_sets] = layer(sets[i % n_sets])
+    issue_us = (time.perf_counter() - t0) / steps * 1e6
     end.record(stream)
     torch.cuda.synchronize()
     ms = start.elapsed_time(end) / steps
+    for i in range(n_sets):  # sets the timed loop did not reach (steps < sets)
+        if last[i] is None:
+            last[i] = layer(sets[i])
+    if outs is not None:
+        outs.extend(last)
+    del last
     per_step = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
     for i, (e0, e1) in enumerate(per_step):
         e0.record(stream)
@@ -228,7 +291,7 @@ def _time_layer(layer, sets, steps: int, warmup: int, outs: list | None = None) 
     stage_ms = [statistics.mean(s_[j] for s_ in stage) for j in range(nev - 1)]
     return {"ms": ms, "p50_us": statistics.median(step_ms) * 1e3,
             "p95_us": sorted(step_ms)[min(len(step_ms) - 1, int(0.95 * (len(step_ms) - 1) + 0.5))] * 1e3,
-            "stage_us": {name: v * 1e3 for name, v in zip(layer.stages, stage_ms)}}
+            "stage_us": {name: v * 1e3 for name, v in zip(layer.stages, stage_ms)}, "host_issue_us": issue_us}
 
 
 def bench_case(case, steps: int, warmup: int, want_cpu: bool, cpu_budget: float) -> dict:
@@ -253,7 +316,9 @@ def bench_case(case, steps: int, warmup: int, want_cpu: bool, cpu_budget: float)
         hit = statistics.mean(len(torch.unique(v["topk_idx"])) for v in sets)
     else:
         hit = statistics.mean(len(torch.unique(o["expert_ids"])) for o in outs[:n_sets])
+    got0 = {k: v.cpu() for k, v in outs[0].items()}  # the last timed call on sets[0]
     del outs
+    harness = measure_like_harness(layer, sets[0], warmup=2, reps=steps)
 
     bytes_step = C.algorithmic_bytes(case, 0) + (C.algorithmic_bytes(case, 1) - C.algorithmic_bytes(case, 0)) * hit
     ms = r["ms"]
@@ -264,7 +329,7 @@ def bench_case(case, steps: int, warmup: int, want_cpu: bool, cpu_budget: float)
         "hbm_frac": bytes_step / (ms * 1e-3) / PEAK_HBM,
         "mfma_frac": C.algorithmic_flops(case) / (ms * 1e-3) / PEAK_FP8,
         "launches_per_step": case.max_gpu_launches,
-        "stage_us": r["stage_us"],
+        "stage_us": r["stage_us"], "host_issue_us": r["host_issue_us"], "harness": harness,
         "rotation_sets": n_sets,
         "dtype": ("e2m1xe4m3->fp32 (E8M0 scales per 32; bf16 out)" if case.format == "mxfp4"
                   else "e4m3xe4m3->fp32 (bf16 in/out)"),
@@ -301,16 +366,22 @@ def bench_case(case, steps: int, warmup: int, want_cpu: bool, cpu_budget: float)
                               "kernel": mx_kernel(case.tokens * case.topk, case.experts),
                               "kernel_us": ex_ms * 1e3, "bytes_per_launch": ex_bytes}
     if want_cpu:
-        _log(f"[bench] {case.id}: CPU oracle baseline")
-        result["cpu_baseline"] = cpu_baseline(case, sets[0], round(hit), cpu_budget)
+        _log(f"[bench] {case.id}: CPU oracle baseline and parity of the timed outputs")
+        base = cpu_baseline(case, sets[0], round(hit), cpu_budget, got0)
+        result["parity"] = base.pop("parity")
+        result["parity_ok"] = result["parity"]["ok"]
+        result["cpu_baseline"] = base
     del sets
     torch.cuda.empty_cache()
     return result
 
 
-def cpu_baseline_ep(case, experts_cpu: dict, received: dict, hit: int, budget_s: float) -> dict:
+def cpu_baseline_ep(case, experts_cpu: dict, received: dict, hit: int, budget_s: float,
+                    got_rows=None) -> dict:
     """The CPU oracle of the local experts (oracle.ep.experts, BF16 schedule) on the rows of
-    the first local experts, doubling until the budget, scaled by the hit local experts."""
+    the first local experts, doubling until the budget, scaled by the hit local experts.
+    With ``got_rows`` (the timed steps' local-expert output rows), the oracle's rows check
+    them: the result's "parity" entry."""
     import torch
 
     from oracle import ep as OE
@@ -322,15 +393,22 @@ def cpu_baseline_ep(case, experts_cpu: dict, received: dict, hit: int, budget_s:
     while True:
         sel = (ids < n).nonzero().flatten()
         t0 = time.perf_counter()
-        OE.experts(case, {k: v[:n] for k, v in experts_cpu.items()}, received["rows"][sel],
-                   received["row_scales"][sel], ids[sel], received["weights"][sel], 0)
+        want = OE.experts(case, {k: v[:n] for k, v in experts_cpu.items()}, received["rows"][sel],
+                          received["row_scales"][sel], ids[sel], received["weights"][sel], 0)
         dt = time.perf_counter() - t0
         sampled = len(set(ids[sel].tolist()))
         if dt * 2 > budget_s or n * 2 > case.experts // case.ep:
             break
         n *= 2
+    parity = None
+    if got_rows is not None:
+        from oracle import metrics
+
+        check = metrics.layer_checks(got_rows[sel], want)
+        parity = {"rows": int(sel.numel()), "local_experts": n, "max_rel": check["max_rel"],
+                  "cosine": check["cosine"], "ok": bool(check["pass"])}
     return {"value": dt * hit / max(sampled, 1) * 1e6, "unit": "us/step", "cores": threads, "kind": "port",
-            "cpu_model": cpu_model(),
+            "cpu_model": cpu_model(), "parity": parity,
             "sample": (f"oracle.ep.experts on the received rows of local experts 0..{n - 1} ({sampled} hit, "
                        f"{sel.numel()} rows, {dt:.2f} s), scaled by {hit}/{sampled} experts; dispatch and combine "
                        f"not included; torch {torch.__version__} CPU, {threads} threads, {cpu_model()}")}
@@ -425,6 +503,7 @@ def bench_ep_share(case, steps: int, warmup: int, want_cpu: bool, cpu_budget: fl
     stage_ms = [statistics.mean(st[j] for st in stage) for j in range(6)]
     # row[1] is recorded after the dispatch and row[2] by the library before its permute
     stage_ms = [stage_ms[0] + stage_ms[1]] + stage_ms[2:]
+    harness = measure_like_harness(lambda _: step(), {}, warmup=2, reps=steps)
     hit = len(torch.unique(received["ids"]))
     bytes_step = C.algorithmic_bytes(case, hit)
     rows_case = dataclasses.replace(case, gpus=1, ep=1, params=dict(case.params, tokens=R, topk=1, experts=local))
@@ -438,7 +517,7 @@ def bench_ep_share(case, steps: int, warmup: int, want_cpu: bool, cpu_budget: fl
         "hit_experts": hit, "bytes_per_step": bytes_step,
         "tb_per_s": bytes_step / (ms * 1e-3) / 1e12, "hbm_frac": bytes_step / (ms * 1e-3) / PEAK_HBM,
         "mfma_frac": 2 * R * 3 * case.intermediate * H / (ms * 1e-3) / PEAK_FP8,
-        "stage_us": {name: x * 1e3 for name, x in zip(names, stage_ms)},
+        "stage_us": {name: x * 1e3 for name, x in zip(names, stage_ms)}, "harness": harness,
         "rotation_sets": 1, "received_rows": R, "sent_rows": T * K,
         "roofline": {"bound": "hbm", "achieved": ex_bytes / (ex_ms * 1e-3) / 1e9, "peak": PEAK_HBM / 1e9,
                      "unit": "GB/s", "frac": ex_bytes / (ex_ms * 1e-3) / PEAK_HBM,
@@ -447,9 +526,12 @@ def bench_ep_share(case, steps: int, warmup: int, want_cpu: bool, cpu_budget: fl
         "dtype": "e2m1xe4m3->fp32 (E8M0 scales per 32; bf16 out)",
     }
     if want_cpu:
-        _log(f"[bench] {case.id}: CPU oracle baseline")
-        result["cpu_baseline"] = cpu_baseline_ep(case, {k: v[k].cpu() for k in weights},
-                                                 {k: x.cpu() for k, x in received.items()}, hit, cpu_budget)
+        _log(f"[bench] {case.id}: CPU oracle baseline and parity of the timed outputs")
+        base = cpu_baseline_ep(case, {k: v[k].cpu() for k in weights}, {k: x.cpu() for k, x in received.items()},
+                               hit, cpu_budget, out.cpu())
+        result["parity"] = base.pop("parity")
+        result["parity_ok"] = result["parity"]["ok"]
+        result["cpu_baseline"] = base
     del v, received
     torch.cuda.empty_cache()
     return result
@@ -459,7 +541,7 @@ def _config_entry(r: dict) -> dict:
     """One config's record under "configs": time, bandwidth, roofline and CPU baseline."""
     keep = ("us_per_step", "p50_us", "p95_us", "tb_per_s", "hbm_frac", "mfma_frac", "hit_experts", "bytes_per_step",
             "launches_per_step", "stage_us", "rotation_sets", "roofline", "stream_ordered", "cpu_baseline", "dtype",
-            "received_rows", "sent_rows")
+            "received_rows", "sent_rows", "host_issue_us", "harness", "parity", "parity_ok")
     return {k: r[k] for k in keep if k in r}
 
 
@@ -470,7 +552,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--case", default=None, help="measure this case only (its line alone)")
     ap.add_argument("--all", action="store_true",
-                    help="also measure the other forms (block, MXFP4, EP share, epilogue variants)")
+                    help="also measure the other forms (block, MXFP4, EP share, epilogue variants, the headline "
+                         "shape with UE8M0 scales and without the router bias)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU oracle work per config")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
@@ -499,7 +582,7 @@ def main() -> int:
         # The five BASELINE.json configs always; the other forms with --all.
         others = [c for c in C.CASES if c.id != head.id]
         if args.all:
-            others += C.BLOCK_CASES + C.MX_CASES + C.EP_CASES + C.VARIANT_CASES
+            others += C.BLOCK_CASES + C.MX_CASES + C.EP_CASES + C.VARIANT_CASES + C.HEADLINE_VARIANTS
     run = bench_ep_share if head.ep > 1 else bench_case
     r = run(head, args.steps, args.warmup, not args.no_cpu_baseline, args.cpu_budget)
     # Each other config runs in a child process of its own, on a fresh device heap: after a
@@ -538,9 +621,16 @@ def main() -> int:
         "mfma_frac": r["mfma_frac"],
         "roofline": r["roofline"],
         "cpu_baseline": r.get("cpu_baseline"),
+        "harness": r.get("harness"), "host_issue_us": r.get("host_issue_us"),
+        "parity_ok": r.get("parity_ok"), "parity": r.get("parity"),
         "configs": {cid: _config_entry(v) for cid, v in results.items()},
     }
     print(json.dumps(line), flush=True)
+    # A config whose timed outputs fail the oracle check fails the run (after the line).
+    failed = [cid for cid, v in results.items() if v.get("parity_ok") is False]
+    if failed:
+        print(f"bench.py: timed outputs differ from the oracle on {failed}", file=sys.stderr)
+        return 1
     return 0
 
 

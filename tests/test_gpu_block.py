@@ -67,6 +67,7 @@ def _compare(case, got, want, exact, rows=None):
 def _dev_block_cases():
     out = [C.development(c) for c in C.BLOCK_CASES]
     out.append(C.development(C.BLOCK_CASES[0], tokens=37))
+    out.append(C.development(C.BLOCK_CASES[0], tokens=13))  # the dense schedule (T <= 16, T*K >= E)
     return out
 
 

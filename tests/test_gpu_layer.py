@@ -38,9 +38,21 @@ def _dev_cases():
     out.append(C.development(C.case("moe-fp8-kimi-k2-t128"), tokens=70, experts=8, topk=4))  # hot experts > 16 rows
     # Rows of 32 K blocks and few gate/up blocks: the expert kernel works gate and up of each
     # block as separate units (with and without a shared expert).
-    out.append(C.development(C.case("moe-fp8-mixtral-t16"), hidden=4096, intermediate=512))
+    out.append(C.development(C.case("moe-fp8-mixtral-t16"), hidden=4096, intermediate=512, tokens=40))
     out.append(C.development(C.case(C.HEADLINE), hidden=4096, tokens=40))
+    out += dense_cases()
     return out
+
+
+def dense_cases():
+    """Geometries of the dense schedule (T <= 16, T*K >= E: every expert's units over all
+    tokens, started before the routing): the shared expert with grouped sigmoid routing, a
+    Zipf bias that leaves most experts unpicked (their units skipped), and one token per
+    expert slot exactly (T*K = E). Tiny and Mixtral take it too; the block form's test has
+    a dense geometry of its own."""
+    return [C.development(C.case(C.HEADLINE), tokens=8),
+            C.development(C.case("moe-fp8-kimi-k2-t128"), tokens=5, experts=16, topk=4),
+            C.development(C.case("moe-fp8-qwen3-30b-a3b-t32"), tokens=2, experts=16, topk=8)]
 
 
 def _to(values, device):
@@ -156,6 +168,12 @@ def test_full_size_layer_on_every_token(cid):
     cpu = {k: v.cpu() for k, v in values.items()}
     del values
     torch.cuda.empty_cache()
+    check_every_token(case, got, cpu)
+
+
+def check_every_token(case, got, cpu):
+    """ids, weights and y of every token of a full-size call against the oracle."""
+    cid = case.id
     # Routing of every token. The kernel's logits are correctly rounded (fp64 accumulation),
     # so its ids must equal the routing of the exact logits, and its weights that routing's
     # within W_RTOL. The reference's logits come from an fp32 GEMV (frontier.py:343), whose

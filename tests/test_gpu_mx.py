@@ -169,15 +169,26 @@ def test_mx_one_call_is_one_kernel_launch():
     assert case.max_gpu_launches == 1
 
 
-def test_mx_single_launch_reports_bad_ids():
+def _bad_ids_cases():
+    base = C.case(MXCASE)
+    # The decode geometry runs k_layer_mx; the batch-shaped one (100 rows per expert, an even
+    # stage count per down part) makes megamoe_mx_layer_forward launch the stream-ordered
+    # kernels, which must leave the outcome in the same status word.
+    return [C.development(base, tokens=8),
+            C.development(base, tokens=200, experts=4, topk=2, hidden=512, intermediate=4096)]
+
+
+@pytest.mark.parametrize("case", _bad_ids_cases(), ids=lambda c: f"T{c.tokens}-E{c.experts}")
+def test_mx_single_launch_reports_bad_ids(case):
     """Bad ids make y NaN and the status word say so; the next good call clears it."""
-    case = C.development(C.case(MXCASE), tokens=8)
+    _log(f"mx single launch bad ids {case.id} T={case.tokens} E={case.experts}")
     layer = submission.MoELayer(case)
     values = workloads.make_inputs(case, 6, "cpu")
     ids = values["topk_idx"].clone()
     ids[3, 1] = case.experts
-    y = layer(_to({**values, "topk_idx": ids}, DEV))["y"]
-    torch.cuda.synchronize()
+    y, kernels = _kernels_of(lambda: layer(_to({**values, "topk_idx": ids}, DEV))["y"])
+    batch = case.tokens * case.topk >= 24 * case.experts
+    assert any(("k_experts_mx_batch" if batch else "k_layer_mx") in k for k in kernels), kernels
     assert torch.isnan(y.float()).all()
     assert layer.gave_up(torch.device(DEV))
     y2 = layer(_to(values, DEV))["y"]

@@ -15,6 +15,7 @@ import sys
 import pytest
 import torch
 
+from test_gpu_layer import dense_cases
 from vibe_megakernel_amd import cases as C
 from vibe_megakernel_amd import submission, workloads
 
@@ -41,7 +42,8 @@ def _dev_cases():
     out += [C.development(c) for c in C.CASES[1:]]
     out.append(C.development(C.case(C.HEADLINE), tokens=37))
     out.append(C.development(C.case("moe-fp8-kimi-k2-t128"), tokens=70, experts=8, topk=4))
-    out.append(C.development(C.case("moe-fp8-mixtral-t16"), hidden=4096, intermediate=512))  # split gate/up
+    out.append(C.development(C.case("moe-fp8-mixtral-t16"), hidden=4096, intermediate=512, tokens=40))  # split gate/up
+    out += dense_cases() + [C.development(C.BLOCK_CASES[0], tokens=13)]
     out += [C.development(c) for c in C.BLOCK_CASES]
     out += [C.development(c) for c in C.VARIANT_CASES]
     return out

@@ -54,9 +54,12 @@ def resource_report(stderr: str) -> dict:
     return out
 
 
-def build_library(verbose: bool = False) -> Path:
-    tmp = OUTPUT.with_suffix(".so.tmp")
-    cmd = [HIPCC, *FLAGS, f"-I{REPO / 'include'}", str(SOURCE), "-o", str(tmp)]
+def build_library(verbose: bool = False, defines: tuple[str, ...] = (), output: Path | None = None) -> Path:
+    """Builds the library (``output``: another path, for a check build with ``defines``, e.g.
+    ``MEGAMOE_AGENT_ACQUIRE=1``; its resource report is not kept)."""
+    out = OUTPUT if output is None else Path(output)
+    tmp = out.with_suffix(".so.tmp")
+    cmd = [HIPCC, *FLAGS, *[f"-D{d}" for d in defines], f"-I{REPO / 'include'}", str(SOURCE), "-o", str(tmp)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{proc.stderr}")
@@ -66,10 +69,17 @@ def build_library(verbose: bool = False) -> Path:
     report = resource_report(proc.stderr)
     if not report:
         raise RuntimeError("hipcc printed no kernel resource report")
-    REPORT.write_text(json.dumps(report, indent=1, sort_keys=True) + "\n")
-    os.replace(tmp, OUTPUT)
-    return OUTPUT
+    if output is None:
+        REPORT.write_text(json.dumps(report, indent=1, sort_keys=True) + "\n")
+    os.replace(tmp, out)
+    return out
 
 
 if __name__ == "__main__":
-    print(build_library(verbose=True))
+    import argparse
+
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("-D", dest="defines", action="append", default=[], help="a macro for hipcc, NAME=VALUE")
+    ap.add_argument("-o", dest="output", default=None, help="library path (default: the in-tree libmegamoe.so)")
+    args = ap.parse_args()
+    print(build_library(verbose=True, defines=tuple(args.defines), output=args.output))

@@ -254,8 +254,23 @@ VARIANT_CASES: tuple[Case, ...] = (
 )
 
 
+# Two variants of the headline shape. "-ue8m0": the DeepSeek family's power-of-two scales
+# (UE8M0, "scale_fmt": "ue8m0" in model_specs.json:187), the weights' and the activations'
+# alike (frontier.py:120,252 pass power=True to fp8_matrix and linear; quantization.py:57-59).
+# "-nobias": the routing without the N(0, 0.1) correction bias. With the bias, the sigmoid
+# squeezes the top scores together and the bias decides most selections, so 64 tokens hit
+# only ~120 of the 256 experts (the headline's timing inputs: 120); without it ~222 are hit,
+# ~2.3 rows each, the uniform-routing expectation that the per-config floors assume.
+HEADLINE_VARIANTS: tuple[Case, ...] = (
+    replace(next(c for c in CASES if c.id == HEADLINE), id=HEADLINE + "-ue8m0", power_of_two=True,
+            note="power-of-two (UE8M0) weight and activation scales"),
+    replace(next(c for c in CASES if c.id == HEADLINE), id=HEADLINE + "-nobias", bias="none",
+            note="no correction bias: ~222 experts hit, ~2.3 rows each"),
+)
+
+
 def case(case_id: str) -> Case:
-    for c in CASES + BLOCK_CASES + MX_CASES + EP_CASES + VARIANT_CASES:
+    for c in CASES + BLOCK_CASES + MX_CASES + EP_CASES + VARIANT_CASES + HEADLINE_VARIANTS:
         if c.id == case_id:
             return c
     raise KeyError(case_id)

@@ -999,6 +999,7 @@ struct PermuteOut {
   int* pairs;    // [gate/up chunks * nbI] zeroed here (NULL: none), counted by the expert kernel
   int ready_stride = 1;  // ints between two chunks' counters
   int* xcd = nullptr;    // the batch form's per-XCD queues (kXcdInts; NULL: none)
+  int ready_min = 0;     // readiness counters zeroed at least (the dense schedule's down chunks)
 };
 
 // The batch form's work split over the XCDs (the lists in expert order, `wide` 2): XCD x
@@ -1243,7 +1244,7 @@ __device__ __forceinline__ void permute_block(const int64_t* __restrict__ ids, i
     store_out<CO>(&out.meta[kMetaQueueDN], 0);
     store_out<CO>(&out.meta[kMetaError], 0);
   }
-  const int dtot = s4 + s2 + s1 + t4 + t2 + t1;
+  const int dtot = max(s4 + s2 + s1 + t4 + t2 + t1, out.ready_min);
   for (int i = tid; i < dtot; i += nt) store_out<CO>(&out.ready[(size_t)i * out.ready_stride], 0);
   if (out.pairs)
     for (int i = tid; i < (S * (s4 + s2 + s1) + t4 + t2 + t1) * nbI; i += nt) store_out<CO>(&out.pairs[i], 0);
@@ -1522,6 +1523,22 @@ struct ReadyWait {
   int max_naps = 2;             // patient waits: naps of ~1000 cycles between polls, doubling up to this
 };
 
+// The acquire that ends a wait for data another workgroup of the same launch wrote. Workgroup
+// scope: the data is written through to memory and no workgroup reads one of its lines before
+// the line's last write, so no cache holds a stale copy; an agent-scope acquire would add a
+// cache invalidation per wait, hundreds of waits per call while other workgroups stream
+// through the same L2s. A build with MEGAMOE_AGENT_ACQUIRE=1 takes agent scope instead: a
+// check build, in which the bit-exactness tests of the single launch must pass unchanged.
+#ifndef MEGAMOE_AGENT_ACQUIRE
+#define MEGAMOE_AGENT_ACQUIRE 0
+#endif
+__device__ __forceinline__ void acquire_after_wait() {
+  if constexpr (MEGAMOE_AGENT_ACQUIRE)
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  else
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
 // Thread 0 polls the count (bounded in time), then the workgroup passes a barrier. The barrier
 // carries no release fence (this workgroup publishes nothing here, and a release would
 // wait for the weight loads in flight); the acquire fence after it keeps the loads that
@@ -1549,7 +1566,7 @@ __device__ __forceinline__ void wait_ready(const ReadyWait& w) {
     }
   }
   __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  acquire_after_wait();
 }
 
 
@@ -1793,11 +1810,43 @@ struct ChunkRows {
   int row0;
   const int* perm;
   int K;
+  int by_token;  // 0: the unit's h and d rows are row0 + r (grouped); 1: out_base + row r's token
+  int out_base;  // (the dense schedule: expert e's rows e*T + t)
 };
 
+// Row r's token: perm[row0 + r] / K (grouped rows), else row0 + r.
 __device__ __forceinline__ int row_token(const ChunkRows& cr, int r) {
   return cr.perm ? cr.perm[cr.row0 + r] / cr.K : cr.row0 + r;
 }
+
+// The row of the unit's h and d where row r goes.
+__device__ __forceinline__ int out_row(const ChunkRows& cr, int r) {
+  return cr.by_token ? cr.out_base + row_token(cr, r) : cr.row0 + r;
+}
+
+// The dense schedule (the host's dense_experts): lists of every expert's gate/up and down
+// units, known before the routing is. Gate/up chunk c: the shared expert's copies first
+// (c < S, its block offset c * nbI), then routed expert c - S; down chunk c: the shared
+// expert first (if any), then the routed experts. Routed expert e's h and d rows are rows
+// e*T + t of the routed rows, t the token. A unit that starts before the routing is known
+// works every token (dense_rows); one that starts after works the expert's routed rows
+// (routed_rows), or nothing if no token picked the expert. Each row's values are the same
+// either way: every MFMA output column depends only on its own row.
+__device__ __forceinline__ int4 dense_gu_chunk(int c, int E, int S, int T, int nbI) {
+  return c < S ? make_int4(E, 0, T, c * nbI) : make_int4(c - S, 0, T, 0);
+}
+__device__ __forceinline__ int4 dense_dn_chunk(int c, int E, int S, int T) {
+  const int sh = S > 0 ? 1 : 0;
+  return c < sh ? make_int4(E, 0, T, 0) : make_int4(c - sh, 0, T, 0);
+}
+__device__ __forceinline__ ChunkRows dense_rows(int e, int T, int K) { return ChunkRows{T, 0, nullptr, K, 1, e * T}; }
+__device__ __forceinline__ ChunkRows routed_rows(int e, int T, int K, const int* offsets, const int* perm) {
+  const int o = offsets[e];
+  return ChunkRows{offsets[e + 1] - o, o, perm, K, 1, e * T};
+}
+// The down chunk a dense gate/up chunk feeds, and the gate/up units a dense down chunk needs.
+__device__ __forceinline__ int dense_dn_of_gu(int c, int S) { return c < S ? 0 : c - S + (S > 0 ? 1 : 0); }
+__device__ __forceinline__ int dense_dn_need(int c, int S, int nbI) { return S > 0 && c == 0 ? S * nbI : nbI; }
 
 
 struct GateUpArgs {
@@ -1818,6 +1867,7 @@ struct GateUpArgs {
   int T, H, I, K, S, E, pow2;
   int swiglu;                   // 0: fp32 product rounded once; 1: bf16 silu, bf16 product
   float limit;                  // > 0: SwiGLU clamp (gate above, up both sides)
+  int dense;                    // the dense schedule: units from dense_gu_chunk, h rows e*T + t
 };
 
 // One gate/up unit: rows [jb*128, jb*128+128) of gate and of up against the chunk's
@@ -1827,7 +1877,7 @@ struct GateUpArgs {
 template <int NCT>
 __device__ __forceinline__ void gateup_unit(const GateUpArgs& a, const uint8_t* wg, const uint8_t* wu, const float* sg,
                             const float* su, const ChunkRows& cr, int jb, uint8_t* hq, float* hs, int ldh,
-                            int rot, float (*red)[64], uint8_t* ring) {
+                            int rot, float (*red)[64], uint8_t* ring, const ReadyWait& ready) {
   const int lane = opaque_lane(), w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int kofs = 16 * (lane >> 4);
   const int H = a.H, nkb = H / kBlock, nbh = scale_ld(ldh / kBlock);
@@ -1842,15 +1892,17 @@ __device__ __forceinline__ void gateup_unit(const GateUpArgs& a, const uint8_t* 
   }
   op.sw[0] = sg;
   op.sw[1] = su;
+  int orow[NCT];  // the h row of each column (a padding column's is never stored)
 #pragma unroll
   for (int c = 0; c < NCT; ++c) {
     const int r = min(16 * c + (lane & 15), cr.n - 1);  // padding columns repeat a valid row
     const int tok = row_token(cr, r);
     op.b[c] = a.xq + (size_t)tok * H + kofs;
     op.sx[c] = a.xs + (size_t)tok * nkb;
+    orow[c] = cr.by_token ? cr.out_base + tok : cr.row0 + r;
   }
   f32x4 acc[4][NCT];
-  stream_gemm<4, NCT, 2, 2>(op, nkb, rot, ring, acc);
+  stream_gemm<4, NCT, 2, 2>(op, nkb, rot, ring, acc, ready);
 
   // g, u = bf16 (frontier.py:184-186), clamped at the SwiGLU limit if one is set
   // (glm53.py:175); h = bf16(silu(fp32 g) * fp32 u) (frontier.py:337, DeepSeek) or
@@ -1882,23 +1934,29 @@ __device__ __forceinline__ void gateup_unit(const GateUpArgs& a, const uint8_t* 
     const float amax = fmaxf(fmaxf(red[0][col], red[1][col]), fmaxf(red[2][col], red[3][col]));
     const float s = act_scale(amax, a.pow2);
     if (col < cr.n) {
-      uint8_t* dst = hq + (size_t)(cr.row0 + col) * ldh + (size_t)jb * kBlock + 32 * w + 4 * (lane >> 4);
+      uint8_t* dst = hq + (size_t)orow[c] * ldh + (size_t)jb * kBlock + 32 * w + 4 * (lane >> 4);
 #pragma unroll
       for (int p = 0; p < 2; ++p) {
         const uint32_t packed = e4m3x4(clamp448(hv[c][p][0] / s), clamp448(hv[c][p][1] / s),
                                        clamp448(hv[c][p][2] / s), clamp448(hv[c][p][3] / s));
         store_coherent(reinterpret_cast<uint32_t*>(dst + 16 * p), packed);
       }
-      if (w == 0 && lane < 16) store_coherent(hs + (size_t)(cr.row0 + col) * nbh + jb, s);
+      if (w == 0 && lane < 16) store_coherent(hs + (size_t)orow[c] * nbh + jb, s);
     }
   }
 }
 
-// Gate/up unit u of the work list: chunk u / nbI, 128-row block u % nbI of the chunk's
-// expert (plus the slice offset of a shared-expert copy).
-__device__ __forceinline__ void gateup_work(const GateUpArgs& a, int u, float (*red)[64], uint8_t* ring) {
+// Gate/up unit u of the work list (of the dense schedule's lists): chunk u / nbI, 128-row
+// block u % nbI of the chunk's expert (plus the slice offset of a shared-expert copy).
+// `ready`: a count to wait for before the activation rows are read (the quantized x of the
+// single launch's dense schedule), after the unit's first weight stages are requested.
+// In the dense schedule, `known`: the routing is known (the unit works its expert's routed
+// rows; else every token).
+__device__ __forceinline__ void gateup_work(const GateUpArgs& a, int u, float (*red)[64], uint8_t* ring,
+                                            const ReadyWait& ready = ReadyWait{nullptr, 0, nullptr},
+                                            bool known = true) {
   const int nbI = a.I / kBlock, nkb = a.H / kBlock;
-  const int4 ch = a.chunks[u / nbI];
+  const int4 ch = a.dense ? dense_gu_chunk(u / nbI, a.E, a.S, a.T, nbI) : a.chunks[u / nbI];
   const int j = u % nbI, jb = ch.w + j;
   const int rot = u % nkb;  // concurrent units start at different K blocks
   const uint8_t *wg, *wu;
@@ -1922,17 +1980,18 @@ __device__ __forceinline__ void gateup_work(const GateUpArgs& a, int u, float (*
     wu = a.up + rowblk * kBlock * a.H;
     sg = a.gate_scale + rowblk * nkb;
     su = a.up_scale + rowblk * nkb;
-    cr = ChunkRows{ch.z, a.offsets[ch.x] + ch.y, a.perm, a.K};
+    cr = !a.dense ? ChunkRows{ch.z, a.offsets[ch.x] + ch.y, a.perm, a.K}
+                  : (known ? routed_rows(ch.x, a.T, a.K, a.offsets, a.perm) : dense_rows(ch.x, a.T, a.K));
     hq = a.hq_r;
     hs = a.hs_r;
     ldh = a.I;
   }
   if (cr.n <= 16)
-    gateup_unit<1>(a, wg, wu, sg, su, cr, jb, hq, hs, ldh, rot, red, ring);
+    gateup_unit<1>(a, wg, wu, sg, su, cr, jb, hq, hs, ldh, rot, red, ring, ready);
   else if (cr.n <= 32)
-    gateup_unit<2>(a, wg, wu, sg, su, cr, jb, hq, hs, ldh, rot, red, ring);
+    gateup_unit<2>(a, wg, wu, sg, su, cr, jb, hq, hs, ldh, rot, red, ring, ready);
   else
-    gateup_unit<4>(a, wg, wu, sg, su, cr, jb, hq, hs, ldh, rot, red, ring);
+    gateup_unit<4>(a, wg, wu, sg, su, cr, jb, hq, hs, ldh, rot, red, ring, ready);
 }
 
 // One half of a gate/up block: rows [jb*128, jb*128+128) of gate (half 0) or of up (half 1)
@@ -2112,6 +2171,8 @@ struct DownArgs {
   float* p_s;     // ks > 1: [ks, T, H]
   const uint8_t* spare;  // 16 rows of the longest weight row, in the workspace
   int T, H, I, K, S, E, ks;
+  int dense;      // the dense schedule: units from dense_dn_chunk, rows e*T + t
+  int rows_r;     // routed rows of d_r and of each part of p_r: T*K, or E*T in the dense schedule
 };
 
 // One down unit: rows [j*128, j*128+128) of a down matrix [H, ldk] against the chunk's
@@ -2131,11 +2192,13 @@ __device__ __forceinline__ void down_unit(const DownArgs& a, const uint8_t* wd, 
   op.lda = ldk;
   op.spare = a.spare;
   op.sw[0] = sd + kb0;
+  int orow[NCT];  // the h (and d) row of each column
 #pragma unroll
   for (int c = 0; c < NCT; ++c) {
     const int r = min(16 * c + (lane & 15), cr.n - 1);
-    op.b[c] = hq + (size_t)(cr.row0 + r) * ldk + (size_t)kb0 * kBlock + kofs;
-    op.sx[c] = hs + (size_t)(cr.row0 + r) * scale_ld(nkb) + kb0;
+    orow[c] = out_row(cr, r);
+    op.b[c] = hq + (size_t)orow[c] * ldk + (size_t)kb0 * kBlock + kofs;
+    op.sx[c] = hs + (size_t)orow[c] * scale_ld(nkb) + kb0;
   }
   f32x4 acc[2][NCT];
   if constexpr (NCT == 4) {
@@ -2145,7 +2208,7 @@ __device__ __forceinline__ void down_unit(const DownArgs& a, const uint8_t* wd, 
     const uint8_t* xrow[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
-      xrow[i] = hq + (size_t)(cr.row0 + min(16 * w + 8 * i + lr, cr.n - 1)) * ldk + (size_t)kb0 * kBlock +
+      xrow[i] = hq + (size_t)out_row(cr, min(16 * w + 8 * i + lr, cr.n - 1)) * ldk + (size_t)kb0 * kBlock +
                 (((lane & 7) ^ lr) << 4);
     stream_gemm_shared(op, xrow, nkbp, rot, ring, acc, ready);
   } else {
@@ -2157,7 +2220,7 @@ __device__ __forceinline__ void down_unit(const DownArgs& a, const uint8_t* wd, 
     if (r < cr.n) {
 #pragma unroll
       for (int p = 0; p < 2; ++p) {
-        const size_t o = (size_t)(cr.row0 + r) * a.H + (size_t)j * kBlock + 32 * w + 16 * p + 4 * (lane >> 4);
+        const size_t o = (size_t)orow[c] * a.H + (size_t)j * kBlock + 32 * w + 16 * p + 4 * (lane >> 4);
         // Device-coherent stores: the combine (a later kernel, or a later unit of the
         // single-launch kernel on another XCD) reads them.
         if (a.ks == 1) {
@@ -2176,15 +2239,18 @@ __device__ __forceinline__ void down_unit(const DownArgs& a, const uint8_t* wd, 
 
 // Down unit v of the work list: chunk v / (nbH*ks), then 128-row block j of the down
 // matrix and K part kp (v % (nbH*ks) = j*ks + kp).
+// In the dense schedule, `known`: the routing is known (the unit works its expert's routed
+// rows; else every token).
 template <bool CO>
-__device__ __forceinline__ void down_work(const DownArgs& a, int v, const ReadyWait& ready, uint8_t* ring) {
+__device__ __forceinline__ void down_work(const DownArgs& a, int v, const ReadyWait& ready, uint8_t* ring,
+                                          bool known = true) {
   const int nbH = a.H / kBlock, nbI = a.I / kBlock;
-  const int4 ch = a.chunks[v / (nbH * a.ks)];
+  const int c = v / (nbH * a.ks);
+  const int4 ch = a.dense ? dense_dn_chunk(c, a.E, a.S, a.T) : a.chunks[c];
   const int rem = v % (nbH * a.ks), j = rem / a.ks, kp = rem % a.ks;
   const int rot = v % (nbI / a.ks);  // concurrent units start at different K blocks
-  const size_t TK = (size_t)a.T * a.K;
   float* pd_s = a.p_s + (size_t)kp * a.T * a.H;
-  float* pd_r = a.p_r + (size_t)kp * TK * a.H;
+  float* pd_r = a.p_r + (size_t)kp * a.rows_r * a.H;
   if (ch.x == a.E) {
     const int ldk = a.S * a.I;
     const ChunkRows cr{ch.z, ch.y, nullptr, a.K};
@@ -2197,7 +2263,9 @@ __device__ __forceinline__ void down_work(const DownArgs& a, int v, const ReadyW
     else
       down_unit<4, CO>(a, wd, sd, ldk, a.hq_s, a.hs_s, cr, j, kp, a.d_s, pd_s, rot, ready, ring);
   } else {
-    const ChunkRows cr{ch.z, a.offsets[ch.x] + ch.y, a.perm, a.K};
+    const ChunkRows cr = !a.dense ? ChunkRows{ch.z, a.offsets[ch.x] + ch.y, a.perm, a.K}
+                                  : (known ? routed_rows(ch.x, a.T, a.K, a.offsets, a.perm)
+                                           : dense_rows(ch.x, a.T, a.K));
     const size_t rowblk = (size_t)ch.x * nbH + j;
     const uint8_t* wd = a.down + rowblk * kBlock * a.I;
     const float* sd = a.down_scale + rowblk * nbI;
@@ -2221,18 +2289,30 @@ struct SlotRows {
   float w[8];
 };
 
-__device__ __forceinline__ void load_slots(const int* __restrict__ inv, const float* __restrict__ wts, int K, int t,
-                                           int s0, SlotRows& r) {
+// Where slot s of token t left its d row: row inv[t*K + s] of the grouped rows, or in the
+// dense schedule (dense_t = T > 0) row ids[t*K + s] * T + t, its expert's row of the token.
+struct SlotMap {
+  const int* inv;
+  const int64_t* ids;
+  int dense_t;
+};
+
+__device__ __forceinline__ void load_slots(const SlotMap& m, const float* __restrict__ wts, int K, int t, int s0,
+                                           SlotRows& r) {
+  if (m.dense_t) {
 #pragma unroll
-  for (int u = 0; u < 8; ++u) {
-    const int s = min(s0 + u, K - 1);  // clamped, unconditional loads
-    r.row[u] = inv[t * K + s];
-    r.w[u] = wts ? wts[t * K + s] : 1.0f;  // no weights: already applied (the MXFP4 form)
+    for (int u = 0; u < 8; ++u) r.row[u] = (int)m.ids[t * K + min(s0 + u, K - 1)] * m.dense_t + t;
+  } else {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) r.row[u] = m.inv[t * K + min(s0 + u, K - 1)];  // clamped, unconditional loads
   }
+#pragma unroll
+  for (int u = 0; u < 8; ++u)
+    r.w[u] = wts ? wts[t * K + min(s0 + u, K - 1)] : 1.0f;  // no weights: already applied (the MXFP4 form)
 }
 
 __device__ __forceinline__ void combine8(const uint16_t* __restrict__ d_r, const uint16_t* __restrict__ d_s,
-                                         const int* __restrict__ inv, const float* __restrict__ wts, int H, int K,
+                                         const SlotMap& inv, const float* __restrict__ wts, int H, int K,
                                          int S, int t, int h0, float (&acc)[8], const SlotRows* first = nullptr) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
@@ -2304,10 +2384,9 @@ __device__ __forceinline__ void sum_parts8(const float* __restrict__ src, size_t
 // The same combine when the down GEMMs were split over ks K parts: d = bf16(sum of the
 // fp32 parts in part order) for every slot row and for the shared row, then as combine8.
 __device__ __forceinline__ void combine8_parts(const float* __restrict__ p_r, const float* __restrict__ p_s, int ks,
-                                               const int* __restrict__ inv, const float* __restrict__ wts, int T,
-                                               int H, int K, int S, int t, int h0, float (&acc)[8],
+                                               const SlotMap& inv, const float* __restrict__ wts, int T,
+                                               int rows_r, int H, int K, int S, int t, int h0, float (&acc)[8],
                                                const SlotRows* first = nullptr) {
-  const size_t TK = (size_t)T * K;
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
   for (int s0 = 0; s0 < K; s0 += 8) {
@@ -2316,11 +2395,14 @@ __device__ __forceinline__ void combine8_parts(const float* __restrict__ p_r, co
       r = *first;
     else
       load_slots(inv, wts, K, t, s0, r);
-    for (int u = 0; u < 8 && s0 + u < K; ++u) {
-      float dv[8];
-      sum_parts8(p_r + (size_t)r.row[u] * H + h0, TK * H, ks, dv);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) acc[i] = __fadd_rn(acc[i], __fmul_rn(dv[i], r.w[u]));
+    for (int u = 0; u < 8; ++u) {
+      if (s0 + u < K) {
+        float dv[8];
+        sum_parts8(p_r + (size_t)r.row[u] * H + h0, (size_t)rows_r * H, ks, dv);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[i] = __fadd_rn(acc[i], __fmul_rn(dv[i], r.w[u]));
+      }
     }
   }
   if (S > 0) {
@@ -2335,7 +2417,7 @@ __device__ __forceinline__ void combine8_parts(const float* __restrict__ p_r, co
 // residual (the block form), y = bf16(residual + bf16(layer output)) (frontier.py:354).
 __global__ __launch_bounds__(256) void k_combine(const uint16_t* __restrict__ d_r, const uint16_t* __restrict__ d_s,
                                                  const float* __restrict__ p_r, const float* __restrict__ p_s, int ks,
-                                                 const int* __restrict__ inv, const float* __restrict__ wts, int T,
+                                                 SlotMap inv, int rows_r, const float* __restrict__ wts, int T,
                                                  int H, int K, int S, const int* __restrict__ meta,
                                                  const uint16_t* __restrict__ residual, uint16_t* __restrict__ y,
                                                  int* __restrict__ status) {
@@ -2349,7 +2431,7 @@ __global__ __launch_bounds__(256) void k_combine(const uint16_t* __restrict__ d_
   const int t = i / per_row, h0 = (i % per_row) * 8;
   float acc[8];
   if (ks > 1)
-    combine8_parts(p_r, p_s, ks, inv, wts, T, H, K, S, t, h0, acc);
+    combine8_parts(p_r, p_s, ks, inv, wts, T, rows_r, H, K, S, t, h0, acc);
   else
     combine8(d_r, d_s, inv, wts, H, K, S, t, h0, acc);
   uint32_t o[4];
@@ -2406,8 +2488,12 @@ __global__ __launch_bounds__(256, 2) void k_experts(ExpertArgs args) {
   __shared__ int slot, flag;
   static_assert(sizeof(ExpertArgs) % 8 == 0, "argument segment layout");
   int* meta = args.gu.meta;
-  const int total_gu = (SPLIT ? 2 : 1) * meta[kMetaUnitsGU];
-  const int total = total_gu + meta[kMetaUnitsDN];
+  // The dense schedule's lists come from the geometry (the permute has run: its counts say
+  // which experts no token picked, and their units are skipped).
+  const bool dense = args.gu.dense != 0;
+  const int nbI0 = args.gu.I / kBlock, sh = args.gu.S > 0 ? 1 : 0;
+  const int total_gu = dense ? (args.gu.S + args.gu.E) * nbI0 : (SPLIT ? 2 : 1) * meta[kMetaUnitsGU];
+  const int total = total_gu + (dense ? (args.gu.E + sh) * (args.dn.H / kBlock) * args.dn.ks : meta[kMetaUnitsDN]);
   // Every unit, the first included, is claimed from the queue: a unit that a down unit
   // waits for is then always held by a running workgroup (one that has not started yet
   // holds nothing), whatever number of workgroups the device keeps resident.
@@ -2433,20 +2519,25 @@ __global__ __launch_bounds__(256, 2) void k_experts(ExpertArgs args) {
     if (threadIdx.x == 0) next = atomicAdd(&meta[kMetaQueueGU], 1);
     if (u < total_gu) {
       bool done = true;
-      if constexpr (SPLIT)
+      if constexpr (SPLIT) {
         done = gateup_work_split(a.gu, u, red, &flag, ring);
-      else
-        gateup_work(a.gu, u, red, ring);
+      } else {
+        const int c = u / nbI;
+        if (!(dense && c >= a.gu.S && a.gu.offsets[c - a.gu.S + 1] == a.gu.offsets[c - a.gu.S]))
+          gateup_work(a.gu, u, red, ring);
+      }
       if (done) {
         publish_fence();
         __syncthreads();
-        if (threadIdx.x == 0) atomicAdd(&a.ready[(size_t)a.dn_of_gu[(SPLIT ? u >> 1 : u) / nbI] * a.ready_stride], 1);
+        const int dc = dense ? dense_dn_of_gu(u / nbI, a.gu.S) : a.dn_of_gu[(SPLIT ? u >> 1 : u) / nbI];
+        if (threadIdx.x == 0) atomicAdd(&a.ready[(size_t)dc * a.ready_stride], 1);
       }
     } else {
-      const int v = u - total_gu, c = v / (nbH * a.dn.ks);
-      const ReadyWait ready{&a.ready[(size_t)c * a.ready_stride], a.dn.chunks[c].x == a.dn.E ? a.dn.S * nbI : nbI,
-                            &meta[kMetaError]};
-      down_work<false>(a.dn, v, ready, ring);
+      const int v = u - total_gu, c = v / (nbH * a.dn.ks), e = c - (a.dn.S > 0 ? 1 : 0);
+      if (!(dense && e >= 0 && a.gu.offsets[e + 1] == a.gu.offsets[e])) {
+        const int need = dense ? dense_dn_need(c, a.dn.S, nbI) : (a.dn.chunks[c].x == a.dn.E ? a.dn.S * nbI : nbI);
+        down_work<false>(a.dn, v, ReadyWait{&a.ready[(size_t)c * a.ready_stride], need, &meta[kMetaError]}, ring);
+      }
     }
     if (threadIdx.x == 0) slot = next;
     __syncthreads();
@@ -2483,12 +2574,13 @@ __global__ __launch_bounds__(256, 2) void k_experts(ExpertArgs args) {
 
 // kCtlStatus is not zeroed: it keeps the last call's outcome (1: a bounded wait gave up and y
 // is NaN) for megamoe_layer_status; the stream-ordered form's combine writes it too.
-constexpr int kCtlQueue = 0, kCtlNormed = 32, kCtlRouted = 64, kCtlSelected = 96, kCtlDown = 160,
+constexpr int kCtlQueue = 0, kCtlNormed = 32, kCtlRouted = 64, kCtlSelected = 96, kCtlQuant = 128, kCtlDown = 160,
               kCtlExited = 192, kCtlError = 224, kCtlStatus = 256;  // one 128-byte line each
 constexpr int kCombineUnit = 256 * 8;  // outputs per combine unit
 
 // Signals: "every norm unit is done", "every router unit is done", "the work lists are
-// written", "every down unit is done". Hundreds of workgroups wait on each at once. Polled
+// written", "every down unit is done", "every row of x is quantized" (the dense schedule's
+// gate/up units wait for it). Hundreds of workgroups wait on each at once. Polled
 // through one word, the waits slowed the workgroups still working by up to 3x (the last
 // DeepSeek-V3 down units took 37-55 us instead of 12-16; measured per unit): every poll is a
 // device-coherent load at the one memory line that holds the word, which every weight stream
@@ -2496,7 +2588,7 @@ constexpr int kCombineUnit = 256 * 8;  // outputs per combine unit
 // which differ in the low and the high address bits that pick a cache and memory channel):
 // the workgroup whose increment completes a count raises all of them, and each waiting
 // workgroup polls the one its index picks.
-constexpr int kSigNormed = 0, kSigRouted = 1, kSigPermuted = 2, kSigDown = 3, kSignals = 4;
+constexpr int kSigNormed = 0, kSigRouted = 1, kSigPermuted = 2, kSigDown = 3, kSigQuant = 4, kSignals = 5;
 constexpr int kSigLines = 16, kSigStride = (4096 + 256) / 4;  // flags per signal; ints between flags
 constexpr int kCtlSig = 512;                                  // the first flag
 // Start flags of the router units that workgroups take by index (LayerArgs::n_first), one
@@ -2530,6 +2622,9 @@ struct LayerArgs {
   int force_timeout;  // test hook: the combine units wait for a flag value never raised, 20 us at most
   int n_first;        // router units [0, n_first) go to the workgroup of the same index (0: none)
   int force_rescue;   // test hook: odd workgroups leave their router unit to the routing units
+  int dense;          // the dense schedule (host: dense_experts); ex.ready then points at counters
+                      // of this kernel's own, zeroed by the last workgroup of each call
+  int n_ready;        // dense: readiness counters to zero at the end (down chunks)
   int pad_;
 };
 
@@ -2609,7 +2704,7 @@ __device__ __forceinline__ bool wait_signal_for(int* ctl, int sig, uint64_t tick
     *lds = came;
   }
   __syncthreads();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  acquire_after_wait();
   const bool came = *lds != 0;
   __syncthreads();
   return came;
@@ -2638,6 +2733,12 @@ __device__ __forceinline__ void layer_select(const LayerArgs& a, int token, uint
                     a.ids, a.wts, token, *reinterpret_cast<SelectLds*>(lds));
 }
 
+// Where the combine finds each slot's d row: the permute's inverse, or in the dense schedule
+// the row of the slot's expert for the token.
+__device__ __forceinline__ SlotMap layer_slots(const LayerArgs& a) {
+  return a.dense ? SlotMap{nullptr, a.ids, a.T} : SlotMap{a.po.inv, nullptr, 0};
+}
+
 // Combine unit c: outputs [c * kCombineUnit, +kCombineUnit) of y, as k_combine (`first`:
 // the thread's first eight slots, loaded already, or NULL).
 __device__ __forceinline__ void layer_combine(const LayerArgs& a, int c, const SlotRows* first = nullptr) {
@@ -2650,10 +2751,11 @@ __device__ __forceinline__ void layer_combine(const LayerArgs& a, int c, const S
   }
   const int t = i / per_row, h0 = (i % per_row) * 8;
   float acc[8];
+  const SlotMap m = layer_slots(a);
   if (a.ks > 1)
-    combine8_parts(dn.p_r, dn.p_s, a.ks, a.po.inv, a.wts, a.T, a.H, a.K, a.S, t, h0, acc, first);
+    combine8_parts(dn.p_r, dn.p_s, a.ks, m, a.wts, a.T, dn.rows_r, a.H, a.K, a.S, t, h0, acc, first);
   else
-    combine8(dn.d_r, dn.d_s, a.po.inv, a.wts, a.H, a.K, a.S, t, h0, acc, first);
+    combine8(dn.d_r, dn.d_s, m, a.wts, a.H, a.K, a.S, t, h0, acc, first);
   uint32_t o[4];
   if (a.residual) {
     const uint4 v = *reinterpret_cast<const uint4*>(a.residual + (size_t)t * a.H + h0);
@@ -2679,6 +2781,25 @@ __device__ __forceinline__ void layer_combine(const LayerArgs& a, int c, const S
 // Measured (A/B, four runs each): DeepSeek-V3 -2.8 us, GLM-5.3-Flash -6.6, Kimi-K2 -4.3.
 __device__ __forceinline__ void touch_shared_weights(const ExpertArgs& ex, int part, int parts) {
   touch_lines<256>(ex.gu.sgate, ex.gu.sup, ex.dn.sdown, (size_t)ex.gu.S * ex.gu.I * ex.gu.H, part, parts);
+}
+
+// In every thread, for a unit of routed expert e in the dense schedule: 0, the routing is not
+// known yet (the permute's signal has not come): the unit works every token; 1, known and some
+// token picked e: the unit works e's routed rows; 2, known and no token picked e: the unit is
+// skipped (no combine reads its rows). Thread 0 decides and the workgroup takes its answer
+// (the units have barriers, so every wavefront must take the same branch).
+__device__ __forceinline__ int dense_state(int* ctl, const int* offsets, int e, int* lds) {
+  if (threadIdx.x == 0) {
+    int st = 0;
+    if (load_count(my_signal_flag(ctl, kSigPermuted)) != 0)
+      st = load_count(&offsets[e + 1]) == load_count(&offsets[e]) ? 2 : 1;
+    *lds = st;
+  }
+  __syncthreads();
+  acquire_after_wait();
+  const int st = *lds;
+  __syncthreads();
+  return st;
 }
 
 template <bool SPLIT>
@@ -2745,9 +2866,12 @@ __global__ __launch_bounds__(256, 2) void k_layer(LayerArgs args) {
       // This token's row of x in E4M3 per 128 (needs nothing else; runs while the router does).
       const int nbh = a.H / kBlock, lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
       const bool back = resume >= 0;  // after a rescued router unit: look again at once
-      if (!back)
+      if (!back) {
         quant_row(a.x + (size_t)t * a.H, a.xq + (size_t)t * a.H, a.xs + (size_t)t * nbh, nbh, a.pow2, lane, wv,
                   reinterpret_cast<float*>(rings));
+        // The dense schedule's gate/up units read every token's row once all are quantized.
+        if (a.dense) publish_count(ctl, kCtlQuant, 1, a.T, kSigQuant, &units[0]);
+      }
       resume = -1;
       bool routed = false;  // the router signal came (and was acquired) in the wait below
       if (n_first) {
@@ -2775,7 +2899,7 @@ __global__ __launch_bounds__(256, 2) void k_layer(LayerArgs args) {
         layer_select<16>(a, t, rings);
       if (publish_count(ctl, kCtlSelected, 1, a.T, -1, &units[0]) == a.T - 1) {
         // Every token is routed: this workgroup runs the permute, then publishes the lists.
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        acquire_after_wait();
         permute_block<true>(a.ids, 0, a.T, a.K, a.E, a.S, a.ex.gu.I / kBlock, a.H / kBlock, a.ks, kChunkRows, 0,
                             a.po, reinterpret_cast<int*>(rings), flags,
                             permute_tile_waves(a.T, a.E, 256, kPermuteLdsInts));
@@ -2801,12 +2925,23 @@ __global__ __launch_bounds__(256, 2) void k_layer(LayerArgs args) {
   // routing units and the permute, the critical path, run: their polls back off to ~3.6 us
   // apart (8 naps) instead of ~0.9 (DeepSeek-V3 -1.7 us, Mixtral -2.2, Qwen3-30B-A3B -0.6,
   // Kimi-K2 0, over two A/B runs; 16 naps measured no better).
-  if (args.ex.gu.S > 0) touch_shared_weights(args.ex, blockIdx.x, gridDim.x);
-  wait_ready(ReadyWait{my_signal_flag(ctl, kSigPermuted), 1, &ctl[kCtlError], kWaitTicks, true, 8});
+  // The dense schedule's lists are known from the geometry: no wait (its units wait for the
+  // quantized x and for each other instead; the combine for the routing).
+  const bool dense = args.dense != 0;
+  if (!dense) {
+    if (args.ex.gu.S > 0) touch_shared_weights(args.ex, blockIdx.x, gridDim.x);
+    wait_ready(ReadyWait{my_signal_flag(ctl, kSigPermuted), 1, &ctl[kCtlError], kWaitTicks, true, 8});
+  }
   if (threadIdx.x == 0) {
-    const bool lists = load_count(my_signal_flag(ctl, kSigPermuted)) != 0;
-    units[0] = lists ? (SPLIT ? 2 : 1) * load_count(&args.po.meta[kMetaUnitsGU]) : 0;
-    units[1] = lists ? load_count(&args.po.meta[kMetaUnitsDN]) : 0;
+    const int nbI = args.ex.gu.I / kBlock, S = args.ex.gu.S, E = args.E;
+    if (dense) {
+      units[0] = (S + E) * nbI;
+      units[1] = (E + (S > 0 ? 1 : 0)) * (args.H / kBlock) * args.ks;
+    } else {
+      const bool lists = load_count(my_signal_flag(ctl, kSigPermuted)) != 0;
+      units[0] = lists ? (SPLIT ? 2 : 1) * load_count(&args.po.meta[kMetaUnitsGU]) : 0;
+      units[1] = lists ? load_count(&args.po.meta[kMetaUnitsDN]) : 0;
+    }
   }
   __syncthreads();
   const int n_gu = units[0], n_dn = units[1];
@@ -2827,20 +2962,35 @@ __global__ __launch_bounds__(256, 2) void k_layer(LayerArgs args) {
     if (u < fixed + n_gu) {
       const int g = u - fixed;
       bool done = true;
-      if constexpr (SPLIT)
+      if constexpr (SPLIT) {
         done = gateup_work_split(a.gu, g, red, &flag, ring);
-      else
+      } else if (dense) {
+        // Every expert's units from the start: before the routing is known a unit works every
+        // token and waits only for the quantized x; after, its expert's routed rows, or
+        // nothing if no token picked the expert.
+        const int c = g / nbI;
+        const int st = c >= a.gu.S ? dense_state(ctl, a.gu.offsets, c - a.gu.S, &flags[0]) : 0;
+        if (st != 2)
+          gateup_work(a.gu, g, red, ring, ReadyWait{my_signal_flag(ctl, kSigQuant), 1, &ctl[kCtlError], kWaitTicks,
+                                                    true, 2}, st == 1);
+      } else {
         gateup_work(a.gu, g, red, ring);
+      }
       if (done) {
         publish_fence();
         __syncthreads();
-        if (threadIdx.x == 0) atomicAdd(&a.ready[(size_t)a.dn_of_gu[(SPLIT ? g >> 1 : g) / nbI] * a.ready_stride], 1);
+        const int dc = dense ? dense_dn_of_gu(g / nbI, a.gu.S) : a.dn_of_gu[(SPLIT ? g >> 1 : g) / nbI];
+        if (threadIdx.x == 0) atomicAdd(&a.ready[(size_t)dc * a.ready_stride], 1);
       }
     } else {
       const int v = u - fixed - n_gu, c = v / (nbH * a.dn.ks);
-      const ReadyWait ready{&a.ready[(size_t)c * a.ready_stride], a.dn.chunks[c].x == a.dn.E ? a.dn.S * nbI : nbI,
-                            &ctl[kCtlError]};
-      down_work<true>(a.dn, v, ready, ring);
+      const int sh = a.dn.S > 0 ? 1 : 0;
+      const int st = dense && c >= sh ? dense_state(ctl, a.gu.offsets, c - sh, &flags[0]) : 0;
+      if (st != 2) {
+        const int need = dense ? dense_dn_need(c, a.dn.S, nbI) : (a.dn.chunks[c].x == a.dn.E ? a.dn.S * nbI : nbI);
+        down_work<true>(a.dn, v, ReadyWait{&a.ready[(size_t)c * a.ready_stride], need, &ctl[kCtlError]}, ring,
+                        st == 1);
+      }
       ++my_down;
     }
     if (threadIdx.x == 0) slot = next;
@@ -2861,11 +3011,13 @@ __global__ __launch_bounds__(256, 2) void k_layer(LayerArgs args) {
     LayerArgs a;
     __builtin_memcpy(&a, (const LayerArgs*)ap, sizeof(a));
     // The first unit's slot rows and weights (written before the lists were published) load
-    // while the down units finish.
+    // while the down units finish. The dense schedule's expert units did not wait for the
+    // routing: the combine does.
+    if (a.dense) wait_signal(ctl, kSigPermuted);
     SlotRows first;
     {
       const int i = (u - experts_end) * (kCombineUnit / 8) + threadIdx.x, per_row = a.H / 8;
-      load_slots(a.po.inv, a.wts, a.K, min(i, a.T * per_row - 1) / per_row, 0, first);
+      load_slots(layer_slots(a), a.wts, a.K, min(i, a.T * per_row - 1) / per_row, 0, first);
     }
     if (n_dn) wait_signal(ctl, kSigDown, 1 + a.force_timeout, a.force_timeout ? (uint64_t)2000 : kWaitTicks);
     bool use_first = true;
@@ -2891,7 +3043,8 @@ __global__ __launch_bounds__(256, 2) void k_layer(LayerArgs args) {
   }
   __syncthreads();
   if (slot) {
-    constexpr int words[] = {kCtlQueue, kCtlNormed, kCtlRouted, kCtlSelected, kCtlDown, kCtlError, kCtlExited};
+    constexpr int words[] = {kCtlQueue, kCtlNormed, kCtlRouted, kCtlSelected, kCtlQuant, kCtlDown, kCtlError,
+                             kCtlExited};
     constexpr int n_words = sizeof(words) / sizeof(words[0]);
     static_assert(n_words + kSignals * kSigLines <= 256, "one store per thread");
     const int i = threadIdx.x;
@@ -2902,6 +3055,9 @@ __global__ __launch_bounds__(256, 2) void k_layer(LayerArgs args) {
                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     for (int b = i; b < n_first; b += 256)
       __hip_atomic_store(&ctl[kCtlStart + b * kStartStride], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int c = i; c < args.n_ready; c += 256)  // the dense schedule's readiness counters
+      __hip_atomic_store(&args.ex.ready[(size_t)c * args.ex.ready_stride], 0, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -3980,9 +4136,10 @@ __device__ __forceinline__ void layer_mx_combine(const LayerMxArgs& a, int c) {
   const int t = i / per_row, h0 = (i % per_row) * 8;
   float acc[8];
   if (a.ks > 1)
-    combine8_parts(dn.pd, nullptr, a.ks, a.po.inv, nullptr, a.T, a.H, a.K, 0, t, h0, acc);
+    combine8_parts(dn.pd, nullptr, a.ks, SlotMap{a.po.inv, nullptr, 0}, nullptr, a.T, a.T * a.K, a.H, a.K, 0, t, h0,
+                   acc);
   else
-    combine8(dn.d, nullptr, a.po.inv, nullptr, a.H, a.K, 0, t, h0, acc);
+    combine8(dn.d, nullptr, SlotMap{a.po.inv, nullptr, 0}, nullptr, a.H, a.K, 0, t, h0, acc);
   uint32_t o[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) o[j] = f32_to_bf16_bits(acc[2 * j]) | (f32_to_bf16_bits(acc[2 * j + 1]) << 16);
@@ -4105,11 +4262,14 @@ constexpr size_t kAlign = 256;
 inline size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
 struct Layout {
-  size_t xn, partial, xq, xs, counts, offsets, meta, perm, inv, gu, dn, dn_of_gu, ready, pairs, hq_r, hs_r, hq_s, hs_s,
-      st_r, st_s, d_r, d_s, p_r, p_s, spare, ctl, total;
+  size_t xn, partial, xq, xs, counts, offsets, meta, perm, inv, gu, dn, dn_of_gu, ready, ready_l, pairs, hq_r, hs_r,
+      hq_s, hs_s, st_r, st_s, d_r, d_s, p_r, p_s, spare, ctl, total;
   int nsplit;
   int ks;  // K parts of each down unit
   int ready_stride;  // ints between two readiness counters
+  int dense;         // dense_experts
+  int rows_r;        // routed rows of h and d: T*K, or E*T in the dense schedule
+  int n_ready_l;     // the single launch's own readiness counters (dense schedule), zeroed per call
 };
 
 // Upper bound of list entries: every hit expert has at most ceil(rows/64) chunks, so the
@@ -4144,7 +4304,25 @@ int down_splits(const megamoe_desc& d) {
 // 231 -> 224 us for the stream-ordered expert kernel, 286 -> 282 us for the single launch),
 // and DeepSeek-V3, Kimi-K2 and Qwen3-30B-A3B measured 3-7% slower split. Depends on the
 // geometry only; both forms give the same bits.
+// Whether the expert units follow the dense schedule: every expert's gate/up and down units
+// over all T tokens, in lists known from the geometry, so they start as soon as x is
+// quantized instead of after the router, the routing and the permute (the single launch's
+// front end: ~30 us with HBM idle), and only the combine waits for the routing. Taken when
+// T <= 16, where any set of an expert's rows is one 16-column MFMA tile (all T tokens cost
+// no more MFMA work or activation reads than the routed rows), and T*K >= E, where every
+// expert can be hit (under uniform routing 1 - (1 - K/E)^T of them are: 99% for the
+// Mixtral shape, 68% for Tiny). An expert the routing leaves unpicked has its units skipped
+// from the moment the routing is known; those started before stream weights no combine
+// reads, which the roofline's algorithmic bytes do not count. Each routed row's bits are the
+// routed schedule's (each MFMA output column depends only on its own row); only the K
+// rotation of a unit, keyed by its place in the lists, differs, and both forms (single
+// launch and stream-ordered) take the same lists. Depends on the geometry only.
+bool dense_experts(const megamoe_desc& d) {
+  return d.tokens <= 16 && (int64_t)d.tokens * d.topk >= d.experts;
+}
+
 bool split_gate_up(const megamoe_desc& d) {
+  if (dense_experts(d)) return false;  // the dense schedule's units are whole blocks
   const size_t hit = (size_t)(d.experts < (int64_t)d.tokens * d.topk ? d.experts : (int64_t)d.tokens * d.topk);
   const size_t units = (hit + (size_t)d.shared_experts) * (size_t)(d.intermediate / kBlock);
   return units < 512 && d.hidden / kBlock >= 32;
@@ -4175,18 +4353,26 @@ Layout make_layout(const megamoe_desc& d) {
   const size_t dn_chunks = max_chunks(d, S > 0 ? 1 : 0);
   L.ready_stride = dn_chunks <= kReadySpreadChunks ? kReadySpread : kReadyLine;
   L.ready = take(dn_chunks * L.ready_stride * sizeof(int));
+  // The dense schedule's down chunks: the routed experts and the shared expert. The single
+  // launch counts them in a region of its own (the stream-ordered form leaves `ready`
+  // counted up, and the permute that zeroes it runs after the single launch's first units).
+  L.dense = dense_experts(d) ? 1 : 0;
+  L.n_ready_l = L.dense ? (int)(E + (S > 0 ? 1 : 0)) : 0;
+  L.ready_l = take((size_t)L.n_ready_l * L.ready_stride * sizeof(int));
   L.pairs = take(max_chunks(d, (int)S) * (I / kBlock) * sizeof(int));
-  L.hq_r = take(T * K * I);
-  L.hs_r = take(T * K * scale_ld((int)(I / kBlock)) * sizeof(float));
+  const size_t R = L.dense ? E * T : T * K;  // routed rows: grouped, or e*T + t
+  L.rows_r = (int)R;
+  L.hq_r = take(R * I);
+  L.hs_r = take(R * scale_ld((int)(I / kBlock)) * sizeof(float));
   L.hq_s = take(T * S * I);
   L.hs_s = take(T * scale_ld((int)(S * I / kBlock)) * sizeof(float));
   const bool split = split_gate_up(d);  // staging of the separate gate and up units
   L.st_r = take(split ? 2 * T * K * I * 2 : 0);
   L.st_s = take(split ? 2 * T * S * I * 2 : 0);
-  L.d_r = take(T * K * H * 2);
+  L.d_r = take(R * H * 2);
   L.d_s = take(T * H * 2);
   L.ks = down_splits(d);
-  L.p_r = take(L.ks > 1 ? L.ks * T * K * H * sizeof(float) : 0);
+  L.p_r = take(L.ks > 1 ? L.ks * R * H * sizeof(float) : 0);
   L.p_s = take(L.ks > 1 && S ? L.ks * T * H * sizeof(float) : 0);
   L.spare = take(16 * (H > I * (S > 1 ? S : 1) ? H : I * (S > 1 ? S : 1)));
   L.ctl = take(kCtlInts * sizeof(int));  // the single-launch kernel's control words
@@ -4220,12 +4406,18 @@ struct DeviceInfo {
   int layer_mx_per_cu = 0;    // resident k_layer_mx workgroups per CU
 };
 
+// The figures of the current device, queried on its first call and kept per device. The
+// mutex covers the fill: two host threads making their first calls at once must not see a
+// half-filled entry (a zero per-CU count would give a launch of no workgroups).
 int device_info(DeviceInfo* out) {
+  static std::mutex mutex;
   static DeviceInfo cache[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return MEGAMOE_ERR_HIP;
+  std::lock_guard<std::mutex> lock(mutex);
   DeviceInfo& di = cache[dev];
   if (di.cus == 0) {
+    DeviceInfo fill;
     int cus = 0, per_cu = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return MEGAMOE_ERR_HIP;
     int per_cu_split = 0;
@@ -4233,23 +4425,24 @@ int device_info(DeviceInfo* out) {
         hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu_split, k_experts<true>, 256, 0) != hipSuccess)
       return MEGAMOE_ERR_HIP;
     per_cu = per_cu_split < per_cu ? per_cu_split : per_cu;
-    di.experts_per_cu = per_cu > 0 ? per_cu : 1;
+    fill.experts_per_cu = per_cu > 0 ? per_cu : 1;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_experts_mx, 256, 0) != hipSuccess)
       return MEGAMOE_ERR_HIP;
-    di.experts_mx_per_cu = per_cu > 0 ? per_cu : 1;
+    fill.experts_mx_per_cu = per_cu > 0 ? per_cu : 1;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_experts_mx_batch, 256, 0) != hipSuccess)
       return MEGAMOE_ERR_HIP;
-    di.batch_mx_per_cu = per_cu > 0 ? per_cu : 1;
+    fill.batch_mx_per_cu = per_cu > 0 ? per_cu : 1;
     int per_cu_split2 = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_layer<false>, 256, 0) != hipSuccess ||
         hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu_split2, k_layer<true>, 256, 0) != hipSuccess)
       return MEGAMOE_ERR_HIP;
     per_cu = per_cu_split2 < per_cu ? per_cu_split2 : per_cu;
-    di.layer_per_cu = per_cu > 0 ? per_cu : 1;
+    fill.layer_per_cu = per_cu > 0 ? per_cu : 1;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_layer_mx, 256, 0) != hipSuccess)
       return MEGAMOE_ERR_HIP;
-    di.layer_mx_per_cu = per_cu > 0 ? per_cu : 1;
-    di.cus = cus > 0 ? cus : 1;
+    fill.layer_mx_per_cu = per_cu > 0 ? per_cu : 1;
+    fill.cus = cus > 0 ? cus : 1;
+    di = fill;
   }
   *out = di;
   return MEGAMOE_OK;
@@ -4333,9 +4526,12 @@ int launch_norm(int rows, int cols, const void* x, const void* w, float eps, int
 }
 
 PermuteOut make_permute_out(const Layout& L, char* ws) {
-  return PermuteOut{(int*)(ws + L.counts), (int*)(ws + L.offsets), (int*)(ws + L.meta), (int*)(ws + L.perm),
-                    (int*)(ws + L.inv),    (int4*)(ws + L.gu),     (int4*)(ws + L.dn),  (int*)(ws + L.dn_of_gu),
-                    (int*)(ws + L.ready),  (int*)(ws + L.pairs), L.ready_stride};
+  PermuteOut po{(int*)(ws + L.counts), (int*)(ws + L.offsets), (int*)(ws + L.meta), (int*)(ws + L.perm),
+                (int*)(ws + L.inv),    (int4*)(ws + L.gu),     (int4*)(ws + L.dn),  (int*)(ws + L.dn_of_gu),
+                (int*)(ws + L.ready),  (int*)(ws + L.pairs), L.ready_stride};
+  // The dense schedule counts every expert's down chunk, hit or not (n_ready_l of them).
+  po.ready_min = L.n_ready_l;
+  return po;
 }
 
 // The expert kernels' arguments for a forward call over workspace `ws`.
@@ -4358,6 +4554,7 @@ void fill_expert_args(const megamoe_desc& d, const Layout& L, const megamoe_tens
   ga.T = T; ga.H = H; ga.I = I; ga.K = K; ga.S = S; ga.E = E; ga.pow2 = d.pow2_scales;
   ga.swiglu = epi ? epi->swiglu : 0;
   ga.limit = epi ? epi->swiglu_limit : 0.0f;
+  ga.dense = L.dense;
   DownArgs& da = ea.dn;
   da.down = t->down; da.down_scale = t->down_scale;
   da.sdown = t->shared_down; da.sdown_scale = t->shared_down_scale;
@@ -4369,9 +4566,18 @@ void fill_expert_args(const megamoe_desc& d, const Layout& L, const megamoe_tens
   da.p_s = (float*)(ws + L.p_s);
   da.ks = L.ks;
   da.T = T; da.H = H; da.I = I; da.K = K; da.S = S; da.E = E;
+  da.dense = L.dense;
+  da.rows_r = L.rows_r;
   ea.dn_of_gu = po.dn_of_gu;
   ea.ready = po.ready;
   ea.ready_stride = po.ready_stride;
+}
+
+// The most gate/up and down units one call's lists can hold (the dense schedule's exactly).
+size_t expert_units_max(const megamoe_desc& d, const Layout& L, bool split) {
+  const size_t nbI = d.intermediate / kBlock, nbH = d.hidden / kBlock, S = d.shared_experts, E = d.experts;
+  if (L.dense) return (S + E) * nbI + (E + (S > 0 ? 1 : 0)) * nbH * L.ks;
+  return (split ? 2 : 1) * max_chunks(d, (int)S) * nbI + max_chunks(d, S > 0 ? 1 : 0) * nbH * L.ks;
 }
 
 // The layer; with `blk`, the block form: RMSNorm of x before the router (the layer then
@@ -4431,8 +4637,7 @@ int forward_impl(const megamoe_desc* desc, const megamoe_tensors* t, hipStream_t
   // As many workgroups as fit on the device at once, and no more than the most units the
   // routing can produce.
   const bool split = split_gate_up(d);
-  const size_t units_max =
-      (split ? 2 : 1) * max_chunks(d, S) * (size_t)nbI + max_chunks(d, S > 0 ? 1 : 0) * (size_t)nbH * L.ks;
+  const size_t units_max = expert_units_max(d, L, split);
   const size_t resident = (size_t)di.cus * di.experts_per_cu;
   const unsigned grid = (unsigned)(units_max < resident ? units_max : resident);
   if (split)
@@ -4443,8 +4648,9 @@ int forward_impl(const megamoe_desc* desc, const megamoe_tensors* t, hipStream_t
   if (mark(4) != hipSuccess) return MEGAMOE_ERR_HIP;
 
   const int rows8 = T * (H / 8);
+  const SlotMap slots = L.dense ? SlotMap{nullptr, t->expert_ids, T} : SlotMap{po.inv, nullptr, 0};
   hipLaunchKernelGGL(k_combine, dim3((rows8 + 255) / 256), dim3(256), 0, st, (const uint16_t*)da.d_r,
-                     (const uint16_t*)da.d_s, (const float*)da.p_r, (const float*)da.p_s, L.ks, (const int*)po.inv,
+                     (const uint16_t*)da.d_s, (const float*)da.p_r, (const float*)da.p_s, L.ks, slots, L.rows_r,
                      (const float*)t->expert_weights, T, H, K, S, (const int*)po.meta,
                      (const uint16_t*)(blk && blk->residual ? t->x : nullptr), (uint16_t*)t->y,
                      (int*)(ws + L.ctl) + kCtlStatus);
@@ -4521,9 +4727,11 @@ int forward_layer_impl(const megamoe_desc* desc, const megamoe_tensors* t, const
   // As many workgroups as fit on the device at once, and no more than the most units the
   // queue can hold.
   const bool split = split_gate_up(d);
-  const size_t units_max = (size_t)la.n_norm + la.n_router + T + (split ? 2 : 1) * max_chunks(d, S) * (size_t)nbI +
-                           max_chunks(d, S > 0 ? 1 : 0) * (size_t)nbH * L.ks +
+  const size_t units_max = (size_t)la.n_norm + la.n_router + T + expert_units_max(d, L, split) +
                            ((size_t)T * H + kCombineUnit - 1) / kCombineUnit;
+  la.dense = L.dense;
+  la.n_ready = L.n_ready_l;
+  if (L.dense) la.ex.ready = (int*)(ws + L.ready_l);
   const size_t resident = (size_t)di.cus * di.layer_per_cu;
   const unsigned grid = (unsigned)(units_max < resident ? units_max : resident);
   // Router units taken by workgroup index: the first round of them, when there are 64 or more
@@ -4546,8 +4754,11 @@ int forward_layer_impl(const megamoe_desc* desc, const megamoe_tensors* t, const
 // -- The MXFP4 form ----------------------------------------------------------------------
 
 // With the output written by the down units (one slot per token, no K split), this stands
-// in for the combine: if the permute flagged bad ids, every element of y is NaN.
-__global__ __launch_bounds__(256) void k_error_fill(const int* __restrict__ meta, size_t n8, uint16_t* __restrict__ y) {
+// in for the combine: if the permute flagged bad ids, every element of y is NaN. `status`
+// (NULL: none) keeps the call's outcome, as k_combine's does.
+__global__ __launch_bounds__(256) void k_error_fill(const int* __restrict__ meta, size_t n8, uint16_t* __restrict__ y,
+                                                    int* __restrict__ status) {
+  if (status && blockIdx.x == 0 && threadIdx.x == 0) *status = meta[kMetaError];
   if (!meta[kMetaError]) return;
   for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n8; i += (size_t)gridDim.x * 256)
     *reinterpret_cast<uint4*>(y + i * 8) = make_uint4(0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u);
@@ -4640,8 +4851,10 @@ void fill_expert_mx_args(const megamoe_desc& d, const LayoutMx& L, const megamoe
   ea.xcd = po.xcd;
 }
 
+// `status` (NULL: none) receives the call's outcome (1: bad expert ids, y is NaN) from the
+// last kernel: the single-launch entry point passes its status word when it falls back here.
 int forward_mx_impl(const megamoe_desc* desc, float limit, const megamoe_mx_tensors* t, hipStream_t st,
-                    hipEvent_t* ev, int64_t base = 0) {
+                    hipEvent_t* ev, int64_t base = 0, int* status = nullptr) {
   int rc = validate_mx(desc);
   if (rc) return rc;
   if (!t || !(limit > 0.0f)) return MEGAMOE_ERR_INVALID_ARGUMENT;
@@ -4701,12 +4914,12 @@ int forward_mx_impl(const megamoe_desc* desc, float limit, const megamoe_mx_tens
   const int rows8 = T * (H / 8);
   if (direct)
     hipLaunchKernelGGL(k_error_fill, dim3((unsigned)((rows8 + 255) / 256 < 1024 ? (rows8 + 255) / 256 : 1024)),
-                       dim3(256), 0, st, (const int*)po.meta, (size_t)rows8, (uint16_t*)t->y);
+                       dim3(256), 0, st, (const int*)po.meta, (size_t)rows8, (uint16_t*)t->y, status);
   else
     hipLaunchKernelGGL(k_combine, dim3((rows8 + 255) / 256), dim3(256), 0, st, (const uint16_t*)da.d,
                        (const uint16_t*)nullptr, (const float*)da.pd, (const float*)nullptr, L.ks,
-                       (const int*)po.inv, (const float*)nullptr, T, H, K, 0, (const int*)po.meta,
-                       (const uint16_t*)nullptr, (uint16_t*)t->y, (int*)nullptr);
+                       SlotMap{po.inv, nullptr, 0}, T * K, (const float*)nullptr, T, H, K, 0, (const int*)po.meta,
+                       (const uint16_t*)nullptr, (uint16_t*)t->y, status);
   MEGAMOE_LAUNCH_CHECK();
   if (mark(3) != hipSuccess) return MEGAMOE_ERR_HIP;
   return MEGAMOE_OK;
@@ -4735,7 +4948,8 @@ int forward_mx_layer_impl(const megamoe_desc* desc, float limit, const megamoe_m
   const int tile_waves = permute_tile_waves(T, E, 256, kPermuteLdsInts);
   if (batch || tile_waves < 0) {  // the stream-ordered kernels, between the caller's two events
     if (mark(0) != hipSuccess) return MEGAMOE_ERR_HIP;
-    if ((rc = forward_mx_impl(desc, limit, t, st, nullptr, base))) return rc;
+    int* status = (int*)((char*)t->workspace + L.ctl) + kCtlStatus;  // megamoe_mx_layer_status reads it
+    if ((rc = forward_mx_impl(desc, limit, t, st, nullptr, base, status))) return rc;
     return mark(1) == hipSuccess ? MEGAMOE_OK : MEGAMOE_ERR_HIP;
   }
   DeviceInfo di;

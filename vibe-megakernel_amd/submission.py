@@ -24,6 +24,7 @@ The fp8 layer and its block and epilogue forms run as ONE kernel launch
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
 
 import torch
@@ -33,6 +34,22 @@ from .cases import Case
 
 _INPUTS = ("x", "router", "router_bias", "gate", "gate_scale", "up", "up_scale", "down", "down_scale",
            "shared_gate", "shared_gate_scale", "shared_up", "shared_up_scale", "shared_down", "shared_down_scale")
+
+
+_RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def _stream_handle(device: torch.device) -> int:
+    """torch's current stream of ``device`` as a HIP stream handle (the raw query skips the
+    Stream object that torch.cuda.current_stream builds on every call)."""
+    if _RAW_STREAM is not None:
+        return _RAW_STREAM(device.index)
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _on(device: torch.device):
+    """A guard making ``device`` current, or none when it is already (the common case)."""
+    return contextlib.nullcontext() if torch.cuda.current_device() == device.index else torch.cuda.device(device)
 
 
 def make_desc(case: Case) -> _lib.Desc:
@@ -72,6 +89,8 @@ class MoELayer:
         self.case = case
         self.lib = _lib.load()
         self.desc = make_desc(case)
+        self._desc_ref = ctypes.byref(self.desc)
+        self._specs = self._input_specs()
         self.mx = case.format == "mxfp4"
         self.single_launch = single_launch
         self.stages = ("layer",) if single_launch else (_lib.STAGES_MX if self.mx else _lib.STAGES)
@@ -84,12 +103,61 @@ class MoELayer:
         # The epilogue variant of the fp8 form: None is the DeepSeek form.
         self.epilogue = (None if self.mx or (case.swiglu == "fp32" and case.swiglu_limit == 0) else
                          _lib.Epilogue(swiglu=int(case.swiglu == "bf16"), swiglu_limit=float(case.swiglu_limit)))
+        self._epi_ref = None if self.epilogue is None else ctypes.byref(self.epilogue)
+        # The pointer fields that come from the inputs, in the C struct's order.
+        self._ptr_names = tuple(n for n in _INPUTS if (n != "router_bias" or case.bias != "none") and
+                                (case.shared_experts or not n.startswith("shared_")))
+
+    def _input_specs(self) -> tuple:
+        """(name, dtype, shape) of every input the case reads, in checking order."""
+        c = self.case
+        T, H, E, K, I, S = c.tokens, c.hidden, c.experts, c.topk, c.intermediate, c.shared_experts
+        u8, f8, f32 = torch.uint8, torch.float8_e4m3fn, torch.float32
+        if c.format == "mxfp4":
+            return (("x", f8, (T, H)), ("x_scales", u8, (T, H // 32)), ("topk_idx", torch.int64, (T, K)),
+                    ("topk_weights", f32, (T, K)), ("l1_blocks", u8, (E, 2 * I, H // 32, 16)),
+                    ("l1_scales", u8, (E, 2 * I, H // 32)), ("l2_blocks", u8, (E, H, I // 32, 16)),
+                    ("l2_scales", u8, (E, H, I // 32)))
+        bh, bi = -(-H // 128), -(-I // 128)
+        specs = [("x", torch.bfloat16, (T, H)), ("router", f32, (E, H))]
+        if c.bias != "none":
+            specs.append(("router_bias", f32, (E,)))
+        if c.norm != "none":
+            specs.append(("ln2", torch.bfloat16, (H,)))
+        specs += [("gate", f8, (E, I, H)), ("gate_scale", f32, (E, bi, bh)), ("up", f8, (E, I, H)),
+                  ("up_scale", f32, (E, bi, bh)), ("down", f8, (E, H, I)), ("down_scale", f32, (E, bh, bi))]
+        if S:
+            bs = -(-(S * I) // 128)
+            specs += [("shared_gate", f8, (S * I, H)), ("shared_gate_scale", f32, (bs, bh)),
+                      ("shared_up", f8, (S * I, H)), ("shared_up_scale", f32, (bs, bh)),
+                      ("shared_down", f8, (H, S * I)), ("shared_down_scale", f32, (bh, bs))]
+        return tuple((name, dtype, torch.Size(shape)) for name, dtype, shape in specs)
+
+    def _check(self, inputs: dict) -> torch.device:
+        """The device of the inputs, after checking every input against the case; raises
+        as _expect does (ValueError, or RuntimeError for inputs off the GPU)."""
+        x = inputs.get("x")
+        if not isinstance(x, torch.Tensor):
+            raise ValueError("inputs must hold 'x'")
+        device = x.device
+        if device.type != "cuda":
+            raise RuntimeError(f"the HIP layer runs on a GPU; inputs are on {device}")
+        Tensor = torch.Tensor
+        for name, dtype, shape in self._specs:
+            t = inputs.get(name)
+            if (not isinstance(t, Tensor) or t.dtype != dtype or t.shape != shape or t.device != device or
+                    not t.is_contiguous()):
+                _expect(t, name, dtype, shape, device)
+        return device
 
     def workspace(self, device: torch.device) -> torch.Tensor:
         """The workspace of calls on torch's current stream of ``device``. Zeroed once when it
         is made: the single-launch kernel needs its control words zero when a call starts and
         leaves them zero when it ends (the other entry points need no initialisation)."""
-        key = (device, torch.cuda.current_stream(device).cuda_stream)
+        return self._workspace_on(device, _stream_handle(device))
+
+    def _workspace_on(self, device: torch.device, stream: int) -> torch.Tensor:
+        key = (device.index, stream)
         ws = self._workspace.get(key)
         if ws is None:
             ws = torch.zeros(self.workspace_bytes, dtype=torch.uint8, device=device)
@@ -97,104 +165,52 @@ class MoELayer:
         return ws
 
     def check_mx_inputs(self, inputs: dict) -> torch.device:
-        c = self.case
-        T, H, E, K, I = c.tokens, c.hidden, c.experts, c.topk, c.intermediate
-        x = inputs.get("x")
-        if not isinstance(x, torch.Tensor):
-            raise ValueError("inputs must hold 'x'")
-        device = x.device
-        if device.type != "cuda":
-            raise RuntimeError(f"the HIP layer runs on a GPU; inputs are on {device}")
-        u8 = torch.uint8
-        _expect(x, "x", torch.float8_e4m3fn, (T, H), device)
-        _expect(inputs.get("x_scales"), "x_scales", u8, (T, H // 32), device)
-        _expect(inputs.get("topk_idx"), "topk_idx", torch.int64, (T, K), device)
-        _expect(inputs.get("topk_weights"), "topk_weights", torch.float32, (T, K), device)
-        _expect(inputs.get("l1_blocks"), "l1_blocks", u8, (E, 2 * I, H // 32, 16), device)
-        _expect(inputs.get("l1_scales"), "l1_scales", u8, (E, 2 * I, H // 32), device)
-        _expect(inputs.get("l2_blocks"), "l2_blocks", u8, (E, H, I // 32, 16), device)
-        _expect(inputs.get("l2_scales"), "l2_scales", u8, (E, H, I // 32), device)
-        return device
+        return self._check(inputs)
 
     def _call_mx(self, inputs: dict, events=None) -> dict:
-        device = self.check_mx_inputs(inputs)
+        device = self._check(inputs)
         c = self.case
         y = torch.empty((c.tokens, c.hidden), dtype=torch.bfloat16, device=device)
-        ws = self.workspace(device)
+        handle = _stream_handle(device)
+        ws = self._workspace_on(device, handle)
         ptr = {name: inputs[name].data_ptr() for name in _lib.MX_TENSOR_FIELDS if name not in ("y", "workspace")}
         tensors = _lib.MxTensors(**ptr, y=y.data_ptr(), workspace=ws.data_ptr(), workspace_bytes=self.workspace_bytes)
-        stream = ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+        stream = ctypes.c_void_p(handle)
         handles = None if events is None else (ctypes.c_void_p * len(events))(*[e.cuda_event for e in events])
         forward = self.lib.megamoe_mx_layer_forward if self.single_launch else self.lib.megamoe_mx_forward
-        with torch.cuda.device(device):
-            _lib.check(forward(ctypes.byref(self.desc), float(c.swiglu_limit), ctypes.byref(tensors), stream, handles),
+        with _on(device):
+            _lib.check(forward(self._desc_ref, float(c.swiglu_limit), ctypes.byref(tensors), stream, handles),
                        f"{c.id}: forward")
         return {"y": y}
 
     def check_inputs(self, inputs: dict) -> torch.device:
-        c = self.case
-        T, H, E, I, S = c.tokens, c.hidden, c.experts, c.intermediate, c.shared_experts
-        x = inputs.get("x")
-        if not isinstance(x, torch.Tensor):
-            raise ValueError("inputs must hold 'x'")
-        device = x.device
-        if device.type != "cuda":
-            raise RuntimeError(f"the HIP layer runs on a GPU; inputs are on {device}")
-        bh, bi = -(-H // 128), -(-I // 128)
-        f8, f32 = torch.float8_e4m3fn, torch.float32
-        _expect(x, "x", torch.bfloat16, (T, H), device)
-        _expect(inputs["router"], "router", f32, (E, H), device)
-        if c.bias != "none":
-            _expect(inputs["router_bias"], "router_bias", f32, (E,), device)
-        if c.norm != "none":
-            _expect(inputs.get("ln2"), "ln2", torch.bfloat16, (H,), device)
-        _expect(inputs["gate"], "gate", f8, (E, I, H), device)
-        _expect(inputs["gate_scale"], "gate_scale", f32, (E, bi, bh), device)
-        _expect(inputs["up"], "up", f8, (E, I, H), device)
-        _expect(inputs["up_scale"], "up_scale", f32, (E, bi, bh), device)
-        _expect(inputs["down"], "down", f8, (E, H, I), device)
-        _expect(inputs["down_scale"], "down_scale", f32, (E, bh, bi), device)
-        if S:
-            bs = -(-(S * I) // 128)
-            _expect(inputs["shared_gate"], "shared_gate", f8, (S * I, H), device)
-            _expect(inputs["shared_gate_scale"], "shared_gate_scale", f32, (bs, bh), device)
-            _expect(inputs["shared_up"], "shared_up", f8, (S * I, H), device)
-            _expect(inputs["shared_up_scale"], "shared_up_scale", f32, (bs, bh), device)
-            _expect(inputs["shared_down"], "shared_down", f8, (H, S * I), device)
-            _expect(inputs["shared_down_scale"], "shared_down_scale", f32, (bh, bs), device)
-        return device
+        return self._check(inputs)
 
     def _call(self, inputs: dict, timed: bool, events=None, noalloc=False):
         if self.mx:
             if timed:
                 raise ValueError("timed() covers the fp8 layer form; use record() for the MXFP4 form")
             return self._call_mx(inputs, events)
-        device = self.check_inputs(inputs)
+        device = self._check(inputs)
         c = self.case
         y = torch.empty((c.tokens, c.hidden), dtype=torch.bfloat16, device=device)
         ids = torch.empty((c.tokens, c.topk), dtype=torch.int64, device=device)
         weights = torch.empty((c.tokens, c.topk), dtype=torch.float32, device=device)
-        ws = None if noalloc else self.workspace(device)
-        ptr = {name: (inputs[name].data_ptr() if name in inputs and (name != "router_bias" or c.bias != "none")
-                      else None) for name in _INPUTS}
-        if not c.shared_experts:
-            for name in _INPUTS:
-                if name.startswith("shared_"):
-                    ptr[name] = None
-        tensors = _lib.Tensors(**ptr, y=y.data_ptr(), expert_ids=ids.data_ptr(),
-                               expert_weights=weights.data_ptr(), workspace=None if ws is None else ws.data_ptr(),
-                               workspace_bytes=0 if ws is None else self.workspace_bytes)
-        stream = ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
-        with torch.cuda.device(device):
+        handle = _stream_handle(device)
+        ws = None if noalloc else self._workspace_on(device, handle)
+        tensors = _lib.Tensors(*[inputs[name].data_ptr() if name in self._ptr_names else None for name in _INPUTS],
+                               y.data_ptr(), ids.data_ptr(), weights.data_ptr(),
+                               None if ws is None else ws.data_ptr(), 0 if ws is None else self.workspace_bytes)
+        stream = ctypes.c_void_p(handle)
+        with _on(device):
             if self.single_launch and not noalloc:
                 blk = None
                 if self.block is not None:
                     blk = ctypes.byref(_lib.Block(norm_weight=inputs["ln2"].data_ptr() if c.norm != "none" else None,
                                                   eps=float(c.norm_eps), weight_in_fp32=int(c.norm == "fp32_weight"),
                                                   residual=int(c.residual)))
-                epi = None if self.epilogue is None else ctypes.byref(self.epilogue)
                 handles = None if events is None else (ctypes.c_void_p * 2)(*[e.cuda_event for e in events])
-                _lib.check(self.lib.megamoe_layer_forward(ctypes.byref(self.desc), ctypes.byref(tensors), blk, epi,
+                _lib.check(self.lib.megamoe_layer_forward(self._desc_ref, ctypes.byref(tensors), blk, self._epi_ref,
                                                           stream, handles), f"{c.id}: forward")
                 return {"y": y, "expert_ids": ids, "expert_weights": weights}
             if noalloc:
