@@ -45,14 +45,15 @@ def _dev_cases():
 
 
 def dense_cases():
-    """Geometries of the dense schedule (T <= 16, T*K >= E: every expert's units over all
-    tokens, started before the routing): the shared expert with grouped sigmoid routing, a
-    Zipf bias that leaves most experts unpicked (their units skipped), and one token per
-    expert slot exactly (T*K = E). Tiny and Mixtral take it too; the block form's test has
-    a dense geometry of its own."""
+    """Geometries of the dense schedule (T <= 16, T*K >= E: every expert's units listed
+    before the routing is known): the shared expert with grouped sigmoid routing, a Zipf bias
+    that leaves most experts unpicked (their units skipped), one token per expert slot
+    exactly (T*K = E), and 64 gate/up blocks per expert. Tiny and Mixtral take it too; the
+    block form's test has a dense geometry of its own."""
     return [C.development(C.case(C.HEADLINE), tokens=8),
             C.development(C.case("moe-fp8-kimi-k2-t128"), tokens=5, experts=16, topk=4),
-            C.development(C.case("moe-fp8-qwen3-30b-a3b-t32"), tokens=2, experts=16, topk=8)]
+            C.development(C.case("moe-fp8-qwen3-30b-a3b-t32"), tokens=2, experts=16, topk=8),
+            C.development(C.case("moe-fp8-mixtral-t16"), intermediate=8192)]
 
 
 def _to(values, device):
