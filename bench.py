@@ -5,7 +5,10 @@
 A step is one call of the layer (router, routing, permute, gate/up + SwiGLU,
 down, combine) on one batch of synthetic inputs already resident in HBM. W
 untimed steps, then K steps bracketed by torch.cuda.synchronize() and device
-events; inputs are generated on the GPU (seed 7301). Steps rotate over as many
+events; inputs are generated on the GPU (seed 7301). Before either form's warmup
+steps the device runs the layer (stream-ordered form) for ~30 ms: after the idle
+of input generation, the first ~20 calls run slower while the device ramps up
+under this load (warm_device). Steps rotate over as many
 independent input sets as it takes to move >= 1 GB per rotation, so the 256 MB
 Infinity Cache cannot hold a step's weights.
 
@@ -149,20 +152,32 @@ def cpu_threads() -> int:
     return min(n, int(env)) if env.isdigit() and int(env) > 0 else n
 
 
-def parity_of(case, got: dict, want: dict, rows: list[int]) -> dict:
-    """The timed call's outputs on ``rows`` against the CPU oracle's (BF16 schedule) on the
-    same inputs: expert ids equal, y within max|y - y_ref| / max|y_ref| <= 1e-2 and cosine
-    >= 0.9999 (the layer's bars)."""
+def parity_of(case, y, want: dict, exact: dict, ids=None) -> dict:
+    """Outputs of a timed call against the CPU oracle on the same inputs, graded as the
+    reference harness grades them: the band rule of megabench/harness/correctness.py:64-85
+    against the FP32 oracle (the error may reach twice the BF16 reference's own), expert ids
+    equal to the reference's, and cosine >= 0.9999 against the BF16 reference schedule. Also
+    reported: max|y - y_ref| / max|y_ref| against that schedule and whether it is <= 1e-2
+    ("max_rel_ok"); the reference's own max_rel against the oracle ("reference_max_rel")
+    shows the noise floor of that figure on these inputs (an E4M3 requantization near a
+    rounding tie turns an ulp of difference upstream into a step of 1/8)."""
+    import torch
+
     from oracle import metrics
 
-    y = got["y"][rows].cpu()
+    y = y.cpu()
     check = metrics.layer_checks(y, want["y"])
-    out = {"tokens": len(rows), "max_rel": check["max_rel"], "cosine": check["cosine"]}
-    ok = check["pass"]
-    if "expert_ids" in want and "expert_ids" in got:
-        same = int((got["expert_ids"][rows].cpu() == want["expert_ids"]).all(dim=1).sum())
-        out["tokens_with_equal_ids"] = same
-        ok = ok and same == len(rows)
+    band = metrics.band(want["y"], y, exact["y"], bf16_rtol=case.bf16_rtol, noise_factor=case.noise_factor)
+    ref = metrics.layer_checks(want["y"], exact["y"].to(torch.float32))
+    out = {"rows": y.shape[0], "band_pass": band["pass"], "relative_error": band["relative_error"],
+           "reference_relative_error": band["reference_relative_error"], "cosine": check["cosine"],
+           "max_rel": check["max_rel"], "max_rel_ok": check["max_rel"] <= metrics.MAX_REL,
+           "reference_max_rel": ref["max_rel"]}
+    ok = band["pass"] and check["cosine"] >= metrics.MIN_COSINE
+    if ids is not None and "expert_ids" in want:
+        same = int((ids.cpu() == want["expert_ids"]).all(dim=1).sum())
+        out["rows_with_equal_ids"] = same
+        ok = ok and same == y.shape[0]
     out["ok"] = bool(ok)
     return out
 
@@ -184,9 +199,11 @@ def cpu_baseline(case, values_gpu, hit: int, budget_s: float, got: dict | None =
         rows = list(range(sample))
         t0 = time.perf_counter()
         if case.format == "mxfp4":
-            reference = mx.reference
+            reference, oracle = mx.reference, mx.oracle
+        elif case.norm != "none" or case.residual:
+            reference, oracle = layer.block_reference, layer.block_oracle
         else:
-            reference = layer.block_reference if (case.norm != "none" or case.residual) else layer.reference
+            reference, oracle = layer.reference, layer.oracle
         out = reference(case, cpu, tokens=rows)
         dt = time.perf_counter() - t0
         ids = cpu["topk_idx"][rows] if case.format == "mxfp4" else out["expert_ids"]
@@ -196,7 +213,11 @@ def cpu_baseline(case, values_gpu, hit: int, budget_s: float, got: dict | None =
         sample *= 2
     s = case.shared_experts
     scale = (hit + s) / max(sampled + s, 1)
-    parity = None if got is None else parity_of(case, got, out, rows)
+    parity = None
+    if got is not None:  # untimed: the FP32 oracle on the same tokens
+        exact = oracle(case, cpu, tokens=rows)
+        parity = parity_of(case, got["y"][rows], out, exact, got["expert_ids"][rows] if "expert_ids" in got else None)
+        parity["tokens"] = parity.pop("rows")
     return {"value": dt * scale * 1e6, "unit": "us/step", "cores": threads, "kind": "port",
             "cpu_model": cpu_model(), "parity": parity,
             "sample": (f"oracle.{reference.__module__.split('.')[-1]}.{reference.__name__} on tokens 0..{sample - 1} of the timed inputs "
@@ -238,6 +259,29 @@ def measure_like_harness(fn, inputs: dict, warmup: int, reps: int) -> dict:
     return {"method": "megabench/harness/benchmark.py:_measure (sync before each rep, same inputs)",
             "reps": reps, "host_p50_us": statistics.median(host), "host_p95_us": _p95(host),
             "event_p50_us": statistics.median(event), "event_p95_us": _p95(event)}
+
+
+DEVICE_WARMUP_MS = 30.0
+
+
+def warm_device(layer, sets, ms: float = DEVICE_WARMUP_MS) -> int:
+    """The device warm-up: the layer, in the form given (the stream-ordered one), run for at
+    least ``ms`` milliseconds before any form's warmup steps. After the device has idled (input
+    generation ends ~20 ms before the first call), the layer runs slower until the device has
+    carried this load for ~20 ms: on the headline shape the first ~20 single-launch calls took
+    876 -> 835 us, so 5 warmup calls left the first timed loop ~13 us per call above the next
+    ones (841). Copy kernels for as long do not remove the ramp; 20 calls of either form do.
+    Returns the number of calls."""
+    import torch
+
+    n, t0 = 0, time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < ms or n < 2:
+        layer(sets[n % len(sets)])
+        n += 1
+        if n % 4 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    return n
 
 
 def _time_layer(layer, sets, steps: int, warmup: int, outs: list | None = None) -> dict:
@@ -309,7 +353,9 @@ def bench_case(case, steps: int, warmup: int, want_cpu: bool, cpu_budget: float)
     sets = [workloads.make_inputs(case, 7301 + i, dev, log=lambda m, i=i: _log(f"[bench] {case.id} set {i}: {m}"))
             for i in range(n_sets)]
     torch.cuda.synchronize()
-    _log(f"[bench] {case.id}: inputs ready; warmup and timing {steps} steps")
+    five = submission.MoELayer(case, single_launch=False) if layer.single_launch else layer
+    warm_calls = warm_device(five, sets)
+    _log(f"[bench] {case.id}: inputs ready, device warmed ({warm_calls} calls); warmup and timing {steps} steps")
     outs: list = []
     r = _time_layer(layer, sets, steps, warmup, outs)
     if case.format == "mxfp4":
@@ -330,6 +376,7 @@ def bench_case(case, steps: int, warmup: int, want_cpu: bool, cpu_budget: float)
         "mfma_frac": C.algorithmic_flops(case) / (ms * 1e-3) / PEAK_FP8,
         "launches_per_step": case.max_gpu_launches,
         "stage_us": r["stage_us"], "host_issue_us": r["host_issue_us"], "harness": harness,
+        "device_warmup": f"{warm_calls} stream-ordered calls ({DEVICE_WARMUP_MS:.0f} ms) before the warmup steps",
         "rotation_sets": n_sets,
         "dtype": ("e2m1xe4m3->fp32 (E8M0 scales per 32; bf16 out)" if case.format == "mxfp4"
                   else "e4m3xe4m3->fp32 (bf16 in/out)"),
@@ -345,7 +392,6 @@ def bench_case(case, steps: int, warmup: int, want_cpu: bool, cpu_budget: float)
                               "kernel_us": k_ms * 1e3, "bytes_per_launch": bytes_step}
         # The stream-ordered kernels of the same layer, for their per-stage times and the
         # expert kernel's own roofline.
-        five = submission.MoELayer(case, single_launch=False)
         r5 = _time_layer(five, sets, steps, warmup)
         kb = kernel_bytes(case, hit)
         ex_ms = r5["stage_us"]["experts"] * 1e-3
@@ -401,12 +447,11 @@ def cpu_baseline_ep(case, experts_cpu: dict, received: dict, hit: int, budget_s:
             break
         n *= 2
     parity = None
-    if got_rows is not None:
-        from oracle import metrics
-
-        check = metrics.layer_checks(got_rows[sel], want)
-        parity = {"rows": int(sel.numel()), "local_experts": n, "max_rel": check["max_rel"],
-                  "cosine": check["cosine"], "ok": bool(check["pass"])}
+    if got_rows is not None:  # untimed: the FP32 oracle of the same rows
+        exact = OE.experts(case, {k: v[:n] for k, v in experts_cpu.items()}, received["rows"][sel],
+                           received["row_scales"][sel], ids[sel], received["weights"][sel], 0, widen=True)
+        parity = parity_of(case, got_rows[sel], {"y": want}, {"y": exact})
+        parity["local_experts"] = n
     return {"value": dt * hit / max(sampled, 1) * 1e6, "unit": "us/step", "cores": threads, "kind": "port",
             "cpu_model": cpu_model(), "parity": parity,
             "sample": (f"oracle.ep.experts on the received rows of local experts 0..{n - 1} ({sampled} hit, "
@@ -541,7 +586,7 @@ def _config_entry(r: dict) -> dict:
     """One config's record under "configs": time, bandwidth, roofline and CPU baseline."""
     keep = ("us_per_step", "p50_us", "p95_us", "tb_per_s", "hbm_frac", "mfma_frac", "hit_experts", "bytes_per_step",
             "launches_per_step", "stage_us", "rotation_sets", "roofline", "stream_ordered", "cpu_baseline", "dtype",
-            "received_rows", "sent_rows", "host_issue_us", "harness", "parity", "parity_ok")
+            "received_rows", "sent_rows", "host_issue_us", "harness", "parity", "parity_ok", "device_warmup")
     return {k: r[k] for k in keep if k in r}
 
 
