@@ -1521,7 +1521,36 @@ struct ReadyWait {
   uint64_t ticks = kWaitTicks;  // the bound, in 100 MHz ticks
   bool patient = false;         // many workgroups wait on this count: poll less often
   int max_naps = 2;             // patient waits: naps of ~1000 cycles between polls, doubling up to this
+  int* claim = nullptr;         // the queue word the workgroup claims its next unit from (NULL: none)
+  int* ticket = nullptr;        // thread 0: where the claimed index goes (read after the unit)
 };
+
+// Claims a unit: thread 0 adds one to the queue word and gets the old value. The address goes
+// through an empty asm into vector registers, which keeps the compiler's atomic optimizer off
+// this atomic: for a uniform address it combines the lanes and reads the result back at once,
+// so the wavefront would wait for the atomic's round trip (1-5 us while hundreds of workgroups
+// claim from the one word) right where it is issued. The pointer stays in the global address
+// space: a flat atomic would also count in lgkmcnt, which every LDS read of the ring waits on.
+__device__ __forceinline__ int claim_ticket(int* queue) {
+  __attribute__((address_space(1))) int* q = (__attribute__((address_space(1))) int*)queue;
+  asm volatile("" : "+v"(q));
+  return __hip_atomic_fetch_add(q, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The claim of the next unit, issued inside a unit's weight stream once its first weight
+// stages are requested (stream_gemm, stream_gemm_shared): its round trip then overlaps the
+// first loads, which the unit waits for anyway. Issued at the start of the unit, the claim's
+// round trip came before the unit's own first loads (its work-list entries, whose wait covers
+// every load issued before them); the gap between two units of a workgroup was ~2 us.
+__device__ __forceinline__ void issue_claim(const ReadyWait& w) {
+  if (w.claim && threadIdx.x == 0) *w.ticket = claim_ticket(w.claim);
+}
+
+__device__ __forceinline__ ReadyWait claiming(ReadyWait w, int* queue, int* ticket) {
+  w.claim = queue;
+  w.ticket = ticket;
+  return w;
+}
 
 // The acquire that ends a wait for data another workgroup of the same launch wrote. Workgroup
 // scope: the data is written through to memory and no workgroup reads one of its lines before
@@ -1634,7 +1663,9 @@ __device__ __forceinline__ void compute_stage(uint32_t slot, const LaneTile& lt,
 // Streams nkb K blocks through the wavefront's LDS ring (D slots) with D-1 stages of loads
 // in flight. With a ReadyWait, the weights of the first stages are requested before the
 // wait and the activations (which another workgroup produces) after it, so the wait's
-// round trip overlaps the first weight loads.
+// round trip overlaps the first weight loads; the claim of the workgroup's next unit, if the
+// ReadyWait carries one, is issued between them (one more vector memory operation after the
+// first weights, which only makes the first stage's vmcnt wait below more conservative).
 //
 // The stream starts at K block `rot` and wraps around (any rot in [0, nkb); callers derive
 // it from the unit index). Units that run at the same time then read different K blocks of
@@ -1677,6 +1708,7 @@ __device__ __forceinline__ void stream_gemm(const Operands<RT, NCT, SG>& op, int
   Stage<NCT, SG> st[D];
 #pragma unroll
   for (int s = 0; s < D - 1; ++s) issue_a(ring + s * kSlot, op, lt, phys(min(s, nkb - 1)), s < nkb);
+  issue_claim(ready);
   wait_ready(ready);
 #pragma unroll
   for (int s = 0; s < D - 1; ++s) load_stage_b(st[s], op, phys(min(s, nkb - 1)));
@@ -1750,6 +1782,7 @@ __device__ __forceinline__ void stream_gemm_shared(const Operands<2, 4, 1>& op, 
   // loads would make the compiler drain every load); only the MFMAs of stages past the
   // end are skipped.
   issue_a(ring, op, lt, phys(0), true);
+  issue_claim(ready);
   wait_ready(ready);
   issue_shared(MEGAMOE_XTILE(0, w), xrow, phys(0), st[0], op);
   issue_a(ring + kSlot, op, lt, phys(min(1, nkb - 1)), 1 < nkb);
@@ -2012,7 +2045,8 @@ __device__ __forceinline__ void gateup_work(const GateUpArgs& a, int u, float (*
 template <int NCT>
 __device__ __forceinline__ bool gateup_half(const GateUpArgs& a, const uint8_t* wt, const float* sc, const ChunkRows& cr, int jb,
                             int half, uint8_t* hq, float* hs, uint16_t* st_mine, const uint16_t* st_other, int ldh,
-                            int* pair, int rot, float (*red)[64], int* flag, uint8_t* ring) {
+                            int* pair, int rot, float (*red)[64], int* flag, uint8_t* ring,
+                            const ReadyWait& claim) {
   const int lane = opaque_lane(), w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int kofs = 16 * (lane >> 4);
   const int H = a.H, nkb = H / kBlock, nbh = scale_ld(ldh / kBlock);
@@ -2030,7 +2064,7 @@ __device__ __forceinline__ bool gateup_half(const GateUpArgs& a, const uint8_t* 
     op.sx[c] = a.xs + (size_t)tok * nkb;
   }
   f32x4 acc[2][NCT];
-  stream_gemm<2, NCT, 1, NCT == 4 ? 3 : 4>(op, nkb, rot, ring, acc);
+  stream_gemm<2, NCT, 1, NCT == 4 ? 3 : 4>(op, nkb, rot, ring, acc, claim);
 
   const float L = a.limit > 0.0f ? a.limit : INFINITY;
   const float lo = half ? -L : -INFINITY;  // up is clamped on both sides, gate above only
@@ -2113,7 +2147,9 @@ __device__ __forceinline__ bool gateup_half(const GateUpArgs& a, const uint8_t* 
 // Gate/up unit u of the work list: block pair u / 2 (chunk (u/2) / nbI, 128-row block
 // (u/2) % nbI of the chunk's expert, plus the slice offset of a shared-expert copy), half
 // u % 2 (gate, then up). Returns true if this unit completed the block of h.
-__device__ __forceinline__ bool gateup_work_split(const GateUpArgs& a, int u, float (*red)[64], int* flag, uint8_t* ring) {
+// `claim`: the claim of the workgroup's next unit, issued inside the weight stream.
+__device__ __forceinline__ bool gateup_work_split(const GateUpArgs& a, int u, float (*red)[64], int* flag, uint8_t* ring,
+                                                  const ReadyWait& claim) {
   const int nbI = a.I / kBlock, nkb = a.H / kBlock;
   const int pair = u >> 1, half = u & 1;
   const int4 ch = a.chunks[pair / nbI];
@@ -2151,11 +2187,11 @@ __device__ __forceinline__ bool gateup_work_split(const GateUpArgs& a, int u, fl
   const uint16_t* other = st + (half ? 0 : st_half);
   int* ctr = a.pairs + pair;
   if (cr.n <= 16)
-    return gateup_half<1>(a, wt, sc, cr, jb, half, hq, hs, mine, other, ldh, ctr, rot, red, flag, ring);
+    return gateup_half<1>(a, wt, sc, cr, jb, half, hq, hs, mine, other, ldh, ctr, rot, red, flag, ring, claim);
   else if (cr.n <= 32)
-    return gateup_half<2>(a, wt, sc, cr, jb, half, hq, hs, mine, other, ldh, ctr, rot, red, flag, ring);
+    return gateup_half<2>(a, wt, sc, cr, jb, half, hq, hs, mine, other, ldh, ctr, rot, red, flag, ring, claim);
   else
-    return gateup_half<4>(a, wt, sc, cr, jb, half, hq, hs, mine, other, ldh, ctr, rot, red, flag, ring);
+    return gateup_half<4>(a, wt, sc, cr, jb, half, hq, hs, mine, other, ldh, ctr, rot, red, flag, ring, claim);
 }
 
 struct DownArgs {
@@ -2499,7 +2535,7 @@ __global__ __launch_bounds__(256, 2) void k_experts(ExpertArgs args) {
   // holds nothing), whatever number of workgroups the device keeps resident.
   if (threadIdx.x == 0) slot = atomicAdd(&meta[kMetaQueueGU], 1);
   __syncthreads();
-  int u = slot, next = 0;
+  int u = slot;
   while (u < total) {
     // The arguments are re-read from the kernel argument segment (where `args`, the only
     // argument, sits at offset 0) through a pointer behind an empty asm, so each unit
@@ -2512,19 +2548,20 @@ __global__ __launch_bounds__(256, 2) void k_experts(ExpertArgs args) {
     const int nbI = a.gu.I / kBlock, nbH = a.dn.H / kBlock;
     uint8_t* ring = rings + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) * kRingWave;
     __syncthreads();
-    // Thread 0 takes the next unit index now and hands it out after this unit: the
-    // atomic's round trip overlaps the unit instead of holding up wavefront 0. A
-    // workgroup on a down unit can only hold later (down) units this way, so no gate/up
-    // unit waits behind a waiting workgroup.
-    if (threadIdx.x == 0) next = atomicAdd(&meta[kMetaQueueGU], 1);
+    // Thread 0 claims the next unit inside this unit's weight stream (issue_claim) and hands
+    // it out after this unit; a unit that streams nothing claims at its end. A workgroup on
+    // a down unit can only hold later (down) units this way, so no gate/up unit waits behind
+    // a waiting workgroup.
+    int ticket = -1;
     if (u < total_gu) {
       bool done = true;
       if constexpr (SPLIT) {
-        done = gateup_work_split(a.gu, u, red, &flag, ring);
+        done = gateup_work_split(a.gu, u, red, &flag, ring,
+                                 claiming(ReadyWait{nullptr, 0, nullptr}, &meta[kMetaQueueGU], &ticket));
       } else {
         const int c = u / nbI;
         if (!(dense && c >= a.gu.S && a.gu.offsets[c - a.gu.S + 1] == a.gu.offsets[c - a.gu.S]))
-          gateup_work(a.gu, u, red, ring);
+          gateup_work(a.gu, u, red, ring, claiming(ReadyWait{nullptr, 0, nullptr}, &meta[kMetaQueueGU], &ticket));
       }
       if (done) {
         publish_fence();
@@ -2536,10 +2573,13 @@ __global__ __launch_bounds__(256, 2) void k_experts(ExpertArgs args) {
       const int v = u - total_gu, c = v / (nbH * a.dn.ks), e = c - (a.dn.S > 0 ? 1 : 0);
       if (!(dense && e >= 0 && a.gu.offsets[e + 1] == a.gu.offsets[e])) {
         const int need = dense ? dense_dn_need(c, a.dn.S, nbI) : (a.dn.chunks[c].x == a.dn.E ? a.dn.S * nbI : nbI);
-        down_work<false>(a.dn, v, ReadyWait{&a.ready[(size_t)c * a.ready_stride], need, &meta[kMetaError]}, ring);
+        down_work<false>(a.dn, v,
+                         claiming(ReadyWait{&a.ready[(size_t)c * a.ready_stride], need, &meta[kMetaError]},
+                                  &meta[kMetaQueueGU], &ticket),
+                         ring);
       }
     }
-    if (threadIdx.x == 0) slot = next;
+    if (threadIdx.x == 0) slot = ticket >= 0 ? ticket : claim_ticket(&meta[kMetaQueueGU]);
     __syncthreads();
     u = slot;
   }
@@ -2958,12 +2998,14 @@ __global__ __launch_bounds__(256, 2) void k_layer(LayerArgs args) {
     const int nbI = a.gu.I / kBlock, nbH = a.dn.H / kBlock;
     uint8_t* ring = rings + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) * kRingWave;
     __syncthreads();
-    if (threadIdx.x == 0) next = n_first + atomicAdd(&ctl[kCtlQueue], 1);
+    // The next unit is claimed inside this unit's weight stream, as in k_experts.
+    int ticket = -1;
+    int* const queue = &ctl[kCtlQueue];
     if (u < fixed + n_gu) {
       const int g = u - fixed;
       bool done = true;
       if constexpr (SPLIT) {
-        done = gateup_work_split(a.gu, g, red, &flag, ring);
+        done = gateup_work_split(a.gu, g, red, &flag, ring, claiming(ReadyWait{nullptr, 0, nullptr}, queue, &ticket));
       } else if (dense) {
         // Every expert's units from the start: before the routing is known a unit works every
         // token and waits only for the quantized x; after, its expert's routed rows, or
@@ -2971,10 +3013,12 @@ __global__ __launch_bounds__(256, 2) void k_layer(LayerArgs args) {
         const int c = g / nbI;
         const int st = c >= a.gu.S ? dense_state(ctl, a.gu.offsets, c - a.gu.S, &flags[0]) : 0;
         if (st != 2)
-          gateup_work(a.gu, g, red, ring, ReadyWait{my_signal_flag(ctl, kSigQuant), 1, &ctl[kCtlError], kWaitTicks,
-                                                    true, 2}, st == 1);
+          gateup_work(a.gu, g, red, ring,
+                      claiming(ReadyWait{my_signal_flag(ctl, kSigQuant), 1, &ctl[kCtlError], kWaitTicks, true, 2},
+                               queue, &ticket),
+                      st == 1);
       } else {
-        gateup_work(a.gu, g, red, ring);
+        gateup_work(a.gu, g, red, ring, claiming(ReadyWait{nullptr, 0, nullptr}, queue, &ticket));
       }
       if (done) {
         publish_fence();
@@ -2988,12 +3032,14 @@ __global__ __launch_bounds__(256, 2) void k_layer(LayerArgs args) {
       const int st = dense && c >= sh ? dense_state(ctl, a.gu.offsets, c - sh, &flags[0]) : 0;
       if (st != 2) {
         const int need = dense ? dense_dn_need(c, a.dn.S, nbI) : (a.dn.chunks[c].x == a.dn.E ? a.dn.S * nbI : nbI);
-        down_work<true>(a.dn, v, ReadyWait{&a.ready[(size_t)c * a.ready_stride], need, &ctl[kCtlError]}, ring,
-                        st == 1);
+        down_work<true>(a.dn, v,
+                        claiming(ReadyWait{&a.ready[(size_t)c * a.ready_stride], need, &ctl[kCtlError]}, queue,
+                                 &ticket),
+                        ring, st == 1);
       }
       ++my_down;
     }
-    if (threadIdx.x == 0) slot = next;
+    if (threadIdx.x == 0) slot = n_first + (ticket >= 0 ? ticket : claim_ticket(queue));
     __syncthreads();
     u = slot;
   }
@@ -3023,7 +3069,7 @@ __global__ __launch_bounds__(256, 2) void k_layer(LayerArgs args) {
     bool use_first = true;
     while (u < total) {
       __syncthreads();
-      if (threadIdx.x == 0) next = n_first + atomicAdd(&ctl[kCtlQueue], 1);
+      if (threadIdx.x == 0) next = n_first + claim_ticket(&ctl[kCtlQueue]);
       layer_combine(a, u - experts_end, use_first ? &first : nullptr);
       use_first = false;
       if (threadIdx.x == 0) slot = next;
