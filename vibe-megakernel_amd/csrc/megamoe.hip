@@ -992,7 +992,7 @@ struct PermuteOut {
   int* meta;     // kMeta*
   int* perm;     // [T*K] grouped row -> token*K + slot
   int* inv;      // [T*K] token*K + slot -> grouped row
-  int4* gu;      // gate/up chunks {expert (E = shared), first row, rows, first 128-block}
+  int4* gu;      // gate/up chunks {expert (E = shared), first grouped row, rows, first 128-block}
   int4* dn;      // down chunks
   int* dn_of_gu; // gate/up chunk -> down chunk of the same rows
   int* ready;    // [down chunks, stride ready_stride] zeroed here, counted by the expert kernel
@@ -1172,7 +1172,7 @@ __device__ __forceinline__ void permute_block(const int64_t* __restrict__ ids, i
       // the experts before it, .w = the chunk's index in its expert's group | group size << 16.
       const int nch = a4 + a2 + a1, first = p4 + p2 + p1;
       for (int i = 0; i < nch; ++i) {
-        const int4 ch = make_int4(e, chunk * i, min(chunk, c - chunk * i), i | (nch << 16));
+        const int4 ch = make_int4(e, off + chunk * i, min(chunk, c - chunk * i), i | (nch << 16));
         store_out<CO>(&out.gu[first + i], ch);
         store_out<CO>(&out.dn[first + i], ch);
         store_out<CO>(&out.dn_of_gu[first + i], first + i);
@@ -1189,19 +1189,19 @@ __device__ __forceinline__ void permute_block(const int64_t* __restrict__ ids, i
       }
     } else {
       for (int i = 0; i < a4; ++i) {
-        const int4 ch = make_int4(e, chunk * i, min(chunk, c - chunk * i), 0);
+        const int4 ch = make_int4(e, off + chunk * i, min(chunk, c - chunk * i), 0);
         store_out<CO>(&out.gu[gbase[0] + gshared[0] + p4 + i], ch);
         store_out<CO>(&out.dn[dbase[0] + dshared[0] + p4 + i], ch);
         store_out<CO>(&out.dn_of_gu[gbase[0] + gshared[0] + p4 + i], dbase[0] + dshared[0] + p4 + i);
       }
       if (a2) {
-        const int4 ch = make_int4(e, chunk * full, rem, 0);
+        const int4 ch = make_int4(e, off + chunk * full, rem, 0);
         store_out<CO>(&out.gu[gbase[1] + gshared[1] + p2], ch);
         store_out<CO>(&out.dn[dbase[1] + dshared[1] + p2], ch);
         store_out<CO>(&out.dn_of_gu[gbase[1] + gshared[1] + p2], dbase[1] + dshared[1] + p2);
       }
       if (a1) {
-        const int4 ch = make_int4(e, chunk * full, rem, 0);
+        const int4 ch = make_int4(e, off + chunk * full, rem, 0);
         store_out<CO>(&out.gu[gbase[2] + gshared[2] + p1], ch);
         store_out<CO>(&out.dn[dbase[2] + dshared[2] + p1], ch);
         store_out<CO>(&out.dn_of_gu[gbase[2] + gshared[2] + p1], dbase[2] + dshared[2] + p1);
@@ -2013,7 +2013,7 @@ __device__ __forceinline__ void gateup_work(const GateUpArgs& a, int u, float (*
     wu = a.up + rowblk * kBlock * a.H;
     sg = a.gate_scale + rowblk * nkb;
     su = a.up_scale + rowblk * nkb;
-    cr = !a.dense ? ChunkRows{ch.z, a.offsets[ch.x] + ch.y, a.perm, a.K}
+    cr = !a.dense ? ChunkRows{ch.z, ch.y, a.perm, a.K}
                   : (known ? routed_rows(ch.x, a.T, a.K, a.offsets, a.perm) : dense_rows(ch.x, a.T, a.K));
     hq = a.hq_r;
     hs = a.hs_r;
@@ -2176,7 +2176,7 @@ __device__ __forceinline__ bool gateup_work_split(const GateUpArgs& a, int u, fl
     const size_t rowblk = (size_t)ch.x * nbI + jb;
     wt = (half ? a.up : a.gate) + rowblk * kBlock * a.H;
     sc = (half ? a.up_scale : a.gate_scale) + rowblk * nkb;
-    cr = ChunkRows{ch.z, a.offsets[ch.x] + ch.y, a.perm, a.K};
+    cr = ChunkRows{ch.z, ch.y, a.perm, a.K};
     hq = a.hq_r;
     hs = a.hs_r;
     ldh = a.I;
@@ -2299,7 +2299,7 @@ __device__ __forceinline__ void down_work(const DownArgs& a, int v, const ReadyW
     else
       down_unit<4, CO>(a, wd, sd, ldk, a.hq_s, a.hs_s, cr, j, kp, a.d_s, pd_s, rot, ready, ring);
   } else {
-    const ChunkRows cr = !a.dense ? ChunkRows{ch.z, a.offsets[ch.x] + ch.y, a.perm, a.K}
+    const ChunkRows cr = !a.dense ? ChunkRows{ch.z, ch.y, a.perm, a.K}
                                   : (known ? routed_rows(ch.x, a.T, a.K, a.offsets, a.perm)
                                            : dense_rows(ch.x, a.T, a.K));
     const size_t rowblk = (size_t)ch.x * nbH + j;
@@ -3531,7 +3531,7 @@ __device__ int gateup_mx_work(const GateUpMxArgs& a, int u, int nwide, uint8_t (
   if (u < nwide * 4 * nbI) {
     const int c = u / (4 * nbI), blk = u % (4 * nbI);
     const int4 ch = a.chunks[c];
-    const ChunkRows cr{ch.z, a.offsets[ch.x] + ch.y, a.perm, a.K};
+    const ChunkRows cr{ch.z, ch.y, a.perm, a.K};
     const int key = (ch.x + a.ebase) * nbI + blk / 4;  // as the narrow unit of the same 128 channels
     const bool two = cr.n > 64;
     if (nst % 2 == 0) {
@@ -3553,7 +3553,7 @@ __device__ int gateup_mx_work(const GateUpMxArgs& a, int u, int nwide, uint8_t (
   const int c = nwide + u / nbI;
   const int4 ch = a.chunks[c];
   const int jb = u % nbI;
-  const ChunkRows cr{ch.z, a.offsets[ch.x] + ch.y, a.perm, a.K};
+  const ChunkRows cr{ch.z, ch.y, a.perm, a.K};
   // The rotation (the first of the nst stages, which sets the fp32 accumulation order)
   // follows the global expert and the 128-channel block, not the unit's place in the queue
   // or its kind, so a row's result does not depend on which other rows share its chunk or
@@ -3718,7 +3718,7 @@ __device__ void down_mx_work(const DownMxArgs& a, int v, int nwide, int* ready_c
   if (v < nwide * 2 * nbH * a.ks) {
     const int c = v / (2 * nbH * a.ks), rem = v % (2 * nbH * a.ks), j64 = rem / a.ks, kp = rem % a.ks;
     const int4 ch = a.chunks[c];
-    const ChunkRows cr{ch.z, a.offsets[ch.x] + ch.y, a.perm, a.K};
+    const ChunkRows cr{ch.z, ch.y, a.perm, a.K};
     const ReadyWait ready{&ready_counts[c], 4 * nbI, error};
     const int key = ((ch.x + a.ebase) * (nbH / 2) + j64 / 4) * a.ks + kp;  // as every unit of these rows
     const bool two = cr.n > 64;
@@ -3741,7 +3741,7 @@ __device__ void down_mx_work(const DownMxArgs& a, int v, int nwide, int* ready_c
   const int c = nwide + v / (nbH * a.ks);
   const int4 ch = a.chunks[c];
   const int rem = v % (nbH * a.ks), j = rem / a.ks, kp = rem % a.ks;
-  const ChunkRows cr{ch.z, a.offsets[ch.x] + ch.y, a.perm, a.K};
+  const ChunkRows cr{ch.z, ch.y, a.perm, a.K};
   const ReadyWait ready{&ready_counts[c], nbI, error};
   // Keyed by 256-row block, as the batch units (k_experts_mx_batch) of the same rows.
   const int key = ((ch.x + a.ebase) * (nbH / 2) + j / 2) * a.ks + kp;
@@ -4121,7 +4121,7 @@ __global__ __launch_bounds__(256, 1) void k_experts_mx_batch(ExpertMxArgs args) 
       const int w0 = a.gu.chunks[u / nbI].w, cg = u / nbI - (w0 & 0xffff), ng = w0 >> 16, r = u - cg * nbI;
       const int c = cg + r % ng, jb = r / ng;
       const int4 ch = a.gu.chunks[c];
-      const ChunkRows cr{ch.z, a.gu.offsets[ch.x] + ch.y, a.gu.perm, a.gu.K};
+      const ChunkRows cr{ch.z, ch.y, a.gu.perm, a.gu.K};
       const int nst = a.gu.H / kMxStageK;
       gateup_mx_batch(a.gu, ch.x, jb, cr, mx_rotation((ch.x + a.gu.ebase) * nbI + jb, nst), lds, red8);
       publish_fence();
@@ -4132,7 +4132,7 @@ __global__ __launch_bounds__(256, 1) void k_experts_mx_batch(ExpertMxArgs args) 
       const int w0 = a.dn.chunks[v / per].w, cg = v / per - (w0 & 0xffff), ng = w0 >> 16, r = v - cg * per;
       const int c = cg + r % ng, j2 = r / ng / ks, kp = r / ng % ks;
       const int4 ch = a.dn.chunks[c];
-      const ChunkRows cr{ch.z, a.dn.offsets[ch.x] + ch.y, a.dn.perm, a.dn.K};
+      const ChunkRows cr{ch.z, ch.y, a.dn.perm, a.dn.K};
       const ReadyWait ready{&a.ready[c], nbI, &meta[kMetaError]};
       const int nstp = a.dn.I / kMxStageK / ks;
       down_mx_batch(a.dn, ch.x, j2, kp, cr, mx_rotation(((ch.x + a.dn.ebase) * nbH2 + j2) * ks + kp, nstp), ready,
