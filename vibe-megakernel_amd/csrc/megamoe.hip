@@ -130,6 +130,14 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// threadIdx.x % 64 behind an empty asm: what the persistent kernels' units derive from it is computed
+// where it is used, not hoisted out of the persistent loop and held (or spilled) across it.
+__device__ __forceinline__ int opaque_lane() {
+  int l = threadIdx.x & 63;
+  asm volatile("" : "+v"(l));
+  return l;
+}
+
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
 
 // Device-coherent stores: relaxed agent-scope atomic stores, which write through the XCD's
@@ -691,37 +699,55 @@ constexpr int kSelectTokens = 1;
 // LDS of one token's routing.
 struct SelectLds {
   float logit[kSelectTokens][kMaxExperts];
+  float choice[kSelectTokens][kMaxExperts];
+  unsigned long long key[kSelectTokens][kMaxExperts];  // VPL >= 8: keys of lane l at [64j + l]
+  float bias[kMaxExperts];                             // the router bias (sigmoid gate)
   float gscore[kSelectTokens][kMaxGroups];
   int pick_id[kSelectTokens][kMaxTopK];
   float pick_val[kSelectTokens][kMaxTopK];
 };
 
+// The gate's probability of a logit (sigmoid), or the logit itself (softmax, whose weights
+// come from the picked logits).
+__device__ __forceinline__ float gate_prob(float logit, int gate) {
+  return gate == MEGAMOE_GATE_SIGMOID ? 1.0f / (1.0f + expf(-logit)) : logit;
+}
+
 // Wavefront `wv` routes token t from the logits in LDS (one wavefront per token, no barrier).
+// The logits and the choices stay in LDS and are read again where needed (a probability is
+// recomputed from its logit by the same expression, so it has the same bits). The selection
+// keys of the lane's VPL experts stay in registers up to VPL 4; from VPL 8 (over 256 experts)
+// they go to LDS and the lane keeps only its largest: with 8 or 16 keys of 64 bits per lane
+// held in registers, the single-launch kernel, whose register budget the expert units set,
+// spilled them to scratch.
 template <int VPL, bool CO>
-__device__ __forceinline__ void route_token(SelectLds& L, int lane, int wv, int t, bool token_ok,
-                                            const float (&bias_v)[VPL], int E, int K, int G, int TG, int gate,
+__device__ __forceinline__ void route_token(SelectLds& L, int lane, int wv, int t, bool token_ok, int E, int K,
+                                            int G, int TG, int gate,
                                             int renorm, float scaling, int64_t* __restrict__ ids_out,
                                             float* __restrict__ w_out) {
-  auto& lds_logit = L.logit;
+  const float* logit_lds = L.logit[wv];
+  float* choice_lds = L.choice[wv];
   auto& gscore = L.gscore;
-  float* choice_lds = lds_logit[wv];
   int* pick_id = L.pick_id[wv];
   float* pick_val = L.pick_val[wv];
-  float logit[VPL], prob[VPL], choice[VPL];
-  bool valid[VPL];
+  // Selection keys of the lane's experts (0: not selectable), built from the choices
+  // (sigmoid + bias, or the logit).
+  constexpr bool kKeysInLds = VPL >= 8;
+  constexpr int VR = kKeysInLds ? 1 : VPL;  // keys held in registers
+  unsigned long long* key_lds = L.key[wv];
+  unsigned long long key[VR];
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
     const int e = lane + 64 * j;
-    valid[j] = token_ok && e < E;
-    logit[j] = valid[j] ? lds_logit[wv][e] : -INFINITY;
-    if (gate == MEGAMOE_GATE_SIGMOID) {
-      const float p = 1.0f / (1.0f + expf(-logit[j]));
-      prob[j] = p;
-      choice[j] = p + bias_v[j];
-    } else {
-      prob[j] = logit[j];
-      choice[j] = logit[j];
-    }
+    const bool valid = token_ok && e < E;
+    const float logit = valid ? logit_lds[e] : -INFINITY;
+    const float choice = gate == MEGAMOE_GATE_SIGMOID ? gate_prob(logit, gate) + L.bias[min(e, E - 1)] : logit;
+    if (G > 1 && valid) choice_lds[e] = choice;
+    const unsigned long long k = valid ? select_key(choice, e) : 0ull;
+    if constexpr (kKeysInLds)
+      key_lds[e] = k;
+    else
+      key[j] = k;
   }
   if (G > 1) {
     // Group score: the sum of the two largest choices of the group (frontier.py:234). A
@@ -731,9 +757,6 @@ __device__ __forceinline__ void route_token(SelectLds& L, int lane, int wv, int 
     const int gs = E / G;
     int lpg = 1;
     while (lpg * 2 * G <= 64) lpg *= 2;
-#pragma unroll
-    for (int j = 0; j < VPL; ++j)
-      if (valid[j]) choice_lds[lane + 64 * j] = choice[j];
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the choices are in LDS
     __builtin_amdgcn_wave_barrier();
     const int grp = lane / lpg, sub = lane % lpg;
@@ -763,19 +786,32 @@ __device__ __forceinline__ void route_token(SelectLds& L, int lane, int wv, int 
     const unsigned long long kept = __ballot(keep);
 #pragma unroll
     for (int j = 0; j < VPL; ++j)
-      if (valid[j] && !((kept >> ((lane + 64 * j) / gs)) & 1ull)) choice[j] = -INFINITY;
+      if (!((kept >> ((lane + 64 * j) / gs)) & 1ull)) {
+        if constexpr (kKeysInLds)
+          key_lds[lane + 64 * j] = 0ull;
+        else
+          key[j] = 0ull;
+      }
   }
+  // With the keys in LDS, the lane's largest one.
+  auto lane_best = [&]() {
+    unsigned long long b = 0ull;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+      const unsigned long long k = key_lds[lane + 64 * j];
+      b = k > b ? k : b;
+    }
+    return b;
+  };
+  if constexpr (kKeysInLds) key[0] = lane_best();
   // K rounds: the wavefront's largest remaining key is the next pick (selection order,
   // frontier.py:236; distributed.py:174); its owner records it and drops it. The maximum
   // is taken over the score codes (the keys' upper halves) first; only when several lanes
   // hold that code does a second maximum over their index parts pick the lowest index.
-  unsigned long long key[VPL];
-#pragma unroll
-  for (int j = 0; j < VPL; ++j) key[j] = valid[j] ? select_key(choice[j], lane + 64 * j) : 0ull;
   for (int r = 0; r < K && token_ok; ++r) {
     unsigned long long best = 0ull;
 #pragma unroll
-    for (int j = 0; j < VPL; ++j) best = key[j] > best ? key[j] : best;
+    for (int j = 0; j < VR; ++j) best = key[j] > best ? key[j] : best;
     const uint32_t hi = (uint32_t)(best >> 32), lo = (uint32_t)best;
     const uint32_t top = wave_max_u32(hi);
     unsigned long long owner = __ballot(hi == top);
@@ -784,13 +820,16 @@ __device__ __forceinline__ void route_token(SelectLds& L, int lane, int wv, int 
       owner = __ballot(hi == top && lo == top_lo);
     }
     if (lane == __ffsll((long long)owner) - 1) {
+      // The key's index part is the complement of its expert.
+      pick_id[r] = (int)(0xffffffffu - lo);
+      if constexpr (kKeysInLds) {
+        key_lds[0xffffffffu - lo] = 0ull;
+        key[0] = lane_best();
+      } else {
 #pragma unroll
-      for (int j = 0; j < VPL; ++j)
-        if (key[j] == best) {
-          pick_id[r] = lane + 64 * j;
-          pick_val[r] = prob[j];
-          key[j] = 0ull;
-        }
+        for (int j = 0; j < VR; ++j)
+          if (key[j] == best) key[j] = 0ull;
+      }
     }
   }
   __builtin_amdgcn_s_waitcnt(0xc07f);
@@ -800,8 +839,11 @@ __device__ __forceinline__ void route_token(SelectLds& L, int lane, int wv, int 
   float my_val = 0.0f;
   if (lane < K) {
     my_id = pick_id[lane];
-    my_val = pick_val[lane];
+    my_val = gate_prob(logit_lds[my_id], gate);
+    pick_val[lane] = my_val;
   }
+  __builtin_amdgcn_s_waitcnt(0xc07f);
+  __builtin_amdgcn_wave_barrier();
   // Weights; sums run in slot order.
   float w = 0.0f;
   if (gate == MEGAMOE_GATE_SIGMOID) {
@@ -820,12 +862,13 @@ __device__ __forceinline__ void route_token(SelectLds& L, int lane, int wv, int 
   } else {
     float m = -INFINITY;
 #pragma unroll
-    for (int j = 0; j < VPL; ++j) m = fmaxf(m, logit[j]);
+    for (int j = 0; j < VPL; ++j)
+      if (lane + 64 * j < E) m = fmaxf(m, logit_lds[lane + 64 * j]);
     m = wave_max(m);
     float s = 0.0f;
 #pragma unroll
     for (int j = 0; j < VPL; ++j)
-      if (valid[j]) s += expf(logit[j] - m);
+      if (lane + 64 * j < E) s += expf(logit_lds[lane + 64 * j] - m);
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
     w = expf(my_val - m) / s * scaling;
@@ -850,12 +893,11 @@ __device__ __forceinline__ void select_token(const double* __restrict__ partial,
   const int t0 = token * kSelectTokens, t = t0 + wv;
   const bool token_ok = t < T;
 
-  float bias_v[VPL];
+  // The bias into LDS (thread i: entries i, i+256, ...), loaded beside the logits' loads.
+  constexpr int NB = (64 * VPL + 255) / 256;
+  float bias_e[NB];
 #pragma unroll
-  for (int j = 0; j < VPL; ++j) {
-    const float v = bias ? bias[min(lane + 64 * j, E - 1)] : 0.0f;
-    bias_v[j] = lane + 64 * j < E ? v : 0.0f;
-  }
+  for (int r = 0; r < NB; ++r) bias_e[r] = bias ? bias[min((int)threadIdx.x + 256 * r, E - 1)] : 0.0f;
 
   // Logits of the workgroup's tokens into LDS: thread i sums the splits (in split order)
   // of entries i, i+256, ... (kSelectTokens * E <= 64 * VPL of them, up to kMaxSplits
@@ -872,7 +914,7 @@ __device__ __forceinline__ void select_token(const double* __restrict__ partial,
     const size_t stride = (size_t)T * E;
     const double* p = partial + (size_t)t0 * E;
     constexpr int NE = (kSelectTokens * 64 * VPL + 255) / 256;  // entries per thread
-    constexpr int R = NE < 2 ? NE : 2;                           // entries per round of loads
+    constexpr int R = VPL >= 8 ? 1 : (NE < 2 ? NE : 2);          // entries per round of loads
 #pragma unroll
     for (int r0 = 0; r0 < NE; r0 += R) {
       double part[R][kMaxSplits];
@@ -897,8 +939,13 @@ __device__ __forceinline__ void select_token(const double* __restrict__ partial,
       }
     }
   }
+#pragma unroll
+  for (int r = 0; r < NB; ++r)
+    if ((int)threadIdx.x + 256 * r < E) L.bias[threadIdx.x + 256 * r] = bias_e[r];
   __syncthreads();
-  if (wv < kSelectTokens) route_token<VPL, CO>(L, lane, wv, t, token_ok, bias_v, E, K, G, TG, gate, renorm, scaling,
+  // The lane behind an empty asm: the experts' indices derived from it are computed here, not
+  // hoisted out of the single-launch kernel's persistent loop and held (or spilled) across it.
+  if (wv < kSelectTokens) route_token<VPL, CO>(L, opaque_lane(), wv, t, token_ok, E, K, G, TG, gate, renorm, scaling,
                                            ids_out, w_out);
 }
 
@@ -1451,13 +1498,6 @@ struct LaneTile {
   int dma, rd0, rd1;
 };
 
-// threadIdx.x % 64 behind an empty asm: what the expert units derive from it is computed
-// where it is used, not hoisted out of the persistent loop and held (or spilled) across it.
-__device__ __forceinline__ int opaque_lane() {
-  int l = threadIdx.x & 63;
-  asm volatile("" : "+v"(l));
-  return l;
-}
 
 __device__ __forceinline__ LaneTile lane_tile(int lda) {
   const int lane = opaque_lane();
@@ -2349,13 +2389,13 @@ __device__ __forceinline__ void load_slots(const SlotMap& m, const float* __rest
 
 __device__ __forceinline__ void combine8(const uint16_t* __restrict__ d_r, const uint16_t* __restrict__ d_s,
                                          const SlotMap& inv, const float* __restrict__ wts, int H, int K,
-                                         int S, int t, int h0, float (&acc)[8], const SlotRows* first = nullptr) {
+                                         int S, int t, int h0, float (&acc)[8], const SlotRows& first, bool use_first) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
   for (int s0 = 0; s0 < K; s0 += 8) {
     SlotRows r;
-    if (s0 == 0 && first)
-      r = *first;
+    if (s0 == 0 && use_first)
+      r = first;
     else
       load_slots(inv, wts, K, t, s0, r);
     uint4 v[8];
@@ -2422,13 +2462,13 @@ __device__ __forceinline__ void sum_parts8(const float* __restrict__ src, size_t
 __device__ __forceinline__ void combine8_parts(const float* __restrict__ p_r, const float* __restrict__ p_s, int ks,
                                                const SlotMap& inv, const float* __restrict__ wts, int T,
                                                int rows_r, int H, int K, int S, int t, int h0, float (&acc)[8],
-                                               const SlotRows* first = nullptr) {
+                                               const SlotRows& first, bool use_first) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
   for (int s0 = 0; s0 < K; s0 += 8) {
     SlotRows r;
-    if (s0 == 0 && first)
-      r = *first;
+    if (s0 == 0 && use_first)
+      r = first;
     else
       load_slots(inv, wts, K, t, s0, r);
 #pragma unroll
@@ -2467,9 +2507,9 @@ __global__ __launch_bounds__(256) void k_combine(const uint16_t* __restrict__ d_
   const int t = i / per_row, h0 = (i % per_row) * 8;
   float acc[8];
   if (ks > 1)
-    combine8_parts(p_r, p_s, ks, inv, wts, T, rows_r, H, K, S, t, h0, acc);
+    combine8_parts(p_r, p_s, ks, inv, wts, T, rows_r, H, K, S, t, h0, acc, SlotRows{}, false);
   else
-    combine8(d_r, d_s, inv, wts, H, K, S, t, h0, acc);
+    combine8(d_r, d_s, inv, wts, H, K, S, t, h0, acc, SlotRows{}, false);
   uint32_t o[4];
   if (residual) {
     const uint4 v = *reinterpret_cast<const uint4*>(residual + (size_t)t * H + h0);
@@ -2779,9 +2819,10 @@ __device__ __forceinline__ SlotMap layer_slots(const LayerArgs& a) {
   return a.dense ? SlotMap{nullptr, a.ids, a.T} : SlotMap{a.po.inv, nullptr, 0};
 }
 
-// Combine unit c: outputs [c * kCombineUnit, +kCombineUnit) of y, as k_combine (`first`:
-// the thread's first eight slots, loaded already, or NULL).
-__device__ __forceinline__ void layer_combine(const LayerArgs& a, int c, const SlotRows* first = nullptr) {
+// Combine unit c: outputs [c * kCombineUnit, +kCombineUnit) of y, as k_combine (with
+// `use_first`, `first` holds the thread's first eight slots, loaded already). The slots pass by
+// value: behind a pointer that may be null they were kept in scratch memory.
+__device__ __forceinline__ void layer_combine(const LayerArgs& a, int c, const SlotRows& first, bool use_first) {
   const DownArgs& dn = a.ex.dn;
   const int i = c * (kCombineUnit / 8) + threadIdx.x, per_row = a.H / 8;
   if (i >= a.T * per_row) return;
@@ -2793,9 +2834,9 @@ __device__ __forceinline__ void layer_combine(const LayerArgs& a, int c, const S
   float acc[8];
   const SlotMap m = layer_slots(a);
   if (a.ks > 1)
-    combine8_parts(dn.p_r, dn.p_s, a.ks, m, a.wts, a.T, dn.rows_r, a.H, a.K, a.S, t, h0, acc, first);
+    combine8_parts(dn.p_r, dn.p_s, a.ks, m, a.wts, a.T, dn.rows_r, a.H, a.K, a.S, t, h0, acc, first, use_first);
   else
-    combine8(dn.d_r, dn.d_s, m, a.wts, a.H, a.K, a.S, t, h0, acc, first);
+    combine8(dn.d_r, dn.d_s, m, a.wts, a.H, a.K, a.S, t, h0, acc, first, use_first);
   uint32_t o[4];
   if (a.residual) {
     const uint4 v = *reinterpret_cast<const uint4*>(a.residual + (size_t)t * a.H + h0);
@@ -3070,7 +3111,7 @@ __global__ __launch_bounds__(256, 2) void k_layer(LayerArgs args) {
     while (u < total) {
       __syncthreads();
       if (threadIdx.x == 0) next = n_first + claim_ticket(&ctl[kCtlQueue]);
-      layer_combine(a, u - experts_end, use_first ? &first : nullptr);
+      layer_combine(a, u - experts_end, first, use_first);
       use_first = false;
       if (threadIdx.x == 0) slot = next;
       __syncthreads();
@@ -4183,9 +4224,9 @@ __device__ __forceinline__ void layer_mx_combine(const LayerMxArgs& a, int c) {
   float acc[8];
   if (a.ks > 1)
     combine8_parts(dn.pd, nullptr, a.ks, SlotMap{a.po.inv, nullptr, 0}, nullptr, a.T, a.T * a.K, a.H, a.K, 0, t, h0,
-                   acc);
+                   acc, SlotRows{}, false);
   else
-    combine8(dn.d, nullptr, SlotMap{a.po.inv, nullptr, 0}, nullptr, a.H, a.K, 0, t, h0, acc);
+    combine8(dn.d, nullptr, SlotMap{a.po.inv, nullptr, 0}, nullptr, a.H, a.K, 0, t, h0, acc, SlotRows{}, false);
   uint32_t o[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) o[j] = f32_to_bf16_bits(acc[2 * j]) | (f32_to_bf16_bits(acc[2 * j + 1]) << 16);
