@@ -914,7 +914,7 @@ __device__ __forceinline__ void select_token(const double* __restrict__ partial,
     const size_t stride = (size_t)T * E;
     const double* p = partial + (size_t)t0 * E;
     constexpr int NE = (kSelectTokens * 64 * VPL + 255) / 256;  // entries per thread
-    constexpr int R = VPL >= 8 ? 1 : (NE < 2 ? NE : 2);          // entries per round of loads
+    constexpr int R = NE < 2 ? NE : 2;                           // entries per round of loads
 #pragma unroll
     for (int r0 = 0; r0 < NE; r0 += R) {
       double part[R][kMaxSplits];
