@@ -2909,6 +2909,15 @@ __global__ __launch_bounds__(256, 2) void k_layer(LayerArgs args) {
       counts = atomicCAS(&ctl[kCtlStart + blockIdx.x * kStartStride], 0, 1) == 0;
       slot = blockIdx.x;
     } else {
+      // The workgroups past the front-end units (with the routed lists) will most likely claim
+      // an expert unit, which cannot start before the permute has published the lists (15-60
+      // us away), so they claim one after another, ~27 ns apart by index, instead of all at
+      // once: hundreds of claims arriving together at the one counter queued for ~5 us, and
+      // the router and routing units' own claims and start flags waited behind them (the
+      // router phase of a Qwen3-30B-A3B-shaped layer ended at ~9 us instead of ~5). A
+      // workgroup that does get a front-end unit runs it as before.
+      if (!args.dense && (int)blockIdx.x >= fixed)
+        for (int k = (int)blockIdx.x - fixed; k > 0; --k) __builtin_amdgcn_s_sleep(1);
       slot = n_first + atomicAdd(&ctl[kCtlQueue], 1);
     }
   }
