@@ -4251,7 +4251,14 @@ __global__ __launch_bounds__(256, 2) void k_layer_mx(LayerMxArgs args) {
   static_assert(sizeof(LayerMxArgs) % 8 == 0 && offsetof(LayerMxArgs, ex) == 0, "argument segment layout");
   static_assert(kPermuteLdsInts * sizeof(int) <= sizeof(rings), "the permute's LDS in the rings");
   int* ctl = args.ctl;
-  if (threadIdx.x == 0) slot = atomicAdd(&ctl[kCtlQueue], 1);
+  // Every unit after the first (the permute) waits for the lists, so the workgroups claim one
+  // after another, ~27 ns apart by index, rather than all at once (as k_layer's past its
+  // front-end units): claims arriving together queue at the one counter, and the permute's
+  // own atomics wait behind them.
+  if (threadIdx.x == 0) {
+    for (int k = (int)blockIdx.x; k > 0; --k) __builtin_amdgcn_s_sleep(1);
+    slot = atomicAdd(&ctl[kCtlQueue], 1);
+  }
   __syncthreads();
   int u = slot;
 
