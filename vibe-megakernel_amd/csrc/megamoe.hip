@@ -922,12 +922,27 @@ __device__ __forceinline__ void select_token(const double* __restrict__ partial,
       for (int r = 0; r < R; ++r) {
         const int i = threadIdx.x + 256 * (r0 + r);
 #pragma unroll
-        for (int q = 0; q < kMaxSplits; ++q) {
-          // Clamped, unconditional loads (entries past the end are dropped below).
-          const double v = p[(size_t)min(q, nsplit - 1) * stride + min(i, n_here - 1)];
-          part[r][q] = q < nsplit ? v : 0.0;
-        }
+        for (int q = 0; q < kMaxSplits; ++q)  // clamped, unconditional loads
+          part[r][q] = p[(size_t)min(q, nsplit - 1) * stride + min(i, n_here - 1)];
       }
+      // Every load of the round is issued before the first add: short of registers in the
+      // single-launch kernel, the compiler otherwise sinks each load to its add and waits
+      // for each in turn (one round trip per split instead of one per round).
+      static_assert(kMaxSplits == 16, "one asm operand per split");
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+        asm volatile(""
+                     : "+v"(part[r][0]), "+v"(part[r][1]), "+v"(part[r][2]), "+v"(part[r][3]), "+v"(part[r][4]),
+                       "+v"(part[r][5]), "+v"(part[r][6]), "+v"(part[r][7]), "+v"(part[r][8]), "+v"(part[r][9]),
+                       "+v"(part[r][10]), "+v"(part[r][11]), "+v"(part[r][12]), "+v"(part[r][13]),
+                       "+v"(part[r][14]), "+v"(part[r][15])
+                     :
+                     : "memory");
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int q = 0; q < kMaxSplits; ++q)
+          if (q >= nsplit) part[r][q] = 0.0;  // entries past the end are dropped below
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         const int i = threadIdx.x + 256 * (r0 + r);
