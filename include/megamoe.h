@@ -211,6 +211,17 @@ typedef struct megamoe_epilogue {
 int megamoe_forward_ex(const megamoe_desc* desc, const megamoe_tensors* t, const megamoe_block* block,
                        const megamoe_epilogue* epilogue, void* stream, void* const* events);
 
+/* megamoe_forward_ex in the W8A16 form: the expert GEMMs read the bf16 rows (x, or the
+ * normalized x of the block form) without quantizing them, and h = bf16(silu(g) * u) stays
+ * in bf16 for the down GEMM: g, u = bf16(dequant(W, s) @ fp32(x)), d = bf16(dequant(W_d, s_d)
+ * @ fp32(h)). The routing, the combine and the tensors are megamoe_forward_ex's; x_scale
+ * work (pow2_scales) does not apply. Replaces frontier.py:180-183 with quantize=False, which
+ * the DeepSeek family uses for every expert GEMM (frontier.py:190, 265-270, DEEPSEEK_FP8_
+ * ACTIVATIONS), in the MoE step of frontier.py:335-354. Stream-ordered (five launches, six
+ * with the block's normalization); `events` as megamoe_forward_ex's. */
+int megamoe_forward_w8a16(const megamoe_desc* desc, const megamoe_tensors* t, const megamoe_block* block,
+                          const megamoe_epilogue* epilogue, void* stream, void* const* events);
+
 /* The layer (block == NULL) or the block, with an optional epilogue variant, as ONE kernel
  * launch: the arguments and results are megamoe_forward_ex's, bit for bit. The reference
  * harness audits each call's kernel launches against the case's budget, one by default
@@ -375,7 +386,8 @@ const char* megamoe_status_string(int status);
  * megamoe_ep_experts and megamoe_ep_combine in 4, plus megamoe_forward_ex and
  * megamoe_combine_by_expert_id in 5, plus megamoe_forward_noalloc in 6, plus
  * megamoe_layer_forward in 7, plus megamoe_layer_status in 8, plus megamoe_mx_layer_forward
- * and megamoe_mx_layer_status in 9, plus megamoe_e4m3_selftest in 10). */
+ * and megamoe_mx_layer_status in 9, plus megamoe_e4m3_selftest in 10, plus
+ * megamoe_forward_w8a16 in 11). */
 int megamoe_abi_version(void);
 
 #ifdef __cplusplus

@@ -11,6 +11,9 @@ Per token t (megabench/tasks/frontier.py:343-354, with ``linear`` of :180-186):
                   (case.swiglu "bf16": bf16(bf16(silu(g)) * u), frontier.py:338 and
                   glm53.py:174; case.swiglu_limit > 0: g, u clamped first, glm53.py:175)
         d       = bf16(deq(W_down[e]) @ deq(E4M3 per 128 of h))
+                  (case.activations "bf16", W8A16, frontier.py:182-183 with
+                  quantize=False: g, u = bf16(deq(W) @ fp32(x[t])), d = bf16(deq(W_down)
+                  @ fp32(h)), nothing quantized)
         acc     = acc + fp32(d) * w[slot]                          frontier.py:349-350
     acc = acc + fp32(shared expert output)                          frontier.py:352
     y[t] = bf16(acc)                                                frontier.py:354 (without
@@ -45,8 +48,13 @@ from . import formats
 from .routing import route
 
 
-def _linear(w_deq: torch.Tensor, act: torch.Tensor, power_of_two: bool, out_dtype) -> torch.Tensor:
-    """frontier.linear with the weight already dequantized: W8A8, fp32 GEMV, one rounding."""
+def _linear(w_deq: torch.Tensor, act: torch.Tensor, power_of_two: bool, out_dtype, quantize: bool = True
+            ) -> torch.Tensor:
+    """frontier.linear (frontier.py:180-186) with the weight already dequantized: W8A8 (the
+    activation quantized to E4M3 per 128 first), or with quantize=False W8A16 (the activation
+    as it is); an fp32 GEMV, one rounding."""
+    if not quantize:
+        return (w_deq @ act.float()).to(out_dtype)
     payload, scales = formats.pack_activation(act, power_of_two)
     return (w_deq @ formats.unpack_activation(payload, scales)).to(out_dtype)
 
@@ -97,10 +105,12 @@ def _layers(case, values: dict, widens, tokens=None) -> list[dict]:
     down = [{} for _ in modes]  # per mode: (row index, slot) -> [H]
     cpu = {k: v.cpu() for k, v in values.items() if k != "x"}
 
+    q = getattr(case, "activations", "fp8") != "bf16"  # W8A8, or W8A16 (quantize=False)
+
     def mlp(wg, wu, wd, m, t):
         bf, act = modes[m], acts[m]
-        h = _swiglu(case, _linear(wg, act[t], pw, bf), _linear(wu, act[t], pw, bf), bf)
-        return _linear(wd, h, pw, bf)
+        h = _swiglu(case, _linear(wg, act[t], pw, bf, q), _linear(wu, act[t], pw, bf, q), bf)
+        return _linear(wd, h, pw, bf, q)
 
     for e in sorted(set(ids_t.flatten().tolist())):
         wg, wu, wd = _expert(cpu, "gate", e), _expert(cpu, "up", e), _expert(cpu, "down", e)

@@ -37,7 +37,7 @@ def test_library_exports_every_declared_function():
 
 def test_version_and_status_strings():
     lib = _lib.load()
-    assert lib.megamoe_abi_version() == _lib.ABI_VERSION == 10
+    assert lib.megamoe_abi_version() == _lib.ABI_VERSION == 11
     texts = {code: _lib.status_string(code) for code in range(7)}
     assert texts[_lib.OK] == "ok" and len(set(texts.values())) == 7
     assert _lib.status_string(99) == "unknown status"

@@ -27,8 +27,9 @@ def _demangle(names):
 
 
 STREAM_KERNELS = [
-    "(anonymous namespace)::k_experts<false>",
-    "(anonymous namespace)::k_experts<true>",
+    "(anonymous namespace)::k_experts<false, false>",
+    "(anonymous namespace)::k_experts<true, false>",
+    "(anonymous namespace)::k_experts<false, true>",  # the W8A16 form
     "(anonymous namespace)::k_experts_mx",
     "(anonymous namespace)::k_experts_mx_batch",
 ]

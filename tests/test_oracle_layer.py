@@ -59,12 +59,14 @@ def _weight(values, name, e=None) -> np.ndarray:
     return E4M3_TABLE[codes] * full
 
 
-def _mlp(wg, wu, wd, x, widen):
+def _mlp(wg, wu, wd, x, widen, quantize=True):
+    """One expert on one row; quantize=False is the W8A16 form (x and h enter as they are)."""
     rnd = (lambda v: v.astype(np.float32).astype(np.float64)) if widen else _bf16
-    xd = _quant_act(x)
+    act = _quant_act if quantize else (lambda v: v)
+    xd = act(x)
     g, u = rnd(wg @ xd), rnd(wu @ xd)
     h = rnd(g / (1.0 + np.exp(-g)) * u)
-    return rnd(wd @ _quant_act(h))
+    return rnd(wd @ act(h))
 
 
 def brute_force(case, values, widen=False):
@@ -72,16 +74,18 @@ def brute_force(case, values, widen=False):
     T, H = x.shape
     rnd = (lambda v: v.astype(np.float32).astype(np.float64)) if widen else _bf16
     xin = x.double().numpy() if widen else x.to(torch.bfloat16).double().numpy()
+    q = case.activations != "bf16"
     y = np.zeros((T, H))
     for t in range(T):
         ids, w = routing.route(case, values["router"].float() @ x[t], values.get("router_bias"))
         acc = np.zeros(H)
         for slot, e in enumerate(ids.tolist()):
-            d = _mlp(_weight(values, "gate", e), _weight(values, "up", e), _weight(values, "down", e), xin[t], widen)
+            d = _mlp(_weight(values, "gate", e), _weight(values, "up", e), _weight(values, "down", e), xin[t], widen,
+                     q)
             acc += d * np.float64(w[slot])
         if case.shared_experts:
             acc += _mlp(_weight(values, "shared_gate"), _weight(values, "shared_up"), _weight(values, "shared_down"),
-                        xin[t], widen)
+                        xin[t], widen, q)
         y[t] = rnd(acc)
     return torch.from_numpy(y)
 
@@ -89,7 +93,8 @@ def brute_force(case, values, widen=False):
 def _cases():
     return [C.development(C.case("moe-fp8-deepseek-v3-t64"), tokens=5, experts=8, topk=3),
             C.development(C.case("moe-fp8-mixtral-t16"), tokens=4),
-            C.development(C.case("moe-fp8-kimi-k2-t128"), tokens=3, experts=8)]
+            C.development(C.case("moe-fp8-kimi-k2-t128"), tokens=3, experts=8),
+            C.development(C.case("moe-fp8-deepseek-v3-t64-w8a16"), tokens=5, experts=8, topk=3)]
 
 
 @pytest.mark.parametrize("case", _cases(), ids=lambda c: c.id)
@@ -147,6 +152,38 @@ def test_brute_force_catches_planted_mistakes(kind):
     with _Planted(kind):
         got = layer.reference(case, values)
     assert not metrics.layer_checks(got["y"], want)["pass"], kind
+
+
+def test_w8a16_brute_force_catches_a_quantized_activation():
+    """The W8A16 oracle quantizing x and h anyway (the W8A8 schedule) fails the W8A16 brute
+    force: E4M3 moves each activation by up to 1/16 of its value."""
+    case = C.development(C.case("moe-fp8-deepseek-v3-t64-w8a16"), tokens=3, experts=8, topk=3)
+    values = workloads.make_inputs(case, 29, "cpu")
+    want = brute_force(case, values)
+    assert metrics.layer_checks(layer.reference(case, values)["y"], want)["pass"]
+    w8a8 = layer.reference(C.development(C.case("moe-fp8-deepseek-v3-t64"), tokens=3, experts=8, topk=3), values)
+    assert not metrics.layer_checks(w8a8["y"], want)["pass"]
+
+
+def test_w8a16_linear_equals_w8a8_on_activations_the_e4m3_grid_holds():
+    """frontier.linear's two forms agree bit for bit where quantizing changes nothing: each
+    128-block of the activation is E4M3 values times 2^k with one element at +-448 * 2^k, so
+    the scale is 2^k and every code is exact (quantization.py:57-59)."""
+    g = torch.Generator().manual_seed(31)
+    codes = torch.randint(0, 256, (512,), generator=g)
+    codes[(codes & 0x7f) == 0x7f] = 0x70  # no NaN codes
+    vals = torch.from_numpy(E4M3_TABLE[codes.numpy()]).float()
+    vals[::128] = 448.0
+    act = (vals * torch.repeat_interleave(2.0 ** torch.tensor([-3.0, 0.0, 2.0, -7.0]), 128)).to(torch.bfloat16)
+    assert torch.equal(act.float(), vals * torch.repeat_interleave(2.0 ** torch.tensor([-3.0, 0.0, 2.0, -7.0]), 128))
+    w = torch.randn((40, 512), generator=g)
+    a8 = layer._linear(w, act, False, torch.bfloat16, True)
+    a16 = layer._linear(w, act, False, torch.bfloat16, False)
+    assert torch.equal(a8, a16)
+    # Off the grid they differ (the activation moves).
+    off = act.float() * 1.01
+    assert not torch.equal(layer._linear(w, off.to(torch.bfloat16), False, torch.bfloat16, True),
+                           layer._linear(w, off.to(torch.bfloat16), False, torch.bfloat16, False))
 
 
 def test_rows_are_independent_and_token_subsets_agree():

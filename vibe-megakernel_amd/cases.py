@@ -91,6 +91,10 @@ class Case:
     # (frontier.py:337, DeepSeek), "bf16" h = bf16(bf16(silu(g)) * u) (frontier.py:338,
     # glm53.py:174-175); swiglu_limit > 0 clamps g and u first in either form.
     swiglu: str = "fp32"
+    # Activations of the fp8 expert GEMMs: "fp8" quantizes x and h to E4M3 per 128 (W8A8,
+    # frontier.py:185-186); "bf16" feeds them in bf16 (W8A16, frontier.py:182-183 with
+    # quantize=False: the DeepSeek family's expert GEMMs, frontier.py:190,265-270).
+    activations: str = "fp8"
 
     def __post_init__(self) -> None:
         if not self.id or self.family != FAMILY or not self.model or not self.phase:
@@ -115,6 +119,8 @@ class Case:
             raise ValueError(f"invalid SwiGLU form in {self.id}")
         if self.format not in FORMATS:
             raise ValueError(f"invalid expert format in {self.id}")
+        if self.activations not in ("fp8", "bf16") or (self.activations == "bf16" and self.format != "fp8"):
+            raise ValueError(f"{self.id}: bf16 activations (W8A16) are a form of the fp8 experts")
         if (self.format == "mxfp4") != (self.router == "given"):
             raise ValueError(f"{self.id}: the MXFP4 form takes its routing as an input, and only it does")
         if self.format == "mxfp4" and (p["hidden"] % 256 or p["intermediate"] % 256 or p.get("shared_experts", 0)
@@ -261,11 +267,16 @@ VARIANT_CASES: tuple[Case, ...] = (
 # squeezes the top scores together and the bias decides most selections, so 64 tokens hit
 # only ~120 of the 256 experts (the headline's timing inputs: 120); without it ~222 are hit,
 # ~2.3 rows each, the uniform-routing expectation that the per-config floors assume.
+# "-w8a16": the expert GEMMs with bf16 activations (frontier.py:180-183, quantize=False),
+# as the DeepSeek family's TileRT numerics run them (frontier.py:190,265-270).
 HEADLINE_VARIANTS: tuple[Case, ...] = (
     replace(next(c for c in CASES if c.id == HEADLINE), id=HEADLINE + "-ue8m0", power_of_two=True,
             note="power-of-two (UE8M0) weight and activation scales"),
     replace(next(c for c in CASES if c.id == HEADLINE), id=HEADLINE + "-nobias", bias="none",
             note="no correction bias: ~222 experts hit, ~2.3 rows each"),
+    replace(next(c for c in CASES if c.id == HEADLINE), id=HEADLINE + "-w8a16", activations="bf16",
+            max_gpu_launches=5,
+            note="W8A16: bf16 activations into the expert GEMMs (stream-ordered, five launches)"),
 )
 
 

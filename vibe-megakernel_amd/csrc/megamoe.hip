@@ -57,6 +57,8 @@ constexpr uint64_t kWaitTicks = 20000000;  // 0.2 s
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 // ---------------------------------------------------------------------------------------
 // Scalar numerics shared by the kernels
@@ -1056,6 +1058,7 @@ __device__ unsigned long long block_exclusive_scan(unsigned long long v, unsigne
 constexpr int kMetaHit = 0, kMetaUnitsGU = 1, kMetaUnitsDN = 2, kMetaQueueGU = 3, kMetaQueueDN = 4,
               kMetaWide = 5, kMetaError = 32, kMetaInts = 64;
 constexpr int kChunkRows = 64;     // rows per chunk of the fp8 form (column tiles of up to 4)
+constexpr int kChunkRowsA16 = 32;  // of its W8A16 form (bf16 activations: column tiles of up to 2)
 constexpr int kChunkRowsMx = 128;  // of the MXFP4 form: wide units over 33-128 rows, narrow up to 32
 
 struct PermuteOut {
@@ -1292,7 +1295,7 @@ __device__ __forceinline__ void permute_block(const int64_t* __restrict__ ids, i
     if (S > 0) {
       for (int i = 0; i * chunk < T; ++i) {
         const int rows = min(chunk, T - chunk * i);
-        const int cls = chunk_class(rows);
+        const int cls = rows == chunk ? 0 : chunk_class(rows);  // a full chunk is counted in s4 (sf)
         const int idx = cls == 0 ? i : 0;        // index within the shared part of the class
         const int per_copy = cls == 0 ? s4 : 1;  // shared chunks of this class per copy
         for (int s = 0; s < S; ++s) {
@@ -1534,11 +1537,21 @@ __device__ __forceinline__ LaneTile lane_tile(int lda) {
   return LaneTile{lr * lda + (((lane & 7) ^ lr) << 4), base + ((g ^ rr) << 4), base + (((g + 4) ^ rr) << 4)};
 }
 
-template <int NCT, int SG>
+template <int NCT, int SG, bool A16 = false>
 struct Stage {
   i32x8 b[NCT];
   float sw[SG];
   float sx[NCT];
+};
+
+// The stage of the W8A16 form (frontier.py:180-183, quantize=False): bf16 activations, no
+// activation scale. Column tile c's 32 K values of the lane come as four chunks of eight
+// (K 16g .. 16g+7, 16g+8 .., 64+16g .., 72+16g .. for lane group g = lane / 16: the K
+// values the fp8 weight operand of the lane holds, in the same order).
+template <int NCT, int SG>
+struct Stage<NCT, SG, true> {
+  i32x4 b[NCT][4];
+  float sw[SG];
 };
 
 template <int RT, int NCT, int SG>
@@ -1577,6 +1590,21 @@ __device__ __forceinline__ void load_stage_b(Stage<NCT, SG>& s, const Operands<R
   for (int c = 0; c < NCT; ++c) s.b[c] = load_k32(op.b[c] + o);
 #pragma unroll
   for (int c = 0; c < NCT; ++c) s.sx[c] = op.sx[c][kb];
+#pragma unroll
+  for (int g = 0; g < SG; ++g) s.sw[g] = op.sw[g][kb];
+}
+
+// W8A16: 4*NCT vector loads, four 16-byte bf16 chunks per column tile (op.b[c] points at
+// the lane's first chunk of K block 0: 2 * kBlock bytes a block, chunks at +0, +16, +128,
+// +144).
+template <int RT, int NCT, int SG>
+__device__ __forceinline__ void load_stage_b(Stage<NCT, SG, true>& s, const Operands<RT, NCT, SG>& op, int kb) {
+  const size_t o = (size_t)kb * 2 * kBlock;
+#pragma unroll
+  for (int c = 0; c < NCT; ++c)
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      s.b[c][q] = *reinterpret_cast<const i32x4*>(op.b[c] + o + (q >> 1) * 128 + (q & 1) * 16);
 #pragma unroll
   for (int g = 0; g < SG; ++g) s.sw[g] = op.sw[g][kb];
 }
@@ -1728,6 +1756,51 @@ __device__ __forceinline__ void compute_stage(uint32_t slot, const LaneTile& lt,
   }
 }
 
+// Eight e4m3 values (two dwords, lowest byte first) as eight bf16: the conversion is exact
+// (every e4m3 value is a bf16 value), two values per instruction.
+__device__ __forceinline__ i32x4 e4m3x8_to_bf16(int lo, int hi) {
+  i32x4 r;
+  r[0] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, false));
+  r[1] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, true));
+  r[2] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, false));
+  r[3] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, true));
+  return r;
+}
+
+// W8A16 stage: each weight tile's 32 e4m3 values of the lane become four bf16 chunks, and
+// four 16x16x32 bf16 MFMAs (chunk q of the weights against chunk q of the activations, the
+// same K values) give the block's product, which the block's weight scale multiplies into
+// the fp32 sum, as in the W8A8 stage (frontier.py:180-183: dequant(W, s) @ fp32(x)).
+template <int RT, int NCT, int SG>
+__device__ __forceinline__ void compute_stage(uint32_t slot, const LaneTile& lt, const Stage<NCT, SG, true>& s,
+                                              f32x4 (&acc)[RT][NCT]) {
+  i32x8 at[RT];
+  read_slot<RT>(at, slot + lt.rd0, slot + lt.rd1);
+  float sw[SG];
+#pragma unroll
+  for (int g = 0; g < SG; ++g) {
+    sw[g] = s.sw[g];
+    asm volatile("" : "+v"(sw[g]));
+  }
+#pragma unroll
+  for (int r = 0; r < RT; ++r) {
+    i32x4 a[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) a[q] = e4m3x8_to_bf16(at[r][2 * q], at[r][2 * q + 1]);
+#pragma unroll
+    for (int c = 0; c < NCT; ++c) {
+      f32x4 p = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a[q]),
+                                                    __builtin_bit_cast(bf16x8, s.b[c][q]), p, 0, 0, 0);
+      const float k = sw[r * SG / RT];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) acc[r][c][v] = __builtin_fmaf(p[v], k, acc[r][c][v]);
+    }
+  }
+}
+
 // Streams nkb K blocks through the wavefront's LDS ring (D slots) with D-1 stages of loads
 // in flight. With a ReadyWait, the weights of the first stages are requested before the
 // wait and the activations (which another workgroup produces) after it, so the wait's
@@ -1747,7 +1820,8 @@ __device__ __forceinline__ void compute_stage(uint32_t slot, const LaneTile& lt,
 // complete in issue order, and the compiler's own counters do not cover the LDS that
 // global_load_lds writes. When stage s is consumed, each of stages s+1 .. s+D-1 has been
 // issued after stage s's weights, as a group of 2*RT weight loads and at least 3*NCT
-// activation loads, so vmcnt <= (D-1)*(2*RT + 3*NCT) implies stage s has landed.
+// activation loads (4*NCT in the W8A16 form), so vmcnt <= (D-1)*(2*RT + 3*NCT) (or 4*NCT)
+// implies stage s has landed.
 // Loads past the last K block are not skipped: a branch around them would merge paths with
 // different load counts, and the compiler then waits for vmcnt 0 before the next MFMA,
 // which drains the pipeline at every stage. They read the spare region instead (every
@@ -1755,7 +1829,7 @@ __device__ __forceinline__ void compute_stage(uint32_t slot, const LaneTile& lt,
 // since non-temporal lines do not stay in L2) into slots nothing reads any more, and they
 // land before any later load into the ring (issue order). The slot a stage overwrites was
 // read (ds_read, issued in program order before the overwriting load) one stage earlier.
-template <int RT, int NCT, int SG, int D>
+template <int RT, int NCT, int SG, int D, bool A16 = false>
 __device__ __forceinline__ void stream_gemm(const Operands<RT, NCT, SG>& op, int nkb, int rot, uint8_t* ring,
                                             f32x4 (&acc)[RT][NCT],
                                             const ReadyWait& ready = ReadyWait{nullptr, 0, nullptr}) {
@@ -1765,7 +1839,7 @@ __device__ __forceinline__ void stream_gemm(const Operands<RT, NCT, SG>& op, int
     return p >= nkb ? p - nkb : p;
   };
   constexpr int kSlot = RT * kTileBytes;
-  constexpr int kAfter = (D - 1) * (2 * RT + 3 * NCT);
+  constexpr int kAfter = (D - 1) * (2 * RT + (A16 ? 4 : 3) * NCT);
   static_assert(D >= 2 && D * kSlot <= kRingWave, "LDS ring");
   const LaneTile lt = lane_tile(op.lda);
   const uint32_t ring_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)ring;
@@ -1773,7 +1847,7 @@ __device__ __forceinline__ void stream_gemm(const Operands<RT, NCT, SG>& op, int
   for (int r = 0; r < RT; ++r)
 #pragma unroll
     for (int c = 0; c < NCT; ++c) acc[r][c] = f32x4{0.f, 0.f, 0.f, 0.f};
-  Stage<NCT, SG> st[D];
+  Stage<NCT, SG, A16> st[D];
 #pragma unroll
   for (int s = 0; s < D - 1; ++s) issue_a(ring + s * kSlot, op, lt, phys(min(s, nkb - 1)), s < nkb);
   issue_claim(ready);
@@ -1969,6 +2043,10 @@ struct GateUpArgs {
   int swiglu;                   // 0: fp32 product rounded once; 1: bf16 silu, bf16 product
   float limit;                  // > 0: SwiGLU clamp (gate above, up both sides)
   int dense;                    // the dense schedule: units from dense_gu_chunk, h rows e*T + t
+  int pad_;
+  const uint16_t* x16;          // W8A16: the bf16 rows [T, H] the experts read (x, or the normalized x)
+  uint16_t* h16_r;              // W8A16: bf16 h of the routed rows [rows_r, I]
+  uint16_t* h16_s;              // W8A16: of the shared rows [T, S*I]
 };
 
 // One gate/up unit: rows [jb*128, jb*128+128) of gate and of up against the chunk's
@@ -2047,12 +2125,68 @@ __device__ __forceinline__ void gateup_unit(const GateUpArgs& a, const uint8_t* 
   }
 }
 
+// The W8A16 gate/up unit (frontier.py:180-183 with quantize=False, the expert GEMMs of the
+// DeepSeek family at frontier.py:265-270): gateup_unit's rows and waves, with the bf16 rows
+// of x as the activations; g and u are rounded to bf16 (frontier.py:183), clamped if a
+// SwiGLU limit is set, and h = bf16(silu(fp32 g) * fp32 u) (frontier.py:337) or
+// bf16(bf16(silu(g)) * u) (glm53.py:174-175) stays in bf16 for the down units (no
+// requantization).
+template <int NCT>
+__device__ __forceinline__ void gateup_unit16(const GateUpArgs& a, const uint8_t* wg, const uint8_t* wu,
+                                              const float* sg, const float* su, const ChunkRows& cr, int jb,
+                                              uint16_t* h, int ldh, int rot, uint8_t* ring, const ReadyWait& ready) {
+  const int lane = opaque_lane(), w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int H = a.H;
+  Operands<4, NCT, 2> op;
+  op.lda = H;
+  op.spare = a.spare;
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const size_t row = (size_t)(32 * w + 16 * r);
+    op.a[r] = wg + row * H;
+    op.a[r + 2] = wu + row * H;
+  }
+  op.sw[0] = sg;
+  op.sw[1] = su;
+  int orow[NCT];
+#pragma unroll
+  for (int c = 0; c < NCT; ++c) {
+    const int r = min(16 * c + (lane & 15), cr.n - 1);  // padding columns repeat a valid row
+    const int tok = row_token(cr, r);
+    op.b[c] = reinterpret_cast<const uint8_t*>(a.x16 + (size_t)tok * H) + 32 * (lane >> 4);
+    op.sx[c] = nullptr;
+    orow[c] = cr.by_token ? cr.out_base + tok : cr.row0 + r;
+  }
+  f32x4 acc[4][NCT];
+  stream_gemm<4, NCT, 2, 2, true>(op, H / kBlock, rot, ring, acc, ready);
+  const bool bf16_silu = a.swiglu != 0;
+  const float L = a.limit > 0.0f ? a.limit : INFINITY;
+#pragma unroll
+  for (int c = 0; c < NCT; ++c) {
+    if (16 * c + (lane & 15) >= cr.n) continue;
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      uint32_t bits[4];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const float g = fminf(round_bf16(acc[p][c][v]), L);
+        const float u = fminf(fmaxf(round_bf16(acc[p + 2][c][v]), -L), L);
+        bits[v] = f32_to_bf16_bits(bf16_silu ? round_bf16(silu(g)) * u : silu(g) * u);
+      }
+      uint16_t* dst = h + (size_t)orow[c] * ldh + (size_t)jb * kBlock + 32 * w + 16 * p + 4 * (lane >> 4);
+      store_coherent(reinterpret_cast<uint64_t*>(dst),
+                     (uint64_t)(bits[0] | (bits[1] << 16)) | ((uint64_t)(bits[2] | (bits[3] << 16)) << 32));
+    }
+  }
+}
+
 // Gate/up unit u of the work list (of the dense schedule's lists): chunk u / nbI, 128-row
 // block u % nbI of the chunk's expert (plus the slice offset of a shared-expert copy).
 // `ready`: a count to wait for before the activation rows are read (the quantized x of the
 // single launch's dense schedule), after the unit's first weight stages are requested.
 // In the dense schedule, `known`: the routing is known (the unit works its expert's routed
 // rows; else every token).
+template <bool A16 = false>
 __device__ __forceinline__ void gateup_work(const GateUpArgs& a, int u, float (*red)[64], uint8_t* ring,
                                             const ReadyWait& ready = ReadyWait{nullptr, 0, nullptr},
                                             bool known = true) {
@@ -2087,12 +2221,20 @@ __device__ __forceinline__ void gateup_work(const GateUpArgs& a, int u, float (*
     hs = a.hs_r;
     ldh = a.I;
   }
-  if (cr.n <= 16)
+  if constexpr (A16) {
+    // Chunks of at most 32 rows (the W8A16 form's permute).
+    uint16_t* h = ch.x == a.E ? a.h16_s : a.h16_r;
+    if (cr.n <= 16)
+      gateup_unit16<1>(a, wg, wu, sg, su, cr, jb, h, ldh, rot, ring, ready);
+    else
+      gateup_unit16<2>(a, wg, wu, sg, su, cr, jb, h, ldh, rot, ring, ready);
+  } else if (cr.n <= 16) {
     gateup_unit<1>(a, wg, wu, sg, su, cr, jb, hq, hs, ldh, rot, red, ring, ready);
-  else if (cr.n <= 32)
+  } else if (cr.n <= 32) {
     gateup_unit<2>(a, wg, wu, sg, su, cr, jb, hq, hs, ldh, rot, red, ring, ready);
-  else
+  } else {
     gateup_unit<4>(a, wg, wu, sg, su, cr, jb, hq, hs, ldh, rot, red, ring, ready);
+  }
 }
 
 // One half of a gate/up block: rows [jb*128, jb*128+128) of gate (half 0) or of up (half 1)
@@ -2277,13 +2419,16 @@ struct DownArgs {
   int T, H, I, K, S, E, ks;
   int dense;      // the dense schedule: units from dense_dn_chunk, rows e*T + t
   int rows_r;     // routed rows of d_r and of each part of p_r: T*K, or E*T in the dense schedule
+  const uint16_t* h16_r;  // W8A16: bf16 h of the routed rows [rows_r, I]
+  const uint16_t* h16_s;  // W8A16: of the shared rows [T, S*I]
 };
 
 // One down unit: rows [j*128, j*128+128) of a down matrix [H, ldk] against the chunk's
 // requantized h rows, over K part kp of a.ks (K blocks [kp*nkb/ks, (kp+1)*nkb/ks)). Wave w
 // owns rows 32w .. 32w+31. With one part the result is d in bf16; with several, each part
 // stores its fp32 partial to pd and the combine adds the parts in order before rounding.
-template <int NCT, bool CO>
+// A16: the W8A16 form; hq then holds the bf16 h rows (2 * ldk bytes a row), hs is unused.
+template <int NCT, bool CO, bool A16 = false>
 __device__ __forceinline__ void down_unit(const DownArgs& a, const uint8_t* wd, const float* sd, int ldk, const uint8_t* hq,
                           const float* hs, const ChunkRows& cr, int j, int kp, uint16_t* d, float* pd,
                           int rot, const ReadyWait& ready, uint8_t* ring) {
@@ -2301,11 +2446,19 @@ __device__ __forceinline__ void down_unit(const DownArgs& a, const uint8_t* wd, 
   for (int c = 0; c < NCT; ++c) {
     const int r = min(16 * c + (lane & 15), cr.n - 1);
     orow[c] = out_row(cr, r);
-    op.b[c] = hq + (size_t)orow[c] * ldk + (size_t)kb0 * kBlock + kofs;
-    op.sx[c] = hs + (size_t)orow[c] * scale_ld(nkb) + kb0;
+    if constexpr (A16) {
+      op.b[c] = hq + ((size_t)orow[c] * ldk + (size_t)kb0 * kBlock) * 2 + 2 * kofs;
+      op.sx[c] = nullptr;
+    } else {
+      op.b[c] = hq + (size_t)orow[c] * ldk + (size_t)kb0 * kBlock + kofs;
+      op.sx[c] = hs + (size_t)orow[c] * scale_ld(nkb) + kb0;
+    }
   }
   f32x4 acc[2][NCT];
-  if constexpr (NCT == 4) {
+  if constexpr (A16) {
+    static_assert(NCT <= 2, "W8A16 chunks hold at most 32 rows");
+    stream_gemm<2, NCT, 1, 4, true>(op, nkbp, rot, ring, acc, ready);
+  } else if constexpr (NCT == 4) {
     // DMA sources of this wave's column tile: lane l moves chunk (l % 8) ^ (l / 8) of row
     // 8i + l / 8 (clamped to the chunk's rows), as the weight tiles.
     const int lr = lane >> 3;
@@ -2345,7 +2498,7 @@ __device__ __forceinline__ void down_unit(const DownArgs& a, const uint8_t* wd, 
 // matrix and K part kp (v % (nbH*ks) = j*ks + kp).
 // In the dense schedule, `known`: the routing is known (the unit works its expert's routed
 // rows; else every token).
-template <bool CO>
+template <bool CO, bool A16 = false>
 __device__ __forceinline__ void down_work(const DownArgs& a, int v, const ReadyWait& ready, uint8_t* ring,
                                           bool known = true) {
   const int nbH = a.H / kBlock, nbI = a.I / kBlock;
@@ -2360,6 +2513,14 @@ __device__ __forceinline__ void down_work(const DownArgs& a, int v, const ReadyW
     const ChunkRows cr{ch.z, ch.y, nullptr, a.K};
     const uint8_t* wd = a.sdown + (size_t)j * kBlock * ldk;
     const float* sd = a.sdown_scale + (size_t)j * (ldk / kBlock);
+    if constexpr (A16) {
+      const uint8_t* h = reinterpret_cast<const uint8_t*>(a.h16_s);
+      if (cr.n <= 16)
+        down_unit<1, CO, true>(a, wd, sd, ldk, h, nullptr, cr, j, kp, a.d_s, pd_s, rot, ready, ring);
+      else
+        down_unit<2, CO, true>(a, wd, sd, ldk, h, nullptr, cr, j, kp, a.d_s, pd_s, rot, ready, ring);
+      return;
+    }
     if (cr.n <= 16)
       down_unit<1, CO>(a, wd, sd, ldk, a.hq_s, a.hs_s, cr, j, kp, a.d_s, pd_s, rot, ready, ring);
     else if (cr.n <= 32)
@@ -2373,6 +2534,14 @@ __device__ __forceinline__ void down_work(const DownArgs& a, int v, const ReadyW
     const size_t rowblk = (size_t)ch.x * nbH + j;
     const uint8_t* wd = a.down + rowblk * kBlock * a.I;
     const float* sd = a.down_scale + rowblk * nbI;
+    if constexpr (A16) {
+      const uint8_t* h = reinterpret_cast<const uint8_t*>(a.h16_r);
+      if (cr.n <= 16)
+        down_unit<1, CO, true>(a, wd, sd, a.I, h, nullptr, cr, j, kp, a.d_r, pd_r, rot, ready, ring);
+      else
+        down_unit<2, CO, true>(a, wd, sd, a.I, h, nullptr, cr, j, kp, a.d_r, pd_r, rot, ready, ring);
+      return;
+    }
     if (cr.n <= 16)
       down_unit<1, CO>(a, wd, sd, a.I, a.hq_r, a.hs_r, cr, j, kp, a.d_r, pd_r, rot, ready, ring);
     else if (cr.n <= 32)
@@ -2584,7 +2753,9 @@ struct ExpertArgs {
 // SPLIT: each 128-row block of gate/up is worked as two units, gate and up, and the one
 // that finishes second forms h (gateup_half); otherwise one unit multiplies both
 // (gateup_unit). The two give the same bits; the host picks one from the geometry.
-template <bool SPLIT>
+// A16: the W8A16 form (bf16 activations and h; whole-block gate/up units, chunks of at most
+// 32 rows).
+template <bool SPLIT, bool A16 = false>
 __global__ __launch_bounds__(256, 2) void k_experts(ExpertArgs args) {
   typedef const __attribute__((address_space(4))) ExpertArgs* ArgsPtr;
   __shared__ float red[4][64];
@@ -2629,7 +2800,8 @@ __global__ __launch_bounds__(256, 2) void k_experts(ExpertArgs args) {
       } else {
         const int c = u / nbI;
         if (!(dense && c >= a.gu.S && a.gu.offsets[c - a.gu.S + 1] == a.gu.offsets[c - a.gu.S]))
-          gateup_work(a.gu, u, red, ring, claiming(ReadyWait{nullptr, 0, nullptr}, &meta[kMetaQueueGU], &ticket));
+          gateup_work<A16>(a.gu, u, red, ring,
+                           claiming(ReadyWait{nullptr, 0, nullptr}, &meta[kMetaQueueGU], &ticket));
       }
       if (done) {
         publish_fence();
@@ -2641,10 +2813,10 @@ __global__ __launch_bounds__(256, 2) void k_experts(ExpertArgs args) {
       const int v = u - total_gu, c = v / (nbH * a.dn.ks), e = c - (a.dn.S > 0 ? 1 : 0);
       if (!(dense && e >= 0 && a.gu.offsets[e + 1] == a.gu.offsets[e])) {
         const int need = dense ? dense_dn_need(c, a.dn.S, nbI) : (a.dn.chunks[c].x == a.dn.E ? a.dn.S * nbI : nbI);
-        down_work<false>(a.dn, v,
-                         claiming(ReadyWait{&a.ready[(size_t)c * a.ready_stride], need, &meta[kMetaError]},
-                                  &meta[kMetaQueueGU], &ticket),
-                         ring);
+        down_work<false, A16>(a.dn, v,
+                              claiming(ReadyWait{&a.ready[(size_t)c * a.ready_stride], need, &meta[kMetaError]},
+                                       &meta[kMetaQueueGU], &ticket),
+                              ring);
       }
     }
     if (threadIdx.x == 0) slot = ticket >= 0 ? ticket : claim_ticket(&meta[kMetaQueueGU]);
@@ -4394,7 +4566,7 @@ inline size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
 struct Layout {
   size_t xn, partial, xq, xs, counts, offsets, meta, perm, inv, gu, dn, dn_of_gu, ready, ready_l, pairs, hq_r, hs_r,
-      hq_s, hs_s, st_r, st_s, d_r, d_s, p_r, p_s, spare, ctl, total;
+      hq_s, hs_s, st_r, st_s, h16_r, h16_s, d_r, d_s, p_r, p_s, spare, ctl, total;
   int nsplit;
   int ks;  // K parts of each down unit
   int ready_stride;  // ints between two readiness counters
@@ -4471,32 +4643,44 @@ Layout make_layout(const megamoe_desc& d) {
   };
   L.xn = take(T * H * 2);  // normalized x of the block form
   L.partial = take((size_t)L.nsplit * T * E * sizeof(double));
-  L.xq = take(T * H);
-  L.xs = take(T * (H / kBlock) * sizeof(float));
   L.counts = take(E * sizeof(int));
   L.offsets = take((E + 1) * sizeof(int));
   L.meta = take(kMetaInts * sizeof(int));
   L.perm = take(T * K * sizeof(int));
   L.inv = take(T * K * sizeof(int));
-  L.gu = take(max_chunks(d, (int)S) * sizeof(int4));
-  L.dn = take(max_chunks(d, S > 0 ? 1 : 0) * sizeof(int4));
-  L.dn_of_gu = take(max_chunks(d, (int)S) * sizeof(int));
+  // The lists hold the chunks of either form (the W8A16 form's are smaller, so more).
+  L.gu = take(max_chunks(d, (int)S, kChunkRowsA16) * sizeof(int4));
+  L.dn = take(max_chunks(d, S > 0 ? 1 : 0, kChunkRowsA16) * sizeof(int4));
+  L.dn_of_gu = take(max_chunks(d, (int)S, kChunkRowsA16) * sizeof(int));
   const size_t dn_chunks = max_chunks(d, S > 0 ? 1 : 0);
   L.ready_stride = dn_chunks <= kReadySpreadChunks ? kReadySpread : kReadyLine;
-  L.ready = take(dn_chunks * L.ready_stride * sizeof(int));
+  L.ready = take(max_chunks(d, S > 0 ? 1 : 0, kChunkRowsA16) * L.ready_stride * sizeof(int));
   // The dense schedule's down chunks: the routed experts and the shared expert. The single
   // launch counts them in a region of its own (the stream-ordered form leaves `ready`
   // counted up, and the permute that zeroes it runs after the single launch's first units).
   L.dense = dense_experts(d) ? 1 : 0;
   L.n_ready_l = L.dense ? (int)(E + (S > 0 ? 1 : 0)) : 0;
   L.ready_l = take((size_t)L.n_ready_l * L.ready_stride * sizeof(int));
-  L.pairs = take(max_chunks(d, (int)S) * (I / kBlock) * sizeof(int));
+  L.pairs = take(max_chunks(d, (int)S, kChunkRowsA16) * (I / kBlock) * sizeof(int));
   const size_t R = L.dense ? E * T : T * K;  // routed rows: grouped, or e*T + t
   L.rows_r = (int)R;
-  L.hq_r = take(R * I);
-  L.hs_r = take(R * scale_ld((int)(I / kBlock)) * sizeof(float));
-  L.hq_s = take(T * S * I);
-  L.hs_s = take(T * scale_ld((int)(S * I / kBlock)) * sizeof(float));
+  // The quantized x and h of the W8A8 form and the bf16 h of the W8A16 form (which
+  // quantizes nothing) share one region.
+  {
+    const size_t q[6] = {align_up(T * H), align_up(T * (H / kBlock) * sizeof(float)), align_up(R * I),
+                         align_up(R * scale_ld((int)(I / kBlock)) * sizeof(float)), align_up(T * S * I),
+                         align_up(T * scale_ld((int)(S * I / kBlock)) * sizeof(float))};
+    const size_t fp8 = q[0] + q[1] + q[2] + q[3] + q[4] + q[5], a16 = align_up(R * I * 2) + align_up(T * S * I * 2);
+    const size_t base = take(fp8 > a16 ? fp8 : a16);
+    L.xq = base;
+    L.xs = L.xq + q[0];
+    L.hq_r = L.xs + q[1];
+    L.hs_r = L.hq_r + q[2];
+    L.hq_s = L.hs_r + q[3];
+    L.hs_s = L.hq_s + q[4];
+    L.h16_r = base;
+    L.h16_s = base + align_up(R * I * 2);
+  }
   const bool split = split_gate_up(d);  // staging of the separate gate and up units
   L.st_r = take(split ? 2 * T * K * I * 2 : 0);
   L.st_s = take(split ? 2 * T * S * I * 2 : 0);
@@ -4686,6 +4870,9 @@ void fill_expert_args(const megamoe_desc& d, const Layout& L, const megamoe_tens
   ga.swiglu = epi ? epi->swiglu : 0;
   ga.limit = epi ? epi->swiglu_limit : 0.0f;
   ga.dense = L.dense;
+  ga.x16 = nullptr;  // set by the W8A16 form
+  ga.h16_r = (uint16_t*)(ws + L.h16_r);
+  ga.h16_s = (uint16_t*)(ws + L.h16_s);
   DownArgs& da = ea.dn;
   da.down = t->down; da.down_scale = t->down_scale;
   da.sdown = t->shared_down; da.sdown_scale = t->shared_down_scale;
@@ -4699,22 +4886,25 @@ void fill_expert_args(const megamoe_desc& d, const Layout& L, const megamoe_tens
   da.T = T; da.H = H; da.I = I; da.K = K; da.S = S; da.E = E;
   da.dense = L.dense;
   da.rows_r = L.rows_r;
+  da.h16_r = ga.h16_r;
+  da.h16_s = ga.h16_s;
   ea.dn_of_gu = po.dn_of_gu;
   ea.ready = po.ready;
   ea.ready_stride = po.ready_stride;
 }
 
 // The most gate/up and down units one call's lists can hold (the dense schedule's exactly).
-size_t expert_units_max(const megamoe_desc& d, const Layout& L, bool split) {
+size_t expert_units_max(const megamoe_desc& d, const Layout& L, bool split, int chunk = kChunkRows) {
   const size_t nbI = d.intermediate / kBlock, nbH = d.hidden / kBlock, S = d.shared_experts, E = d.experts;
   if (L.dense) return (S + E) * nbI + (E + (S > 0 ? 1 : 0)) * nbH * L.ks;
-  return (split ? 2 : 1) * max_chunks(d, (int)S) * nbI + max_chunks(d, S > 0 ? 1 : 0) * nbH * L.ks;
+  return (split ? 2 : 1) * max_chunks(d, (int)S, chunk) * nbI + max_chunks(d, S > 0 ? 1 : 0, chunk) * nbH * L.ks;
 }
 
 // The layer; with `blk`, the block form: RMSNorm of x before the router (the layer then
-// reads the normalized rows) and the residual add in the combine.
+// reads the normalized rows) and the residual add in the combine. With `a16`, the W8A16
+// form: the experts read the bf16 rows (x is not quantized) and keep h in bf16.
 int forward_impl(const megamoe_desc* desc, const megamoe_tensors* t, hipStream_t st, hipEvent_t* ev,
-                 const megamoe_block* blk = nullptr, const megamoe_epilogue* epi = nullptr) {
+                 const megamoe_block* blk = nullptr, const megamoe_epilogue* epi = nullptr, bool a16 = false) {
   int rc = validate(desc);
   if (rc) return rc;
   if (!t) return MEGAMOE_ERR_INVALID_ARGUMENT;
@@ -4749,29 +4939,33 @@ int forward_impl(const megamoe_desc* desc, const megamoe_tensors* t, hipStream_t
   if (mark(1) != hipSuccess) return MEGAMOE_ERR_HIP;
 
   if ((rc = launch_select(d, (const double*)(ws + L.partial), L.nsplit, nullptr, t->router_bias, t->expert_ids,
-                          t->expert_weights, x, (uint8_t*)(ws + L.xq), (float*)(ws + L.xs), st)))
+                          t->expert_weights, a16 ? nullptr : x, (uint8_t*)(ws + L.xq), (float*)(ws + L.xs), st)))
     return rc;
   if (mark(2) != hipSuccess) return MEGAMOE_ERR_HIP;
 
   const PermuteOut po = make_permute_out(L, ws);
   const int nbI = I / kBlock, nbH = H / kBlock;
+  const int chunk = a16 ? kChunkRowsA16 : kChunkRows;
   const uint8_t* shared_w[3] = {t->shared_gate, t->shared_up, t->shared_down};
-  if ((rc = launch_permute(t->expert_ids, 0, T, K, E, S, nbI, nbH, L.ks, kChunkRows, 0, po, st, S > 0 ? shared_w : nullptr,
+  if ((rc = launch_permute(t->expert_ids, 0, T, K, E, S, nbI, nbH, L.ks, chunk, 0, po, st, S > 0 ? shared_w : nullptr,
                            (size_t)S * I * H)))
     return rc;
   if (mark(3) != hipSuccess) return MEGAMOE_ERR_HIP;
 
   ExpertArgs ea;
   fill_expert_args(d, L, t, ws, po, epi, ea);
+  if (a16) ea.gu.x16 = (const uint16_t*)x;
   const GateUpArgs& ga = ea.gu;
   const DownArgs& da = ea.dn;
   // As many workgroups as fit on the device at once, and no more than the most units the
   // routing can produce.
-  const bool split = split_gate_up(d);
-  const size_t units_max = expert_units_max(d, L, split);
+  const bool split = !a16 && split_gate_up(d);
+  const size_t units_max = expert_units_max(d, L, split, chunk);
   const size_t resident = (size_t)di.cus * di.experts_per_cu;
   const unsigned grid = (unsigned)(units_max < resident ? units_max : resident);
-  if (split)
+  if (a16)
+    hipLaunchKernelGGL((k_experts<false, true>), dim3(grid), dim3(256), 0, st, ea);
+  else if (split)
     hipLaunchKernelGGL(k_experts<true>, dim3(grid), dim3(256), 0, st, ea);
   else
     hipLaunchKernelGGL(k_experts<false>, dim3(grid), dim3(256), 0, st, ea);
@@ -5357,7 +5551,7 @@ int scratch_address(void** out) {
 
 extern "C" {
 
-int megamoe_abi_version(void) { return 10; }
+int megamoe_abi_version(void) { return 11; }
 
 const char* megamoe_status_string(int status) {
   switch (status) {
@@ -5500,6 +5694,21 @@ int megamoe_forward_ex(const megamoe_desc* desc, const megamoe_tensors* t, const
     }
   }
   return forward_impl(desc, t, (hipStream_t)stream, events ? ev : nullptr, block, epilogue);
+}
+
+int megamoe_forward_w8a16(const megamoe_desc* desc, const megamoe_tensors* t, const megamoe_block* block,
+                          const megamoe_epilogue* epilogue, void* stream, void* const* events) {
+  if (block && !(block->eps >= 0.0f)) return MEGAMOE_ERR_INVALID_ARGUMENT;
+  if (epilogue && ((epilogue->swiglu != 0 && epilogue->swiglu != 1) || !(epilogue->swiglu_limit >= 0.0f)))
+    return MEGAMOE_ERR_INVALID_ARGUMENT;
+  hipEvent_t ev[kStages + 1];
+  if (events) {
+    for (int i = 0; i < kStages + 1; ++i) {
+      if (!events[i]) return MEGAMOE_ERR_INVALID_ARGUMENT;
+      ev[i] = (hipEvent_t)events[i];
+    }
+  }
+  return forward_impl(desc, t, (hipStream_t)stream, events ? ev : nullptr, block, epilogue, true);
 }
 
 int megamoe_combine_by_expert_id(int32_t tokens, int32_t hidden, int32_t topk, const void* expert_out,

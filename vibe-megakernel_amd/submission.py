@@ -83,7 +83,8 @@ class MoELayer:
     ``single_launch=False`` selects the stream-ordered kernels (megamoe_forward /
     megamoe_forward_ex: router, select + quantization, permute, experts, combine;
     megamoe_mx_forward: permute, experts, combine), whose stage boundaries ``record`` can
-    mark."""
+    mark. The W8A16 form (case.activations "bf16") is stream-ordered only
+    (megamoe_forward_w8a16)."""
 
     def __init__(self, case: Case, single_launch: bool = True):
         self.case = case
@@ -92,7 +93,9 @@ class MoELayer:
         self._desc_ref = ctypes.byref(self.desc)
         self._specs = self._input_specs()
         self.mx = case.format == "mxfp4"
-        self.single_launch = single_launch
+        # The W8A16 form (bf16 activations) runs stream-ordered: megamoe_forward_w8a16.
+        self.a16 = case.activations == "bf16"
+        self.single_launch = single_launch and not self.a16
         self.stages = ("layer",) if single_launch else (_lib.STAGES_MX if self.mx else _lib.STAGES)
         size = ctypes.c_size_t(0)
         sizer = self.lib.megamoe_mx_workspace_bytes if self.mx else self.lib.megamoe_workspace_bytes
@@ -214,10 +217,23 @@ class MoELayer:
                                                           stream, handles), f"{c.id}: forward")
                 return {"y": y, "expert_ids": ids, "expert_weights": weights}
             if noalloc:
-                if self.block is not None or self.epilogue is not None or timed or events is not None:
+                if self.block is not None or self.epilogue is not None or self.a16 or timed or events is not None:
                     raise ValueError("the no-allocation entry point covers the plain layer form")
                 _lib.check(self.lib.megamoe_forward_noalloc(ctypes.byref(self.desc), ctypes.byref(tensors), stream),
                            f"{c.id}: forward (no allocation)")
+                return {"y": y, "expert_ids": ids, "expert_weights": weights}
+            if self.a16:
+                if timed:
+                    raise ValueError("the W8A16 form runs through megamoe_forward_w8a16 (use record() for stages)")
+                blk = None
+                if self.block is not None:
+                    blk = ctypes.byref(_lib.Block(norm_weight=inputs["ln2"].data_ptr() if c.norm != "none" else None,
+                                                  eps=float(c.norm_eps), weight_in_fp32=int(c.norm == "fp32_weight"),
+                                                  residual=int(c.residual)))
+                handles = (None if events is None else
+                           (ctypes.c_void_p * len(events))(*[e.cuda_event for e in events]))
+                _lib.check(self.lib.megamoe_forward_w8a16(ctypes.byref(self.desc), ctypes.byref(tensors), blk,
+                                                          self._epi_ref, stream, handles), f"{c.id}: forward")
                 return {"y": y, "expert_ids": ids, "expert_weights": weights}
             if self.block is not None or self.epilogue is not None:
                 if timed:
