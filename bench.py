@@ -74,6 +74,11 @@ def kernel_bytes(case, hit: int) -> dict:
         bs = math.ceil(S * I / 128)
         gu += 2 * S * I * H + 4 * 2 * bs * bh
         dn += H * S * I + 4 * bh * bs
+    if case.activations == "bf16":
+        # W8A16: x (bf16) in, h (bf16) out / in, d out
+        gu += 2 * T * H + 2 * rows * I + (2 * T * S * I if S else 0)
+        dn += 2 * rows * I + 2 * rows * H + ((2 * T * S * I + 2 * T * H) if S else 0)
+        return {"gate_up": gu, "down": dn}
     # activations in and out: x quantized (T*H + scales) in, h (rows * I + scales) out / in, d out
     gu += T * H + 4 * T * bh + rows * I + 4 * rows * bi + (T * S * I + 4 * T * math.ceil(S * I / 128) if S else 0)
     dn += rows * I + 4 * rows * bi + 2 * rows * H + ((T * S * I + 2 * T * H) if S else 0)
@@ -86,13 +91,17 @@ def mx_kernel(rows: int, experts: int) -> str:
     return "k_experts_mx_batch" if rows >= 24 * experts else "k_experts_mx"
 
 
-def fp8_kernel(case) -> str:
-    """The FP8 expert kernel the library runs: the split gate/up form when the whole-block
-    gate/up units cannot fill one round of a 512-workgroup grid with every expert hit and
-    the rows have 32 or more K blocks (split_gate_up in csrc/megamoe.hip)."""
+def _split(case) -> bool:
+    """split_gate_up in csrc/megamoe.hip: the split gate/up form when the whole-block gate/up
+    units cannot fill one round of a 512-workgroup grid with every expert hit and the rows
+    have 32 or more K blocks (never in the W8A16 form)."""
     hit = min(case.experts, case.tokens * case.topk) + case.shared_experts
-    split = hit * (case.intermediate // 128) < 512 and case.hidden // 128 >= 32
-    return "k_experts<true>" if split else "k_experts<false>"
+    return case.activations != "bf16" and hit * (case.intermediate // 128) < 512 and case.hidden // 128 >= 32
+
+
+def fp8_kernel(case) -> str:
+    """The FP8 expert kernel the library runs (k_experts<split, w8a16>)."""
+    return f"k_experts<{str(_split(case)).lower()}, {str(case.activations == 'bf16').lower()}>"
 
 
 def expert_kernel(case) -> str:
@@ -107,7 +116,7 @@ def layer_kernel(case) -> str:
     k_layer_mx for the MXFP4 form."""
     if case.format == "mxfp4":
         return "k_layer_mx"
-    return fp8_kernel(case).replace("k_experts", "k_layer")
+    return f"k_layer<{str(_split(case)).lower()}>"
 
 
 def measured_traffic(case, kernel: str = "k_experts") -> float | None:
@@ -379,6 +388,7 @@ def bench_case(case, steps: int, warmup: int, want_cpu: bool, cpu_budget: float)
         "device_warmup": f"{warm_calls} stream-ordered calls ({DEVICE_WARMUP_MS:.0f} ms) before the warmup steps",
         "rotation_sets": n_sets,
         "dtype": ("e2m1xe4m3->fp32 (E8M0 scales per 32; bf16 out)" if case.format == "mxfp4"
+                  else "e4m3xbf16->fp32 (W8A16; bf16 in/out)" if case.activations == "bf16"
                   else "e4m3xe4m3->fp32 (bf16 in/out)"),
     }
     if layer.single_launch:
@@ -408,8 +418,8 @@ def bench_case(case, steps: int, warmup: int, want_cpu: bool, cpu_budget: float)
         ex_bytes = kb["gate_up"] + kb["down"]
         result["roofline"] = {"bound": "hbm", "achieved": ex_bytes / (ex_ms * 1e-3) / 1e9, "peak": PEAK_HBM / 1e9,
                               "unit": "GB/s", "frac": ex_bytes / (ex_ms * 1e-3) / PEAK_HBM,
-                              "traffic": measured_traffic(case),
-                              "kernel": mx_kernel(case.tokens * case.topk, case.experts),
+                              "traffic": measured_traffic(case, expert_kernel(case).split("<")[0]),
+                              "kernel": expert_kernel(case),
                               "kernel_us": ex_ms * 1e3, "bytes_per_launch": ex_bytes}
     if want_cpu:
         _log(f"[bench] {case.id}: CPU oracle baseline and parity of the timed outputs")

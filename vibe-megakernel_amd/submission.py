@@ -96,7 +96,7 @@ class MoELayer:
         # The W8A16 form (bf16 activations) runs stream-ordered: megamoe_forward_w8a16.
         self.a16 = case.activations == "bf16"
         self.single_launch = single_launch and not self.a16
-        self.stages = ("layer",) if single_launch else (_lib.STAGES_MX if self.mx else _lib.STAGES)
+        self.stages = ("layer",) if self.single_launch else (_lib.STAGES_MX if self.mx else _lib.STAGES)
         size = ctypes.c_size_t(0)
         sizer = self.lib.megamoe_mx_workspace_bytes if self.mx else self.lib.megamoe_workspace_bytes
         _lib.check(sizer(ctypes.byref(self.desc), ctypes.byref(size)), f"{case.id}: workspace size")
