@@ -116,7 +116,7 @@ def layer_kernel(case) -> str:
     k_layer_mx for the MXFP4 form."""
     if case.format == "mxfp4":
         return "k_layer_mx"
-    return f"k_layer<{str(_split(case)).lower()}>"
+    return f"k_layer<{str(_split(case)).lower()}, {str(case.activations == 'bf16').lower()}>"
 
 
 def measured_traffic(case, kernel: str = "k_experts") -> float | None:

@@ -218,9 +218,17 @@ int megamoe_forward_ex(const megamoe_desc* desc, const megamoe_tensors* t, const
  * work (pow2_scales) does not apply. Replaces frontier.py:180-183 with quantize=False, which
  * the DeepSeek family uses for every expert GEMM (frontier.py:190, 265-270, DEEPSEEK_FP8_
  * ACTIVATIONS), in the MoE step of frontier.py:335-354. Stream-ordered (five launches, six
- * with the block's normalization); `events` as megamoe_forward_ex's. */
+ * with the block's normalization); `events` as megamoe_forward_ex's; the one-launch form is
+ * megamoe_layer_forward_w8a16. */
 int megamoe_forward_w8a16(const megamoe_desc* desc, const megamoe_tensors* t, const megamoe_block* block,
                           const megamoe_epilogue* epilogue, void* stream, void* const* events);
+
+/* megamoe_forward_w8a16 as ONE kernel launch (megamoe_layer_forward's persistent kernel with
+ * the W8A16 expert units): the arguments, the workspace rule (zeroed before its first use)
+ * and the results are megamoe_layer_forward's, and the results equal megamoe_forward_w8a16's
+ * bit for bit. `events` NULL or events[0..1]. Replaces what megamoe_forward_w8a16 replaces. */
+int megamoe_layer_forward_w8a16(const megamoe_desc* desc, const megamoe_tensors* t, const megamoe_block* block,
+                                const megamoe_epilogue* epilogue, void* stream, void* const* events);
 
 /* The layer (block == NULL) or the block, with an optional epilogue variant, as ONE kernel
  * launch: the arguments and results are megamoe_forward_ex's, bit for bit. The reference
@@ -387,7 +395,7 @@ const char* megamoe_status_string(int status);
  * megamoe_combine_by_expert_id in 5, plus megamoe_forward_noalloc in 6, plus
  * megamoe_layer_forward in 7, plus megamoe_layer_status in 8, plus megamoe_mx_layer_forward
  * and megamoe_mx_layer_status in 9, plus megamoe_e4m3_selftest in 10, plus
- * megamoe_forward_w8a16 in 11). */
+ * megamoe_forward_w8a16 and megamoe_layer_forward_w8a16 in 11). */
 int megamoe_abi_version(void);
 
 #ifdef __cplusplus

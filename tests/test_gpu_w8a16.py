@@ -1,6 +1,7 @@
 """GPU parity of the W8A16 form (bf16 activations into the expert GEMMs: frontier.py:180-183
 with quantize=False, the DeepSeek family's experts, frontier.py:190,265-270) against the CPU
-oracle, through megamoe_forward_w8a16.
+oracle, through megamoe_layer_forward_w8a16 (one launch, the submission's path), and that
+form equal bit for bit to the stream-ordered megamoe_forward_w8a16.
 
 Bars as the W8A8 layer's: expert ids bit-exact, weights within 1e-4 relative of the
 reference's, y within the band rule against the widened (FP32) W8A16 oracle and within
@@ -38,7 +39,7 @@ def _to(values, device):
 
 
 def _a16(c):
-    return replace(c, activations="bf16", max_gpu_launches=5)
+    return replace(c, activations="bf16")
 
 
 def _dev_cases():
@@ -61,10 +62,28 @@ def test_w8a16_matches_oracle_on_development_geometry(case):
         values = workloads.make_inputs(case, seed, "cpu")
         want, exact = layer.reference_and_oracle(case, values)
         run = submission.build(case.to_dict())
-        assert not run.layer.single_launch
+        assert run.layer.single_launch and run.layer.a16
         got = run(_to(values, DEV))
         torch.cuda.synchronize()
         _compare(case, got, want, exact)
+
+
+@pytest.mark.parametrize("case", _dev_cases() + [_a16(C.development(C.BLOCK_CASES[0]))], ids=lambda c: c.id)
+def test_w8a16_single_launch_equals_stream_ordered(case):
+    """The one-launch W8A16 form against its five launches, bit for bit, over consecutive calls
+    on one workspace (the control words must come back to zero after each call)."""
+    _log(f"w8a16 single vs stream-ordered {case.id}")
+    one = submission.MoELayer(case)
+    five = submission.MoELayer(case, single_launch=False)
+    assert one.single_launch and not five.single_launch
+    dev = torch.device(DEV)
+    for seed in (5, 6, 7):
+        values = _to(workloads.make_inputs(case, seed, "cpu"), DEV)
+        a, b = one(values), five(values)
+        torch.cuda.synchronize()
+        assert not one.gave_up(dev)
+        for k in a:
+            assert torch.equal(a[k], b[k]), (case.id, seed, k)
 
 
 def test_w8a16_is_not_the_w8a8_layer():
@@ -75,7 +94,7 @@ def test_w8a16_is_not_the_w8a8_layer():
     values = workloads.make_inputs(case, 7, "cpu")
     want, exact = layer.reference_and_oracle(case, values)
     a16 = submission.build(case.to_dict())(_to(values, DEV))
-    a8 = submission.build(replace(case, activations="fp8", max_gpu_launches=1).to_dict())(_to(values, DEV))
+    a8 = submission.build(replace(case, activations="fp8").to_dict())(_to(values, DEV))
     torch.cuda.synchronize()
     e16 = metrics.layer_checks(a16["y"].cpu(), exact["y"].to(torch.bfloat16))
     e8 = metrics.layer_checks(a8["y"].cpu(), exact["y"].to(torch.bfloat16))

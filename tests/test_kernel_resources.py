@@ -48,10 +48,11 @@ def test_expert_stream_kernels_have_no_scratch(kernel):
 # register file. None of them spills a VGPR: the routing keeps its logits, choices and bias in
 # LDS (and, from 512 experts, its selection keys), derives its expert indices from an opaque
 # lane so they are not hoisted out of the persistent loop, and the combine takes its first
-# slots by value. k_layer<false> keeps a 20-byte private segment that no instruction uses.
+# slots by value. k_layer<false, ...> keeps a 20-byte private segment that no instruction uses.
 LAYER_CEILINGS = {
-    "(anonymous namespace)::k_layer<false>": {"vgpr_spills": 0, "scratch_bytes": 20},
-    "(anonymous namespace)::k_layer<true>": {"vgpr_spills": 0, "scratch_bytes": 20},
+    "(anonymous namespace)::k_layer<false, false>": {"vgpr_spills": 0, "scratch_bytes": 20},
+    "(anonymous namespace)::k_layer<true, false>": {"vgpr_spills": 0, "scratch_bytes": 20},
+    "(anonymous namespace)::k_layer<false, true>": {"vgpr_spills": 0, "scratch_bytes": 20},  # the W8A16 form
     "(anonymous namespace)::k_layer_mx": {"vgpr_spills": 0, "scratch_bytes": 0},
 }
 

@@ -26,7 +26,7 @@ SYMBOLS = ("megamoe_workspace_bytes", "megamoe_forward", "megamoe_forward_events
            "megamoe_mx_forward", "megamoe_ep_dispatch", "megamoe_ep_experts", "megamoe_ep_combine",
            "megamoe_forward_ex", "megamoe_combine_by_expert_id", "megamoe_forward_noalloc",
            "megamoe_layer_forward", "megamoe_layer_status", "megamoe_mx_layer_forward", "megamoe_mx_layer_status",
-           "megamoe_e4m3_selftest", "megamoe_forward_w8a16")
+           "megamoe_e4m3_selftest", "megamoe_forward_w8a16", "megamoe_layer_forward_w8a16")
 ABI_VERSION = 11
 
 
@@ -112,6 +112,7 @@ def load() -> ctypes.CDLL:
                                        c_void_p]
     lib.megamoe_forward_ex.argtypes = [P(Desc), P(Tensors), P(Block), P(Epilogue), c_void_p, P(c_void_p)]
     lib.megamoe_forward_w8a16.argtypes = [P(Desc), P(Tensors), P(Block), P(Epilogue), c_void_p, P(c_void_p)]
+    lib.megamoe_layer_forward_w8a16.argtypes = [P(Desc), P(Tensors), P(Block), P(Epilogue), c_void_p, P(c_void_p)]
     lib.megamoe_layer_forward.argtypes = [P(Desc), P(Tensors), P(Block), P(Epilogue), c_void_p, P(c_void_p)]
     lib.megamoe_layer_status.argtypes = [P(Desc), c_void_p, c_size_t, P(ctypes.c_int32), c_void_p]
     lib.megamoe_combine_by_expert_id.argtypes = [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, c_void_p, c_void_p,

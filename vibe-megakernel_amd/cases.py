@@ -275,8 +275,7 @@ HEADLINE_VARIANTS: tuple[Case, ...] = (
     replace(next(c for c in CASES if c.id == HEADLINE), id=HEADLINE + "-nobias", bias="none",
             note="no correction bias: ~222 experts hit, ~2.3 rows each"),
     replace(next(c for c in CASES if c.id == HEADLINE), id=HEADLINE + "-w8a16", activations="bf16",
-            max_gpu_launches=5,
-            note="W8A16: bf16 activations into the expert GEMMs (stream-ordered, five launches)"),
+            note="W8A16: bf16 activations into the expert GEMMs"),
 )
 
 

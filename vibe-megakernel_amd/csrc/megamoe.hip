@@ -3083,7 +3083,8 @@ __device__ __forceinline__ int dense_state(int* ctl, const int* offsets, int e, 
   return st;
 }
 
-template <bool SPLIT>
+// A16: the W8A16 form (bf16 activations into the expert units, chunks of at most 32 rows).
+template <bool SPLIT, bool A16 = false>
 __global__ __launch_bounds__(256, 2) void k_layer(LayerArgs args) {
   typedef const __attribute__((address_space(4))) LayerArgs* ArgsPtr;
   typedef const __attribute__((address_space(4))) ExpertArgs* ExArgsPtr;
@@ -3190,7 +3191,8 @@ __global__ __launch_bounds__(256, 2) void k_layer(LayerArgs args) {
       if (publish_count(ctl, kCtlSelected, 1, a.T, -1, &units[0]) == a.T - 1) {
         // Every token is routed: this workgroup runs the permute, then publishes the lists.
         acquire_after_wait();
-        permute_block<true>(a.ids, 0, a.T, a.K, a.E, a.S, a.ex.gu.I / kBlock, a.H / kBlock, a.ks, kChunkRows, 0,
+        permute_block<true>(a.ids, 0, a.T, a.K, a.E, a.S, a.ex.gu.I / kBlock, a.H / kBlock, a.ks,
+                            A16 ? kChunkRowsA16 : kChunkRows, 0,
                             a.po, reinterpret_cast<int*>(rings), flags,
                             permute_tile_waves(a.T, a.E, 256, kPermuteLdsInts));
         publish_fence();
@@ -3263,12 +3265,12 @@ __global__ __launch_bounds__(256, 2) void k_layer(LayerArgs args) {
         const int c = g / nbI;
         const int st = c >= a.gu.S ? dense_state(ctl, a.gu.offsets, c - a.gu.S, &flags[0]) : 0;
         if (st != 2)
-          gateup_work(a.gu, g, red, ring,
-                      claiming(ReadyWait{my_signal_flag(ctl, kSigQuant), 1, &ctl[kCtlError], kWaitTicks, true, 2},
-                               queue, &ticket),
-                      st == 1);
+          gateup_work<A16>(a.gu, g, red, ring,
+                           claiming(ReadyWait{my_signal_flag(ctl, kSigQuant), 1, &ctl[kCtlError], kWaitTicks, true, 2},
+                                    queue, &ticket),
+                           st == 1);
       } else {
-        gateup_work(a.gu, g, red, ring, claiming(ReadyWait{nullptr, 0, nullptr}, queue, &ticket));
+        gateup_work<A16>(a.gu, g, red, ring, claiming(ReadyWait{nullptr, 0, nullptr}, queue, &ticket));
       }
       if (done) {
         publish_fence();
@@ -3282,10 +3284,10 @@ __global__ __launch_bounds__(256, 2) void k_layer(LayerArgs args) {
       const int st = dense && c >= sh ? dense_state(ctl, a.gu.offsets, c - sh, &flags[0]) : 0;
       if (st != 2) {
         const int need = dense ? dense_dn_need(c, a.dn.S, nbI) : (a.dn.chunks[c].x == a.dn.E ? a.dn.S * nbI : nbI);
-        down_work<true>(a.dn, v,
-                        claiming(ReadyWait{&a.ready[(size_t)c * a.ready_stride], need, &ctl[kCtlError]}, queue,
-                                 &ticket),
-                        ring, st == 1);
+        down_work<true, A16>(a.dn, v,
+                             claiming(ReadyWait{&a.ready[(size_t)c * a.ready_stride], need, &ctl[kCtlError]}, queue,
+                                      &ticket),
+                             ring, st == 1);
       }
       ++my_down;
     }
@@ -4987,7 +4989,7 @@ int forward_impl(const megamoe_desc* desc, const megamoe_tensors* t, hipStream_t
 // The layer (with `blk`, the block form) as one launch of k_layer; see the kernel for the
 // unit queue. `ev` is NULL or two events, recorded before and after the launch.
 int forward_layer_impl(const megamoe_desc* desc, const megamoe_tensors* t, const megamoe_block* blk,
-                       const megamoe_epilogue* epi, hipStream_t st, hipEvent_t* ev) {
+                       const megamoe_epilogue* epi, hipStream_t st, hipEvent_t* ev, bool a16 = false) {
   int rc = validate(desc);
   if (rc) return rc;
   if (!t) return MEGAMOE_ERR_INVALID_ARGUMENT;
@@ -5016,6 +5018,7 @@ int forward_layer_impl(const megamoe_desc* desc, const megamoe_tensors* t, const
   la.x_in = (const uint16_t*)t->x;
   la.xn = (uint16_t*)(ws + L.xn);
   la.x = norm ? la.xn : la.x_in;
+  if (a16) la.ex.gu.x16 = la.x;  // the W8A16 experts read the bf16 rows the router reads
   la.norm_w = norm ? (const uint16_t*)blk->norm_weight : nullptr;
   la.eps = blk ? blk->eps : 0.0f;
   la.weight_in_fp32 = blk ? blk->weight_in_fp32 : 0;
@@ -5051,8 +5054,9 @@ int forward_layer_impl(const megamoe_desc* desc, const megamoe_tensors* t, const
 
   // As many workgroups as fit on the device at once, and no more than the most units the
   // queue can hold.
-  const bool split = split_gate_up(d);
-  const size_t units_max = (size_t)la.n_norm + la.n_router + T + expert_units_max(d, L, split) +
+  const bool split = !a16 && split_gate_up(d);
+  const size_t units_max = (size_t)la.n_norm + la.n_router + T +
+                           expert_units_max(d, L, split, a16 ? kChunkRowsA16 : kChunkRows) +
                            ((size_t)T * H + kCombineUnit - 1) / kCombineUnit;
   la.dense = L.dense;
   la.n_ready = L.n_ready_l;
@@ -5067,7 +5071,9 @@ int forward_layer_impl(const megamoe_desc* desc, const megamoe_tensors* t, const
   const char* rescue = getenv("MEGAMOE_FORCE_RESCUE");
   la.force_rescue = rescue && rescue[0] == '1' ? 1 : 0;
   if (mark(0) != hipSuccess) return MEGAMOE_ERR_HIP;
-  if (split)
+  if (a16)
+    hipLaunchKernelGGL((k_layer<false, true>), dim3(grid), dim3(256), 0, st, la);
+  else if (split)
     hipLaunchKernelGGL(k_layer<true>, dim3(grid), dim3(256), 0, st, la);
   else
     hipLaunchKernelGGL(k_layer<false>, dim3(grid), dim3(256), 0, st, la);
@@ -5589,6 +5595,19 @@ int megamoe_layer_forward(const megamoe_desc* desc, const megamoe_tensors* t, co
     ev[1] = (hipEvent_t)events[1];
   }
   return forward_layer_impl(desc, t, block, epilogue, (hipStream_t)stream, events ? ev : nullptr);
+}
+
+int megamoe_layer_forward_w8a16(const megamoe_desc* desc, const megamoe_tensors* t, const megamoe_block* block,
+                                const megamoe_epilogue* epilogue, void* stream, void* const* events) {
+  if (epilogue && ((epilogue->swiglu != 0 && epilogue->swiglu != 1) || !(epilogue->swiglu_limit >= 0.0f)))
+    return MEGAMOE_ERR_INVALID_ARGUMENT;
+  hipEvent_t ev[2];
+  if (events) {
+    if (!events[0] || !events[1]) return MEGAMOE_ERR_INVALID_ARGUMENT;
+    ev[0] = (hipEvent_t)events[0];
+    ev[1] = (hipEvent_t)events[1];
+  }
+  return forward_layer_impl(desc, t, block, epilogue, (hipStream_t)stream, events ? ev : nullptr, true);
 }
 
 int megamoe_layer_status(const megamoe_desc* desc, const void* workspace, size_t workspace_bytes, int32_t* gave_up,

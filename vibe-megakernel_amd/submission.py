@@ -83,8 +83,8 @@ class MoELayer:
     ``single_launch=False`` selects the stream-ordered kernels (megamoe_forward /
     megamoe_forward_ex: router, select + quantization, permute, experts, combine;
     megamoe_mx_forward: permute, experts, combine), whose stage boundaries ``record`` can
-    mark. The W8A16 form (case.activations "bf16") is stream-ordered only
-    (megamoe_forward_w8a16)."""
+    mark. The W8A16 form (case.activations "bf16") runs through megamoe_layer_forward_w8a16
+    and megamoe_forward_w8a16 likewise."""
 
     def __init__(self, case: Case, single_launch: bool = True):
         self.case = case
@@ -93,9 +93,10 @@ class MoELayer:
         self._desc_ref = ctypes.byref(self.desc)
         self._specs = self._input_specs()
         self.mx = case.format == "mxfp4"
-        # The W8A16 form (bf16 activations) runs stream-ordered: megamoe_forward_w8a16.
+        # The W8A16 form (bf16 activations): megamoe_layer_forward_w8a16 (one launch) or
+        # megamoe_forward_w8a16 (stream-ordered).
         self.a16 = case.activations == "bf16"
-        self.single_launch = single_launch and not self.a16
+        self.single_launch = single_launch
         self.stages = ("layer",) if self.single_launch else (_lib.STAGES_MX if self.mx else _lib.STAGES)
         size = ctypes.c_size_t(0)
         sizer = self.lib.megamoe_mx_workspace_bytes if self.mx else self.lib.megamoe_workspace_bytes
@@ -213,8 +214,9 @@ class MoELayer:
                                                   eps=float(c.norm_eps), weight_in_fp32=int(c.norm == "fp32_weight"),
                                                   residual=int(c.residual)))
                 handles = None if events is None else (ctypes.c_void_p * 2)(*[e.cuda_event for e in events])
-                _lib.check(self.lib.megamoe_layer_forward(self._desc_ref, ctypes.byref(tensors), blk, self._epi_ref,
-                                                          stream, handles), f"{c.id}: forward")
+                forward = self.lib.megamoe_layer_forward_w8a16 if self.a16 else self.lib.megamoe_layer_forward
+                _lib.check(forward(self._desc_ref, ctypes.byref(tensors), blk, self._epi_ref, stream, handles),
+                           f"{c.id}: forward")
                 return {"y": y, "expert_ids": ids, "expert_weights": weights}
             if noalloc:
                 if self.block is not None or self.epilogue is not None or self.a16 or timed or events is not None:
