@@ -45,7 +45,8 @@ def _fp8_cases():
     return [C.development(C.case(C.HEADLINE)), C.case("moe-fp8-tiny-t4"),
             C.development(C.case("moe-fp8-mixtral-t16"), hidden=4096, intermediate=512, tokens=40),  # split gate/up
             C.development(C.BLOCK_CASES[0]),
-            C.development(C.case(C.HEADLINE), tokens=8)]  # the dense schedule with a shared expert
+            C.development(C.case(C.HEADLINE), tokens=8),  # the dense schedule with a shared expert
+            C.development(C.case(C.HEADLINE + "-w8a16"))]  # the W8A16 form
 
 
 @pytest.mark.parametrize("case", _fp8_cases(), ids=lambda c: c.id)
