@@ -8,7 +8,8 @@ depending on the data. So this runs many calls on random development geometries 
 configs' families, the block and epilogue forms, random token counts) with random seeds,
 consecutive calls sharing one workspace, and checks each against the stream-ordered kernels
 bit for bit and the status word after each call (half the calls at 16 tokens or fewer, most
-of them in the dense schedule, whose expert units run before the routing is known). It stops
+of them in the dense schedule, whose expert units run before the routing is known; a quarter
+in the W8A16 form). It stops
 at the first mismatch and names the geometry and seed. MEGAMOE_SOAK_SECONDS sets the time bound (default 20 s).
 """
 
@@ -43,6 +44,8 @@ def _geometries(rng):
                  C.development(C.BLOCK_CASES[0]), C.development(C.VARIANT_CASES[0])]
     while True:
         base = rng.choice(families)
+        if base.format == "fp8" and rng.random() < 0.25:  # a quarter of the calls in the W8A16 form
+            base = C.Case.from_dict({**base.to_dict(), "id": base.id + "-w8a16", "activations": "bf16"})
         # Half the calls at 16 tokens or fewer, where the dense schedule runs (with T*K >= E).
         tokens = rng.randint(1, 16) if rng.random() < 0.5 else rng.randint(17, 130)
         yield C.Case.from_dict({**base.to_dict(), "id": f"{base.id}-soak",
