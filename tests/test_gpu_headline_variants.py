@@ -1,11 +1,13 @@
-"""GPU parity of two variants of the headline DeepSeek-V3 shape, through the C ABI.
+"""GPU parity of the variants of the headline DeepSeek-V3 shape, through the C ABI.
 
 "-ue8m0": power-of-two (UE8M0) scales for the weights and for the activations quantized in
 the layer (x per 128, h per 128), the DeepSeek family's scale format (frontier.py:120,252;
 quantization.py:57-59). "-nobias": the routing without the correction bias, ~222 experts hit
-at ~2.3 rows each. Each is checked on its development geometry (two seeds) and at full size
-on every token against the oracle, and the single launch equals the stream-ordered kernels
-bit for bit on both.
+at ~2.3 rows each. "-w8a16": bf16 activations into the expert GEMMs (frontier.py:180-183,
+quantize=False). "-w8a16-ue8m0": both, the DeepSeek family's expert numerics as the
+reference runs them (frontier.py:252-270). Each is checked on its development geometry (two
+seeds) and at full size on every token against the oracle, and the single launch equals the
+stream-ordered kernels bit for bit on each.
 """
 
 from __future__ import annotations

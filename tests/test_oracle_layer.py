@@ -94,7 +94,8 @@ def _cases():
     return [C.development(C.case("moe-fp8-deepseek-v3-t64"), tokens=5, experts=8, topk=3),
             C.development(C.case("moe-fp8-mixtral-t16"), tokens=4),
             C.development(C.case("moe-fp8-kimi-k2-t128"), tokens=3, experts=8),
-            C.development(C.case("moe-fp8-deepseek-v3-t64-w8a16"), tokens=5, experts=8, topk=3)]
+            C.development(C.case("moe-fp8-deepseek-v3-t64-w8a16"), tokens=5, experts=8, topk=3),
+            C.development(C.case("moe-fp8-deepseek-v3-t64-w8a16-ue8m0"), tokens=5, experts=8, topk=3)]
 
 
 @pytest.mark.parametrize("case", _cases(), ids=lambda c: c.id)

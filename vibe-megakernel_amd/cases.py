@@ -269,6 +269,10 @@ VARIANT_CASES: tuple[Case, ...] = (
 # ~2.3 rows each, the uniform-routing expectation that the per-config floors assume.
 # "-w8a16": the expert GEMMs with bf16 activations (frontier.py:180-183, quantize=False),
 # as the DeepSeek family's TileRT numerics run them (frontier.py:190,265-270).
+# "-w8a16-ue8m0": both at once, the expert numerics of the DeepSeek family as the reference
+# runs them (frontier.py:252-270: power=True for the weights' scales, quantize=False for
+# every expert projection, since gate, up and down are not in DEEPSEEK_FP8_ACTIVATIONS); with
+# no activation quantized, the power-of-two rule reaches only the weights.
 HEADLINE_VARIANTS: tuple[Case, ...] = (
     replace(next(c for c in CASES if c.id == HEADLINE), id=HEADLINE + "-ue8m0", power_of_two=True,
             note="power-of-two (UE8M0) weight and activation scales"),
@@ -276,6 +280,8 @@ HEADLINE_VARIANTS: tuple[Case, ...] = (
             note="no correction bias: ~222 experts hit, ~2.3 rows each"),
     replace(next(c for c in CASES if c.id == HEADLINE), id=HEADLINE + "-w8a16", activations="bf16",
             note="W8A16: bf16 activations into the expert GEMMs"),
+    replace(next(c for c in CASES if c.id == HEADLINE), id=HEADLINE + "-w8a16-ue8m0", activations="bf16",
+            power_of_two=True, note="W8A16 with UE8M0 weight scales: the DeepSeek family's expert numerics"),
 )
 
 
