@@ -9,8 +9,11 @@ configs' families, the block and epilogue forms, random token counts) with rando
 consecutive calls sharing one workspace, and checks each against the stream-ordered kernels
 bit for bit and the status word after each call (half the calls at 16 tokens or fewer, most
 of them in the dense schedule, whose expert units run before the routing is known; a quarter
-in the W8A16 form). It stops
-at the first mismatch and names the geometry and seed. MEGAMOE_SOAK_SECONDS sets the time bound (default 20 s).
+in the W8A16 form). The MXFP4 layer's one launch (k_layer_mx: the permute, the expert units
+and the combine of one queue, the same hand-overs) takes part as well, against its three
+stream-ordered kernels. It stops at the first mismatch and names the geometry and seed.
+MEGAMOE_SOAK_SECONDS sets the time bound (default 20 s), MEGAMOE_SOAK_SEED the stream of
+geometries and seeds (default 20261202).
 """
 
 from __future__ import annotations
@@ -41,7 +44,10 @@ def _geometries(rng):
     families += [C.development(C.case("moe-fp8-kimi-k2-t128"), experts=8, topk=4),  # hot experts
                  C.development(C.case("moe-fp8-mixtral-t16"), hidden=4096, intermediate=512),  # split gate/up
                  C.development(C.case("moe-fp8-kimi-k2-t128"), experts=16, topk=4),  # Zipf: many unpicked
-                 C.development(C.BLOCK_CASES[0]), C.development(C.VARIANT_CASES[0])]
+                 C.development(C.BLOCK_CASES[0]), C.development(C.VARIANT_CASES[0]),
+                 # MXFP4, one launch: ~8 rows per expert or fewer at 64 experts; 16 experts reach
+                 # the batch shape (stream-ordered in both forms) from ~100 tokens.
+                 C.development(C.MX_CASES[0], experts=64), C.development(C.MX_CASES[0])]
     while True:
         base = rng.choice(families)
         if base.format == "fp8" and rng.random() < 0.25:  # a quarter of the calls in the W8A16 form
@@ -52,24 +58,41 @@ def _geometries(rng):
                                 "params": {**base.params, "tokens": tokens}})
 
 
+def _mx_call_inputs(case, seed, weights):
+    """An MXFP4 call's inputs on the geometry's expert weights (generating MXFP4 weights takes
+    most of a call's time): x and the routing anew from the seed, as make_inputs draws them."""
+    x = torch.randn((case.tokens, case.hidden), generator=torch.Generator(device=DEV).manual_seed(seed), device=DEV)
+    values = dict(weights)
+    values["x"], values["x_scales"] = workloads.pack_e4m3_e8m0(x)
+    values["topk_idx"], values["topk_weights"] = workloads.mx_routing(case, seed, DEV)
+    return values
+
+
 def test_randomized_single_launch_soak():
     seconds = float(os.environ.get("MEGAMOE_SOAK_SECONDS", "20"))
-    rng = random.Random(20261202)
+    rng = random.Random(int(os.environ.get("MEGAMOE_SOAK_SEED", "20261202")))
     t_end = time.monotonic() + seconds
     calls = geometries = 0
+    t_note = time.monotonic() + 30.0
     for case in _geometries(rng):
         if time.monotonic() > t_end:
             break
+        if time.monotonic() > t_note:  # a line every 30 s for long runs (shown with pytest -s)
+            _log(f"soak: {calls} calls over {geometries} geometries so far")
+            t_note += 30.0
         geometries += 1
         one = submission.MoELayer(case)
         five = submission.MoELayer(case, single_launch=False)
+        weights = None
         for _ in range(rng.randint(4, 12)):  # consecutive calls on one workspace
             seed = rng.randrange(1 << 30)
             what = f"{case.id} T={case.tokens} H={case.hidden} E={case.experts} K={case.topk} seed {seed}"
-            values = workloads.make_inputs(case, seed, DEV)
+            values = _mx_call_inputs(case, seed, weights) if weights is not None else workloads.make_inputs(case, seed, DEV)
+            if case.format == "mxfp4":
+                weights = {k: v for k, v in values.items() if k.startswith(("l1_", "l2_"))}
             a, b = one(values), five(values)
             torch.cuda.synchronize()
-            for k in ("y", "expert_ids", "expert_weights"):
+            for k in a:  # y, and the fp8 layers' expert ids and weights
                 assert torch.equal(a[k], b[k]), f"{what}: {k} differs after {calls} calls"
             assert not one.gave_up(torch.device(DEV)), f"{what}: a bounded wait gave up"
             calls += 1

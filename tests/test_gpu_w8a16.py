@@ -138,3 +138,25 @@ def test_w8a16_full_size_on_every_token():
     del values
     torch.cuda.empty_cache()
     check_every_token(W8A16, got, cpu)
+
+
+def test_w8a16_dense_single_launch_over_many_calls():
+    """Regression: the W8A16 single launch once quantized x into the region that holds its bf16
+    h, leaving write-through copies of those lines in the routing units' XCD L2s, where a
+    down unit on the same XCD could read a stale h row (NaN in one 128-column block of y,
+    about one call in 470 on this geometry). 3000 consecutive calls of the dense schedule on
+    one workspace, each equal to the stream-ordered form bit for bit."""
+    base = C.development(C.case("moe-fp8-mixtral-t16"), hidden=4096, intermediate=512)
+    case = _a16(replace(base, params={**base.params, "tokens": 4}))
+    _log(f"w8a16 dense, many calls {case.id} T={case.tokens} H={case.hidden} E={case.experts}")
+    one = submission.MoELayer(case)
+    five = submission.MoELayer(case, single_launch=False)
+    assert one.single_launch and one.a16
+    dev = torch.device(DEV)
+    for i in range(3000):
+        values = workloads.make_inputs(case, 1000 + i, DEV)
+        a, b = one(values), five(values)
+        torch.cuda.synchronize()
+        for k in a:
+            assert torch.equal(a[k], b[k]), f"call {i} (seed {1000 + i}): {k} differs"
+        assert not one.gave_up(dev), f"call {i}: a bounded wait gave up"

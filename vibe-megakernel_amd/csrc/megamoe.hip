@@ -3158,9 +3158,15 @@ __global__ __launch_bounds__(256, 2) void k_layer(LayerArgs args) {
       const int nbh = a.H / kBlock, lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
       const bool back = resume >= 0;  // after a rescued router unit: look again at once
       if (!back) {
-        quant_row(a.x + (size_t)t * a.H, a.xq + (size_t)t * a.H, a.xs + (size_t)t * nbh, nbh, a.pow2, lane, wv,
-                  reinterpret_cast<float*>(rings));
-        // The dense schedule's gate/up units read every token's row once all are quantized.
+        // The W8A16 form quantizes nothing: its experts read the bf16 rows, and the region of
+        // the quantized x holds its bf16 h. A write-through store of x there would leave the
+        // line in this XCD's L2, where a down unit on the same XCD, reading the h row that a
+        // gate/up unit on another XCD wrote later, would find the stale copy.
+        if constexpr (!A16)
+          quant_row(a.x + (size_t)t * a.H, a.xq + (size_t)t * a.H, a.xs + (size_t)t * nbh, nbh, a.pow2, lane, wv,
+                    reinterpret_cast<float*>(rings));
+        // The dense schedule's gate/up units read every token's row once all are quantized
+        // (W8A16: once every routing unit has passed its wait for the normalized rows).
         if (a.dense) publish_count(ctl, kCtlQuant, 1, a.T, kSigQuant, &units[0]);
       }
       resume = -1;
@@ -4667,7 +4673,9 @@ Layout make_layout(const megamoe_desc& d) {
   const size_t R = L.dense ? E * T : T * K;  // routed rows: grouped, or e*T + t
   L.rows_r = (int)R;
   // The quantized x and h of the W8A8 form and the bf16 h of the W8A16 form (which
-  // quantizes nothing) share one region.
+  // quantizes nothing) share one region. A call writes only one of the two: in the single
+  // launch, a line written through from one XCD and again from another would leave the
+  // first XCD's L2 with the older copy.
   {
     const size_t q[6] = {align_up(T * H), align_up(T * (H / kBlock) * sizeof(float)), align_up(R * I),
                          align_up(R * scale_ld((int)(I / kBlock)) * sizeof(float)), align_up(T * S * I),
